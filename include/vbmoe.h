@@ -1,0 +1,252 @@
+/*
+ * vbmoe.h — C ABI of the MI355X (gfx950) routed-expert MoE engine.
+ *
+ * One shared library, libvbmoe.so, exports every symbol declared here. Signatures use plain
+ * pointers, sizes and ggml type ids only; device pointers are HIP device addresses and every
+ * `stream` argument is a hipStream_t passed as void* (NULL = the legacy default stream).
+ * All compute entry points are stream-ordered: they enqueue work and return without waiting.
+ *
+ * Errors: every function returns a vbm_status. A non-zero status leaves a message readable with
+ * vbm_last_error() on the calling thread. The mapping mirrors the reference engine's exception
+ * contract (tools/engine/expert_dispatch.cpp:25-49, tools/engine/quantized_cuda.cu:220-226):
+ * shape, route and residency errors are VBM_ERR_INVALID_ARGUMENT (std::invalid_argument there);
+ * device failures and non-finite output are VBM_ERR_RUNTIME (std::runtime_error there).
+ *
+ * Data formats are ggml's (llama.cpp commit 620d2225, "b11669"):
+ *   block_mxfp4 {uint8 e; uint8 qs[16]}   17 B per 32 weights; element i<16 is the low nibble of
+ *                                          qs[i], element i>=16 the high nibble of qs[i-16].
+ *   block_q8_0  {fp16 d; int8 qs[32]}     34 B per 32 values.
+ * Expert banks hold the same bytes re-laid out for 128-bit coalesced loads (see
+ * vbm_bank_upload); vbm_bank_export returns the original ggml bytes, bit for bit.
+ */
+#ifndef VBMOE_H
+#define VBMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum vbm_status {
+    VBM_OK = 0,
+    VBM_ERR_INVALID_ARGUMENT = 1,
+    VBM_ERR_RUNTIME = 2,
+    VBM_ERR_UNSUPPORTED = 3,
+    VBM_ERR_OUT_OF_MEMORY = 4
+} vbm_status;
+
+/* ggml type ids (ggml.h enum ggml_type; MXFP4 = 39 per tests/test_cpu_research.py:56). */
+enum {
+    VBM_TYPE_F32 = 0,
+    VBM_TYPE_F16 = 1,
+    VBM_TYPE_Q8_0 = 8,
+    VBM_TYPE_I32 = 26,
+    VBM_TYPE_MXFP4 = 39
+};
+
+/* Activation of the expert FFN (tools/engine/f32_experts.hpp:14 F32Activation). */
+enum {
+    VBM_ACT_SILU = 0,          /* g / (1 + exp(-g)) * u                                  */
+    VBM_ACT_SWIGLU_OAI = 1     /* x=min(g,7), y=clamp(u,-7,7): x/(1+exp(-1.702x))*(y+1)   */
+};
+
+/* Dot-product accumulation order.
+ *   VBM_ORDER_EXACT: the ggml x86 CPU contract — per 32-block integer dots split in eight
+ *     4-element lanes, per-lane fp32 FMA chains (even/odd blocks for MXFP4), fixed final tree.
+ *     Bit-identical to the CPU vec_dot.
+ *   VBM_ORDER_FAST: per-block integer dots are still exact; the fp32 accumulation order is free. */
+enum { VBM_ORDER_EXACT = 0, VBM_ORDER_FAST = 1 };
+
+const char * vbm_last_error(void);
+int vbm_abi_version(void);
+
+/* ----------------------------------------------------------------------------------------------
+ * Device plumbing (thin wrappers over the HIP runtime so that callers need no HIP headers).
+ * -------------------------------------------------------------------------------------------- */
+vbm_status vbm_device_count(int * count);
+vbm_status vbm_set_device(int device);
+vbm_status vbm_device_name(int device, char * name, size_t capacity);
+vbm_status vbm_mem_info(size_t * free_bytes, size_t * total_bytes);
+vbm_status vbm_malloc(void ** device_ptr, size_t bytes);
+vbm_status vbm_free(void * device_ptr);
+vbm_status vbm_host_alloc(void ** host_ptr, size_t bytes);  /* pinned (hipHostMalloc)          */
+vbm_status vbm_host_free(void * host_ptr);
+vbm_status vbm_memcpy_h2d(void * dst, const void * src, size_t bytes, void * stream);
+vbm_status vbm_memcpy_d2h(void * dst, const void * src, size_t bytes, void * stream);
+vbm_status vbm_memcpy_d2d(void * dst, const void * src, size_t bytes, void * stream);
+vbm_status vbm_memset(void * dst, int value, size_t bytes, void * stream);
+vbm_status vbm_stream_create(void ** stream);               /* non-blocking, default priority  */
+vbm_status vbm_stream_destroy(void * stream);
+vbm_status vbm_stream_synchronize(void * stream);
+vbm_status vbm_device_synchronize(void);
+vbm_status vbm_event_create(void ** event);
+vbm_status vbm_event_destroy(void * event);
+vbm_status vbm_event_record(void * event, void * stream);
+vbm_status vbm_event_synchronize(void * event);
+vbm_status vbm_event_query(void * event, int * done);
+vbm_status vbm_event_elapsed_ms(void * start, void * stop, float * ms);
+
+/* ----------------------------------------------------------------------------------------------
+ * Synthetic inputs. A counter-based generator: every byte is a pure function of
+ * (seed, stream id, element index), so host and device produce identical tensors and any subset
+ * can be regenerated independently. Float tensors are Box-Muller normals computed in double on
+ * the host. Follows the seeded-fixture pattern of tools/trace/make_moe_fixture.py:20-156.
+ * -------------------------------------------------------------------------------------------- */
+/* MXFP4 expert weights in ggml layout: blocks [first_block, first_block + n_blocks) of tensor
+ * `stream`; codes uniform nibbles, exponent byte = 127 + U{exp_lo..exp_hi}. */
+vbm_status vbm_synth_mxfp4_host(uint64_t seed, uint64_t stream, uint64_t first_block,
+                                uint64_t n_blocks, int exp_lo, int exp_hi, void * dst);
+/* Q8_0 weights in ggml layout: int8 codes uniform in [-127,127], fp16 scale = fp16(U(lo,hi)). */
+vbm_status vbm_synth_q8_0_host(uint64_t seed, uint64_t stream, uint64_t first_block,
+                               uint64_t n_blocks, float scale_lo, float scale_hi, void * dst);
+/* fp32 N(mean, std) values [first, first + n) of tensor `stream`. Multithreaded. */
+vbm_status vbm_synth_normal_host(uint64_t seed, uint64_t stream, uint64_t first, uint64_t n,
+                                 float mean, float std_dev, float * dst);
+
+/* ----------------------------------------------------------------------------------------------
+ * Expert banks. A bank holds `n_slots` expert matrices of `rows` x `k` weights of one quantized
+ * type (MXFP4 or Q8_0) in device memory, re-laid out in 32-row tiles so that each lane issues
+ * 16-byte loads and a wavefront reads whole 1 KiB runs. Byte count per slot equals the ggml byte
+ * count (rows * k/32 * 17 or 34); the layout is a permutation, with the exponent byte stored
+ * xor 0x80 (= e - 128 as a signed byte). Replaces the device expert bank of
+ * Mxfp4NativeCudaDown::Impl (tools/engine/quantized_cuda.cu:367-407) and the llama_moe_cache
+ * bank tensors (third_party/patches/llama-b11669-hybrid-experts.patch:2573-2589).
+ *
+ * Fused gate/up banks (interleave = 1): a 2*I-row expert whose ggml rows [0,I) are gate and
+ * [I,2I) up (the fused bank of hybrid-experts.patch:2573-2589) is stored so that each 32-row tile
+ * holds gate rows 16t..16t+15 then up rows 16t..16t+15; the fused kernels depend on it.
+ * -------------------------------------------------------------------------------------------- */
+typedef struct vbm_bank vbm_bank;
+
+vbm_status vbm_bank_create(int type, int64_t rows, int64_t k, int64_t n_slots, int interleave,
+                           vbm_bank ** bank);
+vbm_status vbm_bank_destroy(vbm_bank * bank);
+/* Geometry: bytes of one slot, device base address of the bank. */
+vbm_status vbm_bank_info(const vbm_bank * bank, int * type, int64_t * rows, int64_t * k,
+                         int64_t * n_slots, size_t * slot_bytes, void ** device_base);
+/* Upload one expert (ggml row-major blocks, slot_bytes long) into `slot`. `src` may be host
+ * (pageable or pinned) or device memory (`src_on_device`). Host sources are staged through a
+ * bounded pinned pool and copied on `stream`; the repack runs on the device. */
+vbm_status vbm_bank_upload(vbm_bank * bank, int64_t slot, const void * src, int src_on_device,
+                           void * stream);
+/* Lossless export of one slot back to ggml bytes (host destination; synchronous on `stream`).
+ * Mirrors export_expert (hybrid-experts.patch:2065-2082) and the repack round trip of
+ * tests/test_masked_matmul.cpp:59-72. */
+vbm_status vbm_bank_export(const vbm_bank * bank, int64_t slot, void * dst_host, size_t capacity,
+                           void * stream);
+/* Fill slots [first_slot, first_slot + count) on the device with the synthetic generator; the
+ * expert in slot s gets ggml blocks starting at (first_expert + s - first_slot) * blocks_per_slot
+ * of tensor `stream_id` (identical to vbm_synth_*_host on the same block range). */
+vbm_status vbm_bank_generate(vbm_bank * bank, int64_t first_slot, int64_t count,
+                             uint64_t seed, uint64_t stream_id, int64_t first_expert,
+                             float p0, float p1, void * stream);
+
+/* ----------------------------------------------------------------------------------------------
+ * ggml-level operators (drop-in for the ggml ops of the routed-expert branch).
+ * -------------------------------------------------------------------------------------------- */
+
+/* quantize_row_q8_0 with the x86 contract restated at
+ * third_party/patches/llama-b11669-mxfp4-q8-parity-experimental.patch:41-44,95-96:
+ * per 32 values amax, d = fp16_rn(amax/127), q = RNE(x * (127/amax)) (0 when amax == 0).
+ * `n_rows` rows of `k` floats (row stride `x_stride` floats) -> n_rows * k/32 blocks. */
+vbm_status vbm_quantize_q8_0(const float * x, int64_t n_rows, int64_t k, int64_t x_stride,
+                             void * dst_q8, void * stream);
+
+/* GGML_OP_MUL_MAT_ID on a bank (ggml-cpu ggml_compute_forward_mul_mat_id,
+ * hybrid-experts.patch:559-640; engine NativeCpuExperts::project, tools/engine/native_cpu.cpp:91-104):
+ *   dst[:, r, t] = bank[slot(ids[r,t])] . b[:, r mod b_ne1, t]   (+ bias[:, ids[r,t]] if bias)
+ * - ids: int32 [n_ids, n_tokens] with element stride 1 and token stride ids_stride (ints);
+ *   -1 zeroes that output row (hybrid-experts.patch:617-621); otherwise 0 <= id < n_as.
+ * - expert_to_slot: optional int32 [n_as] device map (NULL = identity); -1 = not resident,
+ *   which is an error (VBM_ERR_INVALID_ARGUMENT, checked on the host copy `expert_to_slot_host`
+ *   when given).
+ * - b: type F32 (quantized on the fly to the bank's vec_dot type, Q8_0) or Q8_0 blocks;
+ *   shape [k, b_ne1, n_tokens] contiguous; b_ne1 is 1 (broadcast) or n_ids.
+ * - bias: optional fp32 [n_as][rows] (ADD_ID, hybrid-experts.patch:1464-1480).
+ * - dst: fp32 [rows, n_ids, n_tokens] contiguous.
+ * - order: VBM_ORDER_EXACT or VBM_ORDER_FAST.
+ * Uses the device grouping pass (vbm_group_by_expert) so every expert's weights stream once per
+ * call, whatever the number of tokens routed to it. */
+vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot,
+                          const int32_t * expert_to_slot_host, int64_t n_as,
+                          int b_type, const void * b, int64_t b_ne1,
+                          const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride,
+                          const float * bias, float * dst, int order, void * stream);
+
+/* GGML_OP_ADD_ID: y[:, r, t] += bias[:, ids[r,t]] for ids != -1 (rows x n_ids x n_tokens). */
+vbm_status vbm_add_id(float * y, const float * bias, const int32_t * ids, int64_t rows,
+                      int64_t n_ids, int64_t n_tokens, int64_t ids_stride, void * stream);
+
+/* GGML_OP_GLU swiglu_oai (alpha, limit) and swiglu (SiLU-gated) over n values:
+ * out[i] = act(gate[i], up[i]); gate/up/out may use row strides (floats). */
+vbm_status vbm_glu(int activation, const float * gate, const float * up, float * out,
+                   int64_t n_rows, int64_t width, int64_t gate_stride, int64_t up_stride,
+                   int64_t out_stride, float alpha, float limit, void * stream);
+
+/* Router: logits (given, or W_r . x with W_r fp32 [n_expert][k_hidden] and optional bias,
+ * computed in the ggml x86 vec_dot_f32 order) -> top-k (value desc, then lower index:
+ * tools/trace/topk-tie-probe.cpp:111-113) -> softmax over the k selected
+ * (gpt-oss SOFTMAX_WEIGHT gating). If `router_w` is NULL the `logits` input is used;
+ * otherwise logits are written to `logits` (may be NULL). ids [n_tokens][k] int32,
+ * weights [n_tokens][k] fp32. `normalize` = 0 gives plain softmax-over-selected. */
+vbm_status vbm_router_topk_softmax(const float * router_w, const float * router_b,
+                                   const float * x, int64_t k_hidden, float * logits,
+                                   int64_t n_expert, int64_t n_tokens, int64_t top_k,
+                                   int32_t * ids, float * weights, void * stream);
+
+/* Token->expert grouping (the MMID row mapping of hybrid-experts.patch:606-631): a stable
+ * counting sort of the (token, rank) pairs by expert.
+ *   counts[n_as], offsets[n_as + 1] (exclusive prefix), rows[n_ids*n_tokens] = token*n_ids+rank
+ *   listed expert by expert, token-major and rank-minor within an expert. -1 ids are skipped.
+ * Invalid ids (outside [-1, n_as)) set *error_flag (device int, optional) to 1. */
+vbm_status vbm_group_by_expert(const int32_t * ids, int64_t n_ids, int64_t n_tokens,
+                               int64_t ids_stride, int64_t n_as, int32_t * counts,
+                               int32_t * offsets, int32_t * rows, int32_t * error_flag,
+                               void * stream);
+
+/* Weighted top-k combine (hybrid-experts.patch:1905-1924 and :1620-1646; ggml MUL then
+ * sequential ADD in rank order): out[:, t] = ((w0*y0 + w1*y1) + w2*y2) + ... with
+ * y [rows, n_ids, n_tokens] and weights [n_ids, n_tokens]. */
+vbm_status vbm_weighted_combine(const float * y, const float * weights, int64_t rows,
+                                int64_t n_ids, int64_t n_tokens, float * out, void * stream);
+
+/* ----------------------------------------------------------------------------------------------
+ * Fused routed-expert layer (expert_branch of hybrid-experts.patch:1394-1683 for one layer:
+ * gate_up MUL_MAT_ID, bias ADD_ID, GLU, Q8_0 requantization, down MUL_MAT_ID, bias ADD_ID,
+ * MUL by the routing weight, rank-ordered sum).
+ * -------------------------------------------------------------------------------------------- */
+typedef struct vbm_moe_layer_desc {
+    const vbm_bank * gate_up;      /* fused 2*I-row bank, interleave = 1                        */
+    const vbm_bank * down;         /* H-row bank, k = I                                         */
+    const float * gate_up_bias;    /* device, [n_slots][2*I] in ggml row order (gate | up), or NULL */
+    const float * down_bias;       /* device, [n_slots][H], or NULL                              */
+    const int32_t * expert_to_slot;/* device [n_expert] or NULL (identity)                       */
+    const float * router_w;        /* device fp32 [n_expert][H] or NULL (logits given)           */
+    const float * router_b;        /* device fp32 [n_expert] or NULL                             */
+    int64_t hidden;                /* H                                                          */
+    int64_t intermediate;          /* I                                                          */
+    int64_t n_expert;
+    int64_t top_k;
+    int activation;                /* VBM_ACT_*                                                  */
+    int order;                     /* VBM_ORDER_*                                                */
+} vbm_moe_layer_desc;
+
+/* Workspace bytes needed by vbm_moe_layer_forward for `max_tokens` tokens. */
+vbm_status vbm_moe_layer_workspace(const vbm_moe_layer_desc * desc, int64_t max_tokens,
+                                   size_t * bytes);
+
+/* x [n_tokens][H] fp32 -> out [n_tokens][H] fp32. `logits` [n_tokens][n_expert] is read when
+ * desc->router_w is NULL and written otherwise (may then be NULL). ids/weights (optional,
+ * [n_tokens][top_k]) receive the routing. `workspace` is device memory of the size above. */
+vbm_status vbm_moe_layer_forward(const vbm_moe_layer_desc * desc, const float * x,
+                                 float * logits, int64_t n_tokens, float * out,
+                                 int32_t * ids, float * weights, void * workspace,
+                                 size_t workspace_bytes, void * stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VBMOE_H */

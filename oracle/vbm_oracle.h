@@ -1,0 +1,110 @@
+/*
+ * vbm_oracle.h — CPU oracle for the routed-expert MoE path. TEST INFRASTRUCTURE ONLY.
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this library,
+ * and only as the checker / the timed CPU baseline; the product (libvbmoe.so) never links it.
+ *
+ * It restates, in plain C, the CPU arithmetic the reference's hot path relies on (ggml x86 at
+ * llama.cpp commit 620d2225, as restated inside the reference repository). Each function cites
+ * the reference lines it follows. Every function exists in a scalar form; the *_fast entry
+ * points (AVX2/FMA/F16C or AVX-512 VNNI, multithreaded) must return identical bits and are
+ * checked against the scalar form by the tests.
+ *
+ * Functions marked "parity unpinned" below have no golden vector, known answer or buildable
+ * reference in the reference repository for their fp32 rounding order (their integer parts and
+ * closed forms are still tested):
+ *   orc_vec_dot_q8_0_q8_0  (fp32 order unpinned; integer block dot pinned by brute force)
+ *   orc_vec_dot_f32        (fp32 order unpinned)
+ *   orc_softmax_selected   (ggml soft_max expf bits unpinned)
+ *   orc_glu                (ggml swiglu_oai / swiglu expf bits unpinned)
+ */
+#ifndef VBM_ORACLE_H
+#define VBM_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORC_TYPE_F32 0
+#define ORC_TYPE_Q8_0 8
+#define ORC_TYPE_MXFP4 39
+#define ORC_ACT_SILU 0
+#define ORC_ACT_SWIGLU_OAI 1
+
+int orc_abi_version(void);
+float orc_fp16_to_fp32(uint16_t h);
+uint16_t orc_fp32_to_fp16(float f);
+float orc_e8m0_half(uint8_t e);
+
+/* quantize_row_q8_0, x86 contract. */
+void orc_quantize_row_q8_0(const float * x, void * y, int64_t k);
+
+/* ggml_vec_dot_mxfp4_q8_0 (n % 64 == 0). */
+float orc_vec_dot_mxfp4_q8_0(int n, const void * vx, const void * vy);
+/* Exact integer dot of one MXFP4 block with one Q8_0 block per the 8-lane VPSIGNB contract;
+ * lanes[8] receives the per-lane integers. */
+int32_t orc_mxfp4_block_lanes(const void * vx, const void * vy, int32_t lanes[8]);
+/* ggml_vec_dot_q8_0_q8_0 (AVX2 contract). */
+float orc_vec_dot_q8_0_q8_0(int n, const void * vx, const void * vy);
+int32_t orc_q8_block_lanes(const void * vx, const void * vy, int32_t lanes[8]);
+/* ggml_vec_dot_f32 (x86 AVX2 order). */
+float orc_vec_dot_f32(int n, const float * x, const float * y);
+
+/* GGML_OP_MUL_MAT_ID (as in vbm_mul_mat_id, ggml layout for `as`). threads <= 0: scalar. */
+int orc_mul_mat_id(int type, const void * as, int64_t k, int64_t rows, int64_t n_as,
+                   int b_type, const void * b, int64_t b_ne1,
+                   const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride,
+                   const float * bias, float * dst, int threads);
+
+/* Stable counting sort of (token, rank) pairs by expert. Returns 0, or -1 on an invalid id. */
+int orc_group_by_expert(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride,
+                        int64_t n_as, int32_t * counts, int32_t * offsets, int32_t * rows);
+
+/* Canonical top-k (value desc, then lower index). */
+void orc_topk(const float * logits, int64_t n, int64_t k, int32_t * ids);
+/* ggml soft_max over the k selected logits (double sum, float scale). */
+void orc_softmax_selected(const float * values, int64_t k, float * out);
+/* Router: logits (given, or W.x + b) -> top-k -> softmax-over-selected for n_tokens. */
+void orc_router(const float * router_w, const float * router_b, const float * x, int64_t hidden,
+                float * logits, int64_t n_expert, int64_t n_tokens, int64_t top_k,
+                int32_t * ids, float * weights);
+
+/* GLU: out = act(gate, up). */
+void orc_glu(int activation, const float * gate, const float * up, float * out, int64_t n,
+             float alpha, float limit);
+
+/* Weighted rank-ordered combine: out[:,t] = ((w0*y0 + w1*y1) + ...). */
+void orc_weighted_combine(const float * y, const float * weights, int64_t rows, int64_t n_ids,
+                          int64_t n_tokens, float * out);
+
+/* One routed-expert layer (the reference expert_branch graph), weights in ggml layout:
+ * gate_up [n_expert][2I rows][H] (rows [0,I) gate, [I,2I) up), down [n_expert][H][I],
+ * biases fp32 or NULL. x [T][H] -> out [T][H]. act_out (optional) [T][k][I] receives the GLU
+ * output before requantization, y_out (optional) [T][k][H] the biased down outputs. */
+typedef struct orc_layer {
+    int type;                      /* ORC_TYPE_MXFP4 or ORC_TYPE_Q8_0 */
+    const void * gate_up;
+    const void * down;
+    const float * gate_up_bias;    /* [n_expert][2I] or NULL */
+    const float * down_bias;       /* [n_expert][H] or NULL  */
+    const float * router_w;        /* [n_expert][H] or NULL  */
+    const float * router_b;        /* [n_expert] or NULL     */
+    int64_t hidden, intermediate, n_expert, top_k;
+    int activation;
+} orc_layer;
+
+int orc_moe_layer(const orc_layer * layer, const float * x, float * logits, int64_t n_tokens,
+                  float * out, int32_t * ids, float * weights, float * act_out, float * y_out,
+                  int threads);
+
+/* Fast (bit-identical) single-row dots used by orc_mul_mat_id when threads > 0. */
+int orc_fast_isa(void);  /* 0 scalar, 2 AVX2, 3 AVX-512 VNNI */
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,219 @@
+"""GPU parity: libvbmoe.so (through its C ABI) against the CPU oracle on identical seeded inputs.
+
+Bar: bit-exact for bank bytes, quantizer output, grouping, expert ids, integer block dots and the
+x86-contract GEMV (whose fp32 order is reproduced); fp32 layer outputs within 1e-3 max relative
+error (max|gpu - cpu| / max|cpu|) and cosine >= 0.99999.
+"""
+import numpy as np
+import pytest
+
+import helpers as H
+
+pytestmark = pytest.mark.gpu
+
+
+def test_bank_upload_export_is_lossless(gpu):
+    for type_id, rows, k, inter in [(H.MX, 5760, 2880, True), (H.MX, 2880, 2880, False), (H.Q8, 1536, 2048, True),
+                                    (H.Q8, 2048, 768, False), (H.MX, 64, 448, False)]:
+        w = H.synth_weights(type_id, 1234, 7, 2, rows, k)
+        bank = H.make_bank(type_id, w, 2, rows, k, inter)
+        per = w.size // 2
+        for e in range(2):
+            assert np.array_equal(bank.export(e), w[e * per:(e + 1) * per]), (type_id, rows, k, inter, e)
+        bank.destroy()
+
+
+def test_device_generator_matches_host_generator(gpu):
+    rows, k, experts = 5760, 2880, 3
+    bank = gpu.Bank(H.MX, rows, k, experts, True)
+    bank.generate(0, experts, 99, 11, 5, -8, -3)
+    per_blocks = rows * (k // 32)
+    for s in range(experts):
+        host = gpu.synth_mxfp4(99, 11, (5 + s) * per_blocks, per_blocks)
+        assert np.array_equal(bank.export(s), host), s
+    qb = gpu.Bank(H.Q8, 768, 2048, 2, False)
+    qb.generate(0, 2, 7, 3, 0, 1e-3, 1e-2)
+    per_blocks = 768 * 64
+    for s in range(2):
+        assert np.array_equal(qb.export(s), gpu.synth_q8_0(7, 3, s * per_blocks, per_blocks)), s
+
+
+def activation_patterns(k: int, rows: int):
+    """tools/trace/hybrid_layer.cpp:593-605 patterns plus N(0,1)."""
+    i = np.arange(k * rows)
+    yield "normal", np.random.default_rng(8).standard_normal(k * rows).astype(np.float32)
+    for sample, mag in enumerate((0.2, 50.0, 500.0)):
+        yield f"sine{mag}", (mag * np.sin(((i + 1) * (sample + 3)) * 0.017)).astype(np.float32)
+    yield "zero", np.zeros(k * rows, np.float32)
+    yield "q8-ties", np.where(i % 32 == 0, 127.0, np.where(i % 32 == 1, -127.0,
+                              np.where(i % 2 == 1, -1.0, 1.0) * (0.5 + ((i + 7) % 31)))).astype(np.float32)
+
+
+def test_quantize_q8_0_bitwise(gpu, orc):
+    k, rows = 2880, 5
+    for name, x in activation_patterns(k, rows):
+        dx = gpu.DeviceBuffer.from_array(x)
+        dq = gpu.DeviceBuffer(rows * (k // 32) * 34)
+        gpu.call("vbm_quantize_q8_0", dx.ptr, rows, k, k, dq.ptr, None)
+        got = dq.download(np.uint8, (rows, k // 32 * 34))
+        assert np.array_equal(got, orc.quantize_q8_0(x.reshape(rows, k))), name
+
+
+@pytest.mark.parametrize("experts,active,tokens,strided,mask", [
+    (4, 1, 1, False, "none"), (7, 3, 2, True, "partial"), (8, 4, 3, False, "all"), (16, 8, 3, True, "partial"),
+    (8, 8, 2, False, "none"), (32, 4, 1, False, "none"),
+])
+def test_mul_mat_id_mxfp4_bitwise_small(gpu, orc, experts, active, tokens, strided, mask):
+    """tests/test_masked_matmul.cpp:76-105 cases: ids (token + 3 rank) % experts, -1 masks, strided ids."""
+    k, rows = 256, 64
+    w = H.synth_weights(H.MX, 3, experts, experts, rows, k)
+    bank = H.make_bank(H.MX, w, experts, rows, k)
+    x = gpu.synth_normal(3, 100 + experts, 0, tokens * k).reshape(tokens, 1, k) * np.float32(0.1)
+    ids = np.array([[(t + r * 3) % experts for r in range(active)] for t in range(tokens)], np.int32)
+    if mask == "partial":
+        ids.reshape(-1)[::2] = -1
+    elif mask == "all":
+        ids[:] = -1
+    stride_ids = np.concatenate([ids, np.zeros((tokens, 1), np.int32)], axis=1) if strided else ids
+    got = H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, stride_ids, active)
+    ref = orc.mul_mat_id(39, w, k, rows, experts, 0, x, 1, stride_ids, active, tokens, stride_ids.shape[1])
+    assert H.bits_equal(got, ref), H.diff_report(got, ref)
+    bank.destroy()
+
+
+def adversarial_mxfp4(experts: int, rows: int, k: int) -> np.ndarray:
+    """tools/trace/hybrid_layer.cpp:964-979 fixture: exponents {0,1,2,120,126,127,128,130}."""
+    nb = k // 32
+    exps = np.array([0, 1, 2, 120, 126, 127, 128, 130], np.uint8)
+    out = np.empty((experts * rows * nb, 17), np.uint8)
+    blocks = np.arange(experts * rows * nb)
+    out[:, 0] = exps[(blocks // nb) % 8]
+    j = np.arange(16)
+    out[:, 1:] = (((blocks[:, None] + j) % 16) | (((blocks[:, None] * 7 + j * 3) % 16) << 4)).astype(np.uint8)
+    return out.reshape(-1)
+
+
+def test_mul_mat_id_mxfp4_adversarial_and_neg128(gpu, orc):
+    """Adversarial exponents and activation code -128 (tests/test_quantized_cuda.cpp:31-53)."""
+    k, rows, experts, tokens = 128, 64, 4, 2
+    w = adversarial_mxfp4(experts, rows, k)
+    bank = H.make_bank(H.MX, w, experts, rows, k)
+    ids = np.array([[0, 2, 1], [3, 0, 2]], np.int32)
+    for sample in range(12):
+        x = np.array([0.0 if sample == 0 else np.sin((i * 13 + sample * 31) * 0.07) * sample
+                      for i in range(tokens * 3 * k)], np.float32).reshape(tokens, 3, k)
+        q = orc.quantize_q8_0(x.reshape(-1, k)).reshape(tokens, 3, -1)
+        if sample == 11:
+            q.reshape(-1, 34)[:, 2] = 128                   # inject -128 codes
+        if sample == 10:
+            q.reshape(-1, 34)[:, 2:] = 128                  # every code -128
+        got = H.mul_mat_id(bank, experts, q, gpu.TYPE_Q8_0, 3, ids, 3)
+        ref = orc.mul_mat_id(39, w, k, rows, experts, 8, q, 3, ids, 3, tokens, 3)
+        assert H.bits_equal(got, ref), (sample, H.diff_report(got, ref))
+    bank.destroy()
+
+
+@pytest.mark.parametrize("tokens", [1, 8, 64])
+def test_mul_mat_id_mxfp4_bitwise_config_shapes(gpu, orc, tokens):
+    """Config 0/1 shapes: E=32, top-4, H=I=2880, down (2880 x 2880) and fused gate_up (5760 x 2880)."""
+    k, experts, active = 2880, 32, 4
+    rng = np.random.default_rng(tokens)
+    ids = np.stack([rng.choice(experts, active, replace=False) for _ in range(tokens)]).astype(np.int32)
+    for rows, inter, name in [(2880, False, "down"), (5760, True, "gate_up")]:
+        w = H.synth_weights(H.MX, 17, 1 if inter else 2, experts, rows, k)
+        bank = H.make_bank(H.MX, w, experts, rows, k, inter)
+        bias = gpu.synth_normal(17, 3, 0, experts * rows, 0.0, 0.02)
+        x = gpu.synth_normal(17, 4 + tokens, 0, tokens * k).reshape(tokens, 1, k)
+        got = H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, ids, active, bias=bias)
+        ref = orc.mul_mat_id(39, w, k, rows, experts, 0, x, 1, ids, active, tokens, active, bias=bias, threads=8)
+        assert H.bits_equal(got, ref), (name, H.diff_report(got, ref))
+        bank.destroy()
+
+
+def test_mul_mat_id_q8_0_bitwise(gpu, orc):
+    """Config 3 shapes: H=2048, I=768, gate (768 x 2048) and down (2048 x 768)."""
+    experts, active, tokens = 16, 8, 6
+    rng = np.random.default_rng(33)
+    ids = np.stack([rng.choice(experts, active, replace=False) for _ in range(tokens)]).astype(np.int32)
+    for rows, k in [(768, 2048), (2048, 768)]:
+        w = H.synth_weights(H.Q8, 21, rows, experts, rows, k)
+        bank = H.make_bank(H.Q8, w, experts, rows, k)
+        x = gpu.synth_normal(21, 5, 0, tokens * k).reshape(tokens, 1, k)
+        got = H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, ids, active)
+        ref = orc.mul_mat_id(8, w, k, rows, experts, 0, x, 1, ids, active, tokens, active, threads=8)
+        assert H.bits_equal(got, ref), (rows, k, H.diff_report(got, ref))
+        bank.destroy()
+
+
+def test_mul_mat_id_slot_map_and_residency_errors(gpu, orc):
+    k, rows, experts = 256, 32, 6
+    w = H.synth_weights(H.MX, 9, 9, experts, rows, k)
+    resident = [4, 1, 5]
+    bank = gpu.Bank(H.MX, rows, k, len(resident))
+    per = w.size // experts
+    for slot, e in enumerate(resident):
+        bank.upload(slot, w[e * per:(e + 1) * per])
+    slot_map = np.full(experts, -1, np.int32)
+    slot_map[resident] = np.arange(len(resident))
+    ids = np.array([[4, 1], [5, 4]], np.int32)
+    x = gpu.synth_normal(9, 1, 0, 2 * k).reshape(2, 1, k)
+    got = H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, ids, 2, slot_map=slot_map, slot_map_host=slot_map)
+    ref = orc.mul_mat_id(39, w, k, rows, experts, 0, x, 1, ids, 2, 2, 2)
+    assert H.bits_equal(got, ref), H.diff_report(got, ref)
+    with pytest.raises(gpu.VbmError) as err:       # non-resident expert (quantized_cuda.cu:224-227)
+        H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, np.array([[0, 1]], np.int32), 2, slot_map=slot_map,
+                     slot_map_host=slot_map)
+    assert err.value.status == 1
+    bank.destroy()
+
+
+def test_grouping_exact(gpu, orc):
+    rng = np.random.default_rng(12)
+    for n_as, n_ids, tokens in [(32, 4, 1), (32, 4, 64), (128, 4, 32), (128, 8, 2048), (7, 3, 5)]:
+        ids = np.stack([rng.choice(n_as, n_ids, replace=False) for _ in range(tokens)]).astype(np.int32)
+        ids[rng.random(ids.shape) < 0.05] = -1
+        d_ids = gpu.DeviceBuffer.from_array(ids)
+        counts, offsets, rows = (gpu.DeviceBuffer(4 * n) for n in (n_as, n_as + 1, n_ids * tokens))
+        err = gpu.DeviceBuffer(4)
+        gpu.call("vbm_group_by_expert", d_ids.ptr, n_ids, tokens, n_ids, n_as, counts.ptr, offsets.ptr, rows.ptr,
+                 err.ptr, None)
+        c, o, r = orc.group_by_expert(ids, n_ids, tokens, n_ids, n_as)
+        assert np.array_equal(counts.download(np.int32, n_as), c)
+        assert np.array_equal(offsets.download(np.int32, n_as + 1), o)
+        assert np.array_equal(rows.download(np.int32, n_ids * tokens)[: o[-1]], r)
+        assert err.download(np.int32, 1)[0] == 0
+
+
+def test_router_ids_exact(gpu, orc):
+    for n_expert, hidden, tokens, top_k in [(32, 2880, 8, 4), (128, 2880, 32, 4), (128, 2048, 16, 8)]:
+        w = gpu.synth_normal(5, 1, 0, n_expert * hidden, 0.0, 0.02).reshape(n_expert, hidden)
+        x = gpu.synth_normal(5, 2, 0, tokens * hidden).reshape(tokens, hidden)
+        dw, dx = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x)
+        dl = gpu.DeviceBuffer(4 * tokens * n_expert)
+        di, dwt = gpu.DeviceBuffer(4 * tokens * top_k), gpu.DeviceBuffer(4 * tokens * top_k)
+        gpu.call("vbm_router_topk_softmax", dw.ptr, None, dx.ptr, hidden, dl.ptr, n_expert, tokens, top_k, di.ptr,
+                 dwt.ptr, None)
+        logits, ids, wts = orc.router(router_w=w, x=x, n_expert=n_expert, n_tokens=tokens, top_k=top_k, hidden=hidden)
+        assert H.bits_equal(dl.download(np.float32, (tokens, n_expert)), logits)
+        assert np.array_equal(di.download(np.int32, (tokens, top_k)), ids)
+        assert np.allclose(dwt.download(np.float32, (tokens, top_k)), wts, rtol=4e-7, atol=0)
+    # Given logits with exact ties: lower index first (topk-tie-probe.cpp:111-113).
+    logits = np.array([[1, 3, 3, 0, 3, 2, 2, 3]], np.float32)
+    dl = gpu.DeviceBuffer.from_array(logits)
+    di, dwt = gpu.DeviceBuffer(16), gpu.DeviceBuffer(16)
+    gpu.call("vbm_router_topk_softmax", None, None, None, 0, dl.ptr, 8, 1, 4, di.ptr, dwt.ptr, None)
+    assert di.download(np.int32, 4).tolist() == [1, 2, 4, 7]
+
+
+def test_combine_bitwise_and_order(gpu, orc):
+    y = gpu.synth_normal(4, 1, 0, 3 * 4 * 2880).reshape(3, 4, 2880) * np.float32(1e3)
+    w = gpu.synth_normal(4, 2, 0, 12).reshape(3, 4)
+    dy, dw, do = gpu.DeviceBuffer.from_array(y), gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer(3 * 2880 * 4)
+    gpu.call("vbm_weighted_combine", dy.ptr, dw.ptr, 2880, 4, 3, do.ptr, None)
+    ref = np.empty((3, 2880), np.float32)
+    orc.load().orc_weighted_combine(y.ctypes.data, w.ctypes.data, 2880, 4, 3, ref.ctypes.data)
+    assert H.bits_equal(do.download(np.float32, (3, 2880)), ref)
+    probe = np.array([1e20, -1e20, 1.0], np.float32).reshape(1, 3, 1)
+    dy, dw, do = gpu.DeviceBuffer.from_array(probe), gpu.DeviceBuffer.from_array(np.ones((1, 3), np.float32)), gpu.DeviceBuffer(4)
+    gpu.call("vbm_weighted_combine", dy.ptr, dw.ptr, 1, 3, 1, do.ptr, None)
+    assert do.download(np.float32, 1)[0] == 1.0

@@ -1,0 +1,76 @@
+"""Build libvbmoe.so (HIP, gfx950) in-tree with direct hipcc invocations.
+
+Usage: python build_lib.py [--jobs N]
+Output: vbmoe/libvbmoe.so next to this file; objects under _build/.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+HOST = HERE / "host"
+OUT_DIR = HERE / "vbmoe"
+BUILD = HERE / "_build"
+LIB = OUT_DIR / "libvbmoe.so"
+INCLUDE = HERE.parent / "include"
+
+ARCH = os.environ.get("VBM_OFFLOAD_ARCH", "gfx950")
+HIP_FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+    "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-command-line-argument",
+    f"-I{INCLUDE}", f"-I{CSRC}",
+]
+
+
+def hipcc() -> str:
+    for candidate in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if candidate and Path(candidate).exists():
+            return candidate
+    raise RuntimeError("hipcc not found")
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp")) + sorted(HOST.glob("*.cpp"))
+
+
+def compile_one(src: Path) -> Path:
+    obj = BUILD / (src.parent.name + "_" + src.name + ".o")
+    cmd = [hipcc(), *HIP_FLAGS, f"-I{HOST}", "-x", "hip", "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"compile failed: {src.name}\n{' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
+    warnings = [line for line in proc.stderr.splitlines() if "warning" in line and "packed-fp32-ops" not in line]
+    if warnings:
+        sys.stderr.write(f"[{src.name}]\n" + "\n".join(warnings[:20]) + "\n")
+    return obj
+
+
+def build(jobs: int = 8) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    OUT_DIR.mkdir(exist_ok=True)
+    srcs = sources()
+    with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
+        objs = list(pool.map(compile_one, srcs))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs), "-lpthread"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed\n{' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
+    args = parser.parse_args()
+    print(build(args.jobs))

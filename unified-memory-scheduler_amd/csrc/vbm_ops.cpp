@@ -1,0 +1,250 @@
+// C ABI: ggml-level operators and the fused routed-expert layer.
+#include "vbm_internal.hpp"
+
+#include <algorithm>
+#include <vector>
+
+using namespace vbm;
+
+namespace {
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+__global__ void zero_kernel(float * p, int64_t n) {
+    const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (i < n) p[i] = 0.0f;
+}
+
+void zero_floats(float * p, int64_t n, hipStream_t stream) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(zero_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, p, n);
+    check_hip(hipGetLastError(), "zero fill launch");
+}
+
+// Synchronous host-side validation of device ids against an expert->slot map (the reference's
+// per-job residency check, tools/engine/quantized_cuda.cu:224-227).
+void validate_ids_on_host(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride, int64_t n_as,
+                          const int32_t * expert_to_slot_host, hipStream_t stream) {
+    std::vector<int32_t> host(static_cast<size_t>(ids_stride * (n_tokens - 1) + n_ids));
+    check_hip(hipMemcpyAsync(host.data(), ids, host.size() * sizeof(int32_t), hipMemcpyDeviceToHost, stream), "ids copy");
+    check_hip(hipStreamSynchronize(stream), "ids copy synchronize");
+    for (int64_t t = 0; t < n_tokens; ++t)
+        for (int64_t r = 0; r < n_ids; ++r) {
+            const int32_t id = host[t * ids_stride + r];
+            if (id == -1) continue;
+            require(id >= 0 && id < n_as, "expert id out of range");
+            require(expert_to_slot_host[id] >= 0, "expert is out of range or not resident");
+        }
+}
+
+struct LayerWorkspace {
+    int32_t * ids;
+    float * weights;
+    float * logits;
+    uint8_t * xq;
+    void * group;
+    float * act;
+    float * y;
+    size_t total;
+};
+
+LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint8_t * base) {
+    LayerWorkspace w{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) { uint8_t * p = base ? base + off : nullptr; off += align_up(bytes); return p; };
+    const int64_t entries = max_tokens * d.top_k;
+    w.ids = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * entries));
+    w.weights = reinterpret_cast<float *>(take(sizeof(float) * entries));
+    w.logits = reinterpret_cast<float *>(take(sizeof(float) * max_tokens * d.n_expert));
+    w.xq = take(static_cast<size_t>(max_tokens * (d.hidden / 32) * 34));
+    w.group = take(group_workspace_bytes(d.n_expert, entries));
+    w.act = reinterpret_cast<float *>(take(sizeof(float) * entries * d.intermediate));
+    w.y = reinterpret_cast<float *>(take(sizeof(float) * entries * d.hidden));
+    w.total = off;
+    return w;
+}
+
+void validate_layer(const vbm_moe_layer_desc * d) {
+    require(d != nullptr && d->gate_up != nullptr && d->down != nullptr, "layer needs gate_up and down banks");
+    const vbm_bank & gu = *d->gate_up, & dn = *d->down;
+    require(gu.interleave == 1, "gate_up bank must be created with interleave = 1");
+    require(gu.type == dn.type, "gate_up and down banks must share a type");
+    require(gu.rows == 2 * d->intermediate && gu.k == d->hidden, "gate_up bank shape must be [2*I rows, H]");
+    require(dn.rows == d->hidden && dn.k == d->intermediate, "down bank shape must be [H rows, I]");
+    require(d->hidden % 64 == 0 && d->intermediate % 64 == 0, "hidden and intermediate must be multiples of 64");
+    require(d->n_expert > 0 && d->n_expert <= 1024 && d->top_k > 0 && d->top_k <= d->n_expert && d->top_k <= 64,
+            "expert count / top_k out of range");
+    require(d->expert_to_slot != nullptr || (gu.n_slots >= d->n_expert && dn.n_slots >= d->n_expert),
+            "identity expert->slot map needs a slot per expert");
+    require(d->activation == VBM_ACT_SILU || d->activation == VBM_ACT_SWIGLU_OAI, "unknown activation");
+}
+
+}  // namespace
+
+extern "C" {
+
+vbm_status vbm_quantize_q8_0(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, void * dst, void * stream) {
+    return guarded([&] {
+        require(x != nullptr && dst != nullptr, "null buffer");
+        launch_quantize_q8_0(x, n_rows, k, x_stride, static_cast<uint8_t *>(dst), as_stream(stream));
+    });
+}
+
+vbm_status vbm_group_by_expert(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride, int64_t n_as,
+                               int32_t * counts, int32_t * offsets, int32_t * rows, int32_t * error_flag, void * stream) {
+    return guarded([&] {
+        require(ids && counts && offsets && rows, "null buffer");
+        const hipStream_t s = as_stream(stream);
+        void * scratch = nullptr;
+        check_hip(hipMallocAsync(&scratch, sizeof(int32_t) * (n_as + 2 + 8), s), "group scratch");
+        GroupBuffers g{};
+        g.counts = counts;
+        g.offsets = offsets;
+        g.rows = rows;
+        g.active = static_cast<int32_t *>(scratch);
+        g.n_active = g.active + n_as;
+        g.error = error_flag ? error_flag : g.n_active + 1;
+        launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
+        check_hip(hipFreeAsync(scratch, s), "group scratch free");
+    });
+}
+
+vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot, const int32_t * expert_to_slot_host,
+                          int64_t n_as, int b_type, const void * b, int64_t b_ne1, const int32_t * ids, int64_t n_ids,
+                          int64_t n_tokens, int64_t ids_stride, const float * bias, float * dst, int order,
+                          void * stream) {
+    return guarded([&] {
+        require(bank && b && ids && dst, "null buffer");
+        require(order == VBM_ORDER_EXACT || order == VBM_ORDER_FAST, "unknown order");
+        require(b_type == VBM_TYPE_F32 || b_type == VBM_TYPE_Q8_0, "b must be F32 or Q8_0");
+        require(n_ids > 0 && n_tokens > 0 && (b_ne1 == 1 || b_ne1 == n_ids), "b_ne1 must be 1 or n_ids");
+        require(ids_stride >= n_ids, "ids stride must be >= n_ids");
+        require(n_as > 0 && n_as <= 1024, "n_as must be in 1..1024");
+        require(expert_to_slot != nullptr || n_as <= bank->n_slots, "identity map needs n_as <= bank slots");
+        const hipStream_t s = as_stream(stream);
+        if (expert_to_slot_host) validate_ids_on_host(ids, n_ids, n_tokens, ids_stride, n_as, expert_to_slot_host, s);
+        const int64_t entries = n_ids * n_tokens;
+        const int64_t n_b = b_ne1 * n_tokens;
+        const size_t q_bytes = b_type == VBM_TYPE_F32 ? static_cast<size_t>(n_b * bank->nb * 34) : 0;
+        const size_t g_bytes = group_workspace_bytes(n_as, entries);
+        void * scratch = nullptr;
+        check_hip(hipMallocAsync(&scratch, align_up(q_bytes) + g_bytes, s), "mul_mat_id scratch");
+        uint8_t * q = static_cast<uint8_t *>(scratch);
+        const GroupBuffers g = carve_group(q + align_up(q_bytes), n_as, entries);
+        if (b_type == VBM_TYPE_F32) launch_quantize_q8_0(static_cast<const float *>(b), n_b, bank->k, bank->k, q, s);
+        launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
+        zero_floats(dst, entries * bank->rows, s);
+        GemvArgs a{};
+        a.bank = bank;
+        a.expert_to_slot = expert_to_slot;
+        a.act_q8 = b_type == VBM_TYPE_F32 ? q : static_cast<const uint8_t *>(b);
+        a.act_stride = bank->nb * 34;
+        a.n_ids = n_ids;
+        a.b_ne1 = b_ne1;
+        a.group = g;
+        a.max_active = std::min<int64_t>(n_as, entries);
+        a.max_per_expert = n_tokens * std::min<int64_t>(n_ids, 1) ;  // an expert appears at most once per token
+        a.bias = bias;
+        a.dst = dst;
+        a.epilogue = 0;
+        launch_gemv(a, s);
+        check_hip(hipFreeAsync(scratch, s), "mul_mat_id scratch free");
+    });
+}
+
+vbm_status vbm_add_id(float * y, const float * bias, const int32_t * ids, int64_t rows, int64_t n_ids, int64_t n_tokens,
+                      int64_t ids_stride, void * stream) {
+    return guarded([&] {
+        require(y && bias && ids && rows > 0 && n_ids > 0 && n_tokens > 0 && ids_stride >= n_ids, "invalid add_id");
+        launch_add_id(y, bias, ids, rows, n_ids, n_tokens, ids_stride, as_stream(stream));
+    });
+}
+
+vbm_status vbm_glu(int activation, const float * gate, const float * up, float * out, int64_t n_rows, int64_t width,
+                   int64_t gate_stride, int64_t up_stride, int64_t out_stride, float alpha, float limit, void * stream) {
+    return guarded([&] {
+        require(gate && up && out && n_rows > 0 && width > 0, "invalid glu");
+        require(activation == VBM_ACT_SILU || activation == VBM_ACT_SWIGLU_OAI, "unknown activation");
+        launch_glu(activation, gate, up, out, n_rows, width, gate_stride, up_stride, out_stride, alpha, limit,
+                   as_stream(stream));
+    });
+}
+
+vbm_status vbm_router_topk_softmax(const float * router_w, const float * router_b, const float * x, int64_t k_hidden,
+                                   float * logits, int64_t n_expert, int64_t n_tokens, int64_t top_k, int32_t * ids,
+                                   float * weights, void * stream) {
+    return guarded([&] {
+        require(ids && weights && logits, "router needs logits, ids and weights buffers");
+        launch_router(router_w, router_b, x, k_hidden, logits, n_expert, n_tokens, top_k, ids, weights, as_stream(stream));
+    });
+}
+
+vbm_status vbm_weighted_combine(const float * y, const float * weights, int64_t rows, int64_t n_ids, int64_t n_tokens,
+                                float * out, void * stream) {
+    return guarded([&] {
+        require(y && weights && out && rows > 0 && n_ids > 0 && n_tokens > 0, "invalid combine");
+        launch_combine(y, weights, rows, n_ids, n_tokens, out, as_stream(stream));
+    });
+}
+
+vbm_status vbm_moe_layer_workspace(const vbm_moe_layer_desc * desc, int64_t max_tokens, size_t * bytes) {
+    return guarded([&] {
+        validate_layer(desc);
+        require(bytes != nullptr && max_tokens > 0, "invalid workspace query");
+        *bytes = plan_layer(*desc, max_tokens, nullptr).total;
+    });
+}
+
+vbm_status vbm_moe_layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits, int64_t n_tokens,
+                                 float * out, int32_t * ids, float * weights, void * workspace, size_t workspace_bytes,
+                                 void * stream) {
+    return guarded([&] {
+        validate_layer(d);
+        require(x && out && workspace && n_tokens > 0, "null buffer");
+        require(d->router_w != nullptr || logits != nullptr, "logits input required when router_w is NULL");
+        const LayerWorkspace w = plan_layer(*d, n_tokens, static_cast<uint8_t *>(workspace));
+        require(workspace_bytes >= w.total, "workspace too small");
+        const hipStream_t s = as_stream(stream);
+        const int64_t K = d->top_k, H = d->hidden, I = d->intermediate, entries = n_tokens * K;
+        int32_t * ids_d = ids ? ids : w.ids;
+        float * w_d = weights ? weights : w.weights;
+        float * logits_d = logits ? logits : w.logits;
+        launch_router(d->router_w, d->router_b, x, H, logits_d, d->n_expert, n_tokens, K, ids_d, w_d, s);
+        launch_quantize_q8_0(x, n_tokens, H, H, w.xq, s);
+        const GroupBuffers g = carve_group(w.group, d->n_expert, entries);
+        launch_group(ids_d, K, n_tokens, K, d->n_expert, g, s);
+
+        GemvArgs a{};
+        a.expert_to_slot = d->expert_to_slot;
+        a.n_ids = K;
+        a.group = g;
+        a.max_active = std::min<int64_t>(d->n_expert, entries);
+        a.max_per_expert = n_tokens;
+        a.activation = d->activation;
+        a.alpha = 1.702f;
+        a.limit = 7.0f;
+        // gate_up + bias + GLU -> act [entries][I]
+        a.bank = d->gate_up;
+        a.act_q8 = w.xq;
+        a.act_stride = (H / 32) * 34;
+        a.b_ne1 = 1;
+        a.bias = d->gate_up_bias;
+        a.dst = w.act;
+        a.epilogue = 1;
+        launch_gemv(a, s);
+        // Q8_0 requantization (in LDS) + down + bias -> y [entries][H]
+        a.bank = d->down;
+        a.act_q8 = nullptr;
+        a.act_f32 = w.act;
+        a.act_stride = I;
+        a.b_ne1 = K;
+        a.bias = d->down_bias;
+        a.dst = w.y;
+        a.epilogue = 0;
+        launch_gemv(a, s);
+        launch_combine(w.y, w_d, H, K, n_tokens, out, s);
+    });
+}
+
+}  // extern "C"

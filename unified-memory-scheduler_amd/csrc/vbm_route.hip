@@ -1,0 +1,296 @@
+// Routing-side kernels: token->expert grouping, Q8_0 activation quantizer, router
+// (logits, top-k, softmax over the selected), weighted rank-ordered combine, ADD_ID, GLU.
+#include "vbm_internal.hpp"
+
+namespace vbm {
+namespace {
+
+constexpr int kGroupThreads = 1024;
+constexpr int kMaxExperts = 1024;
+
+__device__ __forceinline__ float expf_rn(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
+
+// One workgroup. Counting sort of entries i = token * n_ids + rank by expert, stable in i
+// (the (token outer, rank inner) append order of ggml's MMID row mapping). Entries with id -1
+// are skipped; ids outside [-1, n_as) raise the error flag and are skipped.
+__global__ __launch_bounds__(kGroupThreads) void group_kernel(const int32_t * __restrict__ ids, int n_ids,
+                                                               int n_tokens, int64_t ids_stride, int n_as,
+                                                               int32_t * counts, int32_t * offsets, int32_t * rows,
+                                                               int32_t * active, int32_t * n_active, int32_t * error) {
+    __shared__ int s_count[kMaxExperts];
+    __shared__ int s_offset[kMaxExperts + 1];
+    __shared__ int s_error;
+    const int t = threadIdx.x;
+    const int n = n_ids * n_tokens;
+    for (int e = t; e < n_as; e += kGroupThreads) s_count[e] = 0;
+    if (t == 0) s_error = 0;
+    __syncthreads();
+    for (int i = t; i < n; i += kGroupThreads) {
+        const int id = ids[static_cast<int64_t>(i / n_ids) * ids_stride + i % n_ids];
+        if (id == -1) continue;
+        if (id < 0 || id >= n_as) { s_error = 1; continue; }
+        atomicAdd(&s_count[id], 1);
+    }
+    __syncthreads();
+    if (t == 0) {
+        int running = 0, live = 0;
+        for (int e = 0; e < n_as; ++e) {
+            s_offset[e] = running;
+            running += s_count[e];
+            if (s_count[e] > 0) active[live++] = e;
+        }
+        s_offset[n_as] = running;
+        *n_active = live;
+        *error = s_error;
+    }
+    __syncthreads();
+    for (int e = t; e < n_as; e += kGroupThreads) {
+        counts[e] = s_count[e];
+        offsets[e] = s_offset[e];
+    }
+    if (t == 0) offsets[n_as] = s_offset[n_as];
+    // Stable placement: each wave owns experts w, w + waves, ...; it scans the entries in order,
+    // 64 at a time, ranking matches with a ballot.
+    const int lane = t & 63, wave = t >> 6, waves = kGroupThreads / 64;
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    for (int e = wave; e < n_as; e += waves) {
+        if (s_count[e] == 0) continue;
+        int running = s_offset[e];
+        for (int base = 0; base < n; base += 64) {
+            const int i = base + lane;
+            int id = -2;
+            if (i < n) id = ids[static_cast<int64_t>(i / n_ids) * ids_stride + i % n_ids];
+            const uint64_t mask = __ballot(id == e);
+            if (id == e) rows[running + __popcll(mask & below)] = i;
+            running += __popcll(mask);
+        }
+    }
+}
+
+// x86 quantize_row_q8_0: one 32-lane group per block.
+__global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict__ x, int64_t n_rows, int nb,
+                                                       int64_t x_stride, uint8_t * __restrict__ dst) {
+    const int64_t total = n_rows * nb;
+    const int64_t b_global = blockIdx.x * 8ll + (threadIdx.x >> 5);
+    const int e = threadIdx.x & 31;
+    const bool live = b_global < total;
+    const int64_t row = live ? b_global / nb : 0, b = live ? b_global % nb : 0;
+    const float v = live ? x[row * x_stride + b * 32 + e] : 0.0f;
+    float amax = fabsf(v);
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    if (!live) return;
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    float q = rintf(v * id);
+    q = q > 127.0f ? 127.0f : (q < -128.0f ? -128.0f : q);
+    uint8_t * blk = dst + b_global * 34;
+    blk[2 + e] = static_cast<uint8_t>(static_cast<signed char>(q));
+    if (e == 0) {
+        const uint16_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(d));
+        blk[0] = static_cast<uint8_t>(h & 0xFF);
+        blk[1] = static_cast<uint8_t>(h >> 8);
+    }
+}
+
+// Router logits in the x86 ggml_vec_dot_f32 order: 32 lanes = 4 accumulators x 8 floats, each a
+// sequential FMA chain over 32-element steps, then the fixed reduction tree. One 32-lane group
+// per (expert, token).
+__global__ __launch_bounds__(256) void router_logits_kernel(const float * __restrict__ w, const float * __restrict__ bias,
+                                                            const float * __restrict__ x, int hidden, int n_expert,
+                                                            int n_tokens, float * __restrict__ logits) {
+    const int group = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int lane = threadIdx.x & 31;
+    const bool live = group < n_expert * n_tokens;
+    const int e = live ? group % n_expert : 0, t = live ? group / n_expert : 0;
+    const float * wr = w + static_cast<int64_t>(e) * hidden;
+    const float * xr = x + static_cast<int64_t>(t) * hidden;
+    const int np = hidden & ~31;
+    float acc = 0.0f;
+    if (live)
+        for (int i = 0; i < np; i += 32) acc = __builtin_fmaf(wr[i + lane], xr[i + lane], acc);
+    // lane = 8*j + l: sum[j][l]. sum0 += sum2, sum1 += sum3 (lanes +16), sum0 += sum1 (lanes +8).
+    float v = acc + __shfl_down(acc, 16, 32);
+    v = v + __shfl_down(v, 8, 32);
+    // lanes 0..7 hold sum0[l]; t0[l] = s[l] + s[l+4]; then (t0[0]+t0[1]) + (t0[2]+t0[3]).
+    const float t0 = v + __shfl_down(v, 4, 32);
+    const float t1 = t0 + __shfl_down(t0, 1, 32);
+    const float r = t1 + __shfl_down(t1, 2, 32);
+    if (live && lane == 0) {
+        float result = r;
+        for (int i = np; i < hidden; ++i) result += w[static_cast<int64_t>(e) * hidden + i] * x[static_cast<int64_t>(t) * hidden + i];
+        logits[static_cast<int64_t>(t) * n_expert + e] = bias ? result + bias[e] : result;
+    }
+}
+
+// One wave per token: top-k by repeated arg-max (value desc, then lower index), then ggml
+// soft_max over the selected (expf per value, sum in double, scale by (float)(1/sum)).
+__global__ __launch_bounds__(64) void topk_softmax_kernel(const float * __restrict__ logits, int n_expert,
+                                                          int top_k, int32_t * __restrict__ ids,
+                                                          float * __restrict__ weights) {
+    const int t = blockIdx.x;
+    const int lane = threadIdx.x;
+    const float * l = logits + static_cast<int64_t>(t) * n_expert;
+    __shared__ int s_ids[64];
+    __shared__ float s_vals[64];
+    uint64_t taken[16] = {0};  // supports n_expert <= 1024 (64 lanes x 16 strides)
+    for (int j = 0; j < top_k; ++j) {
+        float best = 0.0f;
+        int best_i = -1;
+        for (int s = 0; s * 64 + lane < n_expert; ++s) {
+            const int i = s * 64 + lane;
+            if ((taken[s] >> lane) & 1ull) continue;
+            const float v = l[i];
+            if (best_i < 0 || v > best) { best = v; best_i = i; }
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(best, off);
+            const int oi = __shfl_xor(best_i, off);
+            const bool better = oi >= 0 && (best_i < 0 || ov > best || (ov == best && oi < best_i));
+            if (better) { best = ov; best_i = oi; }
+        }
+        if (best_i >= 0 && (best_i & 63) == lane) taken[best_i >> 6] |= 1ull << lane;
+        if (lane == 0) { s_ids[j] = best_i; s_vals[j] = best; }
+    }
+    __syncthreads();
+    if (lane == 0) {
+        float max = -INFINITY;
+        for (int j = 0; j < top_k; ++j) max = s_vals[j] > max ? s_vals[j] : max;
+        double sum = 0.0;
+        float y[64];
+        for (int j = 0; j < top_k; ++j) {
+            y[j] = expf_rn(s_vals[j] - max);
+            sum += static_cast<double>(y[j]);
+        }
+        const float scale = static_cast<float>(1.0 / sum);
+        for (int j = 0; j < top_k; ++j) {
+            ids[static_cast<int64_t>(t) * top_k + j] = s_ids[j];
+            weights[static_cast<int64_t>(t) * top_k + j] = y[j] * scale;
+        }
+    }
+}
+
+// out[t][i] = ((w0*y0 + w1*y1) + w2*y2) + ... : ggml MUL by the weight then sequential ADD.
+__global__ void combine_kernel(const float * __restrict__ y, const float * __restrict__ w, int64_t rows,
+                               int n_ids, int64_t n_tokens, float * __restrict__ out) {
+    const int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (idx >= rows * n_tokens) return;
+    const int64_t t = idx / rows, i = idx % rows;
+    const float * yt = y + t * n_ids * rows + i;
+    const float * wt = w + t * n_ids;
+    float acc = yt[0] * wt[0];
+    for (int r = 1; r < n_ids; ++r) {
+        const float term = yt[r * rows] * wt[r];
+        acc = acc + term;
+    }
+    out[idx] = acc;
+}
+
+__global__ void add_id_kernel(float * __restrict__ y, const float * __restrict__ bias, const int32_t * __restrict__ ids,
+                              int64_t rows, int n_ids, int64_t n_tokens, int64_t ids_stride) {
+    const int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (idx >= rows * n_ids * n_tokens) return;
+    const int64_t i = idx % rows, j = idx / rows;
+    const int64_t t = j / n_ids, r = j % n_ids;
+    const int id = ids[t * ids_stride + r];
+    if (id < 0) return;
+    y[idx] = y[idx] + bias[static_cast<int64_t>(id) * rows + i];
+}
+
+__global__ void glu_kernel(int activation, const float * __restrict__ gate, const float * __restrict__ up,
+                           float * __restrict__ out, int64_t n_rows, int64_t width, int64_t gs, int64_t us,
+                           int64_t os, float alpha, float limit) {
+    const int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (idx >= n_rows * width) return;
+    const int64_t row = idx / width, i = idx % width;
+    const float g0 = gate[row * gs + i], u0 = up[row * us + i];
+    float v;
+    if (activation == VBM_ACT_SWIGLU_OAI) {
+        const float g = limit < g0 ? limit : g0;
+        const float u = u0 < -limit ? -limit : (limit < u0 ? limit : u0);
+        v = (g / (1.0f + expf_rn(alpha * (-g)))) * (u + 1.0f);
+    } else {
+        v = g0 / (1.0f + expf_rn(-g0)) * u0;
+    }
+    out[row * os + i] = v;
+}
+
+unsigned blocks_for(int64_t n, int threads) { return static_cast<unsigned>((n + threads - 1) / threads); }
+
+}  // namespace
+
+size_t group_workspace_bytes(int64_t n_as, int64_t n_entries) {
+    return static_cast<size_t>(n_as + (n_as + 1) + n_entries + n_as + 1 + 1 + 8) * sizeof(int32_t);
+}
+
+GroupBuffers carve_group(void * base, int64_t n_as, int64_t n_entries) {
+    auto * p = static_cast<int32_t *>(base);
+    GroupBuffers g{};
+    g.counts = p; p += n_as;
+    g.offsets = p; p += n_as + 1;
+    g.rows = p; p += n_entries;
+    g.active = p; p += n_as;
+    g.n_active = p; p += 1;
+    g.error = p;
+    return g;
+}
+
+void launch_group(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride, int64_t n_as,
+                  const GroupBuffers & g, hipStream_t stream) {
+    require(n_as > 0 && n_as <= kMaxExperts, "grouping supports 1..1024 experts");
+    require(n_ids > 0 && n_tokens > 0 && n_ids * n_tokens <= (1ll << 24), "grouping entry count out of range");
+    require(ids_stride >= n_ids, "ids token stride must be >= n_ids");
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(kGroupThreads), 0, stream, ids, static_cast<int>(n_ids),
+                       static_cast<int>(n_tokens), ids_stride, static_cast<int>(n_as), g.counts, g.offsets, g.rows,
+                       g.active, g.n_active, g.error);
+    check_hip(hipGetLastError(), "grouping launch");
+}
+
+void launch_quantize_q8_0(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, uint8_t * dst,
+                          hipStream_t stream) {
+    require(k > 0 && k % 32 == 0 && n_rows > 0 && x_stride >= k, "quantize needs k % 32 == 0 and stride >= k");
+    const int64_t blocks = n_rows * (k / 32);
+    hipLaunchKernelGGL(quantize_kernel, dim3(blocks_for(blocks, 8)), dim3(256), 0, stream, x, n_rows,
+                       static_cast<int>(k / 32), x_stride, dst);
+    check_hip(hipGetLastError(), "quantize launch");
+}
+
+void launch_router(const float * router_w, const float * router_b, const float * x, int64_t hidden, float * logits,
+                   int64_t n_expert, int64_t n_tokens, int64_t top_k, int32_t * ids, float * weights,
+                   hipStream_t stream) {
+    require(n_expert > 0 && n_expert <= 1024 && top_k > 0 && top_k <= n_expert && top_k <= 64 && n_tokens > 0,
+            "router supports 1..1024 experts and top_k <= 64");
+    if (router_w) {
+        require(x != nullptr && logits != nullptr && hidden > 0, "router GEMV needs x, hidden and a logits buffer");
+        hipLaunchKernelGGL(router_logits_kernel, dim3(blocks_for(n_expert * n_tokens, 8)), dim3(256), 0, stream,
+                           router_w, router_b, x, static_cast<int>(hidden), static_cast<int>(n_expert),
+                           static_cast<int>(n_tokens), logits);
+        check_hip(hipGetLastError(), "router logits launch");
+    }
+    hipLaunchKernelGGL(topk_softmax_kernel, dim3(static_cast<unsigned>(n_tokens)), dim3(64), 0, stream, logits,
+                       static_cast<int>(n_expert), static_cast<int>(top_k), ids, weights);
+    check_hip(hipGetLastError(), "top-k launch");
+}
+
+void launch_combine(const float * y, const float * weights, int64_t rows, int64_t n_ids, int64_t n_tokens, float * out,
+                    hipStream_t stream) {
+    hipLaunchKernelGGL(combine_kernel, dim3(blocks_for(rows * n_tokens, 256)), dim3(256), 0, stream, y, weights, rows,
+                       static_cast<int>(n_ids), n_tokens, out);
+    check_hip(hipGetLastError(), "combine launch");
+}
+
+void launch_add_id(float * y, const float * bias, const int32_t * ids, int64_t rows, int64_t n_ids, int64_t n_tokens,
+                   int64_t ids_stride, hipStream_t stream) {
+    hipLaunchKernelGGL(add_id_kernel, dim3(blocks_for(rows * n_ids * n_tokens, 256)), dim3(256), 0, stream, y, bias, ids,
+                       rows, static_cast<int>(n_ids), n_tokens, ids_stride);
+    check_hip(hipGetLastError(), "add_id launch");
+}
+
+void launch_glu(int activation, const float * gate, const float * up, float * out, int64_t n_rows, int64_t width,
+                int64_t gate_stride, int64_t up_stride, int64_t out_stride, float alpha, float limit,
+                hipStream_t stream) {
+    hipLaunchKernelGGL(glu_kernel, dim3(blocks_for(n_rows * width, 256)), dim3(256), 0, stream, activation, gate, up, out,
+                       n_rows, width, gate_stride, up_stride, out_stride, alpha, limit);
+    check_hip(hipGetLastError(), "glu launch");
+}
+
+}  // namespace vbm

@@ -1,0 +1,248 @@
+"""ctypes binding of libvbmoe.so (include/vbmoe.h) plus small numpy helpers.
+
+The library is the product; this module only declares its C signatures and wraps device
+buffers. Importing it never touches the GPU; `load()` raises if libvbmoe.so is missing, so
+callers fail loudly rather than fall back to anything else.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "libvbmoe.so"
+HEADER = Path(__file__).resolve().parents[2] / "include" / "vbmoe.h"
+
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_I32, TYPE_MXFP4 = 0, 1, 8, 26, 39
+ACT_SILU, ACT_SWIGLU_OAI = 0, 1
+ORDER_EXACT, ORDER_FAST = 0, 1
+STATUS = {0: "OK", 1: "INVALID_ARGUMENT", 2: "RUNTIME", 3: "UNSUPPORTED", 4: "OUT_OF_MEMORY"}
+
+vp, sz, i64, u64, i32p, f32p = C.c_void_p, C.c_size_t, C.c_int64, C.c_uint64, C.c_void_p, C.c_void_p
+
+
+class MoeLayerDesc(C.Structure):
+    _fields_ = [
+        ("gate_up", vp), ("down", vp), ("gate_up_bias", vp), ("down_bias", vp), ("expert_to_slot", vp),
+        ("router_w", vp), ("router_b", vp), ("hidden", i64), ("intermediate", i64), ("n_expert", i64),
+        ("top_k", i64), ("activation", C.c_int), ("order", C.c_int),
+    ]
+
+
+# name -> argtypes (all return vbm_status as c_int)
+SIGNATURES = {
+    "vbm_device_count": [C.POINTER(C.c_int)],
+    "vbm_set_device": [C.c_int],
+    "vbm_device_name": [C.c_int, C.c_char_p, sz],
+    "vbm_mem_info": [C.POINTER(sz), C.POINTER(sz)],
+    "vbm_malloc": [C.POINTER(vp), sz],
+    "vbm_free": [vp],
+    "vbm_host_alloc": [C.POINTER(vp), sz],
+    "vbm_host_free": [vp],
+    "vbm_memcpy_h2d": [vp, vp, sz, vp],
+    "vbm_memcpy_d2h": [vp, vp, sz, vp],
+    "vbm_memcpy_d2d": [vp, vp, sz, vp],
+    "vbm_memset": [vp, C.c_int, sz, vp],
+    "vbm_stream_create": [C.POINTER(vp)],
+    "vbm_stream_destroy": [vp],
+    "vbm_stream_synchronize": [vp],
+    "vbm_device_synchronize": [],
+    "vbm_event_create": [C.POINTER(vp)],
+    "vbm_event_destroy": [vp],
+    "vbm_event_record": [vp, vp],
+    "vbm_event_synchronize": [vp],
+    "vbm_event_query": [vp, C.POINTER(C.c_int)],
+    "vbm_event_elapsed_ms": [vp, vp, C.POINTER(C.c_float)],
+    "vbm_synth_mxfp4_host": [u64, u64, u64, u64, C.c_int, C.c_int, vp],
+    "vbm_synth_q8_0_host": [u64, u64, u64, u64, C.c_float, C.c_float, vp],
+    "vbm_synth_normal_host": [u64, u64, u64, u64, C.c_float, C.c_float, vp],
+    "vbm_bank_create": [C.c_int, i64, i64, i64, C.c_int, C.POINTER(vp)],
+    "vbm_bank_destroy": [vp],
+    "vbm_bank_info": [vp, C.POINTER(C.c_int), C.POINTER(i64), C.POINTER(i64), C.POINTER(i64), C.POINTER(sz),
+                      C.POINTER(vp)],
+    "vbm_bank_upload": [vp, i64, vp, C.c_int, vp],
+    "vbm_bank_export": [vp, i64, vp, sz, vp],
+    "vbm_bank_generate": [vp, i64, i64, u64, u64, i64, C.c_float, C.c_float, vp],
+    "vbm_quantize_q8_0": [vp, i64, i64, i64, vp, vp],
+    "vbm_mul_mat_id": [vp, vp, vp, i64, C.c_int, vp, i64, vp, i64, i64, i64, vp, vp, C.c_int, vp],
+    "vbm_add_id": [vp, vp, vp, i64, i64, i64, i64, vp],
+    "vbm_glu": [C.c_int, vp, vp, vp, i64, i64, i64, i64, i64, C.c_float, C.c_float, vp],
+    "vbm_router_topk_softmax": [vp, vp, vp, i64, vp, i64, i64, i64, vp, vp, vp],
+    "vbm_group_by_expert": [vp, i64, i64, i64, i64, vp, vp, vp, vp, vp],
+    "vbm_weighted_combine": [vp, vp, i64, i64, i64, vp, vp],
+    "vbm_moe_layer_workspace": [C.POINTER(MoeLayerDesc), i64, C.POINTER(sz)],
+    "vbm_moe_layer_forward": [C.POINTER(MoeLayerDesc), vp, vp, i64, vp, vp, vp, vp, sz, vp],
+}
+OTHER = {"vbm_last_error": ([], C.c_char_p), "vbm_abi_version": ([], C.c_int)}
+
+_lib = None
+
+
+class VbmError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS.get(status, status)}: {message}")
+        self.status = status
+
+
+def load(path: str | os.PathLike | None = None) -> C.CDLL:
+    """Load libvbmoe.so (raises FileNotFoundError when it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(f"{p} not built; run unified-memory-scheduler_amd/build_lib.py")
+    lib = C.CDLL(str(p))
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = C.c_int
+    for name, (args, res) in OTHER.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = lib
+    return lib
+
+
+def declared_symbols() -> list[str]:
+    """Function names declared in include/vbmoe.h."""
+    import re
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(vbm_[a-z0-9_]+)\s*\(", text)))
+
+
+def call(name: str, *args):
+    lib = load()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        raise VbmError(status, lib.vbm_last_error().decode())
+    return status
+
+
+def ptr(x) -> int | None:
+    if x is None:
+        return None
+    if isinstance(x, DeviceBuffer):
+        return x.ptr
+    if isinstance(x, np.ndarray):
+        return x.ctypes.data
+    return int(x)
+
+
+class DeviceBuffer:
+    """Owning device allocation."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = vp()
+        call("vbm_malloc", C.byref(p), max(self.nbytes, 1))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, arr: np.ndarray, stream=None) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        buf = cls(arr.nbytes)
+        buf.upload(arr, stream)
+        return buf
+
+    def upload(self, arr: np.ndarray, stream=None) -> None:
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        call("vbm_memcpy_h2d", self.ptr, arr.ctypes.data, arr.nbytes, stream)
+        call("vbm_stream_synchronize", stream)
+
+    def download(self, dtype, shape, stream=None) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        call("vbm_memcpy_d2h", out.ctypes.data, self.ptr, out.nbytes, stream)
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            call("vbm_free", self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and _lib is not None:
+                _lib.vbm_free(self.ptr)
+                self.ptr = None
+        except Exception:
+            pass
+
+
+class Bank:
+    """Device expert bank (vbm_bank)."""
+
+    def __init__(self, type_id: int, rows: int, k: int, n_slots: int, interleave: bool = False):
+        h = vp()
+        call("vbm_bank_create", type_id, rows, k, n_slots, int(interleave), C.byref(h))
+        self.handle = h.value
+        self.type_id, self.rows, self.k, self.n_slots = type_id, rows, k, n_slots
+        self.interleave = interleave
+        s = sz()
+        base = vp()
+        call("vbm_bank_info", self.handle, None, None, None, None, C.byref(s), C.byref(base))
+        self.slot_bytes = s.value
+        self.base = base.value
+
+    def upload(self, slot: int, ggml_bytes: np.ndarray, stream=None) -> None:
+        data = np.ascontiguousarray(ggml_bytes, dtype=np.uint8)
+        assert data.nbytes == self.slot_bytes, (data.nbytes, self.slot_bytes)
+        call("vbm_bank_upload", self.handle, slot, data.ctypes.data, 0, stream)
+
+    def export(self, slot: int, stream=None) -> np.ndarray:
+        out = np.empty(self.slot_bytes, dtype=np.uint8)
+        call("vbm_bank_export", self.handle, slot, out.ctypes.data, out.nbytes, stream)
+        return out
+
+    def generate(self, first_slot: int, count: int, seed: int, stream_id: int, first_expert: int,
+                 p0: float, p1: float, stream=None) -> None:
+        call("vbm_bank_generate", self.handle, first_slot, count, seed, stream_id, first_expert, p0, p1, stream)
+
+    def destroy(self) -> None:
+        if self.handle:
+            call("vbm_bank_destroy", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            if self.handle and _lib is not None:
+                _lib.vbm_bank_destroy(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
+# ----------------------------------------------------------------------------------- synthetic
+def synth_mxfp4(seed: int, stream: int, first_block: int, n_blocks: int, exp_lo: int = -8, exp_hi: int = -3) -> np.ndarray:
+    out = np.empty(n_blocks * 17, dtype=np.uint8)
+    call("vbm_synth_mxfp4_host", seed, stream, first_block, n_blocks, exp_lo, exp_hi, out.ctypes.data)
+    return out
+
+
+def synth_q8_0(seed: int, stream: int, first_block: int, n_blocks: int, lo: float = 1e-3, hi: float = 1e-2) -> np.ndarray:
+    out = np.empty(n_blocks * 34, dtype=np.uint8)
+    call("vbm_synth_q8_0_host", seed, stream, first_block, n_blocks, lo, hi, out.ctypes.data)
+    return out
+
+
+def synth_normal(seed: int, stream: int, first: int, n: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    call("vbm_synth_normal_host", seed, stream, first, n, mean, std, out.ctypes.data)
+    return out
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    call("vbm_device_count", C.byref(n))
+    return n.value
+
+
+def device_name(device: int = 0) -> str:
+    buf = C.create_string_buffer(256)
+    call("vbm_device_name", device, buf, 256)
+    return buf.value.decode()
