@@ -1,0 +1,318 @@
+#!/usr/bin/env python3
+"""MoE decode throughput on one MI355X: 120B-shape MXFP4 stack (hidden 2880, 128 experts, top-4,
+intermediate 2880, 36 layers, ~61 GB of expert weights resident in HBM), batch 1 by default.
+
+One step = one decode token through all 36 routed-expert layers (router top-k + softmax on the
+given N(0,1) logits, Q8_0 activation quantization, grouping, gate_up GEMV + biases + SwiGLU-OAI,
+Q8_0 requantization, down GEMV + bias, weighted rank-ordered combine), replayed as one HIP graph.
+Inputs (weights, biases, logits, hidden state) are synthetic, seeded, and resident before timing.
+
+Prints ONE JSON line (stdout). Progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "unified-memory-scheduler_amd"))
+
+import vbmoe as vb  # noqa: E402
+
+METRIC = "MoE decode tok/s (120B-shape, bs1) + expert GEMV HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+MXFP4_ROW_BYTES = 2880 // 32 * 17          # 1530 B per 2880-wide row
+SEED = 20260120
+
+
+def log(msg: str) -> None:
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+class Stack:
+    """36 seeded 120B-shape layers resident on the device."""
+
+    def __init__(self, layers: int, experts: int, hidden: int, inter: int, top_k: int, tokens: int):
+        self.L, self.E, self.H, self.I, self.K, self.T = layers, experts, hidden, inter, top_k, tokens
+        self.gate_up, self.down, self.gu_bias, self.dn_bias, self.descs = [], [], [], [], []
+        t0 = time.time()
+        for l in range(layers):
+            gu = vb.Bank(vb.TYPE_MXFP4, 2 * inter, hidden, experts, True)
+            dn = vb.Bank(vb.TYPE_MXFP4, hidden, inter, experts, False)
+            gu.generate(0, experts, SEED, 16 * l + 1, 0, -8, -3)
+            dn.generate(0, experts, SEED, 16 * l + 2, 0, -8, -3)
+            gub = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 16 * l + 3, 0, experts * 2 * inter, 0.0, 0.02))
+            dnb = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 16 * l + 4, 0, experts * hidden, 0.0, 0.02))
+            self.gate_up.append(gu)
+            self.down.append(dn)
+            self.gu_bias.append(gub)
+            self.dn_bias.append(dnb)
+            self.descs.append(vb.MoeLayerDesc(gu.handle, dn.handle, gub.ptr, dnb.ptr, None, None, None, hidden, inter,
+                                              experts, top_k, vb.ACT_SWIGLU_OAI, vb.ORDER_EXACT))
+            if l % 6 == 5:
+                log(f"generated layers 0..{l} ({(l + 1) * (gu.slot_bytes + dn.slot_bytes) * experts / 1e9:.1f} GB)")
+        vb.call("vbm_device_synchronize")
+        self.weight_bytes = layers * experts * (self.gate_up[0].slot_bytes + self.down[0].slot_bytes)
+        log(f"stack resident: {self.weight_bytes / 1e9:.2f} GB in {time.time() - t0:.1f} s")
+        ws = C.c_size_t()
+        vb.call("vbm_moe_layer_workspace", C.byref(self.descs[0]), tokens, C.byref(ws))
+        self.ws_bytes = ws.value
+        self.ws = vb.DeviceBuffer(ws.value)
+        self.x0 = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 6, 0, tokens * hidden))
+        self.xa = vb.DeviceBuffer(4 * tokens * hidden)
+        self.xb = vb.DeviceBuffer(4 * tokens * hidden)
+        self.logits_cur = vb.DeviceBuffer(4 * layers * tokens * experts)
+        self.ids = vb.DeviceBuffer(4 * layers * tokens * top_k)
+
+    def step_logits_bytes(self) -> int:
+        return 4 * self.L * self.T * self.E
+
+    def enqueue_step(self, stream, events=None) -> None:
+        """x0 -> 36 layers -> xa/xb, reading logits_cur[l]. With `events` ([L][4] list of event handles)
+        the profiled forward brackets both GEMVs of every layer."""
+        vb.call("vbm_memcpy_d2d", self.xa.ptr, self.x0.ptr, 4 * self.T * self.H, stream)
+        src, dst = self.xa, self.xb
+        for l, d in enumerate(self.descs):
+            logits = self.logits_cur.ptr + 4 * l * self.T * self.E
+            ids = self.ids.ptr + 4 * l * self.T * self.K
+            if events is None:
+                vb.call("vbm_moe_layer_forward", C.byref(d), src.ptr, logits, self.T, dst.ptr, ids, None, self.ws.ptr,
+                        self.ws_bytes, stream)
+            else:
+                arr = (C.c_void_p * 4)(*events[l])
+                vb.call("vbm_moe_layer_forward_profiled", C.byref(d), src.ptr, logits, self.T, dst.ptr, ids, None,
+                        self.ws.ptr, self.ws_bytes, C.cast(arr, C.c_void_p), stream)
+            src, dst = dst, src
+
+
+def distinct_experts(ids: np.ndarray) -> int:
+    return int(sum(len(np.unique(ids[l].reshape(-1))) for l in range(ids.shape[0])))
+
+
+def cpu_baseline(args, logits_host: np.ndarray) -> dict:
+    """The CPU oracle (a port of the reference's ggml x86 MXFP4 x Q8_0 path) timed on this host on
+    a bounded sample: the first `--cpu-layers` layers of the same seeded stack, each with all 128
+    experts on the host, for as many tokens as fit in --cpu-seconds; per-token time scaled to 36
+    layers."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle_py
+    oracle_py.load()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    threads = max(1, min(threads, len(os.sched_getaffinity(0))))
+    E, H, I, K = args.experts, 2880, 2880, 4
+    layers = []
+    t0 = time.time()
+    for l in range(args.cpu_layers):
+        blocks_gu, blocks_dn = E * 2 * I * (H // 32), E * H * (I // 32)
+        gu = vb.synth_mxfp4(SEED, 16 * l + 1, 0, blocks_gu)
+        dn = vb.synth_mxfp4(SEED, 16 * l + 2, 0, blocks_dn)
+        layers.append((gu, dn, vb.synth_normal(SEED, 16 * l + 3, 0, E * 2 * I, 0.0, 0.02),
+                       vb.synth_normal(SEED, 16 * l + 4, 0, E * H, 0.0, 0.02)))
+    log(f"cpu baseline: {args.cpu_layers} host layers ready in {time.time() - t0:.1f} s; timing with {threads} threads")
+    x0 = vb.synth_normal(SEED, 6, 0, H).reshape(1, H)
+    done = 0
+    elapsed = 0.0
+    while True:
+        tok = done % logits_host.shape[0]
+        x = x0
+        t = time.perf_counter()
+        for l, (gu, dn, gub, dnb) in enumerate(layers):
+            r = oracle_py.moe_layer(39, gu, dn, gub, dnb, x, H, I, E, K, activation=1,
+                                    logits=logits_host[tok, l].reshape(1, E), threads=threads)
+            x = r["out"]
+        elapsed += time.perf_counter() - t
+        done += 1
+        if (elapsed >= args.cpu_seconds and done >= 2) or done >= 4096:
+            break
+    per_layer_token = elapsed / (done * args.cpu_layers)
+    return {"value": round(1.0 / (per_layer_token * args.layers), 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{done} decode tokens x first {args.cpu_layers} of {args.layers} layers (all {E} experts on host, "
+                      f"bs1) in {elapsed:.1f} s; per-layer time scaled x{args.layers}; oracle fast path "
+                      f"(ISA level {oracle_py.load().orc_fast_isa()})"}
+
+
+def read_traffic(path: Path):
+    """Measured HBM bytes per gate_up launch from the committed rocprofv3 PMC summary, if any."""
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith("traffic_bytes_per_launch:"):
+            try:
+                return int(float(line.split(":", 1)[1].strip()))
+            except ValueError:
+                return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", type=int, default=1, help="decode batch (tokens per step)")
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--experts", type=int, default=128)
+    ap.add_argument("--mode", choices=("graph", "eager"), default="graph")
+    ap.add_argument("--kernel-steps", type=int, default=10, help="steps of the event-timed kernel pass")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-layers", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures the routed-expert path on exactly one GPU; --gpus {args.gpus} "
+              f"(WORLD_SIZE {world}) is not supported: this build has no multi-GPU path.", file=sys.stderr)
+        return 2
+
+    vb.load()
+    assert vb.device_count() >= 1, "no HIP device"
+    vb.call("vbm_set_device", 0)
+    log(f"device: {vb.device_name(0)}")
+    H, I, E, K, L, T = 2880, 2880, args.experts, 4, args.layers, args.tokens
+    stack = Stack(L, E, H, I, K, T)
+    n_steps = args.warmup + args.steps
+    logits_host = vb.synth_normal(SEED, 7, 0, n_steps * L * T * E).reshape(n_steps, L, T, E)
+    logits_all = vb.DeviceBuffer.from_array(logits_host)
+    stream = C.c_void_p()
+    vb.call("vbm_stream_create", C.byref(stream))
+    stream = stream.value
+    step_bytes = stack.step_logits_bytes()
+
+    graph = None
+    if args.mode == "graph":
+        g = C.c_void_p()
+        vb.call("vbm_graph_begin_capture", stream)
+        stack.enqueue_step(stream)
+        vb.call("vbm_graph_end_capture", stream, C.byref(g))
+        graph = g.value
+        log("captured one decode step (36 layers) as a HIP graph")
+
+    def run_step(i: int) -> None:
+        vb.call("vbm_memcpy_d2d", stack.logits_cur.ptr, logits_all.ptr + i * step_bytes, step_bytes, stream)
+        if graph is not None:
+            vb.call("vbm_graph_launch", graph, stream)
+        else:
+            stack.enqueue_step(stream)
+
+    for i in range(args.warmup):
+        run_step(i)
+    vb.call("vbm_stream_synchronize", stream)
+    vb.call("vbm_device_synchronize")
+    ev0, ev1 = C.c_void_p(), C.c_void_p()
+    vb.call("vbm_event_create", C.byref(ev0))
+    vb.call("vbm_event_create", C.byref(ev1))
+    distinct = 0
+    t_wall = time.perf_counter()
+    vb.call("vbm_event_record", ev0.value, stream)
+    for i in range(args.steps):
+        run_step(args.warmup + i)
+    vb.call("vbm_event_record", ev1.value, stream)
+    vb.call("vbm_stream_synchronize", stream)
+    vb.call("vbm_device_synchronize")
+    wall = time.perf_counter() - t_wall
+    ms = C.c_float()
+    vb.call("vbm_event_elapsed_ms", ev0.value, ev1.value, C.byref(ms))
+    ms_total = ms.value
+    for i in range(args.steps):
+        ids = np.stack([np.lexsort((np.arange(E), -logits_host[args.warmup + i, l, t]))[:K]
+                        for l in range(L) for t in range(T)]).reshape(L, T * K)
+        distinct += distinct_experts(ids)
+    tok_s = args.steps * T / (ms_total / 1e3)
+    ms_per_step = ms_total / args.steps
+    expert_bytes = 2 * I * MXFP4_ROW_BYTES + H * MXFP4_ROW_BYTES + (2 * I + H) * 4
+    step_weight_bytes = distinct / args.steps * expert_bytes
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, {tok_s:.1f} tok/s "
+        f"(host wall {wall:.3f} s); step expert bytes {step_weight_bytes / 1e9:.3f} GB -> "
+        f"{step_weight_bytes / (ms_per_step / 1e3) / 1e9:.0f} GB/s")
+
+    # Event-timed kernel pass: the same decode steps, launched eagerly with events around both GEMVs.
+    events = []
+    for _ in range(L):
+        row = []
+        for _ in range(4):
+            e = C.c_void_p()
+            vb.call("vbm_event_create", C.byref(e))
+            row.append(e.value)
+        events.append(row)
+    gu_ms, dn_ms, launches = 0.0, 0.0, 0
+    for i in range(args.kernel_steps):
+        src = (args.warmup + i) % n_steps
+        vb.call("vbm_memcpy_d2d", stack.logits_cur.ptr, logits_all.ptr + src * step_bytes, step_bytes, stream)
+        stack.enqueue_step(stream, events)
+        vb.call("vbm_stream_synchronize", stream)
+        for l in range(L):
+            a, b = C.c_float(), C.c_float()
+            vb.call("vbm_event_elapsed_ms", events[l][0], events[l][1], C.byref(a))
+            vb.call("vbm_event_elapsed_ms", events[l][2], events[l][3], C.byref(b))
+            gu_ms += a.value
+            dn_ms += b.value
+            launches += 1
+    gu_avg_us = gu_ms / launches * 1e3
+    dn_avg_us = dn_ms / launches * 1e3
+    # Algorithmic bytes per gate_up launch at this batch: distinct experts x (5760 rows x 1530 B +
+    # 5760 fp32 biases) + Q8_0 input (T x 3060 B) + fp32 GLU output (T x K x 2880 x 4 B).
+    mean_distinct = distinct / (args.steps * L)
+    gu_bytes = mean_distinct * (2 * I * MXFP4_ROW_BYTES + 2 * I * 4) + T * (H // 32) * 34 + T * K * I * 4
+    dn_bytes = mean_distinct * (H * MXFP4_ROW_BYTES + H * 4) + T * K * I * 4 + T * K * H * 4
+    gu_gbs = gu_bytes / (gu_avg_us * 1e-6) / 1e9
+    dn_gbs = dn_bytes / (dn_avg_us * 1e-6) / 1e9
+    log(f"gate_up GEMV: {gu_avg_us:.2f} us avg over {launches} launches -> {gu_gbs:.0f} GB/s; "
+        f"down GEMV: {dn_avg_us:.2f} us -> {dn_gbs:.0f} GB/s")
+    traffic = read_traffic(REPO / "profiles" / "gemv_gate_up_120b_bs1_pmc.md") if T == 1 else None
+
+    cpu = None
+    if not args.no_cpu and T == 1:
+        cpu = cpu_baseline(args, logits_host[:, :, 0, :])
+        log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads")
+
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i32+f32",
+        "data": "synthetic (seeded MXFP4 codes, e8m0 in [-8,-3], N(0,0.02) biases, N(0,1) logits and hidden state)",
+        "config": {
+            "workload": f"120B-shape MXFP4 MoE decode: {L} layers x {E} experts, top-{K}, hidden {H}, "
+                        f"intermediate {I}, batch {T}, weights resident in HBM",
+            "layers": L, "experts": E, "top_k": K, "hidden": H, "intermediate": I, "batch": T,
+            "resident_weight_bytes": stack.weight_bytes, "launch": args.mode,
+            "expert_bytes_per_step": round(step_weight_bytes),
+            "step_expert_gbs": round(step_weight_bytes / (ms_per_step / 1e3) / 1e9, 1),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "expert_gemv_kernel<MXFP4,MT=1> gate_up (+bias +SwiGLU-OAI epilogue)",
+            "achieved": round(gu_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "bytes_per_launch": round(gu_bytes),
+            "avg_launch_us": round(gu_avg_us, 3),
+            "down_kernel": {"achieved": round(dn_gbs, 1), "avg_launch_us": round(dn_avg_us, 3),
+                            "bytes_per_launch": round(dn_bytes)},
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    if graph is not None:
+        vb.call("vbm_graph_destroy", graph)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -245,6 +245,29 @@ vbm_status vbm_moe_layer_forward(const vbm_moe_layer_desc * desc, const float * 
                                  int32_t * ids, float * weights, void * workspace,
                                  size_t workspace_bytes, void * stream);
 
+/* Same as vbm_moe_layer_forward, also recording events[0..3] (hipEvent_t as void*) on `stream`
+ * immediately before/after the gate_up GEMV and before/after the down GEMV, so callers can time
+ * the two dominant kernels over a live run. No reference counterpart (profiling hook, the
+ * analogue of the scheduler counters of hybrid-experts.patch:143-172). */
+vbm_status vbm_moe_layer_forward_profiled(const vbm_moe_layer_desc * desc, const float * x,
+                                          float * logits, int64_t n_tokens, float * out,
+                                          int32_t * ids, float * weights, void * workspace,
+                                          size_t workspace_bytes, void * const * events,
+                                          void * stream);
+
+/* ----------------------------------------------------------------------------------------------
+ * HIP graph capture of stream-ordered work (per-token layer chains replay without host launch
+ * overhead). Only entry points that do not allocate (the layer forward with a caller workspace,
+ * the router, combine, quantize and device copies) may be captured.
+ * -------------------------------------------------------------------------------------------- */
+vbm_status vbm_graph_begin_capture(void * stream);
+vbm_status vbm_graph_end_capture(void * stream, void ** graph_exec);
+vbm_status vbm_graph_launch(void * graph_exec, void * stream);
+vbm_status vbm_graph_destroy(void * graph_exec);
+
+/* Plain streaming copy kernel (16 B per lane); a known-size HBM reference for counter scaling. */
+vbm_status vbm_copy_kernel(void * dst, const void * src, size_t bytes, void * stream);
+
 #ifdef __cplusplus
 }
 #endif

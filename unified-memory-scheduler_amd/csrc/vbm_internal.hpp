@@ -99,23 +99,44 @@ void launch_glu(int activation, const float * gate, const float * up, float * ou
                 int64_t width, int64_t gate_stride, int64_t up_stride, int64_t out_stride, float alpha,
                 float limit, hipStream_t stream);
 
-// Expert GEMV over grouped jobs. Activation input is Q8_0 blocks (act_q8, row stride in bytes)
-// or fp32 rows (act_f32, row stride in floats) quantized inside the kernel. act_row(j) =
-// b_ne1 == 1 ? j / n_ids : j. Epilogue 0 writes dst[j][rows] (+bias), epilogue 1 (fused
-// gate|up bank) writes the GLU output dst[j][rows/2].
+// Activation rows ("xrows"): one Q8_0-quantized activation vector per token (or per token and
+// rank), expanded for the GEMV's scalar loads. For a row of nb blocks:
+//   codes  [8 slices][nb] x 8 B (4 x f16, MXFP4 consumer) or x 4 B (4 x int8, Q8_0 consumer);
+//          slice k of block b holds elements 4k..4k+3 of the block's 32 codes;
+//   da     [nb] f32 (the block's fp16 scale, widened);
+//   flag   int32: 1 when any code is -128 (selects the VPSIGNB-exact slow path).
+struct XrowLayout {
+    int64_t nb;
+    int weight_type;  // 39 (f16 codes) or 8 (int8 codes)
+    VBM_HD int64_t code_entry() const { return weight_type == 39 ? 8 : 4; }
+    VBM_HD int64_t da_offset() const { return 8 * nb * code_entry(); }
+    VBM_HD int64_t flag_offset() const { return da_offset() + 4 * nb; }
+    VBM_HD int64_t stride() const { return (flag_offset() + 4 + 63) / 64 * 64; }
+};
+
+// fp32 rows -> Q8_0 (x86 contract) -> xrows (and optionally ggml Q8_0 blocks).
+void launch_quantize_expand(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, const XrowLayout & lay,
+                            uint8_t * xrows, uint8_t * q8_blocks, hipStream_t stream);
+// ggml Q8_0 block rows -> xrows.
+void launch_expand_q8(const uint8_t * q8, int64_t n_rows, int64_t row_bytes, const XrowLayout & lay, uint8_t * xrows,
+                      hipStream_t stream);
+
+// Expert GEMV over grouped jobs, reading activation rows (xrows) with act_row(j) =
+// b_ne1 == 1 ? j / n_ids : j. Epilogue 0 writes dst[j][rows] (+bias); epilogue 1 (fused gate|up
+// bank) applies biases and the GLU, quantizes each 32-output block to Q8_0 and writes the down
+// projection's activation row j into dst_xrows.
 struct GemvArgs {
     const vbm_bank * bank;
     const int32_t * expert_to_slot;   // device or null
-    const uint8_t * act_q8;
-    const float * act_f32;
-    int64_t act_stride;               // bytes for q8, floats for f32
+    const uint8_t * xrows;
     int64_t n_ids, b_ne1;
     GroupBuffers group;
     int64_t max_active;               // host bound on the number of active experts
-    int64_t max_per_expert;           // host bound on jobs per expert
     const float * bias;               // [n_as][rows] ggml row order, or null
-    float * dst;
-    int epilogue;                     // 0 plain, 1 GLU
+    float * dst;                      // epilogue 0
+    uint8_t * dst_xrows;              // epilogue 1
+    XrowLayout dst_layout;            // epilogue 1 (the down bank's activation format)
+    int epilogue;                     // 0 plain, 1 GLU + requantize
     int activation;
     float alpha, limit;
 };

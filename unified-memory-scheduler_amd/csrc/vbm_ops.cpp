@@ -42,9 +42,9 @@ struct LayerWorkspace {
     int32_t * ids;
     float * weights;
     float * logits;
-    uint8_t * xq;
+    uint8_t * xrows_x;     // [T] activation rows of the layer input (gate_up format)
     void * group;
-    float * act;
+    uint8_t * xrows_act;   // [T*K] requantized GLU outputs (down format)
     float * y;
     size_t total;
 };
@@ -57,9 +57,11 @@ LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint
     w.ids = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * entries));
     w.weights = reinterpret_cast<float *>(take(sizeof(float) * entries));
     w.logits = reinterpret_cast<float *>(take(sizeof(float) * max_tokens * d.n_expert));
-    w.xq = take(static_cast<size_t>(max_tokens * (d.hidden / 32) * 34));
+    const XrowLayout lx{d.hidden / 32, d.gate_up ? d.gate_up->type : VBM_TYPE_MXFP4};
+    const XrowLayout la{d.intermediate / 32, d.down ? d.down->type : VBM_TYPE_MXFP4};
+    w.xrows_x = take(static_cast<size_t>(max_tokens * lx.stride()));
     w.group = take(group_workspace_bytes(d.n_expert, entries));
-    w.act = reinterpret_cast<float *>(take(sizeof(float) * entries * d.intermediate));
+    w.xrows_act = take(static_cast<size_t>(entries * la.stride()));
     w.y = reinterpret_cast<float *>(take(sizeof(float) * entries * d.hidden));
     w.total = off;
     return w;
@@ -78,6 +80,67 @@ void validate_layer(const vbm_moe_layer_desc * d) {
     require(d->expert_to_slot != nullptr || (gu.n_slots >= d->n_expert && dn.n_slots >= d->n_expert),
             "identity expert->slot map needs a slot per expert");
     require(d->activation == VBM_ACT_SILU || d->activation == VBM_ACT_SWIGLU_OAI, "unknown activation");
+}
+
+
+__global__ void copy_kernel(uint4 * __restrict__ dst, const uint4 * __restrict__ src, size_t n) {
+    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x)
+        dst[i] = src[i];
+}
+
+void record(void * const * events, int i, hipStream_t s) {
+    if (events) check_hip(hipEventRecord(static_cast<hipEvent_t>(events[i]), s), "hipEventRecord");
+}
+
+void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits, int64_t n_tokens, float * out,
+                   int32_t * ids, float * weights, void * workspace, size_t workspace_bytes, void * const * events,
+                   hipStream_t s) {
+    validate_layer(d);
+    require(x && out && workspace && n_tokens > 0, "null buffer");
+    require(d->router_w != nullptr || logits != nullptr, "logits input required when router_w is NULL");
+    const LayerWorkspace w = plan_layer(*d, n_tokens, static_cast<uint8_t *>(workspace));
+    require(workspace_bytes >= w.total, "workspace too small");
+    const int64_t K = d->top_k, H = d->hidden, I = d->intermediate, entries = n_tokens * K;
+    int32_t * ids_d = ids ? ids : w.ids;
+    float * w_d = weights ? weights : w.weights;
+    float * logits_d = logits ? logits : w.logits;
+    launch_router(d->router_w, d->router_b, x, H, logits_d, d->n_expert, n_tokens, K, ids_d, w_d, s);
+    const XrowLayout lx{H / 32, d->gate_up->type}, la{I / 32, d->down->type};
+    launch_quantize_expand(x, n_tokens, H, H, lx, w.xrows_x, nullptr, s);
+    const GroupBuffers g = carve_group(w.group, d->n_expert, entries);
+    launch_group(ids_d, K, n_tokens, K, d->n_expert, g, s);
+
+    GemvArgs a{};
+    a.expert_to_slot = d->expert_to_slot;
+    a.n_ids = K;
+    a.group = g;
+    a.max_active = std::min<int64_t>(d->n_expert, entries);
+    a.activation = d->activation;
+    a.alpha = 1.702f;
+    a.limit = 7.0f;
+    // gate_up + biases + GLU + Q8_0 requantization -> down activation rows [entries]
+    a.bank = d->gate_up;
+    a.xrows = w.xrows_x;
+    a.b_ne1 = 1;
+    a.bias = d->gate_up_bias;
+    a.dst_xrows = w.xrows_act;
+    a.dst_layout = la;
+    a.epilogue = 1;
+    record(events, 0, s);
+    launch_gemv(a, s);
+    record(events, 1, s);
+    // down + bias -> y [entries][H]
+    a.bank = d->down;
+    a.xrows = w.xrows_act;
+    a.b_ne1 = K;
+    a.bias = d->down_bias;
+    a.dst = w.y;
+    a.epilogue = 0;
+    record(events, 2, s);
+    launch_gemv(a, s);
+    record(events, 3, s);
+    launch_combine(w.y, w_d, H, K, n_tokens, out, s);
 }
 
 }  // namespace
@@ -126,25 +189,27 @@ vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot,
         if (expert_to_slot_host) validate_ids_on_host(ids, n_ids, n_tokens, ids_stride, n_as, expert_to_slot_host, s);
         const int64_t entries = n_ids * n_tokens;
         const int64_t n_b = b_ne1 * n_tokens;
-        const size_t q_bytes = b_type == VBM_TYPE_F32 ? static_cast<size_t>(n_b * bank->nb * 34) : 0;
+        const XrowLayout lay{bank->nb, bank->type};
+        const size_t q_bytes = static_cast<size_t>(n_b * lay.stride());
         const size_t g_bytes = group_workspace_bytes(n_as, entries);
         void * scratch = nullptr;
         check_hip(hipMallocAsync(&scratch, align_up(q_bytes) + g_bytes, s), "mul_mat_id scratch");
         uint8_t * q = static_cast<uint8_t *>(scratch);
         const GroupBuffers g = carve_group(q + align_up(q_bytes), n_as, entries);
-        if (b_type == VBM_TYPE_F32) launch_quantize_q8_0(static_cast<const float *>(b), n_b, bank->k, bank->k, q, s);
+        if (b_type == VBM_TYPE_F32)
+            launch_quantize_expand(static_cast<const float *>(b), n_b, bank->k, bank->k, lay, q, nullptr, s);
+        else
+            launch_expand_q8(static_cast<const uint8_t *>(b), n_b, bank->nb * 34, lay, q, s);
         launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
         zero_floats(dst, entries * bank->rows, s);
         GemvArgs a{};
         a.bank = bank;
         a.expert_to_slot = expert_to_slot;
-        a.act_q8 = b_type == VBM_TYPE_F32 ? q : static_cast<const uint8_t *>(b);
-        a.act_stride = bank->nb * 34;
+        a.xrows = q;
         a.n_ids = n_ids;
         a.b_ne1 = b_ne1;
         a.group = g;
         a.max_active = std::min<int64_t>(n_as, entries);
-        a.max_per_expert = n_tokens * std::min<int64_t>(n_ids, 1) ;  // an expert appears at most once per token
         a.bias = bias;
         a.dst = dst;
         a.epilogue = 0;
@@ -199,51 +264,62 @@ vbm_status vbm_moe_layer_workspace(const vbm_moe_layer_desc * desc, int64_t max_
 vbm_status vbm_moe_layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits, int64_t n_tokens,
                                  float * out, int32_t * ids, float * weights, void * workspace, size_t workspace_bytes,
                                  void * stream) {
-    return guarded([&] {
-        validate_layer(d);
-        require(x && out && workspace && n_tokens > 0, "null buffer");
-        require(d->router_w != nullptr || logits != nullptr, "logits input required when router_w is NULL");
-        const LayerWorkspace w = plan_layer(*d, n_tokens, static_cast<uint8_t *>(workspace));
-        require(workspace_bytes >= w.total, "workspace too small");
-        const hipStream_t s = as_stream(stream);
-        const int64_t K = d->top_k, H = d->hidden, I = d->intermediate, entries = n_tokens * K;
-        int32_t * ids_d = ids ? ids : w.ids;
-        float * w_d = weights ? weights : w.weights;
-        float * logits_d = logits ? logits : w.logits;
-        launch_router(d->router_w, d->router_b, x, H, logits_d, d->n_expert, n_tokens, K, ids_d, w_d, s);
-        launch_quantize_q8_0(x, n_tokens, H, H, w.xq, s);
-        const GroupBuffers g = carve_group(w.group, d->n_expert, entries);
-        launch_group(ids_d, K, n_tokens, K, d->n_expert, g, s);
+    return guarded([&] { layer_forward(d, x, logits, n_tokens, out, ids, weights, workspace, workspace_bytes, nullptr,
+                                       as_stream(stream)); });
+}
 
-        GemvArgs a{};
-        a.expert_to_slot = d->expert_to_slot;
-        a.n_ids = K;
-        a.group = g;
-        a.max_active = std::min<int64_t>(d->n_expert, entries);
-        a.max_per_expert = n_tokens;
-        a.activation = d->activation;
-        a.alpha = 1.702f;
-        a.limit = 7.0f;
-        // gate_up + bias + GLU -> act [entries][I]
-        a.bank = d->gate_up;
-        a.act_q8 = w.xq;
-        a.act_stride = (H / 32) * 34;
-        a.b_ne1 = 1;
-        a.bias = d->gate_up_bias;
-        a.dst = w.act;
-        a.epilogue = 1;
-        launch_gemv(a, s);
-        // Q8_0 requantization (in LDS) + down + bias -> y [entries][H]
-        a.bank = d->down;
-        a.act_q8 = nullptr;
-        a.act_f32 = w.act;
-        a.act_stride = I;
-        a.b_ne1 = K;
-        a.bias = d->down_bias;
-        a.dst = w.y;
-        a.epilogue = 0;
-        launch_gemv(a, s);
-        launch_combine(w.y, w_d, H, K, n_tokens, out, s);
+vbm_status vbm_moe_layer_forward_profiled(const vbm_moe_layer_desc * d, const float * x, float * logits,
+                                          int64_t n_tokens, float * out, int32_t * ids, float * weights,
+                                          void * workspace, size_t workspace_bytes, void * const * events,
+                                          void * stream) {
+    return guarded([&] {
+        require(events != nullptr && events[0] && events[1] && events[2] && events[3], "four events required");
+        layer_forward(d, x, logits, n_tokens, out, ids, weights, workspace, workspace_bytes, events, as_stream(stream));
+    });
+}
+
+vbm_status vbm_graph_begin_capture(void * stream) {
+    return guarded([&] {
+        require(stream != nullptr, "graph capture needs a non-default stream");
+        check_hip(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    });
+}
+
+vbm_status vbm_graph_end_capture(void * stream, void ** graph_exec) {
+    return guarded([&] {
+        require(graph_exec != nullptr, "graph_exec is null");
+        hipGraph_t graph = nullptr;
+        check_hip(hipStreamEndCapture(as_stream(stream), &graph), "hipStreamEndCapture");
+        hipGraphExec_t exec = nullptr;
+        const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        check_hip(e, "hipGraphInstantiate");
+        *graph_exec = exec;
+    });
+}
+
+vbm_status vbm_graph_launch(void * graph_exec, void * stream) {
+    return guarded([&] {
+        require(graph_exec != nullptr, "graph_exec is null");
+        check_hip(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), as_stream(stream)), "hipGraphLaunch");
+    });
+}
+
+vbm_status vbm_graph_destroy(void * graph_exec) {
+    return guarded([&] {
+        if (graph_exec) check_hip(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
+    });
+}
+
+vbm_status vbm_copy_kernel(void * dst, const void * src, size_t bytes, void * stream) {
+    return guarded([&] {
+        require(dst && src && bytes % 16 == 0, "copy needs 16-byte multiples");
+        const size_t n = bytes / 16;
+        if (!n) return;
+        const unsigned blocks = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 1u << 20));
+        hipLaunchKernelGGL(copy_kernel, dim3(blocks), dim3(256), 0, as_stream(stream),
+                           static_cast<uint4 *>(dst), static_cast<const uint4 *>(src), n);
+        check_hip(hipGetLastError(), "copy launch");
     });
 }
 

@@ -74,6 +74,12 @@ SIGNATURES = {
     "vbm_weighted_combine": [vp, vp, i64, i64, i64, vp, vp],
     "vbm_moe_layer_workspace": [C.POINTER(MoeLayerDesc), i64, C.POINTER(sz)],
     "vbm_moe_layer_forward": [C.POINTER(MoeLayerDesc), vp, vp, i64, vp, vp, vp, vp, sz, vp],
+    "vbm_moe_layer_forward_profiled": [C.POINTER(MoeLayerDesc), vp, vp, i64, vp, vp, vp, vp, sz, vp, vp],
+    "vbm_graph_begin_capture": [vp],
+    "vbm_graph_end_capture": [vp, C.POINTER(vp)],
+    "vbm_graph_launch": [vp, vp],
+    "vbm_graph_destroy": [vp],
+    "vbm_copy_kernel": [vp, vp, sz, vp],
 }
 OTHER = {"vbm_last_error": ([], C.c_char_p), "vbm_abi_version": ([], C.c_int)}
 
