@@ -61,13 +61,12 @@ class Stack:
         vb.call("vbm_device_synchronize")
         self.weight_bytes = layers * experts * (self.gate_up[0].slot_bytes + self.down[0].slot_bytes)
         log(f"stack resident: {self.weight_bytes / 1e9:.2f} GB in {time.time() - t0:.1f} s")
-        ws = C.c_size_t()
-        vb.call("vbm_moe_layer_workspace", C.byref(self.descs[0]), tokens, C.byref(ws))
-        self.ws_bytes = ws.value
-        self.ws = vb.DeviceBuffer(ws.value)
+        descs = (vb.MoeLayerDesc * layers)(*self.descs)
+        plan = C.c_void_p()
+        vb.call("vbm_decode_plan_create", descs, layers, C.byref(plan))
+        self.plan = plan.value
         self.x0 = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 6, 0, tokens * hidden))
-        self.xa = vb.DeviceBuffer(4 * tokens * hidden)
-        self.xb = vb.DeviceBuffer(4 * tokens * hidden)
+        self.out = vb.DeviceBuffer(4 * tokens * hidden)
         self.logits_cur = vb.DeviceBuffer(4 * layers * tokens * experts)
         self.ids = vb.DeviceBuffer(4 * layers * tokens * top_k)
 
@@ -75,21 +74,15 @@ class Stack:
         return 4 * self.L * self.T * self.E
 
     def enqueue_step(self, stream, events=None) -> None:
-        """x0 -> 36 layers -> xa/xb, reading logits_cur[l]. With `events` ([L][4] list of event handles)
-        the profiled forward brackets both GEMVs of every layer."""
-        vb.call("vbm_memcpy_d2d", self.xa.ptr, self.x0.ptr, 4 * self.T * self.H, stream)
-        src, dst = self.xa, self.xb
-        for l, d in enumerate(self.descs):
-            logits = self.logits_cur.ptr + 4 * l * self.T * self.E
-            ids = self.ids.ptr + 4 * l * self.T * self.K
-            if events is None:
-                vb.call("vbm_moe_layer_forward", C.byref(d), src.ptr, logits, self.T, dst.ptr, ids, None, self.ws.ptr,
-                        self.ws_bytes, stream)
-            else:
-                arr = (C.c_void_p * 4)(*events[l])
-                vb.call("vbm_moe_layer_forward_profiled", C.byref(d), src.ptr, logits, self.T, dst.ptr, ids, None,
-                        self.ws.ptr, self.ws_bytes, C.cast(arr, C.c_void_p), stream)
-            src, dst = dst, src
+        """x0 -> 36 layers -> out through the fused decode plan (two kernels per layer), reading
+        logits_cur. With `events` ([L][4] event handles) kernels A and B of every layer are
+        bracketed."""
+        ev = None
+        if events is not None:
+            flat = [e for row in events for e in row]
+            ev = (C.c_void_p * len(flat))(*flat)
+        vb.call("vbm_decode_step", self.plan, self.x0.ptr, self.logits_cur.ptr, self.out.ptr, self.ids.ptr, None,
+                C.cast(ev, C.c_void_p) if ev is not None else None, stream)
 
 
 def distinct_experts(ids: np.ndarray) -> int:
@@ -166,6 +159,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.tokens != 1:
+        print("bench.py times the single-token decode path; batched decode is covered by the parity tests.",
+              file=sys.stderr)
+        return 2
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures the routed-expert path on exactly one GPU; --gpus {args.gpus} "
               f"(WORLD_SIZE {world}) is not supported: this build has no multi-GPU path.", file=sys.stderr)
@@ -256,15 +253,17 @@ def main() -> int:
             launches += 1
     gu_avg_us = gu_ms / launches * 1e3
     dn_avg_us = dn_ms / launches * 1e3
-    # Algorithmic bytes per gate_up launch at this batch: distinct experts x (5760 rows x 1530 B +
-    # 5760 fp32 biases) + Q8_0 input (T x 3060 B) + fp32 GLU output (T x K x 2880 x 4 B).
+    # Algorithmic bytes per launch of kernel A: K experts x (5760 rows x 1530 B + 5760 fp32 biases)
+    # + logits (E x 4 B) + previous layer outputs (K x 2880 x 4 B) + Q8_0 down activations out
+    # (K x 3060 B). Kernel B: K experts x (2880 x 1530 B + 2880 x 4 B) + activations in (K x 3060 B)
+    # + outputs (K x 2880 x 4 B).
     mean_distinct = distinct / (args.steps * L)
-    gu_bytes = mean_distinct * (2 * I * MXFP4_ROW_BYTES + 2 * I * 4) + T * (H // 32) * 34 + T * K * I * 4
-    dn_bytes = mean_distinct * (H * MXFP4_ROW_BYTES + H * 4) + T * K * I * 4 + T * K * H * 4
+    gu_bytes = mean_distinct * (2 * I * MXFP4_ROW_BYTES + 2 * I * 4) + E * 4 + K * H * 4 + K * (I // 32) * 34
+    dn_bytes = mean_distinct * (H * MXFP4_ROW_BYTES + H * 4) + K * (I // 32) * 34 + K * H * 4
     gu_gbs = gu_bytes / (gu_avg_us * 1e-6) / 1e9
     dn_gbs = dn_bytes / (dn_avg_us * 1e-6) / 1e9
-    log(f"gate_up GEMV: {gu_avg_us:.2f} us avg over {launches} launches -> {gu_gbs:.0f} GB/s; "
-        f"down GEMV: {dn_avg_us:.2f} us -> {dn_gbs:.0f} GB/s")
+    log(f"kernel A (route + combine + quantize + gate_up GEMV): {gu_avg_us:.2f} us avg over {launches} launches -> "
+        f"{gu_gbs:.0f} GB/s; kernel B (down GEMV): {dn_avg_us:.2f} us -> {dn_gbs:.0f} GB/s")
     traffic = read_traffic(REPO / "profiles" / "gemv_gate_up_120b_bs1_pmc.md") if T == 1 else None
 
     cpu = None
@@ -290,12 +289,13 @@ def main() -> int:
                         f"intermediate {I}, batch {T}, weights resident in HBM",
             "layers": L, "experts": E, "top_k": K, "hidden": H, "intermediate": I, "batch": T,
             "resident_weight_bytes": stack.weight_bytes, "launch": args.mode,
+            "kernels_per_layer": 2,
             "expert_bytes_per_step": round(step_weight_bytes),
             "step_expert_gbs": round(step_weight_bytes / (ms_per_step / 1e3) / 1e9, 1),
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "expert_gemv_kernel<MXFP4,MT=1> gate_up (+bias +SwiGLU-OAI epilogue)",
+            "kernel": "decode_gate_up_kernel<MXFP4> (combine + Q8_0 + top-k/softmax + gate_up GEMV + bias + SwiGLU-OAI + requant)",
             "achieved": round(gu_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -14,11 +14,12 @@ def block_bytes(type_id: int) -> int:
     return 17 if type_id == MX else 34
 
 
-def synth_weights(type_id: int, seed: int, stream: int, experts: int, rows: int, k: int) -> np.ndarray:
+def synth_weights(type_id: int, seed: int, stream: int, experts: int, rows: int, k: int,
+                  q8_scale=(1e-3, 1e-2)) -> np.ndarray:
     n = experts * rows * (k // 32)
     if type_id == MX:
         return vb.synth_mxfp4(seed, stream, 0, n)
-    return vb.synth_q8_0(seed, stream, 0, n)
+    return vb.synth_q8_0(seed, stream, 0, n, *q8_scale)
 
 
 def make_bank(type_id: int, ggml: np.ndarray, experts: int, rows: int, k: int, interleave=False) -> vb.Bank:

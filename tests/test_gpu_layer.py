@@ -15,13 +15,13 @@ class Layer:
     """Seeded synthetic layer: tensors are pure functions of (seed, layer, tensor id)."""
 
     def __init__(self, vb, type_id, hidden, inter, experts, top_k, seed, layer=0, router=True, biases=True,
-                 activation=1):
+                 activation=1, q8_scale=(1e-3, 1e-2)):
         self.vb, self.type_id = vb, type_id
         self.H, self.I, self.E, self.K = hidden, inter, experts, top_k
         self.activation = activation
         base = 16 * layer
-        self.gu = H.synth_weights(type_id, seed, base + 1, experts, 2 * inter, hidden)
-        self.dn = H.synth_weights(type_id, seed, base + 2, experts, hidden, inter)
+        self.gu = H.synth_weights(type_id, seed, base + 1, experts, 2 * inter, hidden, q8_scale)
+        self.dn = H.synth_weights(type_id, seed, base + 2, experts, hidden, inter, q8_scale)
         self.gu_b = vb.synth_normal(seed, base + 3, 0, experts * 2 * inter, 0.0, 0.02) if biases else None
         self.dn_b = vb.synth_normal(seed, base + 4, 0, experts * hidden, 0.0, 0.02) if biases else None
         self.rw = vb.synth_normal(seed, base + 5, 0, experts * hidden, 0.0, 0.02).reshape(experts, hidden) if router else None

@@ -23,6 +23,7 @@
 // Epilogue 1 (fused gate|up bank): the workgroup's 64 rows are gate rows 32p..32p+31 and up rows
 // 32p..32p+31, i.e. exactly one 32-element Q8_0 block p of the GLU output; it applies the biases
 // and the GLU, requantizes (x86 contract) and writes the down projection's activation row.
+#include "vbm_device.hpp"
 #include "vbm_internal.hpp"
 
 namespace vbm {
@@ -53,18 +54,6 @@ constexpr int kThreads = 512;
 constexpr int kChunk = 4;        // tokens reduced per barrier
 
 __device__ __forceinline__ half2_t as_half2(unsigned v) { return __builtin_bit_cast(half2_t, v); }
-
-// exp() for the GLU: rounded from double so it matches a correctly rounded expf in practice.
-__device__ __forceinline__ float expf_rn(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
-
-__device__ __forceinline__ float glu(int activation, float g0, float u0, float alpha, float limit) {
-    if (activation == VBM_ACT_SWIGLU_OAI) {
-        const float g = limit < g0 ? limit : g0;                           // std::min(gate, limit)
-        const float u = u0 < -limit ? -limit : (limit < u0 ? limit : u0);  // std::clamp(up, -l, l)
-        return (g / (1.0f + expf_rn(alpha * (-g)))) * (u + 1.0f);
-    }
-    return g0 / (1.0f + expf_rn(-g0)) * u0;
-}
 
 // Contract minus true product for one 4-element slice: +256*w for every element whose
 // activation code is -128 and whose weight is negative (VPSIGNB keeps -128 when negating).
@@ -117,141 +106,176 @@ struct KernelArgs {
     float alpha, limit;
 };
 
-// One lane's weights: G groups (8 MXFP4 / 4 Q8_0 blocks each: 16 B codes + 8 B exponents or
-// scales) and up to 6 tail blocks.
-template <int G>
-struct LaneWeights {
-    u32x4 c[G];
-    uint2 m[G];
-    unsigned tc[3];
-    unsigned tm[2];
+constexpr int kDepth = 4;    // weight groups in flight per lane (ring buffer)
+
+// One group of one lane: 16 B of codes (8 MXFP4 blocks x 2 B or 4 Q8_0 blocks x 4 B) and 8 B of
+// exponents (MXFP4) or fp16 scales (Q8_0).
+struct Group {
+    u32x4 c;
+    u32x2 m;
 };
 
-template <int TYPE, int G>
-__device__ __forceinline__ void load_lane(LaneWeights<G> & w, const uint8_t * codes_tile, const uint8_t * meta_tile,
-                                          int k, int r, int groups, int tail) {
-    const uint8_t * cp = codes_tile + (k * 32 + r) * 16;
-    const uint8_t * mp = meta_tile + r * 8;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        if (g < groups) {
-            w.c[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(cp + g * 4096));
-            const u32x2 mv = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(mp + g * 256));
-            w.m[g] = make_uint2(mv.x, mv.y);
-        }
-    }
-    constexpr int kCode = TYPE == 39 ? 2 : 4, kMeta = TYPE == 39 ? 1 : 2;
-    const uint8_t * tcp = codes_tile + groups * 4096 + (k * 32 + r) * (tail * kCode);
-    const uint8_t * tmp = meta_tile + groups * 256 + r * tail * kMeta;
-#pragma unroll
-    for (int i = 0; i < 3; ++i)
-        if (4 * i < tail * kCode) w.tc[i] = *reinterpret_cast<const unsigned *>(tcp + 4 * i);
-    unsigned m0 = 0, m1 = 0;
-    for (int i = 0; i < tail * kMeta; ++i) {
-        const unsigned byte = tmp[i];
-        if (i < 4) m0 |= byte << (8 * i);
-        else m1 |= byte << (8 * (i - 4));
-    }
-    w.tm[0] = m0;
-    w.tm[1] = m1;
+__device__ __forceinline__ Group load_group(const uint8_t * cp, const uint8_t * mp, int g) {
+    Group r;
+    r.c = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(cp + g * 4096));
+    r.m = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(mp + g * 256));
+    return r;
 }
 
-// One MXFP4 block of one lane: bytes SEL, SEL+1 of `dw` are the slice's 4 nibbles; the
-// activation slice (4 f16 codes) and the block scale are wave-uniform.
-template <bool SLOW, int SEL>
-__device__ __forceinline__ void mx_block(unsigned dw, int e, u32x2 a, float d, float & acc) {
+// One MXFP4 block of one lane for MT tokens: bytes SEL, SEL+1 of `dw` are the slice's 4 nibbles;
+// the activation slice (4 f16 codes, 8 B per block) and the block scale of each token are read
+// from LDS with wave-uniform addresses (broadcast).
+template <int MT, bool SLOW, int SEL, int PAR>
+__device__ __forceinline__ void mx_block(unsigned dw, int e, int b, const uint8_t * la, const float * lda,
+                                         int tok_bytes, int mcount, float (&acc)[MT][2]) {
     const half2_t w01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, SEL);
     const half2_t w23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, SEL + 1);
-    float v = __builtin_amdgcn_fdot2(w23, as_half2(a.y), 0.0f, false);
-    v = __builtin_amdgcn_fdot2(w01, as_half2(a.x), v, false);
-    if (SLOW) v += neg128_fix_half(w01, w23, a.x, a.y);
-    const float s = __builtin_amdgcn_ldexpf(d, e);
-    acc = __builtin_fmaf(s, v, acc);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (m < mcount) {
+            const u32x2 a = *reinterpret_cast<const u32x2 *>(la + m * tok_bytes + b * 8);
+            const float d = *reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(lda) + m * tok_bytes + b * 4);
+            float v = __builtin_amdgcn_fdot2(w23, as_half2(a.y), 0.0f, false);
+            v = __builtin_amdgcn_fdot2(w01, as_half2(a.x), v, false);
+            if (SLOW) v += neg128_fix_half(w01, w23, a.x, a.y);
+            const float s = __builtin_amdgcn_ldexpf(d, e);
+            acc[m][PAR] = __builtin_fmaf(s, v, acc[m][PAR]);
+        }
+    }
 }
 
-// All blocks of one token for one lane (MXFP4): returns even + odd chain.
-template <bool SLOW, int G>
-__device__ __forceinline__ float mx_token(const LaneWeights<G> & w, cptr act, const float * __restrict__ da_g,
-                                          int groups, int tail) {
-    const __attribute__((address_space(4))) u32x2 * a = (const __attribute__((address_space(4))) u32x2 *)(act);
-    const __attribute__((address_space(4))) float * da = as_const<float>(da_g);
-    float even = 0.0f, odd = 0.0f;
+// Eight MXFP4 blocks (one group, starting at block b) for MT tokens.
+template <int MT, bool SLOW>
+__device__ __forceinline__ void mx_group(const Group & grp, int b, const uint8_t * la, const float * lda, int tok_bytes,
+                                         int mcount, float (&acc)[MT][2]) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        if (g < groups) {
-            u32x4 c = w.c[g];
-            uint2 ex = w.m[g];
-            // Decode inside the token loop: hoisting 180 decoded weights out of it would halve
-            // occupancy for no gain at one token per expert.
-            asm volatile("" : "+v"(c), "+v"(ex.x), "+v"(ex.y));
+    for (int q = 0; q < 4; ++q) {
+        const unsigned dw = q == 0 ? grp.c.x : (q == 1 ? grp.c.y : (q == 2 ? grp.c.z : grp.c.w));
+        const unsigned ew = q < 2 ? grp.m.x : grp.m.y;
+        mx_block<MT, SLOW, 0, 0>(dw, static_cast<signed char>(ew >> ((2 * q & 3) * 8)), b + 2 * q, la, lda, tok_bytes,
+                                 mcount, acc);
+        mx_block<MT, SLOW, 2, 1>(dw, static_cast<signed char>(ew >> (((2 * q + 1) & 3) * 8)), b + 2 * q + 1, la, lda,
+                                 tok_bytes, mcount, acc);
+    }
+}
+
+template <int MT, bool SLOW>
+__device__ __forceinline__ void q8_block(unsigned w, unsigned short dbits, int b, const uint8_t * la, const float * lda,
+                                         int tok_bytes, int mcount, float (&acc)[MT][2]) {
+    const float dw = half_bits_to_float(dbits);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const unsigned dw = q == 0 ? c.x : (q == 1 ? c.y : (q == 2 ? c.z : c.w));
-                const unsigned ew = q < 2 ? ex.x : ex.y;
-                const int b = g * 8 + 2 * q;
-                mx_block<SLOW, 0>(dw, static_cast<signed char>(ew >> ((2 * q & 3) * 8)), a[b], da[b], even);
-                mx_block<SLOW, 2>(dw, static_cast<signed char>(ew >> (((2 * q + 1) & 3) * 8)), a[b + 1], da[b + 1], odd);
+    for (int m = 0; m < MT; ++m) {
+        if (m < mcount) {
+            const unsigned a = *reinterpret_cast<const unsigned *>(la + m * tok_bytes + b * 4);
+            const float d = *reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(lda) + m * tok_bytes + b * 4);
+            int v = __builtin_amdgcn_sdot4(static_cast<int>(w), static_cast<int>(a), 0, false);
+            if (SLOW) v += neg128_fix_i8(w, a);
+            const float s = dw * d;
+            acc[m][0] = __builtin_fmaf(s, static_cast<float>(v), acc[m][0]);
+        }
+    }
+}
+
+// Four Q8_0 blocks (one group, starting at block b) for MT tokens: one chain per lane.
+template <int MT, bool SLOW>
+__device__ __forceinline__ void q8_group(const Group & grp, int b, const uint8_t * la, const float * lda, int tok_bytes,
+                                         int mcount, float (&acc)[MT][2]) {
+    q8_block<MT, SLOW>(grp.c.x, static_cast<unsigned short>(grp.m.x), b, la, lda, tok_bytes, mcount, acc);
+    q8_block<MT, SLOW>(grp.c.y, static_cast<unsigned short>(grp.m.x >> 16), b + 1, la, lda, tok_bytes, mcount, acc);
+    q8_block<MT, SLOW>(grp.c.z, static_cast<unsigned short>(grp.m.y), b + 2, la, lda, tok_bytes, mcount, acc);
+    q8_block<MT, SLOW>(grp.c.w, static_cast<unsigned short>(grp.m.y >> 16), b + 3, la, lda, tok_bytes, mcount, acc);
+}
+
+// Issues the first kDepth groups of one lane's row slice (before activation staging, so the
+// weight stream is already in flight while the activation arrives).
+__device__ __forceinline__ void preload_ring(Group (&ring)[kDepth], const uint8_t * cp, const uint8_t * mp, int groups,
+                                             bool live) {
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i) {
+        ring[i] = Group{};
+        if (live && i < groups) ring[i] = load_group(cp, mp, i);
+    }
+}
+
+// Streams one lane's row slice once through the kDepth-deep register ring, applying every
+// staged token to each group as it arrives.
+template <int TYPE, int MT, bool SLOW>
+__device__ __forceinline__ void stream_lane(Group (&ring)[kDepth], const uint8_t * codes_tile, const uint8_t * meta_tile,
+                                            int k, int r, int nb, bool live, const uint8_t * la, const float * lda,
+                                            int tok_bytes, int mcount, float (&acc)[MT][2]) {
+    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
+    const int groups = nb / kGroupBlocks, tail = nb % kGroupBlocks;
+    const uint8_t * cp = codes_tile + (k * 32 + r) * 16;
+    const uint8_t * mp = meta_tile + r * 8;
+    for (int g0 = 0; g0 < groups; g0 += kDepth) {
+#pragma unroll
+        for (int i = 0; i < kDepth; ++i) {
+            const int g = g0 + i;
+            if (g < groups) {
+                const Group cur = ring[i];
+                if (live && g + kDepth < groups) ring[i] = load_group(cp, mp, g + kDepth);
+                if (TYPE == 39) mx_group<MT, SLOW>(cur, g * 8, la, lda, tok_bytes, mcount, acc);
+                else q8_group<MT, SLOW>(cur, g * 4, la, lda, tok_bytes, mcount, acc);
             }
         }
     }
-#pragma unroll
-    for (int bt = 0; bt < 6; bt += 2) {
-        if (bt < tail) {
-            const int b = groups * 8 + bt;
-            const unsigned ew = bt < 4 ? w.tm[0] : w.tm[1];
-            const int sh = (bt & 3) * 8;
-            mx_block<SLOW, 0>(w.tc[bt / 2], static_cast<signed char>(ew >> sh), a[b], da[b], even);
-            mx_block<SLOW, 2>(w.tc[bt / 2], static_cast<signed char>(ew >> (sh + 8)), a[b + 1], da[b + 1], odd);
+    // Tail blocks past the last full group (MXFP4: nb % 8 in {0,2,4,6}; Q8_0: nb % 4).
+    constexpr int kCode = TYPE == 39 ? 2 : 4, kMeta = TYPE == 39 ? 1 : 2;
+    const uint8_t * tcp = codes_tile + groups * 4096 + (k * 32 + r) * (tail * kCode);
+    const uint8_t * tmp = meta_tile + groups * 256 + r * tail * kMeta;
+    for (int bt = 0; bt < tail; bt += (TYPE == 39 ? 2 : 1)) {
+        const unsigned cw = live ? *reinterpret_cast<const unsigned *>(tcp + bt * kCode) : 0u;
+        if (TYPE == 39) {
+            const int e0 = live ? static_cast<signed char>(tmp[bt]) : 0;
+            const int e1 = live ? static_cast<signed char>(tmp[bt + 1]) : 0;
+            mx_block<MT, SLOW, 0, 0>(cw, e0, groups * 8 + bt, la, lda, tok_bytes, mcount, acc);
+            mx_block<MT, SLOW, 2, 1>(cw, e1, groups * 8 + bt + 1, la, lda, tok_bytes, mcount, acc);
+        } else {
+            const unsigned short dbits = live ? *reinterpret_cast<const unsigned short *>(tmp + bt * 2) : 0;
+            q8_block<MT, SLOW>(cw, dbits, groups * 4 + bt, la, lda, tok_bytes, mcount, acc);
         }
     }
-    return even + odd;
 }
 
-template <bool SLOW>
-__device__ __forceinline__ void q8_block(unsigned w, unsigned short dbits, unsigned a, float d, float & acc) {
-    int v = __builtin_amdgcn_sdot4(static_cast<int>(w), static_cast<int>(a), 0, false);
-    if (SLOW) v += neg128_fix_i8(w, a);
-    const float s = half_bits_to_float(dbits) * d;
-    acc = __builtin_fmaf(s, static_cast<float>(v), acc);
+// Final tree over the eight lane slices (cpu_mxfp4_vnni.cpp:64-67):
+// ((l0+l4)+(l2+l6))+((l1+l5)+(l3+l7)); `l` points at slice 0 of one row, slices 64 floats apart.
+__device__ __forceinline__ float lane_tree(const float * l) {
+    const float s0 = l[4 * 64] + l[0], s1 = l[5 * 64] + l[1 * 64];
+    const float s2 = l[6 * 64] + l[2 * 64], s3 = l[7 * 64] + l[3 * 64];
+    return (s0 + s2) + (s1 + s3);
 }
 
-// All blocks of one token for one lane (Q8_0 weights): one chain.
-template <bool SLOW, int G>
-__device__ __forceinline__ float q8_token(const LaneWeights<G> & w, cptr act, const float * __restrict__ da_g,
-                                          int groups, int tail) {
-    const __attribute__((address_space(4))) unsigned * a = (const __attribute__((address_space(4))) unsigned *)(act);
-    const __attribute__((address_space(4))) float * da = as_const<float>(da_g);
-    float acc = 0.0f;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        if (g < groups) {
-            u32x4 c = w.c[g];
-            uint2 sc = w.m[g];
-            asm volatile("" : "+v"(c), "+v"(sc.x), "+v"(sc.y));
-            const int b = g * 4;
-            q8_block<SLOW>(c.x, static_cast<unsigned short>(sc.x), a[b], da[b], acc);
-            q8_block<SLOW>(c.y, static_cast<unsigned short>(sc.x >> 16), a[b + 1], da[b + 1], acc);
-            q8_block<SLOW>(c.z, static_cast<unsigned short>(sc.y), a[b + 2], da[b + 2], acc);
-            q8_block<SLOW>(c.w, static_cast<unsigned short>(sc.y >> 16), a[b + 3], da[b + 3], acc);
-        }
+// GLU of one 32-element output block (wave lanes 0..31; gate from local row (lane/16)*32 +
+// lane%16 of `vals`, up from that row + 16), then x86 Q8_0 quantization into activation row
+// `out` at block p.
+__device__ __forceinline__ void glu_requant_block(const float * vals, int lane, int p, uint8_t * out, const XrowLayout & L,
+                                                  int activation, float alpha, float limit) {
+    const int lr = (lane >> 4) * 32 + (lane & 15);
+    const float act = glu(activation, vals[lr], vals[lr + 16], alpha, limit);
+    float amax = fabsf(act);
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    float q = rintf(act * id);
+    q = q > 127.0f ? 127.0f : (q < -128.0f ? -128.0f : q);
+    const int sk = lane >> 2, pos = lane & 3;
+    if (L.weight_type == 39)
+        reinterpret_cast<_Float16 *>(out + (static_cast<int64_t>(sk) * L.nb + p) * 8)[pos] = static_cast<_Float16>(q);
+    else
+        reinterpret_cast<signed char *>(out + (static_cast<int64_t>(sk) * L.nb + p) * 4)[pos] = static_cast<signed char>(q);
+    if (lane == 0) {
+        reinterpret_cast<float *>(out + L.da_offset())[p] = static_cast<float>(static_cast<_Float16>(d));
+        if (p == 0) *reinterpret_cast<int *>(out + L.flag_offset()) = 0;   // requantized codes are never -128
     }
-#pragma unroll
-    for (int bt = 0; bt < 3; ++bt) {
-        if (bt < tail) {
-            const unsigned mw = bt < 2 ? w.tm[0] : w.tm[1];
-            q8_block<SLOW>(w.tc[bt], static_cast<unsigned short>(mw >> ((bt & 1) * 16)), a[groups * 4 + bt],
-                           da[groups * 4 + bt], acc);
-        }
-    }
-    return acc;
 }
 
-template <int TYPE, int G>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 12 ? 4 : 3))) void expert_gemv_kernel(KernelArgs A) {
-    __shared__ float red[kChunk][8][64];
-    __shared__ float vals[kChunk][64];
-    // Per-expert metadata is read through the constant address space so it stays scalar (a
-    // generic-pointer load would be treated as divergent and push the activation loads to VMEM).
+template <int TYPE, int MT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void expert_gemv_kernel(KernelArgs A) {
+    __shared__ float red[MT][8][64];
+    __shared__ float vals[MT][64];
+    __shared__ int s_flag;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_tok[];   // MT activation rows
+    // Per-expert metadata is read through the constant address space so it stays scalar.
     const int a_index = blockIdx.y;
     if (a_index >= *as_const<int32_t>(A.n_active)) return;
     const int expert = as_const<int32_t>(A.active)[a_index];
@@ -266,76 +290,196 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(G <= 1
     const int lane = threadIdx.x & 63;
     const int r = lane & 31;
     const int tile = blockIdx.x * 2 + (lane >> 5);
-    const bool live = tile * 32 < S.rows;
+    const bool live = tile * 32 < S.rows;                              // the last tile pair may be half
+    const uint8_t * slot_base = A.bank + static_cast<size_t>(slot) * S.slot_bytes;
+    const uint8_t * codes_tile = slot_base + static_cast<size_t>(live ? tile : 0) * 32 * nb * (TYPE == 39 ? 16 : 32);
+    const uint8_t * meta_tile = slot_base + S.codes_bytes + static_cast<size_t>(live ? tile : 0) * 32 * nb * (TYPE == 39 ? 1 : 2);
+    const int copy_bytes = static_cast<int>(A.lay.flag_offset());        // codes + scales of a row
+    const int tok_bytes = (copy_bytes + 15) & ~15;
+    const uint8_t * la = lds_tok + static_cast<int64_t>(k) * nb * A.lay.code_entry();
+    const float * lda = reinterpret_cast<const float *>(lds_tok + A.lay.da_offset());
+
     constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
-    const int groups = nb / kGroupBlocks, tail = nb % kGroupBlocks;
+    const int groups = nb / kGroupBlocks;
+    const uint8_t * cp = codes_tile + (k * 32 + r) * 16;
+    const uint8_t * mp = meta_tile + r * 8;
 
-    LaneWeights<G> w = {};   // lanes past the last row keep zero weights and compute zeros
-    if (live) {
-        const uint8_t * slot_base = A.bank + static_cast<size_t>(slot) * S.slot_bytes;
-        const uint8_t * codes_tile = slot_base + static_cast<size_t>(tile) * 32 * nb * (TYPE == 39 ? 16 : 32);
-        const uint8_t * meta_tile = slot_base + S.codes_bytes + static_cast<size_t>(tile) * 32 * nb * (TYPE == 39 ? 1 : 2);
-        load_lane<TYPE, G>(w, codes_tile, meta_tile, k, r, groups, tail);
-    }
-    const int64_t act_slice = static_cast<int64_t>(k) * nb * A.lay.code_entry();
-
-    for (int c0 = 0; c0 < count; c0 += kChunk) {
-        const int mcount = count - c0 < kChunk ? count - c0 : kChunk;
+    for (int c0 = 0; c0 < count; c0 += MT) {
+        const int mcount = count - c0 < MT ? count - c0 : MT;
+        Group ring[kDepth];
+        preload_ring(ring, cp, mp, groups, live);
+        // Stage the chunk's activation rows (and their -128 flags) in LDS.
+        if (threadIdx.x == 0) s_flag = 0;
+        __syncthreads();
+        int flag = 0;
         for (int mi = 0; mi < mcount; ++mi) {
             const int64_t j = jobs[c0 + mi];
             const int64_t row = A.b_ne1 == 1 ? j / A.n_ids : j;
             const uint8_t * xr = A.xrows + row * A.lay.stride();
-            cptr act = as_const<uint8_t>(wave_uniform(xr + act_slice));
-            const float * da = wave_uniform(reinterpret_cast<const float *>(xr + A.lay.da_offset()));
-            const int flag = *as_const<int>(wave_uniform(xr + A.lay.flag_offset()));
-            // Uniform control flow here keeps the activation loads scalar.
-            float v;
-            if (TYPE == 39) v = flag ? mx_token<true, G>(w, act, da, groups, tail) : mx_token<false, G>(w, act, da, groups, tail);
-            else v = flag ? q8_token<true, G>(w, act, da, groups, tail) : q8_token<false, G>(w, act, da, groups, tail);
-            red[mi][k][lane] = v;
+            uint8_t * dst = lds_tok + mi * tok_bytes;
+            for (int i = threadIdx.x; i * 16 < copy_bytes - 15; i += kThreads)
+                *reinterpret_cast<u32x4 *>(dst + i * 16) = *reinterpret_cast<const u32x4 *>(xr + i * 16);
+            for (int i = (copy_bytes & ~15) + threadIdx.x * 4; i < copy_bytes; i += kThreads * 4)
+                *reinterpret_cast<unsigned *>(dst + i) = *reinterpret_cast<const unsigned *>(xr + i);
+            if (threadIdx.x == 0) flag |= *reinterpret_cast<const int *>(xr + A.lay.flag_offset());
         }
+        if (threadIdx.x == 0 && flag) s_flag = 1;
         __syncthreads();
-        // Final tree over the eight lanes (cpu_mxfp4_vnni.cpp:64-67): ((l0+l4)+(l2+l6))+((l1+l5)+(l3+l7)).
-        const int mi = k;                       // wave mi reduces token mi of the chunk
-        if (mi < mcount && live) {
-            const float * l = &red[mi][0][lane];
-            const float s0 = l[4 * 64] + l[0], s1 = l[5 * 64] + l[1 * 64];
-            const float s2 = l[6 * 64] + l[2 * 64], s3 = l[7 * 64] + l[3 * 64];
-            float v = (s0 + s2) + (s1 + s3);
-            const int grow = static_cast<int>(ggml_row(static_cast<int64_t>(tile) * 32 + r, S.rows, S.interleave));
-            if (A.bias) v = v + A.bias[static_cast<size_t>(expert) * S.rows + grow];
-            if (A.epilogue == 0) A.dst[static_cast<size_t>(jobs[c0 + mi]) * S.rows + grow] = v;
-            else vals[mi][lane] = v;
+        float acc[MT][2];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m][0] = acc[m][1] = 0.0f;
+        if (s_flag) stream_lane<TYPE, MT, true>(ring, codes_tile, meta_tile, k, r, nb, live, la, lda, tok_bytes, mcount, acc);
+        else stream_lane<TYPE, MT, false>(ring, codes_tile, meta_tile, k, r, nb, live, la, lda, tok_bytes, mcount, acc);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) red[m][k][lane] = acc[m][0] + acc[m][1];
+        __syncthreads();
+        for (int mi = k; mi < mcount; mi += 8) {                       // wave k reduces tokens k, k+8, ...
+            if (live) {
+                float v = lane_tree(&red[mi][0][lane]);
+                const int grow = static_cast<int>(ggml_row(static_cast<int64_t>(tile) * 32 + r, S.rows, S.interleave));
+                if (A.bias) v = v + A.bias[static_cast<size_t>(expert) * S.rows + grow];
+                if (A.epilogue == 0) A.dst[static_cast<size_t>(jobs[c0 + mi]) * S.rows + grow] = v;
+                else vals[mi][lane] = v;
+            }
         }
         if (A.epilogue == 1) {
             __syncthreads();
-            // Wave mi, lanes 0..31: GLU output element p*32 + lane, gate from local row
-            // (lane/16)*32 + lane%16 and up from that row + 16; then Q8_0 (x86 contract).
-            if (mi < mcount && lane < 32) {
-                const int lr = (lane >> 4) * 32 + (lane & 15);
-                const float act = glu(A.activation, vals[mi][lr], vals[mi][lr + 16], A.alpha, A.limit);
-                float amax = fabsf(act);
-                for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-                const float d = amax / 127.0f;
-                const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-                float q = rintf(act * id);
-                q = q > 127.0f ? 127.0f : (q < -128.0f ? -128.0f : q);
-                const XrowLayout L = A.dst_lay;
-                uint8_t * out = A.dst_xrows + static_cast<size_t>(jobs[c0 + mi]) * L.stride();
-                const int p = blockIdx.x;                           // output block index
-                const int sk = lane >> 2, pos = lane & 3;
-                if (L.weight_type == 39)
-                    reinterpret_cast<_Float16 *>(out + (static_cast<int64_t>(sk) * L.nb + p) * 8)[pos] = static_cast<_Float16>(q);
-                else
-                    reinterpret_cast<signed char *>(out + (static_cast<int64_t>(sk) * L.nb + p) * 4)[pos] = static_cast<signed char>(q);
-                if (lane == 0) {
-                    reinterpret_cast<float *>(out + L.da_offset())[p] = static_cast<float>(static_cast<_Float16>(d));
-                    if (p == 0) *reinterpret_cast<int *>(out + L.flag_offset()) = 0;   // requantized codes are never -128
-                }
-            }
+            for (int mi = k; mi < mcount; mi += 8)
+                if (lane < 32)
+                    glu_requant_block(vals[mi], lane, blockIdx.x, A.dst_xrows + static_cast<size_t>(jobs[c0 + mi]) * A.dst_lay.stride(),
+                                      A.dst_lay, A.activation, A.alpha, A.limit);
         }
         __syncthreads();
     }
+}
+
+// ------------------------------------------------------------------------------ fused decode
+// Single-token decode, kernel A of a layer: the previous layer's weighted rank combine (or the
+// layer input), x86 Q8_0 quantization, top-k + softmax over the given logits, and the gate_up
+// GEMV of this workgroup's (tile pair, rank) with biases, GLU and requantization into the down
+// projection's activation row. Wave 0 routes while waves 1..7 combine; every workgroup does both
+// redundantly (a few KiB from L2), which removes four dependent launches per layer. Workgroup
+// (0,0) publishes the routing and the down work list for kernel B (the generic expert GEMV).
+struct DecodeArgs {
+    const uint8_t * bank;
+    Shape shape;
+    const int32_t * expert_to_slot;
+    XrowLayout lay;            // gate_up activation format (nb = hidden / 32)
+    const float * logits;      // [n_expert] of this layer
+    int n_expert, top_k;
+    const float * x_in;        // [hidden] layer input, or null to combine the previous layer
+    const float * prev_y;      // [top_k][hidden] previous layer's biased down outputs
+    const float * prev_w;      // [top_k] previous layer's routing weights
+    int hidden;
+    const float * bias;        // gate_up bias [n_expert][rows] (ggml row order) or null
+    uint8_t * act_rows;        // [top_k] down activation rows
+    XrowLayout act_lay;
+    int32_t * route_ids;       // [top_k] this layer's routing
+    float * route_w;           // [top_k]
+    GroupBuffers grp;          // this layer's down work list
+    int activation;
+    float alpha, limit;
+};
+
+template <int TYPE>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void decode_gate_up_kernel(DecodeArgs A) {
+    __shared__ float red[8][64];
+    __shared__ float vals[64];
+    __shared__ int32_t s_ids[64];
+    __shared__ float s_w[64];
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
+    const int H = A.hidden, nb = H / 32;
+    float * xs = reinterpret_cast<float *>(lds_dyn);
+    uint8_t * act = lds_dyn + ((H * 4 + 15) & ~15);
+    const int k = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, r = lane & 31;
+    const int rank = blockIdx.y;
+    if (k == 0) {
+        wave_topk_softmax(A.logits, A.n_expert, A.top_k, s_ids, s_w);
+    } else {
+        const int K = A.top_k;
+        for (int i = threadIdx.x - 64; i < H; i += kThreads - 64) {
+            float v;
+            if (A.x_in) {
+                v = A.x_in[i];
+            } else {  // ggml MUL by the weight, then sequential ADD in rank order
+                v = A.prev_y[i] * A.prev_w[0];
+                for (int q = 1; q < K; ++q) {
+                    const float term = A.prev_y[static_cast<int64_t>(q) * H + i] * A.prev_w[q];
+                    v = v + term;
+                }
+            }
+            xs[i] = v;
+        }
+    }
+    __syncthreads();
+    const int expert = s_ids[rank];
+    const int slot = A.expert_to_slot ? A.expert_to_slot[expert] : expert;
+    const bool slot_ok = slot >= 0 && slot < A.shape.n_slots;
+    const Shape S = A.shape;
+    const int tile = blockIdx.x * 2 + (lane >> 5);
+    const bool live = slot_ok && tile * 32 < S.rows;
+    const uint8_t * slot_base = A.bank + static_cast<size_t>(slot_ok ? slot : 0) * S.slot_bytes;
+    const uint8_t * codes_tile = slot_base + static_cast<size_t>(live ? tile : 0) * 32 * nb * (TYPE == 39 ? 16 : 32);
+    const uint8_t * meta_tile = slot_base + S.codes_bytes + static_cast<size_t>(live ? tile : 0) * 32 * nb * (TYPE == 39 ? 1 : 2);
+    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
+    Group ring[kDepth];
+    preload_ring(ring, codes_tile + (k * 32 + r) * 16, meta_tile + r * 8, nb / kGroupBlocks, live);
+
+    // x86 quantize_row_q8_0 of the layer input into the LDS activation row: one 32-lane group per
+    // block, 16 blocks per round.
+    const XrowLayout L = A.lay;
+    for (int b = threadIdx.x >> 5; b < nb; b += kThreads / 32) {
+        const int e = threadIdx.x & 31;
+        const float x = xs[b * 32 + e];
+        float amax = fabsf(x);
+        for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+        const float d = amax / 127.0f;
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        float q = rintf(x * id);
+        q = q > 127.0f ? 127.0f : (q < -128.0f ? -128.0f : q);
+        const int sk = e >> 2, pos = e & 3;
+        if (TYPE == 39) reinterpret_cast<_Float16 *>(act + (static_cast<int64_t>(sk) * nb + b) * 8)[pos] = static_cast<_Float16>(q);
+        else reinterpret_cast<signed char *>(act + (static_cast<int64_t>(sk) * nb + b) * 4)[pos] = static_cast<signed char>(q);
+        if (e == 0) reinterpret_cast<float *>(act + L.da_offset())[b] = static_cast<float>(static_cast<_Float16>(d));
+    }
+    __syncthreads();
+    float acc[1][2] = {{0.0f, 0.0f}};
+    stream_lane<TYPE, 1, false>(ring, codes_tile, meta_tile, k, r, nb, live,
+                                act + static_cast<int64_t>(k) * nb * L.code_entry(),
+                                reinterpret_cast<const float *>(act + L.da_offset()), 0, 1, acc);
+    red[k][lane] = acc[0][0] + acc[0][1];
+    __syncthreads();
+    if (k == 0 && live) {
+        float v = lane_tree(&red[0][lane]);
+        const int grow = static_cast<int>(ggml_row(static_cast<int64_t>(tile) * 32 + r, S.rows, S.interleave));
+        if (A.bias) v = v + A.bias[static_cast<size_t>(expert) * S.rows + grow];
+        vals[lane] = v;
+    }
+    __syncthreads();
+    if (k == 0 && lane < 32 && slot_ok)
+        glu_requant_block(vals, lane, blockIdx.x, A.act_rows + static_cast<size_t>(rank) * A.act_lay.stride(), A.act_lay,
+                          A.activation, A.alpha, A.limit);
+    if (blockIdx.x == 0 && blockIdx.y == 0 && static_cast<int>(threadIdx.x) < A.top_k) {
+        const int t = threadIdx.x;
+        const int e = s_ids[t];
+        A.route_ids[t] = e;
+        A.route_w[t] = s_w[t];
+        A.grp.active[t] = e;
+        A.grp.counts[e] = 1;
+        A.grp.offsets[e] = t;
+        A.grp.rows[t] = t;
+        if (t == 0) *A.grp.n_active = A.top_k;
+    }
+}
+
+template <int TYPE>
+void launch_decode_typed(const DecodeArgs & a, hipStream_t stream) {
+    const size_t lds = ((static_cast<size_t>(a.hidden) * 4 + 15) & ~static_cast<size_t>(15)) +
+                       static_cast<size_t>(a.lay.flag_offset());
+    const dim3 grid(static_cast<unsigned>(a.shape.rows / 64), static_cast<unsigned>(a.top_k));
+    hipLaunchKernelGGL((decode_gate_up_kernel<TYPE>), grid, dim3(kThreads), lds, stream, a);
+    check_hip(hipGetLastError(), "decode gate_up launch");
 }
 
 // ------------------------------------------------------------------------------ activation rows
@@ -407,20 +551,20 @@ __global__ __launch_bounds__(256) void expand_q8_kernel(const uint8_t * __restri
     if (threadIdx.x == 0) *reinterpret_cast<int *>(out + L.flag_offset()) = s_flag;
 }
 
-template <int TYPE, int G>
+template <int TYPE, int MT>
 void launch_typed(const GemvArgs & g, const KernelArgs & ka, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>((ka.shape.rows + 63) / 64), static_cast<unsigned>(g.max_active));
-    hipLaunchKernelGGL((expert_gemv_kernel<TYPE, G>), grid, dim3(kThreads), 0, stream, ka);
+    const size_t tok_bytes = (static_cast<size_t>(ka.lay.flag_offset()) + 15) & ~static_cast<size_t>(15);
+    hipLaunchKernelGGL((expert_gemv_kernel<TYPE, MT>), grid, dim3(kThreads), MT * tok_bytes, stream, ka);
     check_hip(hipGetLastError(), "expert GEMV launch");
 }
 
 template <int TYPE>
-void launch_g(const GemvArgs & g, const KernelArgs & ka, hipStream_t stream) {
-    const int groups = ka.shape.nb / (TYPE == 39 ? 8 : 4);
-    if (groups <= 4) launch_typed<TYPE, 4>(g, ka, stream);
-    else if (groups <= 8) launch_typed<TYPE, 8>(g, ka, stream);
-    else if (groups <= 12) launch_typed<TYPE, 12>(g, ka, stream);
-    else launch_typed<TYPE, 16>(g, ka, stream);
+void launch_mt(const GemvArgs & g, const KernelArgs & ka, hipStream_t stream) {
+    if (g.max_per_expert <= 1) launch_typed<TYPE, 1>(g, ka, stream);
+    else if (g.max_per_expert <= 2) launch_typed<TYPE, 2>(g, ka, stream);
+    else if (g.max_per_expert <= 4) launch_typed<TYPE, 4>(g, ka, stream);
+    else launch_typed<TYPE, 8>(g, ka, stream);
 }
 
 }  // namespace
@@ -472,8 +616,39 @@ void launch_gemv(const GemvArgs & g, hipStream_t stream) {
     ka.activation = g.activation;
     ka.alpha = g.alpha;
     ka.limit = g.limit;
-    if (bank.type == VBM_TYPE_MXFP4) launch_g<39>(g, ka, stream);
-    else launch_g<8>(g, ka, stream);
+    if (bank.type == VBM_TYPE_MXFP4) launch_mt<39>(g, ka, stream);
+    else launch_mt<8>(g, ka, stream);
+}
+
+void launch_decode_gate_up(const DecodeGateUpArgs & d, hipStream_t stream) {
+    const vbm_bank & bank = *d.bank;
+    require(bank.interleave && bank.rows % 64 == 0, "decode gate_up needs an interleaved bank with rows % 64 == 0");
+    require(d.top_k >= 1 && d.top_k <= 64 && d.n_expert >= d.top_k && d.n_expert <= 1024, "routing shape out of range");
+    require(d.hidden == bank.k && d.hidden <= 4096, "hidden size mismatch");
+    DecodeArgs a{};
+    a.bank = bank.base;
+    a.shape = Shape{static_cast<int>(bank.nb), static_cast<int>(bank.rows), bank.interleave, bank.slot_bytes,
+                    bank.geometry().codes_bytes(), bank.n_slots};
+    a.expert_to_slot = d.expert_to_slot;
+    a.lay = XrowLayout{bank.nb, bank.type};
+    a.logits = d.logits;
+    a.n_expert = static_cast<int>(d.n_expert);
+    a.top_k = static_cast<int>(d.top_k);
+    a.x_in = d.x_in;
+    a.prev_y = d.prev_y;
+    a.prev_w = d.prev_w;
+    a.hidden = static_cast<int>(d.hidden);
+    a.bias = d.bias;
+    a.act_rows = d.act_rows;
+    a.act_lay = d.act_layout;
+    a.route_ids = d.route_ids;
+    a.route_w = d.route_w;
+    a.grp = d.group;
+    a.activation = d.activation;
+    a.alpha = d.alpha;
+    a.limit = d.limit;
+    if (bank.type == VBM_TYPE_MXFP4) launch_decode_typed<39>(a, stream);
+    else launch_decode_typed<8>(a, stream);
 }
 
 }  // namespace vbm

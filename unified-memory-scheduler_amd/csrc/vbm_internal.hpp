@@ -132,6 +132,7 @@ struct GemvArgs {
     int64_t n_ids, b_ne1;
     GroupBuffers group;
     int64_t max_active;               // host bound on the number of active experts
+    int64_t max_per_expert;           // host bound on jobs per expert (selects the token chunk)
     const float * bias;               // [n_as][rows] ggml row order, or null
     float * dst;                      // epilogue 0
     uint8_t * dst_xrows;              // epilogue 1
@@ -141,5 +142,25 @@ struct GemvArgs {
     float alpha, limit;
 };
 void launch_gemv(const GemvArgs & a, hipStream_t stream);
+
+// Kernel A of the fused single-token decode (see vbm_gemv.hip).
+struct DecodeGateUpArgs {
+    const vbm_bank * bank;            // interleaved gate|up bank
+    const int32_t * expert_to_slot;
+    const float * logits;             // [n_expert]
+    int64_t n_expert, top_k, hidden;
+    const float * x_in;               // layer input, or null to combine prev_y with prev_w
+    const float * prev_y;
+    const float * prev_w;
+    const float * bias;
+    uint8_t * act_rows;
+    XrowLayout act_layout;
+    int32_t * route_ids;
+    float * route_w;
+    GroupBuffers group;
+    int activation;
+    float alpha, limit;
+};
+void launch_decode_gate_up(const DecodeGateUpArgs & d, hipStream_t stream);
 
 }  // namespace vbm

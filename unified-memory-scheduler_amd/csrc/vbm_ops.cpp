@@ -2,9 +2,23 @@
 #include "vbm_internal.hpp"
 
 #include <algorithm>
+#include <memory>
 #include <vector>
 
 using namespace vbm;
+
+struct vbm_decode_plan {
+    std::vector<vbm_moe_layer_desc> layers;
+    int64_t L = 0, H = 0, I = 0, E = 0, K = 0;
+    int device = 0;
+    uint8_t * workspace = nullptr;
+    int32_t * route_ids = nullptr;   // [L][K]
+    float * route_w = nullptr;       // [L][K]
+    GroupBuffers group{};
+    uint8_t * act_rows = nullptr;    // [K] down activation rows
+    XrowLayout act_layout{};
+    float * y = nullptr;             // [K][H]
+};
 
 namespace {
 
@@ -116,6 +130,7 @@ void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits
     a.n_ids = K;
     a.group = g;
     a.max_active = std::min<int64_t>(d->n_expert, entries);
+    a.max_per_expert = n_tokens;                 // top-k experts are distinct within a token
     a.activation = d->activation;
     a.alpha = 1.702f;
     a.limit = 7.0f;
@@ -210,6 +225,7 @@ vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot,
         a.b_ne1 = b_ne1;
         a.group = g;
         a.max_active = std::min<int64_t>(n_as, entries);
+        a.max_per_expert = entries;
         a.bias = bias;
         a.dst = dst;
         a.epilogue = 0;
@@ -320,6 +336,107 @@ vbm_status vbm_copy_kernel(void * dst, const void * src, size_t bytes, void * st
         hipLaunchKernelGGL(copy_kernel, dim3(blocks), dim3(256), 0, as_stream(stream),
                            static_cast<uint4 *>(dst), static_cast<const uint4 *>(src), n);
         check_hip(hipGetLastError(), "copy launch");
+    });
+}
+
+vbm_status vbm_decode_plan_create(const vbm_moe_layer_desc * layers, int64_t n_layers, vbm_decode_plan ** out) {
+    return guarded([&] {
+        require(out != nullptr && layers != nullptr && n_layers > 0, "invalid decode plan arguments");
+        *out = nullptr;
+        for (int64_t l = 0; l < n_layers; ++l) {
+            validate_layer(&layers[l]);
+            require(layers[l].router_w == nullptr, "fused decode needs given router logits (router_w == NULL)");
+            require(layers[l].hidden == layers[0].hidden && layers[l].intermediate == layers[0].intermediate &&
+                        layers[l].n_expert == layers[0].n_expert && layers[l].top_k == layers[0].top_k &&
+                        layers[l].gate_up->type == layers[0].gate_up->type,
+                    "all decode layers must share one shape and type");
+            require(layers[l].gate_up->rows % 64 == 0, "fused decode needs 2*intermediate % 64 == 0");
+        }
+        auto plan = std::make_unique<vbm_decode_plan>();
+        plan->layers.assign(layers, layers + n_layers);
+        plan->L = n_layers;
+        plan->H = layers[0].hidden;
+        plan->I = layers[0].intermediate;
+        plan->E = layers[0].n_expert;
+        plan->K = layers[0].top_k;
+        check_hip(hipGetDevice(&plan->device), "hipGetDevice");
+        plan->act_layout = XrowLayout{plan->I / 32, layers[0].down->type};
+        const size_t route = align_up(sizeof(int32_t) * plan->L * plan->K);
+        const size_t weights = align_up(sizeof(float) * plan->L * plan->K);
+        const size_t group = align_up(group_workspace_bytes(plan->E, plan->K));
+        const size_t act = align_up(static_cast<size_t>(plan->K * plan->act_layout.stride()));
+        const size_t y = align_up(sizeof(float) * plan->K * plan->H);
+        check_hip(hipMalloc(reinterpret_cast<void **>(&plan->workspace), route + weights + group + act + y),
+                  "decode plan workspace");
+        uint8_t * p = plan->workspace;
+        plan->route_ids = reinterpret_cast<int32_t *>(p); p += route;
+        plan->route_w = reinterpret_cast<float *>(p); p += weights;
+        plan->group = carve_group(p, plan->E, plan->K); p += group;
+        plan->act_rows = p; p += act;
+        plan->y = reinterpret_cast<float *>(p);
+        *out = plan.release();
+    });
+}
+
+vbm_status vbm_decode_plan_destroy(vbm_decode_plan * plan) {
+    return guarded([&] {
+        if (!plan) return;
+        (void)hipDeviceSynchronize();
+        if (plan->workspace) (void)hipFree(plan->workspace);
+        delete plan;
+    });
+}
+
+vbm_status vbm_decode_step(vbm_decode_plan * plan, const float * x, const float * logits, float * out, int32_t * ids,
+                           float * weights, void * const * events, void * stream) {
+    return guarded([&] {
+        require(plan != nullptr && x && logits && out, "null buffer");
+        const hipStream_t s = as_stream(stream);
+        const int64_t K = plan->K, H = plan->H, E = plan->E;
+        for (int64_t l = 0; l < plan->L; ++l) {
+            const vbm_moe_layer_desc & d = plan->layers[l];
+            void * const * ev = events ? events + 4 * l : nullptr;
+            DecodeGateUpArgs a{};
+            a.bank = d.gate_up;
+            a.expert_to_slot = d.expert_to_slot;
+            a.logits = logits + l * E;
+            a.n_expert = E;
+            a.top_k = K;
+            a.hidden = H;
+            a.x_in = l == 0 ? x : nullptr;
+            a.prev_y = plan->y;
+            a.prev_w = l == 0 ? nullptr : plan->route_w + (l - 1) * K;
+            a.bias = d.gate_up_bias;
+            a.act_rows = plan->act_rows;
+            a.act_layout = plan->act_layout;
+            a.route_ids = plan->route_ids + l * K;
+            a.route_w = plan->route_w + l * K;
+            a.group = plan->group;
+            a.activation = d.activation;
+            a.alpha = 1.702f;
+            a.limit = 7.0f;
+            record(ev, 0, s);
+            launch_decode_gate_up(a, s);
+            record(ev, 1, s);
+            GemvArgs b{};
+            b.bank = d.down;
+            b.expert_to_slot = d.expert_to_slot;
+            b.xrows = plan->act_rows;
+            b.n_ids = K;
+            b.b_ne1 = K;
+            b.group = plan->group;
+            b.max_active = K;
+            b.max_per_expert = 1;
+            b.bias = d.down_bias;
+            b.dst = plan->y;
+            b.epilogue = 0;
+            record(ev, 2, s);
+            launch_gemv(b, s);
+            record(ev, 3, s);
+        }
+        launch_combine(plan->y, plan->route_w + (plan->L - 1) * K, H, K, 1, out, s);
+        if (ids) check_hip(hipMemcpyAsync(ids, plan->route_ids, sizeof(int32_t) * plan->L * K, hipMemcpyDeviceToDevice, s), "ids copy");
+        if (weights) check_hip(hipMemcpyAsync(weights, plan->route_w, sizeof(float) * plan->L * K, hipMemcpyDeviceToDevice, s), "weights copy");
     });
 }
 

@@ -1,5 +1,6 @@
 // Routing-side kernels: token->expert grouping, Q8_0 activation quantizer, router
 // (logits, top-k, softmax over the selected), weighted rank-ordered combine, ADD_ID, GLU.
+#include "vbm_device.hpp"
 #include "vbm_internal.hpp"
 
 namespace vbm {
@@ -8,61 +9,74 @@ namespace {
 constexpr int kGroupThreads = 1024;
 constexpr int kMaxExperts = 1024;
 
-__device__ __forceinline__ float expf_rn(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
+constexpr int kMaxStagedIds = 16384;
 
 // One workgroup. Counting sort of entries i = token * n_ids + rank by expert, stable in i
 // (the (token outer, rank inner) append order of ggml's MMID row mapping). Entries with id -1
 // are skipped; ids outside [-1, n_as) raise the error flag and are skipped.
+//   1. ids -> LDS, per-expert counts with LDS atomics (order-independent);
+//   2. exclusive scans of counts (offsets) and of (count > 0) (active list) in parallel;
+//   3. stable placement: each wave owns experts w, w + 16, ... and ranks its matches over the
+//      entries in order, 64 at a time, with a ballot.
 __global__ __launch_bounds__(kGroupThreads) void group_kernel(const int32_t * __restrict__ ids, int n_ids,
                                                                int n_tokens, int64_t ids_stride, int n_as,
                                                                int32_t * counts, int32_t * offsets, int32_t * rows,
                                                                int32_t * active, int32_t * n_active, int32_t * error) {
     __shared__ int s_count[kMaxExperts];
-    __shared__ int s_offset[kMaxExperts + 1];
+    __shared__ int s_offset[kMaxExperts];
+    __shared__ int s_wave_sum[2][kGroupThreads / 64];
+    __shared__ int s_ids[kMaxStagedIds];
     __shared__ int s_error;
-    const int t = threadIdx.x;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int n = n_ids * n_tokens;
+    const bool staged = n <= kMaxStagedIds;
     for (int e = t; e < n_as; e += kGroupThreads) s_count[e] = 0;
     if (t == 0) s_error = 0;
     __syncthreads();
     for (int i = t; i < n; i += kGroupThreads) {
-        const int id = ids[static_cast<int64_t>(i / n_ids) * ids_stride + i % n_ids];
-        if (id == -1) continue;
-        if (id < 0 || id >= n_as) { s_error = 1; continue; }
-        atomicAdd(&s_count[id], 1);
+        int id = ids[static_cast<int64_t>(i / n_ids) * ids_stride + i % n_ids];
+        if (id != -1 && (id < 0 || id >= n_as)) { s_error = 1; id = -2; }
+        if (staged) s_ids[i] = id;
+        if (id >= 0) atomicAdd(&s_count[id], 1);
     }
     __syncthreads();
-    if (t == 0) {
-        int running = 0, live = 0;
-        for (int e = 0; e < n_as; ++e) {
-            s_offset[e] = running;
-            running += s_count[e];
-            if (s_count[e] > 0) active[live++] = e;
+    // Two-level exclusive scans over experts e = t (n_as <= 1024 = one expert per thread).
+    const int c = t < n_as ? s_count[t] : 0;
+    const int live = c > 0 ? 1 : 0;
+    int inc_c = c, inc_l = live;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int oc = __shfl_up(inc_c, off), ol = __shfl_up(inc_l, off);
+        if (lane >= off) { inc_c += oc; inc_l += ol; }
+    }
+    if (lane == 63) { s_wave_sum[0][wave] = inc_c; s_wave_sum[1][wave] = inc_l; }
+    __syncthreads();
+    int base_c = 0, base_l = 0;
+    for (int w = 0; w < wave; ++w) { base_c += s_wave_sum[0][w]; base_l += s_wave_sum[1][w]; }
+    const int ex_c = base_c + inc_c - c, ex_l = base_l + inc_l - live;
+    if (t < n_as) {
+        s_offset[t] = ex_c;
+        counts[t] = c;
+        offsets[t] = ex_c;
+        if (live) active[ex_l] = t;
+        if (t == n_as - 1) {
+            offsets[n_as] = ex_c + c;
+            *n_active = ex_l + live;
         }
-        s_offset[n_as] = running;
-        *n_active = live;
-        *error = s_error;
     }
+    if (t == 0) *error = s_error;
     __syncthreads();
-    for (int e = t; e < n_as; e += kGroupThreads) {
-        counts[e] = s_count[e];
-        offsets[e] = s_offset[e];
-    }
-    if (t == 0) offsets[n_as] = s_offset[n_as];
-    // Stable placement: each wave owns experts w, w + waves, ...; it scans the entries in order,
-    // 64 at a time, ranking matches with a ballot.
-    const int lane = t & 63, wave = t >> 6, waves = kGroupThreads / 64;
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    for (int e = wave; e < n_as; e += waves) {
+    for (int e = wave; e < n_as; e += kGroupThreads / 64) {
         if (s_count[e] == 0) continue;
         int running = s_offset[e];
         for (int base = 0; base < n; base += 64) {
             const int i = base + lane;
             int id = -2;
-            if (i < n) id = ids[static_cast<int64_t>(i / n_ids) * ids_stride + i % n_ids];
+            if (i < n) id = staged ? s_ids[i] : ids[static_cast<int64_t>(i / n_ids) * ids_stride + i % n_ids];
             const uint64_t mask = __ballot(id == e);
             if (id == e) rows[running + __popcll(mask & below)] = i;
             running += __popcll(mask);
+            if (running == s_offset[e] + s_count[e]) break;
         }
     }
 }
@@ -122,51 +136,12 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float * __rest
     }
 }
 
-// One wave per token: top-k by repeated arg-max (value desc, then lower index), then ggml
-// soft_max over the selected (expf per value, sum in double, scale by (float)(1/sum)).
+// One wave per token: top-k + softmax over the selected (wave_topk_softmax).
 __global__ __launch_bounds__(64) void topk_softmax_kernel(const float * __restrict__ logits, int n_expert,
                                                           int top_k, int32_t * __restrict__ ids,
                                                           float * __restrict__ weights) {
-    const int t = blockIdx.x;
-    const int lane = threadIdx.x;
-    const float * l = logits + static_cast<int64_t>(t) * n_expert;
-    __shared__ int s_ids[64];
-    __shared__ float s_vals[64];
-    uint64_t taken[16] = {0};  // supports n_expert <= 1024 (64 lanes x 16 strides)
-    for (int j = 0; j < top_k; ++j) {
-        float best = 0.0f;
-        int best_i = -1;
-        for (int s = 0; s * 64 + lane < n_expert; ++s) {
-            const int i = s * 64 + lane;
-            if ((taken[s] >> lane) & 1ull) continue;
-            const float v = l[i];
-            if (best_i < 0 || v > best) { best = v; best_i = i; }
-        }
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(best, off);
-            const int oi = __shfl_xor(best_i, off);
-            const bool better = oi >= 0 && (best_i < 0 || ov > best || (ov == best && oi < best_i));
-            if (better) { best = ov; best_i = oi; }
-        }
-        if (best_i >= 0 && (best_i & 63) == lane) taken[best_i >> 6] |= 1ull << lane;
-        if (lane == 0) { s_ids[j] = best_i; s_vals[j] = best; }
-    }
-    __syncthreads();
-    if (lane == 0) {
-        float max = -INFINITY;
-        for (int j = 0; j < top_k; ++j) max = s_vals[j] > max ? s_vals[j] : max;
-        double sum = 0.0;
-        float y[64];
-        for (int j = 0; j < top_k; ++j) {
-            y[j] = expf_rn(s_vals[j] - max);
-            sum += static_cast<double>(y[j]);
-        }
-        const float scale = static_cast<float>(1.0 / sum);
-        for (int j = 0; j < top_k; ++j) {
-            ids[static_cast<int64_t>(t) * top_k + j] = s_ids[j];
-            weights[static_cast<int64_t>(t) * top_k + j] = y[j] * scale;
-        }
-    }
+    const int64_t t = blockIdx.x;
+    wave_topk_softmax(logits + t * n_expert, n_expert, top_k, ids + t * top_k, weights + t * top_k);
 }
 
 // out[t][i] = ((w0*y0 + w1*y1) + w2*y2) + ... : ggml MUL by the weight then sequential ADD.

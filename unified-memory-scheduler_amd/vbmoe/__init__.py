@@ -80,6 +80,9 @@ SIGNATURES = {
     "vbm_graph_launch": [vp, vp],
     "vbm_graph_destroy": [vp],
     "vbm_copy_kernel": [vp, vp, sz, vp],
+    "vbm_decode_plan_create": [C.POINTER(MoeLayerDesc), i64, C.POINTER(vp)],
+    "vbm_decode_plan_destroy": [vp],
+    "vbm_decode_step": [vp, vp, vp, vp, vp, vp, vp, vp],
 }
 OTHER = {"vbm_last_error": ([], C.c_char_p), "vbm_abi_version": ([], C.c_int)}
 
