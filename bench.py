@@ -122,7 +122,7 @@ def cpu_baseline(args, logits_host: np.ndarray) -> dict:
             x = r["out"]
         elapsed += time.perf_counter() - t
         done += 1
-        if (elapsed >= args.cpu_seconds and done >= 2) or done >= 4096:
+        if (elapsed >= args.cpu_seconds and done >= 2) or done >= 1_000_000:
             break
     per_layer_token = elapsed / (done * args.cpu_layers)
     return {"value": round(1.0 / (per_layer_token * args.layers), 3), "unit": "tok/s", "cores": threads, "kind": "port",
@@ -154,9 +154,12 @@ def main() -> int:
     ap.add_argument("--experts", type=int, default=128)
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph")
     ap.add_argument("--kernel-steps", type=int, default=10, help="steps of the event-timed kernel pass")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-layers", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="after the run, launch a plain device copy of BYTES three times (a known-traffic "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.tokens != 1:
@@ -229,7 +232,7 @@ def main() -> int:
         f"(host wall {wall:.3f} s); step expert bytes {step_weight_bytes / 1e9:.3f} GB -> "
         f"{step_weight_bytes / (ms_per_step / 1e3) / 1e9:.0f} GB/s")
 
-    # Event-timed kernel pass: the same decode steps, launched eagerly with events around both GEMVs.
+    # Event-timed kernel pass: the same decode steps, launched eagerly with events around both kernels.
     events = []
     for _ in range(L):
         row = []
@@ -264,7 +267,7 @@ def main() -> int:
     dn_gbs = dn_bytes / (dn_avg_us * 1e-6) / 1e9
     log(f"kernel A (route + combine + quantize + gate_up GEMV): {gu_avg_us:.2f} us avg over {launches} launches -> "
         f"{gu_gbs:.0f} GB/s; kernel B (down GEMV): {dn_avg_us:.2f} us -> {dn_gbs:.0f} GB/s")
-    traffic = read_traffic(REPO / "profiles" / "gemv_gate_up_120b_bs1_pmc.md") if T == 1 else None
+    traffic = read_traffic(REPO / "profiles" / "decode_gate_up_120b_bs1_pmc.md")
 
     cpu = None
     if not args.no_cpu and T == 1:
@@ -295,7 +298,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_gate_up_kernel<MXFP4> (combine + Q8_0 + top-k/softmax + gate_up GEMV + bias + SwiGLU-OAI + requant)",
+            "kernel": "decode_gate_up_kernel<MXFP4> (routing + combine + Q8_0 + gate_up GEMV + bias + SwiGLU-OAI + requant)",
             "achieved": round(gu_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -309,6 +312,13 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+    if args.copy_probe > 0:
+        n = args.copy_probe // 16 * 16
+        src, dst = vb.DeviceBuffer(n), vb.DeviceBuffer(n)
+        for _ in range(3):
+            vb.call("vbm_copy_kernel", dst.ptr, src.ptr, n, stream)
+        vb.call("vbm_stream_synchronize", stream)
+        log(f"copy probe: 3 x {n} B")
     if graph is not None:
         vb.call("vbm_graph_destroy", graph)
     return 0

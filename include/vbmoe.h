@@ -259,22 +259,22 @@ vbm_status vbm_moe_layer_forward_profiled(const vbm_moe_layer_desc * desc, const
  * Fused single-token decode through a stack of routed-expert layers whose router logits are
  * given (the decode step of llama_decode over build_moe_ffn's routed-expert part,
  * hybrid-experts.patch:1394-1924, for one token). Per layer two kernels run:
- *   A: previous layer's weighted rank combine (or the input), Q8_0 quantization, top-k +
- *      softmax, gate_up GEMV + biases + GLU + Q8_0 requantization;
+ *   A: top-k + softmax routing, the previous layer's weighted rank combine (or the input),
+ *      Q8_0 quantization, gate_up GEMV + biases + GLU + Q8_0 requantization;
  *   B: down GEMV + bias;
  * and one final kernel combines the last layer. Each layer's output is bit-identical to
  * vbm_moe_layer_forward with n_tokens = 1. The plan owns its workspace, so a step allocates
- * nothing and can be captured in a HIP graph. All layers share one shape and type; every
- * layer's router_w must be NULL.
+ * nothing and can be captured in a HIP graph; steps on one plan must not overlap. All layers
+ * share one shape and type; every layer's router_w must be NULL.
  * -------------------------------------------------------------------------------------------- */
 typedef struct vbm_decode_plan vbm_decode_plan;
 
 vbm_status vbm_decode_plan_create(const vbm_moe_layer_desc * layers, int64_t n_layers,
                                   vbm_decode_plan ** plan);
 vbm_status vbm_decode_plan_destroy(vbm_decode_plan * plan);
-/* x [hidden] -> out [hidden]; logits [n_layers][n_expert]; ids / weights optional
- * [n_layers][top_k] outputs. events: optional [n_layers][4] hipEvent_t (as void*) recorded
- * before/after kernel A and before/after kernel B of every layer (NULL: none). */
+/* x [hidden] (16-byte aligned) -> out [hidden]; logits [n_layers][n_expert]; ids / weights
+ * optional [n_layers][top_k] outputs. events: optional [n_layers][4] hipEvent_t (as void*)
+ * recorded before/after kernel A and before/after kernel B of every layer (NULL: none). */
 vbm_status vbm_decode_step(vbm_decode_plan * plan, const float * x, const float * logits,
                            float * out, int32_t * ids, float * weights, void * const * events,
                            void * stream);

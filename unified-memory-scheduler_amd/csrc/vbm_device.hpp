@@ -67,4 +67,90 @@ __device__ __forceinline__ void wave_topk_softmax(const float * logits, int n, i
     }
 }
 
+// Lane-crossing moves inside a row of 16 lanes (DPP): quad_perm [1,0,3,2] = 0xB1, quad_perm
+// [2,3,0,1] = 0x4E, row_half_mirror = 0x141, row_mirror = 0x140.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// Maximum over each aligned group of four lanes (all four active).
+__device__ __forceinline__ float quad_max(float v) {
+    v = fmaxf(v, dpp_move<0xB1>(v));
+    return fmaxf(v, dpp_move<0x4E>(v));
+}
+
+// Maximum over each half-wave (lanes 0..31, 32..63), all 32 lanes of the half active: quads,
+// then mirrored halves of 8 and rows of 16 (DPP), then the two rows through a swizzle with
+// xor mask 16.
+__device__ __forceinline__ float half_wave_max(float v) {
+    v = quad_max(v);
+    v = fmaxf(v, dpp_move<0x141>(v));
+    v = fmaxf(v, dpp_move<0x140>(v));
+    return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F)));
+}
+
+constexpr int kMaxRouteExperts = 1024;
+
+// Routing logit as staged for the rank count: NaN reads as -inf so the ranks stay a permutation.
+__device__ __forceinline__ float route_key(float v) { return v != v ? -INFINITY : v; }
+
+// Whole-workgroup top-k over n <= kMaxRouteExperts logits already staged in s_val (route_key) with
+// s_rank zeroed, in the total order (value desc, then lower index;
+// tools/trace/topk-tie-probe.cpp:111-113): the rank of every candidate is the number of elements
+// that precede it, counted in 32-element chunks by independent threads and summed with LDS
+// atomics, so there is no serial chain of k wave reductions. On return s_ids[j] is pick j
+// (j < k). s_val must be 16-byte aligned. All NT threads of the workgroup must call it; it
+// starts with a barrier.
+template <int NT>
+__device__ __forceinline__ void block_topk(int n, int k, const float * s_val, int * s_rank, int32_t * s_ids) {
+    __syncthreads();
+    const int nq = (n + 31) >> 5;
+    for (int w = threadIdx.x; w < n * nq; w += NT) {
+        const int q = w / n, c = w - q * n;
+        const float vc = s_val[c];
+        const int j0 = 32 * q;
+        int cnt = 0;
+        if (j0 + 32 <= n) {   // full chunk: eight 16-byte LDS reads, all issued before use
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = reinterpret_cast<const float4 *>(s_val + j0)[u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int j = j0 + 4 * u;
+                cnt += (v[u].x > vc || (v[u].x == vc && j < c)) ? 1 : 0;
+                cnt += (v[u].y > vc || (v[u].y == vc && j + 1 < c)) ? 1 : 0;
+                cnt += (v[u].z > vc || (v[u].z == vc && j + 2 < c)) ? 1 : 0;
+                cnt += (v[u].w > vc || (v[u].w == vc && j + 3 < c)) ? 1 : 0;
+            }
+        } else {
+            for (int j = j0; j < n; ++j) {
+                const float vj = s_val[j];
+                cnt += (vj > vc || (vj == vc && j < c)) ? 1 : 0;
+            }
+        }
+        if (cnt) atomicAdd(&s_rank[c], cnt);
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < n; c += NT) {
+        const int r = s_rank[c];
+        if (r < k) s_ids[r] = c;
+    }
+    __syncthreads();
+}
+
+// ggml soft_max over the k selected logits, in pick order (expf(v - max), sum in double, scale by
+// (float)(1/sum)); called by one full wave, returns the weight of pick `lane` (lane < k).
+__device__ __forceinline__ float route_softmax(const float * s_val, const int32_t * s_ids, int k, int lane) {
+    float max = -INFINITY;
+    for (int j = 0; j < k; ++j) {
+        const float v = s_val[s_ids[j]];
+        max = v > max ? v : max;
+    }
+    const float e = lane < k ? expf_rn(s_val[s_ids[lane]] - max) : 0.0f;
+    double sum = 0.0;
+    for (int j = 0; j < k; ++j) sum += static_cast<double>(__shfl(e, j));
+    return e * static_cast<float>(1.0 / sum);
+}
+
 }  // namespace vbm

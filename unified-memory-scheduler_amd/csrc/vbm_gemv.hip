@@ -51,7 +51,6 @@ __device__ __forceinline__ T * wave_uniform(T * p) {
 }
 
 constexpr int kThreads = 512;
-constexpr int kChunk = 4;        // tokens reduced per barrier
 
 __device__ __forceinline__ half2_t as_half2(unsigned v) { return __builtin_bit_cast(half2_t, v); }
 
@@ -106,8 +105,6 @@ struct KernelArgs {
     float alpha, limit;
 };
 
-constexpr int kDepth = 4;    // weight groups in flight per lane (ring buffer)
-
 // One group of one lane: 16 B of codes (8 MXFP4 blocks x 2 B or 4 Q8_0 blocks x 4 B) and 8 B of
 // exponents (MXFP4) or fp16 scales (Q8_0).
 struct Group {
@@ -115,10 +112,13 @@ struct Group {
     u32x2 m;
 };
 
+// MLDS: the workgroup staged its tiles' exponents / scales in LDS, so only the codes are loaded.
+template <bool MLDS>
 __device__ __forceinline__ Group load_group(const uint8_t * cp, const uint8_t * mp, int g) {
     Group r;
     r.c = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(cp + g * 4096));
-    r.m = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(mp + g * 256));
+    if (MLDS) r.m = u32x2{0u, 0u};
+    else r.m = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(mp + g * 256));
     return r;
 }
 
@@ -146,12 +146,12 @@ __device__ __forceinline__ void mx_block(unsigned dw, int e, int b, const uint8_
 
 // Eight MXFP4 blocks (one group, starting at block b) for MT tokens.
 template <int MT, bool SLOW>
-__device__ __forceinline__ void mx_group(const Group & grp, int b, const uint8_t * la, const float * lda, int tok_bytes,
-                                         int mcount, float (&acc)[MT][2]) {
+__device__ __forceinline__ void mx_group(const u32x4 & c, const u32x2 & m, int b, const uint8_t * la, const float * lda,
+                                         int tok_bytes, int mcount, float (&acc)[MT][2]) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const unsigned dw = q == 0 ? grp.c.x : (q == 1 ? grp.c.y : (q == 2 ? grp.c.z : grp.c.w));
-        const unsigned ew = q < 2 ? grp.m.x : grp.m.y;
+        const unsigned dw = q == 0 ? c.x : (q == 1 ? c.y : (q == 2 ? c.z : c.w));
+        const unsigned ew = q < 2 ? m.x : m.y;
         mx_block<MT, SLOW, 0, 0>(dw, static_cast<signed char>(ew >> ((2 * q & 3) * 8)), b + 2 * q, la, lda, tok_bytes,
                                  mcount, acc);
         mx_block<MT, SLOW, 2, 1>(dw, static_cast<signed char>(ew >> (((2 * q + 1) & 3) * 8)), b + 2 * q + 1, la, lda,
@@ -178,61 +178,289 @@ __device__ __forceinline__ void q8_block(unsigned w, unsigned short dbits, int b
 
 // Four Q8_0 blocks (one group, starting at block b) for MT tokens: one chain per lane.
 template <int MT, bool SLOW>
-__device__ __forceinline__ void q8_group(const Group & grp, int b, const uint8_t * la, const float * lda, int tok_bytes,
-                                         int mcount, float (&acc)[MT][2]) {
-    q8_block<MT, SLOW>(grp.c.x, static_cast<unsigned short>(grp.m.x), b, la, lda, tok_bytes, mcount, acc);
-    q8_block<MT, SLOW>(grp.c.y, static_cast<unsigned short>(grp.m.x >> 16), b + 1, la, lda, tok_bytes, mcount, acc);
-    q8_block<MT, SLOW>(grp.c.z, static_cast<unsigned short>(grp.m.y), b + 2, la, lda, tok_bytes, mcount, acc);
-    q8_block<MT, SLOW>(grp.c.w, static_cast<unsigned short>(grp.m.y >> 16), b + 3, la, lda, tok_bytes, mcount, acc);
+__device__ __forceinline__ void q8_group(const u32x4 & c, const u32x2 & m, int b, const uint8_t * la, const float * lda,
+                                         int tok_bytes, int mcount, float (&acc)[MT][2]) {
+    q8_block<MT, SLOW>(c.x, static_cast<unsigned short>(m.x), b, la, lda, tok_bytes, mcount, acc);
+    q8_block<MT, SLOW>(c.y, static_cast<unsigned short>(m.x >> 16), b + 1, la, lda, tok_bytes, mcount, acc);
+    q8_block<MT, SLOW>(c.z, static_cast<unsigned short>(m.y), b + 2, la, lda, tok_bytes, mcount, acc);
+    q8_block<MT, SLOW>(c.w, static_cast<unsigned short>(m.y >> 16), b + 3, la, lda, tok_bytes, mcount, acc);
 }
 
-// Issues the first kDepth groups of one lane's row slice (before activation staging, so the
-// weight stream is already in flight while the activation arrives).
-__device__ __forceinline__ void preload_ring(Group (&ring)[kDepth], const uint8_t * cp, const uint8_t * mp, int groups,
-                                             bool live) {
+// Weight groups a lane keeps in flight. The gate_up decode kernel (two workgroups per CU on most
+// CUs) streams through a 6-deep ring so compute overlaps the arrivals; the down decode kernel
+// (about 1.4 workgroups per CU) issues its whole row slice (K <= 3072 MXFP4: 11-12 groups) at
+// once; the batched kernel keeps a 4-deep ring because its per-token accumulators need the
+// registers.
+template <int TYPE>
+constexpr int gate_up_depth() {
+    return TYPE == 39 ? 6 : 4;
+}
+template <int TYPE>
+constexpr int down_depth() {
+    return TYPE == 39 ? 12 : 8;
+}
+constexpr int kBatchDepth = 4;
+
+// The blocks past the last full group of a lane's row slice (nb is even: MXFP4 tail in
+// {0,2,4,6}, Q8_0 tail in {0,2}): MXFP4 keeps two blocks per code dword and two exponents per
+// meta halfword, Q8_0 one block per code dword and one fp16 scale per meta halfword.
+struct Tail {
+    unsigned c[3];
+    unsigned m[3];
+};
+
+template <int TYPE, bool MLDS>
+__device__ __forceinline__ void preload_tail(Tail & t, const uint8_t * codes_tile, const uint8_t * meta_tile, int k,
+                                             int r, int nb, bool live) {
+    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4, kCode = TYPE == 39 ? 2 : 4, kMeta = TYPE == 39 ? 1 : 2;
+    const int groups = nb / kGroupBlocks, tail = nb % kGroupBlocks;
+    const int n = TYPE == 39 ? tail / 2 : tail;
+    const uint8_t * tcp = codes_tile + groups * 4096 + (k * 32 + r) * (tail * kCode);
+    const uint8_t * tmp = meta_tile + groups * 256 + r * tail * kMeta;
 #pragma unroll
-    for (int i = 0; i < kDepth; ++i) {
-        ring[i] = Group{};
-        if (live && i < groups) ring[i] = load_group(cp, mp, i);
+    for (int i = 0; i < 3; ++i) {
+        t.c[i] = 0u;
+        t.m[i] = 0u;
+        if (live && i < n) {
+            t.c[i] = __builtin_nontemporal_load(reinterpret_cast<const unsigned *>(tcp + 4 * i));
+            if (!MLDS) t.m[i] = *reinterpret_cast<const unsigned short *>(tmp + 2 * i);
+        }
     }
 }
 
-// Streams one lane's row slice once through the kDepth-deep register ring, applying every
-// staged token to each group as it arrives.
-template <int TYPE, int MT, bool SLOW>
-__device__ __forceinline__ void stream_lane(Group (&ring)[kDepth], const uint8_t * codes_tile, const uint8_t * meta_tile,
-                                            int k, int r, int nb, bool live, const uint8_t * la, const float * lda,
-                                            int tok_bytes, int mcount, float (&acc)[MT][2]) {
+// Issues the first D groups of one lane's row slice (before activation staging, so the weight
+// stream is in flight while the activation row arrives).
+template <int TYPE, int D, bool MLDS>
+__device__ __forceinline__ void preload_ring(Group (&ring)[D], const uint8_t * codes_tile, const uint8_t * meta_tile,
+                                             int k, int r, int nb, bool live) {
     constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
-    const int groups = nb / kGroupBlocks, tail = nb % kGroupBlocks;
+    const int groups = nb / kGroupBlocks;
     const uint8_t * cp = codes_tile + (k * 32 + r) * 16;
     const uint8_t * mp = meta_tile + r * 8;
-    for (int g0 = 0; g0 < groups; g0 += kDepth) {
 #pragma unroll
-        for (int i = 0; i < kDepth; ++i) {
+    for (int i = 0; i < D; ++i) {
+        ring[i] = Group{};
+        if (live && i < groups) ring[i] = load_group<MLDS>(cp, mp, i);
+    }
+}
+
+// Streams the full groups of one lane's row slice once through the D-deep register ring,
+// applying every staged token to each group as it arrives. With MLDS, `meta_tile` is the
+// lane's tile exponents / scales staged in LDS.
+template <int TYPE, int MT, bool SLOW, int D, bool MLDS>
+__device__ __forceinline__ void stream_groups(Group (&ring)[D], const uint8_t * codes_tile, const uint8_t * meta_tile,
+                                              int k, int r, int nb, bool live, const uint8_t * la, const float * lda,
+                                              int tok_bytes, int mcount, float (&acc)[MT][2]) {
+    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
+    const int groups = nb / kGroupBlocks;
+    const uint8_t * cp = codes_tile + (k * 32 + r) * 16;
+    const uint8_t * mp = meta_tile + r * 8;
+    for (int g0 = 0; g0 < groups; g0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
             const int g = g0 + i;
             if (g < groups) {
                 const Group cur = ring[i];
-                if (live && g + kDepth < groups) ring[i] = load_group(cp, mp, g + kDepth);
-                if (TYPE == 39) mx_group<MT, SLOW>(cur, g * 8, la, lda, tok_bytes, mcount, acc);
-                else q8_group<MT, SLOW>(cur, g * 4, la, lda, tok_bytes, mcount, acc);
+                if (live && g + D < groups) ring[i] = load_group<MLDS>(cp, mp, g + D);
+                const u32x2 m = MLDS ? *reinterpret_cast<const u32x2 *>(mp + g * 256) : cur.m;
+                if (TYPE == 39) mx_group<MT, SLOW>(cur.c, m, g * 8, la, lda, tok_bytes, mcount, acc);
+                else q8_group<MT, SLOW>(cur.c, m, g * 4, la, lda, tok_bytes, mcount, acc);
             }
         }
     }
-    // Tail blocks past the last full group (MXFP4: nb % 8 in {0,2,4,6}; Q8_0: nb % 4).
-    constexpr int kCode = TYPE == 39 ? 2 : 4, kMeta = TYPE == 39 ? 1 : 2;
-    const uint8_t * tcp = codes_tile + groups * 4096 + (k * 32 + r) * (tail * kCode);
-    const uint8_t * tmp = meta_tile + groups * 256 + r * tail * kMeta;
-    for (int bt = 0; bt < tail; bt += (TYPE == 39 ? 2 : 1)) {
-        const unsigned cw = live ? *reinterpret_cast<const unsigned *>(tcp + bt * kCode) : 0u;
-        if (TYPE == 39) {
-            const int e0 = live ? static_cast<signed char>(tmp[bt]) : 0;
-            const int e1 = live ? static_cast<signed char>(tmp[bt + 1]) : 0;
-            mx_block<MT, SLOW, 0, 0>(cw, e0, groups * 8 + bt, la, lda, tok_bytes, mcount, acc);
-            mx_block<MT, SLOW, 2, 1>(cw, e1, groups * 8 + bt + 1, la, lda, tok_bytes, mcount, acc);
-        } else {
-            const unsigned short dbits = live ? *reinterpret_cast<const unsigned short *>(tmp + bt * 2) : 0;
-            q8_block<MT, SLOW>(cw, dbits, groups * 4 + bt, la, lda, tok_bytes, mcount, acc);
+}
+
+// The tail blocks of one lane's row slice (after its full groups: block order is chain order).
+// With MLDS the exponents / scales come from the lane's tile meta staged in LDS (`meta_lds`).
+template <int TYPE, int MT, bool SLOW, bool MLDS>
+__device__ __forceinline__ void apply_tail(const Tail & tl, const uint8_t * meta_lds, int r, int nb, const uint8_t * la,
+                                           const float * lda, int tok_bytes, int mcount, float (&acc)[MT][2]) {
+    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4, kMeta = TYPE == 39 ? 1 : 2;
+    const int groups = nb / kGroupBlocks, tail = nb % kGroupBlocks;
+    const int n = TYPE == 39 ? tail / 2 : tail;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        if (i < n) {
+            const unsigned m = MLDS ? *reinterpret_cast<const unsigned short *>(meta_lds + groups * 256 + r * tail * kMeta + 2 * i)
+                                    : tl.m[i];
+            if (TYPE == 39) {
+                const int b = groups * 8 + 2 * i;
+                mx_block<MT, SLOW, 0, 0>(tl.c[i], static_cast<signed char>(m & 0xFFu), b, la, lda, tok_bytes, mcount, acc);
+                mx_block<MT, SLOW, 2, 1>(tl.c[i], static_cast<signed char>(m >> 8), b + 1, la, lda, tok_bytes, mcount, acc);
+            } else {
+                q8_block<MT, SLOW>(tl.c[i], static_cast<unsigned short>(m), groups * 4 + i, la, lda, tok_bytes, mcount, acc);
+            }
+        }
+    }
+}
+
+// Stages the exponents / scales of a workgroup's (up to) two consecutive tiles: loads are issued
+// into registers first (ahead of the code stream, so waiting for them never waits for codes),
+// then written to LDS by store_meta.
+template <int TYPE>
+__device__ __forceinline__ int meta_tile_bytes(int nb) {
+    return 32 * nb * (TYPE == 39 ? 1 : 2);
+}
+// Up to 2 * NT * 16 bytes (two tiles of K <= 4096 at NT = 512, one tile at NT = 256).
+template <int NT>
+__device__ __forceinline__ void load_meta(u32x4 (&st)[2], const uint8_t * meta, int bytes) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int off = (threadIdx.x + i * NT) * 16;
+        st[i] = u32x4{0u, 0u, 0u, 0u};
+        if (off < bytes) st[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(meta + off));
+    }
+}
+template <int NT>
+__device__ __forceinline__ void store_meta(const u32x4 (&st)[2], uint8_t * lds, int bytes) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int off = (threadIdx.x + i * NT) * 16;
+        if (off < bytes) *reinterpret_cast<u32x4 *>(lds + off) = st[i];
+    }
+}
+
+// ------------------------------------------------------------------------ decode block math
+// In the single-token decode kernels every (row, block) scale is precomputed once per workgroup
+// into an LDS table (MXFP4: ldexp(d_act, e - 128); Q8_0: fp16(d_w) * d_act, the same operations
+// the batched path does per lane), laid out [tile][block / 4][row][block % 4] so one 16-byte read
+// per lane brings four consecutive blocks without bank conflicts.
+
+// v_dot2_f32_f16 with an inline zero accumulator (one VOP3P instruction instead of a register
+// clear plus v_dot2c).
+__device__ __forceinline__ float dot2_zero(half2_t a, half2_t b) {
+    float r;
+    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+template <int SEL, int PAR>
+__device__ __forceinline__ void mx_block_s(unsigned dw, float s, u32x2 a, float (&acc)[2]) {
+    const half2_t w01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, SEL);
+    const half2_t w23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, SEL + 1);
+    float v = dot2_zero(w23, as_half2(a.y));
+    v = __builtin_amdgcn_fdot2(w01, as_half2(a.x), v, false);
+    acc[PAR] = __builtin_fmaf(s, v, acc[PAR]);
+}
+
+__device__ __forceinline__ void q8_block_s(unsigned w, float s, unsigned a, float (&acc)[2]) {
+    const int v = __builtin_amdgcn_sdot4(static_cast<int>(w), static_cast<int>(a), 0, false);
+    acc[0] = __builtin_fmaf(s, static_cast<float>(v), acc[0]);
+}
+
+// Streams one lane's row slice (full groups through the D-deep ring, then the tail) against one
+// token: `la` is the wave's activation slice (8 B per block for MXFP4, 4 B for Q8_0), `ls` the
+// lane's row in the scale table.
+template <int TYPE, int D>
+__device__ __forceinline__ void decode_stream(Group (&ring)[D], const Tail & tl, const uint8_t * codes_tile, int k, int r,
+                                              int nb, bool live, const uint8_t * la, const float * ls,
+                                              float (&acc)[2]) {
+    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
+    const int groups = nb / kGroupBlocks, tail = nb % kGroupBlocks;
+    const uint8_t * cp = codes_tile + (k * 32 + r) * 16;
+    for (int g0 = 0; g0 < groups; g0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const int g = g0 + i;
+            if (g < groups) {
+                const u32x4 c = ring[i].c;
+                if (live && g + D < groups) ring[i] = load_group<true>(cp, nullptr, g + D);
+                if (TYPE == 39) {
+                    const float4 s0 = *reinterpret_cast<const float4 *>(ls + (2 * g) * 128);
+                    const float4 s1 = *reinterpret_cast<const float4 *>(ls + (2 * g + 1) * 128);
+                    const u32x4 a0 = *reinterpret_cast<const u32x4 *>(la + (8 * g) * 8);
+                    const u32x4 a1 = *reinterpret_cast<const u32x4 *>(la + (8 * g + 2) * 8);
+                    const u32x4 a2 = *reinterpret_cast<const u32x4 *>(la + (8 * g + 4) * 8);
+                    const u32x4 a3 = *reinterpret_cast<const u32x4 *>(la + (8 * g + 6) * 8);
+                    mx_block_s<0, 0>(c.x, s0.x, a0.xy, acc);
+                    mx_block_s<2, 1>(c.x, s0.y, a0.zw, acc);
+                    mx_block_s<0, 0>(c.y, s0.z, a1.xy, acc);
+                    mx_block_s<2, 1>(c.y, s0.w, a1.zw, acc);
+                    mx_block_s<0, 0>(c.z, s1.x, a2.xy, acc);
+                    mx_block_s<2, 1>(c.z, s1.y, a2.zw, acc);
+                    mx_block_s<0, 0>(c.w, s1.z, a3.xy, acc);
+                    mx_block_s<2, 1>(c.w, s1.w, a3.zw, acc);
+                } else {
+                    const float4 s0 = *reinterpret_cast<const float4 *>(ls + g * 128);
+                    const u32x2 a01 = *reinterpret_cast<const u32x2 *>(la + (4 * g) * 4);
+                    const u32x2 a23 = *reinterpret_cast<const u32x2 *>(la + (4 * g + 2) * 4);
+                    q8_block_s(c.x, s0.x, a01.x, acc);
+                    q8_block_s(c.y, s0.y, a01.y, acc);
+                    q8_block_s(c.z, s0.z, a23.x, acc);
+                    q8_block_s(c.w, s0.w, a23.y, acc);
+                }
+            }
+        }
+    }
+    const int n = TYPE == 39 ? tail / 2 : tail;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        if (i < n) {
+            if (TYPE == 39) {
+                const int b = groups * 8 + 2 * i;
+                const u32x4 a = *reinterpret_cast<const u32x4 *>(la + b * 8);
+                mx_block_s<0, 0>(tl.c[i], ls[(b >> 2) * 128 + (b & 3)], a.xy, acc);
+                mx_block_s<2, 1>(tl.c[i], ls[((b + 1) >> 2) * 128 + ((b + 1) & 3)], a.zw, acc);
+            } else {
+                const int b = groups * 4 + i;
+                q8_block_s(tl.c[i], ls[(b >> 2) * 128 + (b & 3)], *reinterpret_cast<const unsigned *>(la + b * 4), acc);
+            }
+        }
+    }
+}
+
+// Builds the scale table of a workgroup's NTILES tiles from the staged tile meta (`lmeta`, bank
+// layout) and the activation block scales `da`: one thread per (tile, group, row), lanes of a
+// half-wave on consecutive rows of one group.
+template <int TYPE, int NT, int NTILES>
+__device__ __forceinline__ void build_scales(float * lscale, const uint8_t * lmeta, const float * da, int nb, int mbytes) {
+    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
+    const int groups = nb / kGroupBlocks, tail = nb % kGroupBlocks;
+    const int g1 = groups + (tail ? 1 : 0);
+    const int nb4 = (nb + 3) / 4;
+    const int r = threadIdx.x & 31;
+    for (int tg = threadIdx.x >> 5; tg < NTILES * g1; tg += NT / 32) {
+        const int t = tg >= g1 ? 1 : 0, g = tg - t * g1;
+        const uint8_t * m = lmeta + t * mbytes;
+        float * out = lscale + (t * nb4 * 32 + r) * 4;
+        const int b0 = g * kGroupBlocks;
+        if (g < groups) {
+            const u32x2 mv = *reinterpret_cast<const u32x2 *>(m + g * 256 + r * 8);
+            if (TYPE == 39) {
+                const float4 d0 = *reinterpret_cast<const float4 *>(da + b0);
+                const float4 d1 = *reinterpret_cast<const float4 *>(da + b0 + 4);
+                float4 s0, s1;
+                s0.x = __builtin_amdgcn_ldexpf(d0.x, static_cast<signed char>(mv.x));
+                s0.y = __builtin_amdgcn_ldexpf(d0.y, static_cast<signed char>(mv.x >> 8));
+                s0.z = __builtin_amdgcn_ldexpf(d0.z, static_cast<signed char>(mv.x >> 16));
+                s0.w = __builtin_amdgcn_ldexpf(d0.w, static_cast<signed char>(mv.x >> 24));
+                s1.x = __builtin_amdgcn_ldexpf(d1.x, static_cast<signed char>(mv.y));
+                s1.y = __builtin_amdgcn_ldexpf(d1.y, static_cast<signed char>(mv.y >> 8));
+                s1.z = __builtin_amdgcn_ldexpf(d1.z, static_cast<signed char>(mv.y >> 16));
+                s1.w = __builtin_amdgcn_ldexpf(d1.w, static_cast<signed char>(mv.y >> 24));
+                *reinterpret_cast<float4 *>(out + (2 * g) * 128) = s0;
+                *reinterpret_cast<float4 *>(out + (2 * g + 1) * 128) = s1;
+            } else {
+                const float4 d0 = *reinterpret_cast<const float4 *>(da + b0);
+                float4 s0;
+                s0.x = half_bits_to_float(static_cast<uint16_t>(mv.x)) * d0.x;
+                s0.y = half_bits_to_float(static_cast<uint16_t>(mv.x >> 16)) * d0.y;
+                s0.z = half_bits_to_float(static_cast<uint16_t>(mv.y)) * d0.z;
+                s0.w = half_bits_to_float(static_cast<uint16_t>(mv.y >> 16)) * d0.w;
+                *reinterpret_cast<float4 *>(out + g * 128) = s0;
+            }
+        } else {   // partial last group: the tail blocks, meta packed per row
+            for (int j = 0; j < tail; ++j) {
+                const int b = b0 + j;
+                float sv;
+                if (TYPE == 39) {
+                    sv = __builtin_amdgcn_ldexpf(da[b], static_cast<signed char>(m[groups * 256 + r * tail + j]));
+                } else {
+                    const uint8_t * q = m + groups * 256 + (r * tail + j) * 2;
+                    sv = half_bits_to_float(static_cast<uint16_t>(q[0] | (q[1] << 8))) * da[b];
+                }
+                out[(b >> 2) * 128 + (b & 3)] = sv;
+            }
         }
     }
 }
@@ -252,8 +480,7 @@ __device__ __forceinline__ void glu_requant_block(const float * vals, int lane, 
                                                   int activation, float alpha, float limit) {
     const int lr = (lane >> 4) * 32 + (lane & 15);
     const float act = glu(activation, vals[lr], vals[lr + 16], alpha, limit);
-    float amax = fabsf(act);
-    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    const float amax = half_wave_max(fabsf(act));
     const float d = amax / 127.0f;
     const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
     float q = rintf(act * id);
@@ -299,15 +526,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const uint8_t * la = lds_tok + static_cast<int64_t>(k) * nb * A.lay.code_entry();
     const float * lda = reinterpret_cast<const float *>(lds_tok + A.lay.da_offset());
 
-    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
-    const int groups = nb / kGroupBlocks;
-    const uint8_t * cp = codes_tile + (k * 32 + r) * 16;
-    const uint8_t * mp = meta_tile + r * 8;
-
+    constexpr int D = kBatchDepth;
     for (int c0 = 0; c0 < count; c0 += MT) {
         const int mcount = count - c0 < MT ? count - c0 : MT;
-        Group ring[kDepth];
-        preload_ring(ring, cp, mp, groups, live);
+        Group ring[D];
+        preload_ring<TYPE, D, false>(ring, codes_tile, meta_tile, k, r, nb, live);
         // Stage the chunk's activation rows (and their -128 flags) in LDS.
         if (threadIdx.x == 0) s_flag = 0;
         __syncthreads();
@@ -328,8 +551,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         float acc[MT][2];
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[m][0] = acc[m][1] = 0.0f;
-        if (s_flag) stream_lane<TYPE, MT, true>(ring, codes_tile, meta_tile, k, r, nb, live, la, lda, tok_bytes, mcount, acc);
-        else stream_lane<TYPE, MT, false>(ring, codes_tile, meta_tile, k, r, nb, live, la, lda, tok_bytes, mcount, acc);
+        Tail tl;
+        if (s_flag) {
+            stream_groups<TYPE, MT, true, D, false>(ring, codes_tile, meta_tile, k, r, nb, live, la, lda, tok_bytes, mcount,
+                                                    acc);
+            preload_tail<TYPE, false>(tl, codes_tile, meta_tile, k, r, nb, live);
+            apply_tail<TYPE, MT, true, false>(tl, nullptr, r, nb, la, lda, tok_bytes, mcount, acc);
+        } else {
+            stream_groups<TYPE, MT, false, D, false>(ring, codes_tile, meta_tile, k, r, nb, live, la, lda, tok_bytes, mcount,
+                                                     acc);
+            preload_tail<TYPE, false>(tl, codes_tile, meta_tile, k, r, nb, live);
+            apply_tail<TYPE, MT, false, false>(tl, nullptr, r, nb, la, lda, tok_bytes, mcount, acc);
+        }
 #pragma unroll
         for (int m = 0; m < MT; ++m) red[m][k][lane] = acc[m][0] + acc[m][1];
         __syncthreads();
@@ -354,12 +587,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 }
 
 // ------------------------------------------------------------------------------ fused decode
-// Single-token decode, kernel A of a layer: the previous layer's weighted rank combine (or the
-// layer input), x86 Q8_0 quantization, top-k + softmax over the given logits, and the gate_up
-// GEMV of this workgroup's (tile pair, rank) with biases, GLU and requantization into the down
-// projection's activation row. Wave 0 routes while waves 1..7 combine; every workgroup does both
-// redundantly (a few KiB from L2), which removes four dependent launches per layer. Workgroup
-// (0,0) publishes the routing and the down work list for kernel B (the generic expert GEMV).
+// Single-token decode runs two launches per layer.
+// Kernel A (gate_up, 512 threads = 8 lane slices x 64 rows): every workgroup routes (top-k +
+//   softmax over the layer's given logits; a few hundred bytes from L2) and, with the same
+//   loads in flight, combines the previous layer (ggml MUL by the routing weight, then ADD in
+//   rank order) or takes the input; it then issues its expert's weights, quantizes the input to
+//   Q8_0, runs the gate_up GEMV of its tile pair with biases, GLU and requantization into one
+//   32-element block of the rank's down activation row. Workgroup (0,0) publishes the routing.
+// Kernel B (down, 256 threads = 8 lane slices x 32 rows, so its 360 workgroups spread over all
+//   CUs): loads the activation row and the routed expert id together, streams the down weights
+//   of one tile and writes y[rank] with the down bias.
+// A single launch per layer with device-side readiness counters (down workgroups prefetching
+// while gate_up runs) measured slower: producer-to-consumer signalling across XCDs took several
+// microseconds under full HBM load, more than a kernel boundary.
 struct DecodeArgs {
     const uint8_t * bank;
     Shape shape;
@@ -370,116 +610,302 @@ struct DecodeArgs {
     const float * x_in;        // [hidden] layer input, or null to combine the previous layer
     const float * prev_y;      // [top_k][hidden] previous layer's biased down outputs
     const float * prev_w;      // [top_k] previous layer's routing weights
-    int hidden;
     const float * bias;        // gate_up bias [n_expert][rows] (ggml row order) or null
     uint8_t * act_rows;        // [top_k] down activation rows
     XrowLayout act_lay;
     int32_t * route_ids;       // [top_k] this layer's routing
     float * route_w;           // [top_k]
-    GroupBuffers grp;          // this layer's down work list
     int activation;
     float alpha, limit;
 };
 
-template <int TYPE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void decode_gate_up_kernel(DecodeArgs A) {
-    __shared__ float red[8][64];
-    __shared__ float vals[64];
-    __shared__ int32_t s_ids[64];
-    __shared__ float s_w[64];
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
-    const int H = A.hidden, nb = H / 32;
-    float * xs = reinterpret_cast<float *>(lds_dyn);
-    uint8_t * act = lds_dyn + ((H * 4 + 15) & ~15);
-    const int k = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63, r = lane & 31;
-    const int rank = blockIdx.y;
-    if (k == 0) {
-        wave_topk_softmax(A.logits, A.n_expert, A.top_k, s_ids, s_w);
-    } else {
-        const int K = A.top_k;
-        for (int i = threadIdx.x - 64; i < H; i += kThreads - 64) {
-            float v;
-            if (A.x_in) {
-                v = A.x_in[i];
-            } else {  // ggml MUL by the weight, then sequential ADD in rank order
-                v = A.prev_y[i] * A.prev_w[0];
-                for (int q = 1; q < K; ++q) {
-                    const float term = A.prev_y[static_cast<int64_t>(q) * H + i] * A.prev_w[q];
-                    v = v + term;
+constexpr int kDownThreads = 256;
+
+// The layer input into `xs` (fp32, LDS): x, or the previous layer's combine (ggml MUL by the
+// routing weight, then ADD in rank order), eight elements per thread with the loads of up to four
+// ranks in flight together.
+__device__ __forceinline__ void combine_input(const DecodeArgs & A, float * xs, int H) {
+    for (int e0 = threadIdx.x * 8; e0 < H; e0 += kThreads * 8) {
+        float x[8];
+        if (A.x_in) {
+            const float4 lo = *reinterpret_cast<const float4 *>(A.x_in + e0);
+            const float4 hi = *reinterpret_cast<const float4 *>(A.x_in + e0 + 4);
+            x[0] = lo.x; x[1] = lo.y; x[2] = lo.z; x[3] = lo.w;
+            x[4] = hi.x; x[5] = hi.y; x[6] = hi.z; x[7] = hi.w;
+        } else {
+            for (int q0 = 0; q0 < A.top_k; q0 += 4) {
+                float4 lo[4], hi[4];
+                float w[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (q0 + j < A.top_k) {
+                        const float * y = A.prev_y + static_cast<int64_t>(q0 + j) * H + e0;
+                        lo[j] = *reinterpret_cast<const float4 *>(y);
+                        hi[j] = *reinterpret_cast<const float4 *>(y + 4);
+                        w[j] = A.prev_w[q0 + j];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (q0 + j < A.top_k) {
+                        const float y[8] = {lo[j].x, lo[j].y, lo[j].z, lo[j].w, hi[j].x, hi[j].y, hi[j].z, hi[j].w};
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            const float term = y[i] * w[j];
+                            x[i] = q0 + j == 0 ? term : x[i] + term;
+                        }
+                    }
                 }
             }
-            xs[i] = v;
+        }
+        *reinterpret_cast<float4 *>(xs + e0) = make_float4(x[0], x[1], x[2], x[3]);
+        *reinterpret_cast<float4 *>(xs + e0 + 4) = make_float4(x[4], x[5], x[6], x[7]);
+    }
+}
+
+// x86 quantize_row_q8_0 of `xs` into the activation row `act` (codes + block scales): four
+// threads per 32-element block, eight elements each, block maximum over the quad (DPP).
+template <int TYPE>
+__device__ __forceinline__ void quantize_input(const float * xs, uint8_t * act, const XrowLayout & L, int nb) {
+    for (int t = threadIdx.x; t < 4 * nb; t += kThreads) {
+        const int b = t >> 2, part = t & 3;
+        const int e0 = b * 32 + part * 8;
+        const float4 lo = *reinterpret_cast<const float4 *>(xs + e0);
+        const float4 hi = *reinterpret_cast<const float4 *>(xs + e0 + 4);
+        const float x[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
+        amax = quad_max(amax);
+        const float d = amax / 127.0f;
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        float q[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float v = rintf(x[i] * id);
+            q[i] = v > 127.0f ? 127.0f : (v < -128.0f ? -128.0f : v);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t sk = 2 * part + h;
+            if (TYPE == 39) {
+                half2_t p0, p1;
+                p0.x = static_cast<_Float16>(q[4 * h]); p0.y = static_cast<_Float16>(q[4 * h + 1]);
+                p1.x = static_cast<_Float16>(q[4 * h + 2]); p1.y = static_cast<_Float16>(q[4 * h + 3]);
+                u32x2 v;
+                v.x = __builtin_bit_cast(unsigned, p0);
+                v.y = __builtin_bit_cast(unsigned, p1);
+                *reinterpret_cast<u32x2 *>(act + (sk * nb + b) * 8) = v;
+            } else {
+                unsigned v = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    v |= static_cast<unsigned>(static_cast<uint8_t>(static_cast<signed char>(q[4 * h + i]))) << (8 * i);
+                *reinterpret_cast<unsigned *>(act + (sk * nb + b) * 4) = v;
+            }
+        }
+        if (part == 0) reinterpret_cast<float *>(act + L.da_offset())[b] = static_cast<float>(static_cast<_Float16>(d));
+    }
+}
+
+// Dynamic LDS of kernel A: [xs: hidden fp32][meta of 2 tiles][activation row][scale table].
+template <int TYPE>
+size_t gate_up_lds_bytes(int nb) {
+    return static_cast<size_t>(nb) * 128 + 2 * 32 * static_cast<size_t>(nb) * (TYPE == 39 ? 1 : 2) +
+           ((static_cast<size_t>(nb) * (TYPE == 39 ? 68 : 36) + 15) & ~static_cast<size_t>(15)) +
+           static_cast<size_t>((nb + 3) / 4) * 1024;
+}
+// Dynamic LDS of kernel B: [meta of 1 tile][activation row][scale table of 1 tile].
+template <int TYPE>
+size_t down_lds_bytes(int nb) {
+    return 32 * static_cast<size_t>(nb) * (TYPE == 39 ? 1 : 2) +
+           ((static_cast<size_t>(nb) * (TYPE == 39 ? 68 : 36) + 15) & ~static_cast<size_t>(15)) +
+           static_cast<size_t>((nb + 3) / 4) * 512;
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void decode_gate_up_kernel(DecodeArgs A) {
+    constexpr int D = gate_up_depth<TYPE>();
+    __shared__ float red[8][64];
+    __shared__ float vals[64];
+    __shared__ __attribute__((aligned(16))) float s_val[kMaxRouteExperts];
+    __shared__ int s_rank[kMaxRouteExperts];
+    __shared__ int32_t s_ids[64];
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
+    const Shape S = A.shape;
+    const int nb = S.nb;
+    float * xs = reinterpret_cast<float *>(lds_dyn);
+    uint8_t * lmeta = lds_dyn + nb * 128;
+    uint8_t * act = lmeta + 2 * meta_tile_bytes<TYPE>(nb);
+    float * lscale = reinterpret_cast<float *>(act + ((A.lay.flag_offset() + 15) & ~15ll));
+    const int k = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, r = lane & 31;
+    const int pair = blockIdx.x, rank = blockIdx.y;
+
+    // The routing logits and the layer input are loaded together; only then the routing decides
+    // which weights to stream.
+    const int n = A.n_expert;
+    float lg[kMaxRouteExperts / kThreads];
+#pragma unroll
+    for (int i = 0; i < kMaxRouteExperts / kThreads; ++i) {
+        const int c = threadIdx.x + i * kThreads;
+        lg[i] = c < n ? A.logits[c] : 0.0f;
+    }
+    combine_input(A, xs, nb * 32);
+#pragma unroll
+    for (int i = 0; i < kMaxRouteExperts / kThreads; ++i) {
+        const int c = threadIdx.x + i * kThreads;
+        if (c < n) {
+            s_val[c] = route_key(lg[i]);
+            s_rank[c] = 0;
         }
     }
-    __syncthreads();
+    block_topk<kThreads>(n, A.top_k, s_val, s_rank, s_ids);
     const int expert = s_ids[rank];
     const int slot = A.expert_to_slot ? A.expert_to_slot[expert] : expert;
-    const bool slot_ok = slot >= 0 && slot < A.shape.n_slots;
-    const Shape S = A.shape;
-    const int tile = blockIdx.x * 2 + (lane >> 5);
+    const bool slot_ok = slot >= 0 && slot < S.n_slots;
+    const int tile = pair * 2 + (lane >> 5);
     const bool live = slot_ok && tile * 32 < S.rows;
     const uint8_t * slot_base = A.bank + static_cast<size_t>(slot_ok ? slot : 0) * S.slot_bytes;
     const uint8_t * codes_tile = slot_base + static_cast<size_t>(live ? tile : 0) * 32 * nb * (TYPE == 39 ? 16 : 32);
-    const uint8_t * meta_tile = slot_base + S.codes_bytes + static_cast<size_t>(live ? tile : 0) * 32 * nb * (TYPE == 39 ? 1 : 2);
-    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
-    Group ring[kDepth];
-    preload_ring(ring, codes_tile + (k * 32 + r) * 16, meta_tile + r * 8, nb / kGroupBlocks, live);
+    const int mbytes = meta_tile_bytes<TYPE>(nb);
+    u32x4 mst[2];
+    load_meta<kThreads>(mst, slot_base + S.codes_bytes + static_cast<size_t>(pair) * 2 * mbytes, slot_ok ? 2 * mbytes : 0);
+    Group ring[D];
+    Tail tl;
+    preload_ring<TYPE, D, true>(ring, codes_tile, nullptr, k, r, nb, live);
+    preload_tail<TYPE, true>(tl, codes_tile, nullptr, k, r, nb, live);
+    const int grow = static_cast<int>(ggml_row(static_cast<int64_t>(tile) * 32 + r, S.rows, S.interleave));
+    float bias_v = 0.0f;
+    if (k == 0 && live && A.bias) bias_v = A.bias[static_cast<size_t>(expert) * S.rows + grow];
 
-    // x86 quantize_row_q8_0 of the layer input into the LDS activation row: one 32-lane group per
-    // block, 16 blocks per round.
-    const XrowLayout L = A.lay;
-    for (int b = threadIdx.x >> 5; b < nb; b += kThreads / 32) {
-        const int e = threadIdx.x & 31;
-        const float x = xs[b * 32 + e];
-        float amax = fabsf(x);
-        for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-        const float d = amax / 127.0f;
-        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-        float q = rintf(x * id);
-        q = q > 127.0f ? 127.0f : (q < -128.0f ? -128.0f : q);
-        const int sk = e >> 2, pos = e & 3;
-        if (TYPE == 39) reinterpret_cast<_Float16 *>(act + (static_cast<int64_t>(sk) * nb + b) * 8)[pos] = static_cast<_Float16>(q);
-        else reinterpret_cast<signed char *>(act + (static_cast<int64_t>(sk) * nb + b) * 4)[pos] = static_cast<signed char>(q);
-        if (e == 0) reinterpret_cast<float *>(act + L.da_offset())[b] = static_cast<float>(static_cast<_Float16>(d));
-    }
+    quantize_input<TYPE>(xs, act, A.lay, nb);
+    store_meta<kThreads>(mst, lmeta, 2 * mbytes);
     __syncthreads();
-    float acc[1][2] = {{0.0f, 0.0f}};
-    stream_lane<TYPE, 1, false>(ring, codes_tile, meta_tile, k, r, nb, live,
-                                act + static_cast<int64_t>(k) * nb * L.code_entry(),
-                                reinterpret_cast<const float *>(act + L.da_offset()), 0, 1, acc);
-    red[k][lane] = acc[0][0] + acc[0][1];
+    build_scales<TYPE, kThreads, 2>(lscale, lmeta, reinterpret_cast<const float *>(act + A.lay.da_offset()), nb, mbytes);
     __syncthreads();
-    if (k == 0 && live) {
+    float acc[2] = {0.0f, 0.0f};
+    decode_stream<TYPE, D>(ring, tl, codes_tile, k, r, nb, live, act + static_cast<int64_t>(k) * nb * A.lay.code_entry(),
+                           lscale + ((lane >> 5) * ((nb + 3) / 4) * 32 + r) * 4, acc);
+    red[k][lane] = acc[0] + acc[1];
+    __syncthreads();
+    if (k == 0) {
         float v = lane_tree(&red[0][lane]);
-        const int grow = static_cast<int>(ggml_row(static_cast<int64_t>(tile) * 32 + r, S.rows, S.interleave));
-        if (A.bias) v = v + A.bias[static_cast<size_t>(expert) * S.rows + grow];
+        if (A.bias) v = v + bias_v;
         vals[lane] = v;
     }
     __syncthreads();
-    if (k == 0 && lane < 32 && slot_ok)
-        glu_requant_block(vals, lane, blockIdx.x, A.act_rows + static_cast<size_t>(rank) * A.act_lay.stride(), A.act_lay,
-                          A.activation, A.alpha, A.limit);
-    if (blockIdx.x == 0 && blockIdx.y == 0 && static_cast<int>(threadIdx.x) < A.top_k) {
-        const int t = threadIdx.x;
-        const int e = s_ids[t];
-        A.route_ids[t] = e;
-        A.route_w[t] = s_w[t];
-        A.grp.active[t] = e;
-        A.grp.counts[e] = 1;
-        A.grp.offsets[e] = t;
-        A.grp.rows[t] = t;
-        if (t == 0) *A.grp.n_active = A.top_k;
+    if (k == 0) {
+        if (lane < 32 && slot_ok)
+            glu_requant_block(vals, lane, pair, A.act_rows + static_cast<size_t>(rank) * A.act_lay.stride(), A.act_lay,
+                              A.activation, A.alpha, A.limit);
+        if (pair == 0 && rank == 0) {
+            const float w = route_softmax(s_val, s_ids, A.top_k, lane);
+            if (lane < A.top_k) {
+                A.route_ids[lane] = s_ids[lane];
+                A.route_w[lane] = w;
+            }
+        }
+    }
+}
+
+struct DecodeDownArgs {
+    const uint8_t * bank;
+    Shape shape;
+    const int32_t * expert_to_slot;
+    XrowLayout lay;            // down activation format (nb = intermediate / 32)
+    const uint8_t * act_rows;  // [top_k] activation rows written by kernel A
+    const int32_t * route_ids; // [top_k]
+    const float * bias;        // down bias [n_expert][rows] or null
+    float * y;                 // [top_k][rows]
+};
+
+// Kernel B: one 32-row tile of one rank; wave w holds lane slices 2w (lanes 0..31) and 2w + 1
+// (lanes 32..63) of the tile's rows.
+template <int TYPE>
+__global__ __launch_bounds__(kDownThreads) void decode_down_kernel(DecodeDownArgs A) {
+    constexpr int D = down_depth<TYPE>();
+    __shared__ float red[8][32];
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
+    const Shape S = A.shape;
+    const int nb = S.nb;
+    uint8_t * lmeta = lds_dyn;
+    uint8_t * act = lmeta + meta_tile_bytes<TYPE>(nb);
+    float * lscale = reinterpret_cast<float *>(act + ((A.lay.flag_offset() + 15) & ~15ll));
+    const int lane = threadIdx.x & 63, r = lane & 31;
+    const int k = (threadIdx.x >> 6) * 2 + (lane >> 5);
+    const int tile = blockIdx.x, rank = blockIdx.y;
+    // The activation row (independent of the routing) is loaded together with the expert id.
+    const int copy_bytes = static_cast<int>(A.lay.flag_offset());   // codes + block scales
+    const uint8_t * xr = A.act_rows + static_cast<size_t>(rank) * A.lay.stride();
+    u32x4 stage[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int off = (threadIdx.x + i * kDownThreads) * 16;
+        stage[i] = u32x4{0u, 0u, 0u, 0u};
+        if (off + 16 <= copy_bytes) stage[i] = *reinterpret_cast<const u32x4 *>(xr + off);
+        else if (off < copy_bytes) stage[i].xy = *reinterpret_cast<const u32x2 *>(xr + off);   // 8-byte remainder
+    }
+    const int expert = as_const<int32_t>(A.route_ids)[rank];
+    const int slot = A.expert_to_slot ? as_const<int32_t>(A.expert_to_slot)[expert] : expert;
+    const bool slot_ok = slot >= 0 && slot < S.n_slots;
+    const uint8_t * slot_base = A.bank + static_cast<size_t>(slot_ok ? slot : 0) * S.slot_bytes;
+    const uint8_t * codes_tile = slot_base + static_cast<size_t>(tile) * 32 * nb * (TYPE == 39 ? 16 : 32);
+    const int mbytes = meta_tile_bytes<TYPE>(nb);
+    u32x4 mst[2];
+    load_meta<kDownThreads>(mst, slot_base + S.codes_bytes + static_cast<size_t>(tile) * mbytes, slot_ok ? mbytes : 0);
+    Group ring[D];
+    Tail tl;
+    preload_ring<TYPE, D, true>(ring, codes_tile, nullptr, k, r, nb, slot_ok);
+    preload_tail<TYPE, true>(tl, codes_tile, nullptr, k, r, nb, slot_ok);
+    const int row = tile * 32 + r;
+    float bias_v = 0.0f;
+    if (k == 0 && slot_ok && A.bias) bias_v = A.bias[static_cast<size_t>(expert) * S.rows + row];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int off = (threadIdx.x + i * kDownThreads) * 16;
+        if (off + 16 <= copy_bytes) *reinterpret_cast<u32x4 *>(act + off) = stage[i];
+        else if (off < copy_bytes) *reinterpret_cast<u32x2 *>(act + off) = stage[i].xy;
+    }
+    store_meta<kDownThreads>(mst, lmeta, mbytes);
+    __syncthreads();
+    build_scales<TYPE, kDownThreads, 1>(lscale, lmeta, reinterpret_cast<const float *>(act + A.lay.da_offset()), nb,
+                                        mbytes);
+    __syncthreads();
+    float acc[2] = {0.0f, 0.0f};
+    decode_stream<TYPE, D>(ring, tl, codes_tile, k, r, nb, slot_ok, act + static_cast<int64_t>(k) * nb * A.lay.code_entry(),
+                           lscale + r * 4, acc);
+    red[k][r] = acc[0] + acc[1];
+    __syncthreads();
+    if (threadIdx.x < 32) {
+        const float * l = &red[0][r];
+        const float s0 = l[4 * 32] + l[0], s1 = l[5 * 32] + l[1 * 32];
+        const float s2 = l[6 * 32] + l[2 * 32], s3 = l[7 * 32] + l[3 * 32];
+        float v = (s0 + s2) + (s1 + s3);           // lane_tree over slices 32 floats apart
+        if (A.bias) v = v + bias_v;
+        if (!slot_ok) v = __builtin_nanf("");      // expert not resident in this bank: loud output
+        A.y[static_cast<size_t>(rank) * S.rows + row] = v;
     }
 }
 
 template <int TYPE>
 void launch_decode_typed(const DecodeArgs & a, hipStream_t stream) {
-    const size_t lds = ((static_cast<size_t>(a.hidden) * 4 + 15) & ~static_cast<size_t>(15)) +
-                       static_cast<size_t>(a.lay.flag_offset());
+    const size_t lds = gate_up_lds_bytes<TYPE>(a.shape.nb);
+    if (lds > 65536)
+        check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_gate_up_kernel<TYPE>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)),
+                  "decode gate_up LDS attribute");
     const dim3 grid(static_cast<unsigned>(a.shape.rows / 64), static_cast<unsigned>(a.top_k));
     hipLaunchKernelGGL((decode_gate_up_kernel<TYPE>), grid, dim3(kThreads), lds, stream, a);
     check_hip(hipGetLastError(), "decode gate_up launch");
+}
+
+template <int TYPE>
+void launch_decode_down_typed(const DecodeDownArgs & a, int top_k, hipStream_t stream) {
+    const size_t lds = down_lds_bytes<TYPE>(a.shape.nb);
+    const dim3 grid(static_cast<unsigned>(a.shape.rows / 32), static_cast<unsigned>(top_k));
+    hipLaunchKernelGGL((decode_down_kernel<TYPE>), grid, dim3(kDownThreads), lds, stream, a);
+    check_hip(hipGetLastError(), "decode down launch");
 }
 
 // ------------------------------------------------------------------------------ activation rows
@@ -623,8 +1049,12 @@ void launch_gemv(const GemvArgs & g, hipStream_t stream) {
 void launch_decode_gate_up(const DecodeGateUpArgs & d, hipStream_t stream) {
     const vbm_bank & bank = *d.bank;
     require(bank.interleave && bank.rows % 64 == 0, "decode gate_up needs an interleaved bank with rows % 64 == 0");
-    require(d.top_k >= 1 && d.top_k <= 64 && d.n_expert >= d.top_k && d.n_expert <= 1024, "routing shape out of range");
+    require(d.top_k >= 1 && d.top_k <= 64 && d.n_expert >= d.top_k && d.n_expert <= kMaxRouteExperts,
+            "routing shape out of range");
     require(d.hidden == bank.k && d.hidden <= 4096, "hidden size mismatch");
+    require(d.act_layout.nb == bank.rows / 64 && d.act_layout.weight_type == bank.type,
+            "down activation layout does not match the gate_up bank");
+    require(d.x_in != nullptr || (d.prev_y != nullptr && d.prev_w != nullptr), "decode layer input missing");
     DecodeArgs a{};
     a.bank = bank.base;
     a.shape = Shape{static_cast<int>(bank.nb), static_cast<int>(bank.rows), bank.interleave, bank.slot_bytes,
@@ -637,18 +1067,35 @@ void launch_decode_gate_up(const DecodeGateUpArgs & d, hipStream_t stream) {
     a.x_in = d.x_in;
     a.prev_y = d.prev_y;
     a.prev_w = d.prev_w;
-    a.hidden = static_cast<int>(d.hidden);
     a.bias = d.bias;
     a.act_rows = d.act_rows;
     a.act_lay = d.act_layout;
     a.route_ids = d.route_ids;
     a.route_w = d.route_w;
-    a.grp = d.group;
     a.activation = d.activation;
     a.alpha = d.alpha;
     a.limit = d.limit;
     if (bank.type == VBM_TYPE_MXFP4) launch_decode_typed<39>(a, stream);
     else launch_decode_typed<8>(a, stream);
+}
+
+void launch_decode_down(const DecodeDownParams & d, hipStream_t stream) {
+    const vbm_bank & bank = *d.bank;
+    require(d.top_k >= 1 && d.top_k <= 64, "top_k out of range");
+    require(bank.nb <= 128 && d.act_layout.nb == bank.nb && d.act_layout.weight_type == bank.type,
+            "down activation layout does not match the down bank");
+    DecodeDownArgs a{};
+    a.bank = bank.base;
+    a.shape = Shape{static_cast<int>(bank.nb), static_cast<int>(bank.rows), bank.interleave, bank.slot_bytes,
+                    bank.geometry().codes_bytes(), bank.n_slots};
+    a.expert_to_slot = d.expert_to_slot;
+    a.lay = d.act_layout;
+    a.act_rows = d.act_rows;
+    a.route_ids = d.route_ids;
+    a.bias = d.bias;
+    a.y = d.y;
+    if (bank.type == VBM_TYPE_MXFP4) launch_decode_down_typed<39>(a, static_cast<int>(d.top_k), stream);
+    else launch_decode_down_typed<8>(a, static_cast<int>(d.top_k), stream);
 }
 
 }  // namespace vbm

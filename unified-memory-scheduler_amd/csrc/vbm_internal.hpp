@@ -143,13 +143,14 @@ struct GemvArgs {
 };
 void launch_gemv(const GemvArgs & a, hipStream_t stream);
 
-// Kernel A of the fused single-token decode (see vbm_gemv.hip).
+// Kernel A of the fused single-token decode: routing, input combine + Q8_0, gate_up GEMV, GLU,
+// requantization into the down activation rows.
 struct DecodeGateUpArgs {
     const vbm_bank * bank;            // interleaved gate|up bank
     const int32_t * expert_to_slot;
     const float * logits;             // [n_expert]
     int64_t n_expert, top_k, hidden;
-    const float * x_in;               // layer input, or null to combine prev_y with prev_w
+    const float * x_in;               // layer input (16-byte aligned), or null to combine prev_y with prev_w
     const float * prev_y;
     const float * prev_w;
     const float * bias;
@@ -157,10 +158,22 @@ struct DecodeGateUpArgs {
     XrowLayout act_layout;
     int32_t * route_ids;
     float * route_w;
-    GroupBuffers group;
     int activation;
     float alpha, limit;
 };
 void launch_decode_gate_up(const DecodeGateUpArgs & d, hipStream_t stream);
+
+// Kernel B of the fused single-token decode: down GEMV + bias of every routed rank into y.
+struct DecodeDownParams {
+    const vbm_bank * bank;
+    const int32_t * expert_to_slot;
+    const uint8_t * act_rows;         // [top_k] activation rows from kernel A
+    XrowLayout act_layout;
+    const int32_t * route_ids;        // [top_k]
+    int64_t top_k;
+    const float * bias;               // [n_expert][hidden] or null
+    float * y;                        // [top_k][hidden]
+};
+void launch_decode_down(const DecodeDownParams & d, hipStream_t stream);
 
 }  // namespace vbm

@@ -14,7 +14,6 @@ struct vbm_decode_plan {
     uint8_t * workspace = nullptr;
     int32_t * route_ids = nullptr;   // [L][K]
     float * route_w = nullptr;       // [L][K]
-    GroupBuffers group{};
     uint8_t * act_rows = nullptr;    // [K] down activation rows
     XrowLayout act_layout{};
     float * y = nullptr;             // [K][H]
@@ -363,15 +362,13 @@ vbm_status vbm_decode_plan_create(const vbm_moe_layer_desc * layers, int64_t n_l
         plan->act_layout = XrowLayout{plan->I / 32, layers[0].down->type};
         const size_t route = align_up(sizeof(int32_t) * plan->L * plan->K);
         const size_t weights = align_up(sizeof(float) * plan->L * plan->K);
-        const size_t group = align_up(group_workspace_bytes(plan->E, plan->K));
         const size_t act = align_up(static_cast<size_t>(plan->K * plan->act_layout.stride()));
         const size_t y = align_up(sizeof(float) * plan->K * plan->H);
-        check_hip(hipMalloc(reinterpret_cast<void **>(&plan->workspace), route + weights + group + act + y),
+        check_hip(hipMalloc(reinterpret_cast<void **>(&plan->workspace), route + weights + act + y),
                   "decode plan workspace");
         uint8_t * p = plan->workspace;
         plan->route_ids = reinterpret_cast<int32_t *>(p); p += route;
         plan->route_w = reinterpret_cast<float *>(p); p += weights;
-        plan->group = carve_group(p, plan->E, plan->K); p += group;
         plan->act_rows = p; p += act;
         plan->y = reinterpret_cast<float *>(p);
         *out = plan.release();
@@ -391,6 +388,7 @@ vbm_status vbm_decode_step(vbm_decode_plan * plan, const float * x, const float 
                            float * weights, void * const * events, void * stream) {
     return guarded([&] {
         require(plan != nullptr && x && logits && out, "null buffer");
+        require(reinterpret_cast<uintptr_t>(x) % 16 == 0, "decode input must be 16-byte aligned");
         const hipStream_t s = as_stream(stream);
         const int64_t K = plan->K, H = plan->H, E = plan->E;
         for (int64_t l = 0; l < plan->L; ++l) {
@@ -411,27 +409,23 @@ vbm_status vbm_decode_step(vbm_decode_plan * plan, const float * x, const float 
             a.act_layout = plan->act_layout;
             a.route_ids = plan->route_ids + l * K;
             a.route_w = plan->route_w + l * K;
-            a.group = plan->group;
             a.activation = d.activation;
             a.alpha = 1.702f;
             a.limit = 7.0f;
             record(ev, 0, s);
             launch_decode_gate_up(a, s);
             record(ev, 1, s);
-            GemvArgs b{};
+            DecodeDownParams b{};
             b.bank = d.down;
             b.expert_to_slot = d.expert_to_slot;
-            b.xrows = plan->act_rows;
-            b.n_ids = K;
-            b.b_ne1 = K;
-            b.group = plan->group;
-            b.max_active = K;
-            b.max_per_expert = 1;
+            b.act_rows = plan->act_rows;
+            b.act_layout = plan->act_layout;
+            b.route_ids = plan->route_ids + l * K;
+            b.top_k = K;
             b.bias = d.down_bias;
-            b.dst = plan->y;
-            b.epilogue = 0;
+            b.y = plan->y;
             record(ev, 2, s);
-            launch_gemv(b, s);
+            launch_decode_down(b, s);
             record(ev, 3, s);
         }
         launch_combine(plan->y, plan->route_w + (plan->L - 1) * K, H, K, 1, out, s);
