@@ -278,6 +278,11 @@ vbm_status vbm_decode_plan_destroy(vbm_decode_plan * plan);
 vbm_status vbm_decode_step(vbm_decode_plan * plan, const float * x, const float * logits,
                            float * out, int32_t * ids, float * weights, void * const * events,
                            void * stream);
+/* One kernel of one layer of the step (which = 0: kernel A, 1: kernel B) on the plan's current
+ * state, for timing and profiling a kernel in isolation; both are idempotent, so repeated
+ * launches stream the same bytes. */
+vbm_status vbm_decode_kernel(vbm_decode_plan * plan, int64_t layer, int which, const float * x,
+                             const float * logits, void * stream);
 
 /* ----------------------------------------------------------------------------------------------
  * HIP graph capture of stream-ordered work (per-token layer chains replay without host launch

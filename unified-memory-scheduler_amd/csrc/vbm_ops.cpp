@@ -384,53 +384,83 @@ vbm_status vbm_decode_plan_destroy(vbm_decode_plan * plan) {
     });
 }
 
+}  // extern "C"
+
+namespace {
+
+void decode_launch_a(const vbm_decode_plan * plan, int64_t l, const float * x, const float * logits, hipStream_t s) {
+    const vbm_moe_layer_desc & d = plan->layers[l];
+    const int64_t K = plan->K;
+    DecodeGateUpArgs a{};
+    a.bank = d.gate_up;
+    a.expert_to_slot = d.expert_to_slot;
+    a.logits = logits + l * plan->E;
+    a.n_expert = plan->E;
+    a.top_k = K;
+    a.hidden = plan->H;
+    a.x_in = l == 0 ? x : nullptr;
+    a.prev_y = plan->y;
+    a.prev_w = l == 0 ? nullptr : plan->route_w + (l - 1) * K;
+    a.bias = d.gate_up_bias;
+    a.act_rows = plan->act_rows;
+    a.act_layout = plan->act_layout;
+    a.route_ids = plan->route_ids + l * K;
+    a.route_w = plan->route_w + l * K;
+    a.activation = d.activation;
+    a.alpha = 1.702f;
+    a.limit = 7.0f;
+    launch_decode_gate_up(a, s);
+}
+
+void decode_launch_b(const vbm_decode_plan * plan, int64_t l, hipStream_t s) {
+    const vbm_moe_layer_desc & d = plan->layers[l];
+    DecodeDownParams b{};
+    b.bank = d.down;
+    b.expert_to_slot = d.expert_to_slot;
+    b.act_rows = plan->act_rows;
+    b.act_layout = plan->act_layout;
+    b.route_ids = plan->route_ids + l * plan->K;
+    b.top_k = plan->K;
+    b.bias = d.down_bias;
+    b.y = plan->y;
+    launch_decode_down(b, s);
+}
+
+}  // namespace
+
+extern "C" {
+
 vbm_status vbm_decode_step(vbm_decode_plan * plan, const float * x, const float * logits, float * out, int32_t * ids,
                            float * weights, void * const * events, void * stream) {
     return guarded([&] {
         require(plan != nullptr && x && logits && out, "null buffer");
         require(reinterpret_cast<uintptr_t>(x) % 16 == 0, "decode input must be 16-byte aligned");
         const hipStream_t s = as_stream(stream);
-        const int64_t K = plan->K, H = plan->H, E = plan->E;
+        const int64_t K = plan->K, H = plan->H;
         for (int64_t l = 0; l < plan->L; ++l) {
-            const vbm_moe_layer_desc & d = plan->layers[l];
             void * const * ev = events ? events + 4 * l : nullptr;
-            DecodeGateUpArgs a{};
-            a.bank = d.gate_up;
-            a.expert_to_slot = d.expert_to_slot;
-            a.logits = logits + l * E;
-            a.n_expert = E;
-            a.top_k = K;
-            a.hidden = H;
-            a.x_in = l == 0 ? x : nullptr;
-            a.prev_y = plan->y;
-            a.prev_w = l == 0 ? nullptr : plan->route_w + (l - 1) * K;
-            a.bias = d.gate_up_bias;
-            a.act_rows = plan->act_rows;
-            a.act_layout = plan->act_layout;
-            a.route_ids = plan->route_ids + l * K;
-            a.route_w = plan->route_w + l * K;
-            a.activation = d.activation;
-            a.alpha = 1.702f;
-            a.limit = 7.0f;
             record(ev, 0, s);
-            launch_decode_gate_up(a, s);
+            decode_launch_a(plan, l, x, logits, s);
             record(ev, 1, s);
-            DecodeDownParams b{};
-            b.bank = d.down;
-            b.expert_to_slot = d.expert_to_slot;
-            b.act_rows = plan->act_rows;
-            b.act_layout = plan->act_layout;
-            b.route_ids = plan->route_ids + l * K;
-            b.top_k = K;
-            b.bias = d.down_bias;
-            b.y = plan->y;
             record(ev, 2, s);
-            launch_decode_down(b, s);
+            decode_launch_b(plan, l, s);
             record(ev, 3, s);
         }
         launch_combine(plan->y, plan->route_w + (plan->L - 1) * K, H, K, 1, out, s);
         if (ids) check_hip(hipMemcpyAsync(ids, plan->route_ids, sizeof(int32_t) * plan->L * K, hipMemcpyDeviceToDevice, s), "ids copy");
         if (weights) check_hip(hipMemcpyAsync(weights, plan->route_w, sizeof(float) * plan->L * K, hipMemcpyDeviceToDevice, s), "weights copy");
+    });
+}
+
+vbm_status vbm_decode_kernel(vbm_decode_plan * plan, int64_t layer, int which, const float * x, const float * logits,
+                             void * stream) {
+    return guarded([&] {
+        require(plan != nullptr && x && logits, "null buffer");
+        require(layer >= 0 && layer < plan->L && (which == 0 || which == 1), "layer or kernel out of range");
+        require(reinterpret_cast<uintptr_t>(x) % 16 == 0, "decode input must be 16-byte aligned");
+        const hipStream_t s = as_stream(stream);
+        if (which == 0) decode_launch_a(plan, layer, x, logits, s);
+        else decode_launch_b(plan, layer, s);
     });
 }
 

@@ -83,6 +83,7 @@ SIGNATURES = {
     "vbm_decode_plan_create": [C.POINTER(MoeLayerDesc), i64, C.POINTER(vp)],
     "vbm_decode_plan_destroy": [vp],
     "vbm_decode_step": [vp, vp, vp, vp, vp, vp, vp, vp],
+    "vbm_decode_kernel": [vp, i64, C.c_int, vp, vp, vp],
 }
 OTHER = {"vbm_last_error": ([], C.c_char_p), "vbm_abi_version": ([], C.c_int)}
 
