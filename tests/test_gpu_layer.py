@@ -15,10 +15,11 @@ class Layer:
     """Seeded synthetic layer: tensors are pure functions of (seed, layer, tensor id)."""
 
     def __init__(self, vb, type_id, hidden, inter, experts, top_k, seed, layer=0, router=True, biases=True,
-                 activation=1, q8_scale=(1e-3, 1e-2)):
+                 activation=1, q8_scale=(1e-3, 1e-2), order=None):
         self.vb, self.type_id = vb, type_id
         self.H, self.I, self.E, self.K = hidden, inter, experts, top_k
         self.activation = activation
+        self.order = vb.ORDER_EXACT if order is None else order
         base = 16 * layer
         self.gu = H.synth_weights(type_id, seed, base + 1, experts, 2 * inter, hidden, q8_scale)
         self.dn = H.synth_weights(type_id, seed, base + 2, experts, hidden, inter, q8_scale)
@@ -35,7 +36,7 @@ class Layer:
         vb = self.vb
         return vb.MoeLayerDesc(self.gu_bank.handle, self.dn_bank.handle, vb.ptr(self.d_gu_b), vb.ptr(self.d_dn_b),
                                None, vb.ptr(self.d_rw), None, self.H, self.I, self.E, self.K, self.activation,
-                               vb.ORDER_EXACT)
+                               self.order)
 
     def forward_gpu(self, x, logits=None):
         vb = self.vb

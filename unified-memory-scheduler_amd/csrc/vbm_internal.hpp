@@ -143,6 +143,41 @@ struct GemvArgs {
 };
 void launch_gemv(const GemvArgs & a, hipStream_t stream);
 
+// Activation row of the MFMA grouped GEMM: row-major codes (f16 for MXFP4 weights, int8 for
+// Q8_0), fp16-rounded fp32 block scales, and the row's -128 flag; 256-byte aligned stride.
+struct GemmRowLayout {
+    int64_t nb;
+    int weight_type;
+    VBM_HD int64_t code_bytes() const { return nb * 32 * (weight_type == 39 ? 2 : 1); }
+    VBM_HD int64_t da_offset() const { return code_bytes(); }
+    VBM_HD int64_t flag_offset() const { return da_offset() + 4 * nb; }
+    VBM_HD int64_t stride() const { return (flag_offset() + 4 + 255) / 256 * 256; }
+};
+void launch_gemm_rows_from_f32(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, const GemmRowLayout & lay,
+                               uint8_t * rows, hipStream_t stream);
+void launch_gemm_rows_from_q8(const uint8_t * q8, int64_t n_rows, int64_t row_bytes, const GemmRowLayout & lay,
+                              uint8_t * rows, hipStream_t stream);
+
+// Grouped expert GEMM on MFMA (exact block dots, fp32 accumulation across blocks).
+struct GemmParams {
+    const vbm_bank * bank;
+    const int32_t * expert_to_slot;
+    const uint8_t * rows_in;          // activation rows, row index = job / n_ids (b_ne1 == 1) or job
+    GemmRowLayout lay;
+    int64_t n_ids, b_ne1, n_as, n_entries;
+    GroupBuffers group;
+    void * tiles;                     // gemm_tiles_bytes(n_as, n_entries) of scratch
+    const float * bias;
+    float * dst;                      // epilogue 0: [job][rows]
+    uint8_t * rows_out;               // epilogue 1: GLU + Q8_0 rows per job (out_layout)
+    GemmRowLayout out_layout;
+    int epilogue, activation;
+    float alpha, limit;
+};
+int64_t gemm_max_tiles(int64_t n_as, int64_t n_entries);
+size_t gemm_tiles_bytes(int64_t n_as, int64_t n_entries);
+void launch_grouped_gemm(const GemmParams & p, hipStream_t stream);
+
 // Kernel A of the fused single-token decode: routing, input combine + Q8_0, gate_up GEMV, GLU,
 // requantization into the down activation rows.
 struct DecodeGateUpArgs {

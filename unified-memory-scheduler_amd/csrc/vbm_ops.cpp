@@ -51,6 +51,14 @@ void validate_ids_on_host(const int32_t * ids, int64_t n_ids, int64_t n_tokens, 
         }
 }
 
+// Layers of at least this many tokens use the MFMA grouped GEMM when the caller asks for the fast
+// accumulation order; below it the exact GEMV path is used (its results satisfy either order).
+constexpr int64_t kGemmMinTokens = 16;
+
+bool use_gemm(const vbm_moe_layer_desc & d, int64_t n_tokens) {
+    return d.order == VBM_ORDER_FAST && n_tokens >= kGemmMinTokens;
+}
+
 struct LayerWorkspace {
     int32_t * ids;
     float * weights;
@@ -58,6 +66,7 @@ struct LayerWorkspace {
     uint8_t * xrows_x;     // [T] activation rows of the layer input (gate_up format)
     void * group;
     uint8_t * xrows_act;   // [T*K] requantized GLU outputs (down format)
+    void * tiles;          // GEMM tile lists (fast order only)
     float * y;
     size_t total;
 };
@@ -70,11 +79,16 @@ LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint
     w.ids = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * entries));
     w.weights = reinterpret_cast<float *>(take(sizeof(float) * entries));
     w.logits = reinterpret_cast<float *>(take(sizeof(float) * max_tokens * d.n_expert));
-    const XrowLayout lx{d.hidden / 32, d.gate_up ? d.gate_up->type : VBM_TYPE_MXFP4};
-    const XrowLayout la{d.intermediate / 32, d.down ? d.down->type : VBM_TYPE_MXFP4};
-    w.xrows_x = take(static_cast<size_t>(max_tokens * lx.stride()));
+    const int type = d.gate_up ? d.gate_up->type : VBM_TYPE_MXFP4;
+    const XrowLayout lx{d.hidden / 32, type};
+    const XrowLayout la{d.intermediate / 32, type};
+    const GemmRowLayout gx{d.hidden / 32, type};
+    const GemmRowLayout ga{d.intermediate / 32, type};
+    const bool gemm = use_gemm(d, max_tokens);
+    w.xrows_x = take(static_cast<size_t>(max_tokens * (gemm ? gx.stride() : lx.stride())));
     w.group = take(group_workspace_bytes(d.n_expert, entries));
-    w.xrows_act = take(static_cast<size_t>(entries * la.stride()));
+    w.xrows_act = take(static_cast<size_t>(entries * (gemm ? ga.stride() : la.stride())));
+    w.tiles = gemm ? take(gemm_tiles_bytes(d.n_expert, entries)) : nullptr;
     w.y = reinterpret_cast<float *>(take(sizeof(float) * entries * d.hidden));
     w.total = off;
     return w;
@@ -119,9 +133,49 @@ void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits
     float * w_d = weights ? weights : w.weights;
     float * logits_d = logits ? logits : w.logits;
     launch_router(d->router_w, d->router_b, x, H, logits_d, d->n_expert, n_tokens, K, ids_d, w_d, s);
+    const GroupBuffers g = carve_group(w.group, d->n_expert, entries);
+    if (use_gemm(*d, n_tokens)) {
+        // Prefill-sized groups: MFMA grouped GEMM (exact block dots, fp32 accumulation order).
+        const GemmRowLayout gx{H / 32, d->gate_up->type}, ga{I / 32, d->down->type};
+        launch_gemm_rows_from_f32(x, n_tokens, H, H, gx, w.xrows_x, s);
+        launch_group(ids_d, K, n_tokens, K, d->n_expert, g, s);
+        GemmParams p{};
+        p.expert_to_slot = d->expert_to_slot;
+        p.n_ids = K;
+        p.n_as = d->n_expert;
+        p.n_entries = entries;
+        p.group = g;
+        p.tiles = w.tiles;
+        p.activation = d->activation;
+        p.alpha = 1.702f;
+        p.limit = 7.0f;
+        p.bank = d->gate_up;
+        p.rows_in = w.xrows_x;
+        p.lay = gx;
+        p.b_ne1 = 1;
+        p.bias = d->gate_up_bias;
+        p.rows_out = w.xrows_act;
+        p.out_layout = ga;
+        p.epilogue = 1;
+        record(events, 0, s);
+        launch_grouped_gemm(p, s);
+        record(events, 1, s);
+        p.bank = d->down;
+        p.rows_in = w.xrows_act;
+        p.lay = ga;
+        p.b_ne1 = K;
+        p.bias = d->down_bias;
+        p.dst = w.y;
+        p.rows_out = nullptr;
+        p.epilogue = 0;
+        record(events, 2, s);
+        launch_grouped_gemm(p, s);
+        record(events, 3, s);
+        launch_combine(w.y, w_d, H, K, n_tokens, out, s);
+        return;
+    }
     const XrowLayout lx{H / 32, d->gate_up->type}, la{I / 32, d->down->type};
     launch_quantize_expand(x, n_tokens, H, H, lx, w.xrows_x, nullptr, s);
-    const GroupBuffers g = carve_group(w.group, d->n_expert, entries);
     launch_group(ids_d, K, n_tokens, K, d->n_expert, g, s);
 
     GemvArgs a{};
@@ -203,6 +257,38 @@ vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot,
         if (expert_to_slot_host) validate_ids_on_host(ids, n_ids, n_tokens, ids_stride, n_as, expert_to_slot_host, s);
         const int64_t entries = n_ids * n_tokens;
         const int64_t n_b = b_ne1 * n_tokens;
+        if (order == VBM_ORDER_FAST && n_tokens >= kGemmMinTokens) {
+            const GemmRowLayout gl{bank->nb, bank->type};
+            const size_t q_bytes = align_up(static_cast<size_t>(n_b * gl.stride()));
+            const size_t g_bytes = align_up(group_workspace_bytes(n_as, entries));
+            void * scratch = nullptr;
+            check_hip(hipMallocAsync(&scratch, q_bytes + g_bytes + gemm_tiles_bytes(n_as, entries), s), "mul_mat_id scratch");
+            uint8_t * q = static_cast<uint8_t *>(scratch);
+            const GroupBuffers g = carve_group(q + q_bytes, n_as, entries);
+            if (b_type == VBM_TYPE_F32)
+                launch_gemm_rows_from_f32(static_cast<const float *>(b), n_b, bank->k, bank->k, gl, q, s);
+            else
+                launch_gemm_rows_from_q8(static_cast<const uint8_t *>(b), n_b, bank->nb * 34, gl, q, s);
+            launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
+            zero_floats(dst, entries * bank->rows, s);
+            GemmParams p{};
+            p.bank = bank;
+            p.expert_to_slot = expert_to_slot;
+            p.rows_in = q;
+            p.lay = gl;
+            p.n_ids = n_ids;
+            p.b_ne1 = b_ne1;
+            p.n_as = n_as;
+            p.n_entries = entries;
+            p.group = g;
+            p.tiles = q + q_bytes + g_bytes;
+            p.bias = bias;
+            p.dst = dst;
+            p.epilogue = 0;
+            launch_grouped_gemm(p, s);
+            check_hip(hipFreeAsync(scratch, s), "mul_mat_id scratch free");
+            return;
+        }
         const XrowLayout lay{bank->nb, bank->type};
         const size_t q_bytes = static_cast<size_t>(n_b * lay.stride());
         const size_t g_bytes = group_workspace_bytes(n_as, entries);
