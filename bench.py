@@ -131,6 +131,74 @@ def cpu_baseline(args, logits_host: np.ndarray) -> dict:
                       f"(ISA level {oracle_py.load().orc_fast_isa()})"}
 
 
+INT8_MFMA_PEAK_TOPS = 5000.0
+
+
+def prefill_measure(args) -> dict:
+    """Q8_0 MoE prefill through the MFMA grouped GEMM: hidden 2048, 128 experts, top-8,
+    intermediate 768, separate gate/up/down (fused gate|up bank), SiLU, no biases, 2048 tokens of
+    N(0,1) activations and N(0,1) router logits; one layer forward in the fast accumulation order
+    (exact integer block dots). Timed with events around the layer and around both GEMMs."""
+    Hp, Ip, Ep, Kp, Tp = 2048, 768, 128, 8, 2048
+    gu = vb.Bank(vb.TYPE_Q8_0, 2 * Ip, Hp, Ep, True)
+    dn = vb.Bank(vb.TYPE_Q8_0, Hp, Ip, Ep, False)
+    gu.generate(0, Ep, SEED, 901, 0, 1e-3, 1e-2)
+    dn.generate(0, Ep, SEED, 902, 0, 1e-3, 1e-2)
+    desc = vb.MoeLayerDesc(gu.handle, dn.handle, None, None, None, None, None, Hp, Ip, Ep, Kp, vb.ACT_SILU,
+                           vb.ORDER_FAST)
+    x = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 903, 0, Tp * Hp))
+    logits = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 904, 0, Tp * Ep))
+    out = vb.DeviceBuffer(4 * Tp * Hp)
+    ws = C.c_size_t()
+    vb.call("vbm_moe_layer_workspace", C.byref(desc), Tp, C.byref(ws))
+    work = vb.DeviceBuffer(ws.value)
+    stream = C.c_void_p()
+    vb.call("vbm_stream_create", C.byref(stream))
+    stream = stream.value
+    ev = []
+    for _ in range(6):
+        e = C.c_void_p()
+        vb.call("vbm_event_create", C.byref(e))
+        ev.append(e.value)
+    kern = (C.c_void_p * 4)(*ev[2:6])
+    reps = args.prefill_reps
+    totals = np.zeros(3)
+    for i in range(2 + reps):
+        vb.call("vbm_event_record", ev[0], stream)
+        vb.call("vbm_moe_layer_forward_profiled", C.byref(desc), x.ptr, logits.ptr, Tp, out.ptr, None, None, work.ptr,
+                ws.value, C.cast(kern, C.c_void_p), stream)
+        vb.call("vbm_event_record", ev[1], stream)
+        vb.call("vbm_stream_synchronize", stream)
+        if i >= 2:
+            t = [C.c_float() for _ in range(3)]
+            vb.call("vbm_event_elapsed_ms", ev[0], ev[1], C.byref(t[0]))
+            vb.call("vbm_event_elapsed_ms", ev[2], ev[3], C.byref(t[1]))
+            vb.call("vbm_event_elapsed_ms", ev[4], ev[5], C.byref(t[2]))
+            totals += [v.value for v in t]
+    layer_ms, gu_ms, dn_ms = totals / reps
+    ops_gu = 2.0 * Tp * Kp * (2 * Ip) * Hp
+    ops_dn = 2.0 * Tp * Kp * Hp * Ip
+    gu_tops = ops_gu / (gu_ms * 1e-3) / 1e12
+    dn_tops = ops_dn / (dn_ms * 1e-3) / 1e12
+    weight_bytes = Ep * (gu.slot_bytes + dn.slot_bytes)
+    gu.destroy()
+    dn.destroy()
+    log(f"prefill (Q8_0, 2048 tokens, 128 experts top-8): layer {layer_ms:.3f} ms -> {Tp / (layer_ms * 1e-3):.0f} tok/s; "
+        f"gate_up GEMM {gu_ms * 1e3:.1f} us ({gu_tops:.1f} TOPS), down GEMM {dn_ms * 1e3:.1f} us ({dn_tops:.1f} TOPS)")
+    return {
+        "workload": "Q8_0 MoE prefill layer: 2048 tokens, hidden 2048, 128 experts, top-8, intermediate 768, SiLU",
+        "value": round(Tp / (layer_ms * 1e-3), 1), "unit": "tok/s", "layer_ms": round(layer_ms, 4),
+        "order": "fast (exact int8 block dots, fp32 accumulation across blocks)",
+        "gate_up_gemm": {"us": round(gu_ms * 1e3, 2), "int8_tops": round(gu_tops, 2),
+                         "frac_of_mfma_peak": round(gu_tops / INT8_MFMA_PEAK_TOPS, 4)},
+        "down_gemm": {"us": round(dn_ms * 1e3, 2), "int8_tops": round(dn_tops, 2),
+                      "frac_of_mfma_peak": round(dn_tops / INT8_MFMA_PEAK_TOPS, 4)},
+        "mfma_peak_tops": INT8_MFMA_PEAK_TOPS,
+        "expert_weight_bytes": weight_bytes,
+        "weight_stream_gbs": round(weight_bytes / ((gu_ms + dn_ms) * 1e-3) / 1e9, 1),
+    }
+
+
 def read_traffic(path: Path):
     """Measured HBM bytes per gate_up launch from the committed rocprofv3 PMC summary, if any."""
     if not path.exists():
@@ -157,6 +225,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-layers", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the Q8_0 prefill GEMM measurement")
+    ap.add_argument("--prefill-reps", type=int, default=5)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="after the run, launch a plain device copy of BYTES three times (a known-traffic "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -273,6 +343,8 @@ def main() -> int:
         f"{gu_gbs:.0f} GB/s; kernel B (down GEMV): {dn_avg_us:.2f} us -> {dn_gbs:.0f} GB/s")
     traffic = read_traffic(REPO / "profiles" / "decode_gate_up_120b_bs1_pmc.md")
 
+    prefill = None if args.no_prefill else prefill_measure(args)
+
     cpu = None
     if not args.no_cpu and T == 1:
         cpu = cpu_baseline(args, logits_host[:, :, 0, :])
@@ -314,6 +386,7 @@ def main() -> int:
                             "bytes_per_launch": round(dn_bytes)},
         },
         "cpu_baseline": cpu,
+        "prefill": prefill,
     }
     print(json.dumps(result), flush=True)
     if args.copy_probe > 0:
