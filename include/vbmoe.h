@@ -285,6 +285,53 @@ vbm_status vbm_decode_kernel(vbm_decode_plan * plan, int64_t layer, int which, c
                              const float * logits, void * stream);
 
 /* ----------------------------------------------------------------------------------------------
+ * Causal expert admission over one shared pool of n_slots expert slots serving n_layers routed
+ * layers (host-side control state; no device calls). Restates llama_moe_cache::admit
+ * (third_party/patches/llama-b11669-hybrid-experts.patch:3087-3242), write_dispatch (:3059-3084)
+ * and the admission helpers (:3543-3574). Slots [0, n_used) are the reserved per-rank zero slots
+ * of misses; anchors follow them (vbm_admission_set_anchors). Keys are layer * n_expert + expert.
+ * -------------------------------------------------------------------------------------------- */
+#define VBM_ADMIT_CLASSIC 0  /* recent-frequency margin, lowest-recent victim (the default)   */
+#define VBM_ADMIT_LRU 1      /* free slot or least recently seen; the reference uses margin 1   */
+#define VBM_ADMIT_RANKED 2   /* classic with seed-priority / recency tie-breaks                 */
+
+typedef struct vbm_admission vbm_admission;
+
+vbm_status vbm_admission_create(int64_t n_layers, int64_t n_expert, int64_t n_used, int64_t n_slots,
+                                int64_t recent_window, int32_t margin, int policy,
+                                vbm_admission ** out);
+vbm_status vbm_admission_destroy(vbm_admission * a);
+/* Frozen-plan seed (llama-b11669-hybrid-experts.patch:2659-2680): the next free slot from n_used
+ * upward; earlier seeds get the higher seed priority. Only before the first dispatch. */
+vbm_status vbm_admission_seed(vbm_admission * a, int64_t layer, int64_t expert, int32_t * slot);
+/* Reserve `anchors` protected slots after the zero slots (admission floor = n_used + anchors). */
+vbm_status vbm_admission_set_anchors(vbm_admission * a, int32_t anchors);
+/* One single-token dispatch of `layer`: selected[n_used] expert ids in rank order. hits[n_used]
+ * (optional) receives residency before admission; the admissions made are returned in order as
+ * (admitted_slots[i], admitted_experts[i], evicted_keys[i] or -1), i < *n_admitted <= n_used. */
+vbm_status vbm_admission_admit(vbm_admission * a, int64_t layer, const int32_t * selected,
+                               int32_t * hits, int32_t * admitted_slots, int32_t * admitted_experts,
+                               int32_t * evicted_keys, int64_t * n_admitted);
+/* Dispatch packing for n_tokens tokens: ids / weights [n_tokens][n_used] -> out
+ * [n_tokens][4][n_used] = (-1 or cpu expert id, slot or rank, 0 or weight, 0 or 1 miss mask);
+ * cold_rank >= 0 sends token 0's rank to the transient scratch slot n_slots. */
+vbm_status vbm_admission_write_dispatch(const vbm_admission * a, int64_t layer, const int32_t * ids,
+                                        const float * weights, int64_t n_tokens, int32_t cold_rank,
+                                        float * out);
+vbm_status vbm_admission_slot_map(const vbm_admission * a, int64_t layer, int32_t * map);
+/* stats[4] = dispatch calls, hits before admission, admissions, evictions. */
+vbm_status vbm_admission_stats(const vbm_admission * a, uint64_t * stats);
+/* llama_moe_colder_admission / probation_margin / anchor_slots / cold_gpu_budget /
+ * gpu_slot_limit; -1 where the reference asserts. */
+int vbm_moe_colder_admission(int candidate_frequency, int candidate_seed_priority,
+                             uint64_t candidate_last_seen, int current_frequency,
+                             int current_seed_priority, uint64_t current_last_seen);
+int vbm_moe_probation_margin(int observed_lifetime, uint64_t future_hits);
+int vbm_moe_anchor_slots(int capacity, int reserved, int seeds);
+int vbm_moe_cold_gpu_budget(int cold_experts);
+int32_t vbm_moe_gpu_slot_limit(int32_t resident_slots, int cold_gpu);
+
+/* ----------------------------------------------------------------------------------------------
  * HIP graph capture of stream-ordered work (per-token layer chains replay without host launch
  * overhead). Only entry points that do not allocate (the layer forward with a caller workspace,
  * the router, combine, quantize and device copies) may be captured.

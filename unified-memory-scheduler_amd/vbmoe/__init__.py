@@ -84,8 +84,25 @@ SIGNATURES = {
     "vbm_decode_plan_destroy": [vp],
     "vbm_decode_step": [vp, vp, vp, vp, vp, vp, vp, vp],
     "vbm_decode_kernel": [vp, i64, C.c_int, vp, vp, vp],
+    "vbm_admission_create": [i64, i64, i64, i64, i64, C.c_int32, C.c_int, C.POINTER(vp)],
+    "vbm_admission_destroy": [vp],
+    "vbm_admission_seed": [vp, i64, i64, vp],
+    "vbm_admission_set_anchors": [vp, C.c_int32],
+    "vbm_admission_admit": [vp, i64, vp, vp, vp, vp, vp, C.POINTER(i64)],
+    "vbm_admission_write_dispatch": [vp, i64, vp, vp, i64, C.c_int32, vp],
+    "vbm_admission_slot_map": [vp, i64, vp],
+    "vbm_admission_stats": [vp, vp],
 }
-OTHER = {"vbm_last_error": ([], C.c_char_p), "vbm_abi_version": ([], C.c_int)}
+OTHER = {
+    "vbm_last_error": ([], C.c_char_p),
+    "vbm_abi_version": ([], C.c_int),
+    "vbm_moe_colder_admission": ([C.c_int, C.c_int, u64, C.c_int, C.c_int, u64], C.c_int),
+    "vbm_moe_probation_margin": ([C.c_int, u64], C.c_int),
+    "vbm_moe_anchor_slots": ([C.c_int, C.c_int, C.c_int], C.c_int),
+    "vbm_moe_cold_gpu_budget": ([C.c_int], C.c_int),
+    "vbm_moe_gpu_slot_limit": ([C.c_int32, C.c_int], C.c_int32),
+}
+ADMIT_CLASSIC, ADMIT_LRU, ADMIT_RANKED = 0, 1, 2
 
 _lib = None
 
