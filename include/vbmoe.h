@@ -332,6 +332,55 @@ int vbm_moe_cold_gpu_budget(int cold_experts);
 int32_t vbm_moe_gpu_slot_limit(int32_t resident_slots, int cold_gpu);
 
 /* ----------------------------------------------------------------------------------------------
+ * Single-GPU host-RAM expert tier for single-token decode (the cold-expert path of the reference's
+ * llama_moe_cache: admission, staged uploads and publish-after-event,
+ * llama-b11669-hybrid-experts.patch:2727-3298). Every expert of every layer is kept in pinned
+ * host memory in the device bank layout; n_slots device slots shared by all layers hold the
+ * resident set under causal admission; the first top_k of them (the admission's reserved zero
+ * slots) stage the current layer's remaining misses. Misses are computed on the GPU after their
+ * copy (no CPU expert path). A step synchronizes once per layer (the routing must reach the host
+ * before the admission), so it cannot be captured in a graph.
+ * -------------------------------------------------------------------------------------------- */
+typedef struct {
+    int type;                            /* VBM_TYPE_MXFP4 or VBM_TYPE_Q8_0 */
+    int64_t hidden, intermediate, n_layers, n_expert, top_k;
+    int activation;
+    int64_t n_slots;                     /* device pool in expert groups (> top_k) */
+    int64_t recent_window;               /* admission history, in dispatches per layer (8..256) */
+    int32_t margin;
+    int policy;                          /* VBM_ADMIT_* */
+    const float * const * gate_up_bias;  /* host array of n_layers device pointers, or NULL */
+    const float * const * down_bias;     /* host array of n_layers device pointers, or NULL */
+} vbm_tier_desc;
+
+typedef struct {
+    uint64_t dispatches, hits, admissions, evictions, staged, uploaded_bytes;
+    double copy_ms;                      /* copy-stream busy time (events around each layer's copies) */
+} vbm_tier_stats;
+
+typedef struct vbm_tier vbm_tier;
+
+vbm_status vbm_tier_create(const vbm_tier_desc * desc, vbm_tier ** tier);
+vbm_status vbm_tier_destroy(vbm_tier * tier);
+/* Pinned host bytes the tier holds (all experts of all layers). */
+vbm_status vbm_tier_host_bytes(const vbm_tier * tier, size_t * bytes);
+/* Store one expert from ggml bytes (gate|up rows then down rows of block_mxfp4 / block_q8_0). */
+vbm_status vbm_tier_set_expert(vbm_tier * tier, int64_t layer, int64_t expert, const void * gate_up_ggml,
+                               const void * down_ggml, void * stream);
+/* Store every expert from the seeded generator of vbm_bank_generate: layer l's gate|up experts
+ * use stream id layer_stride * l + gate_up_stream, its down experts layer_stride * l + down_stream.
+ * Both stores must precede seeding and stepping. */
+vbm_status vbm_tier_generate(vbm_tier * tier, uint64_t seed, uint64_t layer_stride, uint64_t gate_up_stream,
+                             uint64_t down_stream, float p0, float p1, void * stream);
+/* Frozen-plan seed: admit (layer, expert) into the next slot and copy it there. */
+vbm_status vbm_tier_seed(vbm_tier * tier, int64_t layer, int64_t expert);
+/* x [hidden] (16-byte aligned) -> out [hidden]; logits [n_layers][n_expert]; ids optional
+ * [n_layers][top_k]. Bit-identical to vbm_decode_step on resident banks holding the same experts. */
+vbm_status vbm_tier_step(vbm_tier * tier, const float * x, const float * logits, float * out, int32_t * ids,
+                         void * stream);
+vbm_status vbm_tier_get_stats(const vbm_tier * tier, vbm_tier_stats * stats);
+
+/* ----------------------------------------------------------------------------------------------
  * HIP graph capture of stream-ordered work (per-token layer chains replay without host launch
  * overhead). Only entry points that do not allocate (the layer forward with a caller workspace,
  * the router, combine, quantize and device copies) may be captured.

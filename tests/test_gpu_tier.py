@@ -1,0 +1,109 @@
+"""Host-RAM expert tier (vbm_tier_*) on the GPU: every token's output must be bit-identical to the
+fully resident decode plan holding the same experts, routing identical, and the tier's admission
+counters equal to the Python restatement fed with the same routes."""
+import ctypes as C
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[1] / "oracle"))
+import admission as ref  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+SEED = 515
+
+
+def routed_logits(rng, L, E, K, tokens):
+    """Logits whose top-K per layer follows a Zipf-like trace with reuse (as in the tier config)."""
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    p /= p.sum()
+    perms = [rng.permutation(E) for _ in range(L)]
+    prev = [None] * L
+    out = np.empty((tokens, L, E), np.float32)
+    chosen = []
+    for t in range(tokens):
+        row = []
+        for l in range(L):
+            sel = prev[l] if prev[l] is not None and rng.random() < 0.6 else \
+                [int(perms[l][i]) for i in rng.choice(E, K, replace=False, p=p)]
+            prev[l] = sel
+            lg = rng.standard_normal(E).astype(np.float32)
+            for r, e in enumerate(sel):
+                lg[e] = 10.0 - r
+            out[t, l] = lg
+            row.append(sel)
+        chosen.append(row)
+    return out, chosen
+
+
+@pytest.mark.parametrize("type_id,policy,margin", [(39, 0, 4), (39, 1, 1), (8, 2, 2)])
+def test_tier_matches_resident_plan(gpu, type_id, policy, margin):
+    vb = gpu
+    L, E, K, H, I, slots = 3, 16, 4, 256, 256, 4 + 9
+    act = vb.ACT_SWIGLU_OAI if type_id == 39 else vb.ACT_SILU
+    p0, p1 = (-8, -3) if type_id == 39 else (1e-4, 5e-4)
+    biases = []
+    for l in range(L):
+        gb = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 16 * l + 3, 0, E * 2 * I, 0.0, 0.02))
+        db = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 16 * l + 4, 0, E * H, 0.0, 0.02))
+        biases.append((gb, db))
+    # resident reference: per-layer banks holding every expert
+    banks, descs = [], []
+    for l in range(L):
+        gu = vb.Bank(type_id, 2 * I, H, E, True)
+        dn = vb.Bank(type_id, H, I, E, False)
+        gu.generate(0, E, SEED, 16 * l + 1, 0, p0, p1)
+        dn.generate(0, E, SEED, 16 * l + 2, 0, p0, p1)
+        banks.append((gu, dn))
+        descs.append(vb.MoeLayerDesc(gu.handle, dn.handle, biases[l][0].ptr, biases[l][1].ptr, None, None, None, H, I,
+                                     E, K, act, vb.ORDER_EXACT))
+    plan = C.c_void_p()
+    vb.call("vbm_decode_plan_create", (vb.MoeLayerDesc * L)(*descs), L, C.byref(plan))
+    # tier over the same experts
+    gub = (C.c_void_p * L)(*[b[0].ptr for b in biases])
+    dnb = (C.c_void_p * L)(*[b[1].ptr for b in biases])
+    desc = vb.TierDesc(type_id, H, I, L, E, K, act, slots, 8, margin, policy,
+                       C.cast(gub, C.POINTER(C.c_void_p)), C.cast(dnb, C.POINTER(C.c_void_p)))
+    tier = C.c_void_p()
+    vb.call("vbm_tier_create", C.byref(desc), C.byref(tier))
+    vb.call("vbm_tier_generate", tier.value, SEED, 16, 1, 2, p0, p1, None)
+    py = ref.Admission(L, E, K, slots, 8, margin, policy)
+    for l, e in ((0, 3), (2, 5)):
+        vb.call("vbm_tier_seed", tier.value, l, e)
+        py.seed(l, e)
+    rng = np.random.default_rng(type_id + policy)
+    tokens = 30
+    logits, chosen = routed_logits(rng, L, E, K, tokens)
+    x = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 6, 0, H))
+    dl = vb.DeviceBuffer(logits[0].nbytes)
+    o1, o2 = vb.DeviceBuffer(4 * H), vb.DeviceBuffer(4 * H)
+    i1, i2 = vb.DeviceBuffer(4 * L * K), vb.DeviceBuffer(4 * L * K)
+    staged = 0
+    for t in range(tokens):
+        dl.upload(logits[t])
+        vb.call("vbm_decode_step", plan.value, x.ptr, dl.ptr, o1.ptr, i1.ptr, None, None, None)
+        vb.call("vbm_tier_step", tier.value, x.ptr, dl.ptr, o2.ptr, i2.ptr, None)
+        vb.call("vbm_stream_synchronize", None)
+        a, b = o1.download(np.float32, H), o2.download(np.float32, H)
+        ia, ib = i1.download(np.int32, (L, K)), i2.download(np.int32, (L, K))
+        assert np.array_equal(ia, ib) and ia.tolist() == chosen[t], t
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), t
+        for l in range(L):
+            hits, made = py.admit(l, chosen[t][l])
+            admitted = {e for _, e, _ in made}
+            staged += sum(1 for r, e in enumerate(chosen[t][l]) if not hits[r] and e not in admitted)
+    st = vb.TierStats()
+    vb.call("vbm_tier_get_stats", tier.value, C.byref(st))
+    print(f"[tier type={type_id} policy={policy}] hits={st.hits}/{tokens * L * K} admissions={st.admissions} "
+          f"evictions={st.evictions} staged={st.staged} uploaded={st.uploaded_bytes}", flush=True)
+    assert (st.dispatches, st.hits, st.admissions, st.evictions) == (tokens * L, py.hits, py.admissions, py.evictions)
+    assert st.staged == staged and st.admissions > 0
+    assert st.staged > 0 or policy == ref.LRU          # lru with margin 1 admits every miss
+    vb.call("vbm_tier_destroy", tier.value)
+    vb.call("vbm_decode_plan_destroy", plan.value)
+    for gu, dn in banks:
+        gu.destroy()
+        dn.destroy()

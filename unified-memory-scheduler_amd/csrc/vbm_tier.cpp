@@ -1,0 +1,303 @@
+// Single-GPU host-RAM expert tier for single-token decode.
+//
+// Every expert of every layer lives in pinned host memory, already in the device bank layout, so
+// staging one is a plain hipMemcpyAsync of its two slots (gate|up and down). A shared pool of
+// n_slots device slots (one gate|up bank and one down bank serving all layers, like the reference's
+// per-device slot group) holds the resident set under causal admission (vbm_admission_*); its
+// first top_k slots, the admission's reserved zero slots, stage the current layer's remaining
+// misses. Per layer:
+//   1. the router kernel selects the layer's experts; their ids come back to the host (the
+//      reference's dispatch op reads them on the host too, llama-b11669-hybrid-experts.patch:
+//      3244-3298);
+//   2. admission runs (llama-b11669-hybrid-experts.patch:3087-3242); admitted experts are copied
+//      into their victim slots and the remaining misses into the staging slots, on a side stream;
+//   3. the layer's expert->slot map is published and the decode kernels run only after the copy
+//      stream's event (publish after event, llama-b11669-hybrid-experts.patch:2953-3005).
+// Because step 1 waits for the layer's routing, every kernel that could read an overwritten slot
+// has already finished, so eviction never races a reader.
+#include "vbm_internal.hpp"
+
+#include <algorithm>
+#include <memory>
+#include <vector>
+
+using namespace vbm;
+
+struct vbm_tier {
+    vbm_tier_desc desc{};
+    int device = 0;
+    vbm_bank * gate_up = nullptr;     // n_slots slots; the first top_k stage misses
+    vbm_bank * down = nullptr;
+    vbm_admission * admission = nullptr;
+    uint8_t * host_store = nullptr;   // pinned: [layer][expert] (gate_up slot bytes, down slot bytes)
+    size_t gu_bytes = 0, dn_bytes = 0;
+    hipStream_t copy_stream = nullptr;
+    hipEvent_t copy_begin = nullptr, copy_end = nullptr;
+    int32_t * host_ids = nullptr;     // pinned [top_k]
+    int32_t * host_map = nullptr;     // pinned [n_expert]
+    int32_t * dev_map = nullptr;      // [n_expert]
+    uint8_t * workspace = nullptr;
+    int32_t * route_ids = nullptr;    // [L][K]
+    float * route_w = nullptr;        // [L][K]
+    uint8_t * act_rows = nullptr;
+    XrowLayout act_layout{};
+    float * y = nullptr;
+    std::vector<const float *> gu_bias, dn_bias;
+    vbm_tier_stats stats{};
+    bool started = false;             // seeded or stepped: the pool's slots are live
+
+    ~vbm_tier() {
+        (void)hipSetDevice(device);
+        (void)hipDeviceSynchronize();
+        if (admission) vbm_admission_destroy(admission);
+        if (gate_up) vbm_bank_destroy(gate_up);
+        if (down) vbm_bank_destroy(down);
+        if (host_store) (void)hipHostFree(host_store);
+        if (host_ids) (void)hipHostFree(host_ids);
+        if (host_map) (void)hipHostFree(host_map);
+        if (dev_map) (void)hipFree(dev_map);
+        if (workspace) (void)hipFree(workspace);
+        if (copy_begin) (void)hipEventDestroy(copy_begin);
+        if (copy_end) (void)hipEventDestroy(copy_end);
+        if (copy_stream) (void)hipStreamDestroy(copy_stream);
+    }
+
+    uint8_t * host_expert(int64_t layer, int64_t expert) const {
+        return host_store + (static_cast<size_t>(layer) * desc.n_expert + expert) * (gu_bytes + dn_bytes);
+    }
+};
+
+namespace {
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+void check_status(vbm_status st, const char * what) {
+    if (st != VBM_OK) fail(st, std::string(what) + ": " + vbm_last_error());
+}
+
+// Copies the host copy of (layer, expert) into device slot `slot` of both banks (copy stream).
+void stage(vbm_tier & t, int64_t layer, int64_t expert, int64_t slot) {
+    const uint8_t * src = t.host_expert(layer, expert);
+    check_hip(hipMemcpyAsync(t.gate_up->base + static_cast<size_t>(slot) * t.gu_bytes, src, t.gu_bytes,
+                             hipMemcpyHostToDevice, t.copy_stream), "tier gate_up stage");
+    check_hip(hipMemcpyAsync(t.down->base + static_cast<size_t>(slot) * t.dn_bytes, src + t.gu_bytes, t.dn_bytes,
+                             hipMemcpyHostToDevice, t.copy_stream), "tier down stage");
+    t.stats.uploaded_bytes += t.gu_bytes + t.dn_bytes;
+}
+
+}  // namespace
+
+extern "C" {
+
+vbm_status vbm_tier_create(const vbm_tier_desc * d, vbm_tier ** out) {
+    return guarded([&] {
+        require(d != nullptr && out != nullptr, "null argument");
+        *out = nullptr;
+        require(d->type == VBM_TYPE_MXFP4 || d->type == VBM_TYPE_Q8_0, "tier type must be MXFP4 or Q8_0");
+        require(d->hidden > 0 && d->hidden % 64 == 0 && d->hidden <= 4096 && d->intermediate > 0 &&
+                    d->intermediate % 64 == 0 && d->intermediate <= 4096, "tier shape out of range");
+        require(d->n_layers > 0 && d->n_expert > 0 && d->n_expert <= 1024 && d->top_k > 0 && d->top_k <= 64 &&
+                    d->top_k <= d->n_expert, "tier routing shape out of range");
+        require(d->activation == VBM_ACT_SILU || d->activation == VBM_ACT_SWIGLU_OAI, "unknown activation");
+        auto t = std::make_unique<vbm_tier>();
+        t->desc = *d;
+        check_hip(hipGetDevice(&t->device), "hipGetDevice");
+        const int64_t L = d->n_layers, E = d->n_expert, K = d->top_k, H = d->hidden, I = d->intermediate;
+        check_status(vbm_admission_create(L, E, K, d->n_slots, d->recent_window, d->margin, d->policy, &t->admission),
+                     "tier admission");
+        // device pool: slots [0, n_slots) resident (the first top_k are the admission's reserved
+        // zero slots, used here as the staging slots of the current layer's misses)
+        check_status(vbm_bank_create(d->type, 2 * I, H, d->n_slots, 1, &t->gate_up), "tier gate_up bank");
+        check_status(vbm_bank_create(d->type, H, I, d->n_slots, 0, &t->down), "tier down bank");
+        t->gu_bytes = t->gate_up->slot_bytes;
+        t->dn_bytes = t->down->slot_bytes;
+        const size_t store = static_cast<size_t>(L * E) * (t->gu_bytes + t->dn_bytes);
+        check_hip(hipHostMalloc(reinterpret_cast<void **>(&t->host_store), store, hipHostMallocDefault),
+                  "tier pinned host store");
+        check_hip(hipHostMalloc(reinterpret_cast<void **>(&t->host_ids), sizeof(int32_t) * K, hipHostMallocDefault),
+                  "tier pinned ids");
+        check_hip(hipHostMalloc(reinterpret_cast<void **>(&t->host_map), sizeof(int32_t) * E, hipHostMallocDefault),
+                  "tier pinned map");
+        check_hip(hipMalloc(reinterpret_cast<void **>(&t->dev_map), sizeof(int32_t) * E), "tier map");
+        check_hip(hipStreamCreateWithFlags(&t->copy_stream, hipStreamNonBlocking), "tier copy stream");
+        check_hip(hipEventCreate(&t->copy_begin), "tier event");
+        check_hip(hipEventCreate(&t->copy_end), "tier event");
+        t->act_layout = XrowLayout{I / 32, d->type};
+        const size_t route = align_up(sizeof(int32_t) * L * K), wts = align_up(sizeof(float) * L * K);
+        const size_t act = align_up(static_cast<size_t>(K * t->act_layout.stride()));
+        const size_t y = align_up(sizeof(float) * K * H);
+        check_hip(hipMalloc(reinterpret_cast<void **>(&t->workspace), route + wts + act + y), "tier workspace");
+        uint8_t * p = t->workspace;
+        t->route_ids = reinterpret_cast<int32_t *>(p); p += route;
+        t->route_w = reinterpret_cast<float *>(p); p += wts;
+        t->act_rows = p; p += act;
+        t->y = reinterpret_cast<float *>(p);
+        t->gu_bias.assign(static_cast<size_t>(L), nullptr);
+        t->dn_bias.assign(static_cast<size_t>(L), nullptr);
+        for (int64_t l = 0; l < L; ++l) {
+            if (d->gate_up_bias) t->gu_bias[l] = d->gate_up_bias[l];
+            if (d->down_bias) t->dn_bias[l] = d->down_bias[l];
+        }
+        *out = t.release();
+    });
+}
+
+vbm_status vbm_tier_destroy(vbm_tier * t) {
+    return guarded([&] { delete t; });
+}
+
+vbm_status vbm_tier_host_bytes(const vbm_tier * t, size_t * bytes) {
+    return guarded([&] {
+        require(t != nullptr && bytes != nullptr, "null argument");
+        *bytes = static_cast<size_t>(t->desc.n_layers * t->desc.n_expert) * (t->gu_bytes + t->dn_bytes);
+    });
+}
+
+vbm_status vbm_tier_set_expert(vbm_tier * t, int64_t layer, int64_t expert, const void * gate_up_ggml,
+                               const void * down_ggml, void * stream) {
+    return guarded([&] {
+        require(t != nullptr && gate_up_ggml != nullptr && down_ggml != nullptr, "null argument");
+        require(layer >= 0 && layer < t->desc.n_layers && expert >= 0 && expert < t->desc.n_expert,
+                "expert out of range");
+        require(!t->started, "experts must be stored before the tier is seeded or stepped");
+        const hipStream_t s = as_stream(stream);
+        // repack through staging slot 0 (a reserved slot) and keep the device layout bytes
+        check_status(vbm_bank_upload(t->gate_up, 0, gate_up_ggml, 0, stream), "tier gate_up repack");
+        check_status(vbm_bank_upload(t->down, 0, down_ggml, 0, stream), "tier down repack");
+        uint8_t * dst = t->host_expert(layer, expert);
+        check_hip(hipMemcpyAsync(dst, t->gate_up->base, t->gu_bytes, hipMemcpyDeviceToHost, s), "tier store");
+        check_hip(hipMemcpyAsync(dst + t->gu_bytes, t->down->base, t->dn_bytes, hipMemcpyDeviceToHost, s), "tier store");
+        check_hip(hipStreamSynchronize(s), "tier store synchronize");
+    });
+}
+
+vbm_status vbm_tier_generate(vbm_tier * t, uint64_t seed, uint64_t layer_stride, uint64_t gate_up_stream,
+                             uint64_t down_stream, float p0, float p1, void * stream) {
+    return guarded([&] {
+        require(t != nullptr, "null tier");
+        require(!t->started, "experts must be stored before the tier is seeded or stepped");
+        const hipStream_t s = as_stream(stream);
+        const int64_t E = t->desc.n_expert;
+        const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(t->gate_up->n_slots, E));
+        for (int64_t l = 0; l < t->desc.n_layers; ++l)
+            for (int64_t e0 = 0; e0 < E; e0 += chunk) {
+                const int64_t n = std::min(chunk, E - e0);
+                check_status(vbm_bank_generate(t->gate_up, 0, n, seed, layer_stride * l + gate_up_stream, e0, p0, p1, stream),
+                             "tier generate");
+                check_status(vbm_bank_generate(t->down, 0, n, seed, layer_stride * l + down_stream, e0, p0, p1, stream),
+                             "tier generate");
+                for (int64_t i = 0; i < n; ++i) {
+                    uint8_t * dst = t->host_expert(l, e0 + i);
+                    check_hip(hipMemcpyAsync(dst, t->gate_up->base + i * t->gu_bytes, t->gu_bytes, hipMemcpyDeviceToHost, s),
+                              "tier store");
+                    check_hip(hipMemcpyAsync(dst + t->gu_bytes, t->down->base + i * t->dn_bytes, t->dn_bytes,
+                                             hipMemcpyDeviceToHost, s), "tier store");
+                }
+                check_hip(hipStreamSynchronize(s), "tier generate synchronize");
+            }
+    });
+}
+
+vbm_status vbm_tier_seed(vbm_tier * t, int64_t layer, int64_t expert) {
+    return guarded([&] {
+        require(t != nullptr, "null tier");
+        int32_t slot = -1;
+        check_status(vbm_admission_seed(t->admission, layer, expert, &slot), "tier seed");
+        t->started = true;
+        stage(*t, layer, expert, slot);
+        check_hip(hipStreamSynchronize(t->copy_stream), "tier seed synchronize");
+    });
+}
+
+vbm_status vbm_tier_step(vbm_tier * t, const float * x, const float * logits, float * out, int32_t * ids, void * stream) {
+    return guarded([&] {
+        require(t != nullptr && x && logits && out, "null buffer");
+        require(reinterpret_cast<uintptr_t>(x) % 16 == 0, "decode input must be 16-byte aligned");
+        const hipStream_t s = as_stream(stream);
+        const vbm_tier_desc & d = t->desc;
+        const int64_t L = d.n_layers, E = d.n_expert, K = d.top_k, H = d.hidden;
+        t->started = true;
+        std::vector<int32_t> hits(static_cast<size_t>(K)), slots(static_cast<size_t>(K)),
+            experts(static_cast<size_t>(K)), evicted(static_cast<size_t>(K));
+        for (int64_t l = 0; l < L; ++l) {
+            // 1. routing of this layer, back to the host
+            launch_router(nullptr, nullptr, nullptr, H, const_cast<float *>(logits + l * E), E, 1, K,
+                          t->route_ids + l * K, t->route_w + l * K, s);
+            check_hip(hipMemcpyAsync(t->host_ids, t->route_ids + l * K, sizeof(int32_t) * K, hipMemcpyDeviceToHost, s),
+                      "tier ids");
+            check_hip(hipStreamSynchronize(s), "tier ids synchronize");
+            // 2. admission, then copies of admitted experts and staged misses
+            int64_t n_admitted = 0;
+            check_status(vbm_admission_admit(t->admission, l, t->host_ids, hits.data(), slots.data(), experts.data(),
+                                             evicted.data(), &n_admitted), "tier admission");
+            ++t->stats.dispatches;
+            check_hip(hipEventRecord(t->copy_begin, t->copy_stream), "tier copy event");
+            const uint64_t before = t->stats.uploaded_bytes;
+            for (int64_t i = 0; i < n_admitted; ++i) stage(*t, l, experts[i], slots[i]);
+            check_status(vbm_admission_slot_map(t->admission, l, t->host_map), "tier slot map");
+            for (int64_t r = 0; r < K; ++r) {
+                t->stats.hits += hits[r];
+                const int32_t e = t->host_ids[r];
+                if (t->host_map[e] < 0) {         // miss without admission: reserved slot r
+                    stage(*t, l, e, r);
+                    t->host_map[e] = static_cast<int32_t>(r);
+                    ++t->stats.staged;
+                }
+            }
+            t->stats.admissions += static_cast<uint64_t>(n_admitted);
+            for (int64_t i = 0; i < n_admitted; ++i) t->stats.evictions += evicted[i] >= 0;
+            check_hip(hipMemcpyAsync(t->dev_map, t->host_map, sizeof(int32_t) * E, hipMemcpyHostToDevice, t->copy_stream),
+                      "tier map upload");
+            check_hip(hipEventRecord(t->copy_end, t->copy_stream), "tier copy event");
+            // 3. publish after the copies: the layer's kernels wait for the copy stream
+            check_hip(hipStreamWaitEvent(s, t->copy_end, 0), "tier publish");
+            DecodeGateUpArgs a{};
+            a.bank = t->gate_up;
+            a.expert_to_slot = t->dev_map;
+            a.logits = logits + l * E;
+            a.n_expert = E;
+            a.top_k = K;
+            a.hidden = H;
+            a.x_in = l == 0 ? x : nullptr;
+            a.prev_y = t->y;
+            a.prev_w = l == 0 ? nullptr : t->route_w + (l - 1) * K;
+            a.bias = t->gu_bias[l];
+            a.act_rows = t->act_rows;
+            a.act_layout = t->act_layout;
+            a.route_ids = t->route_ids + l * K;
+            a.route_w = t->route_w + l * K;
+            a.activation = d.activation;
+            a.alpha = 1.702f;
+            a.limit = 7.0f;
+            launch_decode_gate_up(a, s);
+            DecodeDownParams b{};
+            b.bank = t->down;
+            b.expert_to_slot = t->dev_map;
+            b.act_rows = t->act_rows;
+            b.act_layout = t->act_layout;
+            b.route_ids = t->route_ids + l * K;
+            b.top_k = K;
+            b.bias = t->dn_bias[l];
+            b.y = t->y;
+            launch_decode_down(b, s);
+            if (t->stats.uploaded_bytes != before) {
+                check_hip(hipEventSynchronize(t->copy_end), "tier copy timing");
+                float ms = 0.0f;
+                check_hip(hipEventElapsedTime(&ms, t->copy_begin, t->copy_end), "tier copy timing");
+                t->stats.copy_ms += ms;
+            }
+        }
+        launch_combine(t->y, t->route_w + (L - 1) * K, H, K, 1, out, s);
+        if (ids) check_hip(hipMemcpyAsync(ids, t->route_ids, sizeof(int32_t) * L * K, hipMemcpyDeviceToDevice, s), "ids copy");
+    });
+}
+
+vbm_status vbm_tier_get_stats(const vbm_tier * t, vbm_tier_stats * stats) {
+    return guarded([&] {
+        require(t != nullptr && stats != nullptr, "null argument");
+        *stats = t->stats;
+    });
+}
+
+}  // extern "C"

@@ -23,6 +23,21 @@ STATUS = {0: "OK", 1: "INVALID_ARGUMENT", 2: "RUNTIME", 3: "UNSUPPORTED", 4: "OU
 vp, sz, i64, u64, i32p, f32p = C.c_void_p, C.c_size_t, C.c_int64, C.c_uint64, C.c_void_p, C.c_void_p
 
 
+class TierDesc(C.Structure):
+    _fields_ = [
+        ("type", C.c_int), ("hidden", i64), ("intermediate", i64), ("n_layers", i64), ("n_expert", i64),
+        ("top_k", i64), ("activation", C.c_int), ("n_slots", i64), ("recent_window", i64), ("margin", C.c_int32),
+        ("policy", C.c_int), ("gate_up_bias", C.POINTER(vp)), ("down_bias", C.POINTER(vp)),
+    ]
+
+
+class TierStats(C.Structure):
+    _fields_ = [
+        ("dispatches", u64), ("hits", u64), ("admissions", u64), ("evictions", u64), ("staged", u64),
+        ("uploaded_bytes", u64), ("copy_ms", C.c_double),
+    ]
+
+
 class MoeLayerDesc(C.Structure):
     _fields_ = [
         ("gate_up", vp), ("down", vp), ("gate_up_bias", vp), ("down_bias", vp), ("expert_to_slot", vp),
@@ -92,6 +107,14 @@ SIGNATURES = {
     "vbm_admission_write_dispatch": [vp, i64, vp, vp, i64, C.c_int32, vp],
     "vbm_admission_slot_map": [vp, i64, vp],
     "vbm_admission_stats": [vp, vp],
+    "vbm_tier_create": [C.POINTER(TierDesc), C.POINTER(vp)],
+    "vbm_tier_destroy": [vp],
+    "vbm_tier_host_bytes": [vp, C.POINTER(sz)],
+    "vbm_tier_set_expert": [vp, i64, i64, vp, vp, vp],
+    "vbm_tier_generate": [vp, u64, u64, u64, u64, C.c_float, C.c_float, vp],
+    "vbm_tier_seed": [vp, i64, i64],
+    "vbm_tier_step": [vp, vp, vp, vp, vp, vp],
+    "vbm_tier_get_stats": [vp, C.POINTER(TierStats)],
 }
 OTHER = {
     "vbm_last_error": ([], C.c_char_p),
