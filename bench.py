@@ -199,6 +199,79 @@ def prefill_measure(args) -> dict:
     }
 
 
+def tier_measure(args, stack) -> dict:
+    """Host-RAM tiered experts on one GPU: the same 36-layer 120B-shape stack with every expert in
+    pinned host memory, an HBM pool of 16 GiB of expert groups (1296 x 13,253,760 B) under causal
+    (classic) admission, misses staged with hipMemcpyAsync on a side stream. Trace: 512 decode
+    tokens; per layer a seeded permutation of the experts with Zipf(1.1) popularity, and with
+    probability 0.6 the previous token's set is reused."""
+    L, E, K, H, I = stack.L, stack.E, stack.K, stack.H, stack.I
+    group_bytes = stack.gate_up[0].slot_bytes + stack.down[0].slot_bytes
+    n_slots = (16 << 30) // group_bytes
+    gub = (C.c_void_p * L)(*[b.ptr for b in stack.gu_bias])
+    dnb = (C.c_void_p * L)(*[b.ptr for b in stack.dn_bias])
+    desc = vb.TierDesc(vb.TYPE_MXFP4, H, I, L, E, K, vb.ACT_SWIGLU_OAI, n_slots, 64, 4, vb.ADMIT_CLASSIC,
+                       C.cast(gub, C.POINTER(C.c_void_p)), C.cast(dnb, C.POINTER(C.c_void_p)))
+    t0 = time.time()
+    tier = C.c_void_p()
+    vb.call("vbm_tier_create", C.byref(desc), C.byref(tier))
+    vb.call("vbm_tier_generate", tier.value, SEED, 16, 1, 2, -8.0, -3.0, None)
+    host = C.c_size_t()
+    vb.call("vbm_tier_host_bytes", tier.value, C.byref(host))
+    log(f"tier: {host.value / 1e9:.1f} GB of experts in pinned host memory, {n_slots} device slots "
+        f"({n_slots * group_bytes / 2**30:.1f} GiB), ready in {time.time() - t0:.1f} s")
+    rng = np.random.default_rng(SEED)
+    tokens = args.tier_tokens
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    p /= p.sum()
+    perms = [rng.permutation(E) for _ in range(L)]
+    prev = [None] * L
+    logits = np.empty((tokens, L, E), np.float32)
+    for t in range(tokens):
+        for l in range(L):
+            sel = prev[l] if prev[l] is not None and rng.random() < 0.6 else \
+                [int(perms[l][i]) for i in rng.choice(E, K, replace=False, p=p)]
+            prev[l] = sel
+            lg = rng.standard_normal(E).astype(np.float32)
+            lg[sel] = 10.0 - np.arange(K, dtype=np.float32)
+            logits[t, l] = lg
+    dl = vb.DeviceBuffer.from_array(logits)
+    out = vb.DeviceBuffer(4 * H)
+    step = 4 * L * E
+    stream = C.c_void_p()
+    vb.call("vbm_stream_create", C.byref(stream))
+    stream = stream.value
+    ev0, ev1 = C.c_void_p(), C.c_void_p()
+    vb.call("vbm_event_create", C.byref(ev0))
+    vb.call("vbm_event_create", C.byref(ev1))
+    wall = time.perf_counter()
+    vb.call("vbm_event_record", ev0.value, stream)
+    for t in range(tokens):
+        vb.call("vbm_tier_step", tier.value, stack.x0.ptr, dl.ptr + t * step, out.ptr, None, stream)
+    vb.call("vbm_event_record", ev1.value, stream)
+    vb.call("vbm_stream_synchronize", stream)
+    wall = time.perf_counter() - wall
+    ms = C.c_float()
+    vb.call("vbm_event_elapsed_ms", ev0.value, ev1.value, C.byref(ms))
+    st = vb.TierStats()
+    vb.call("vbm_tier_get_stats", tier.value, C.byref(st))
+    vb.call("vbm_tier_destroy", tier.value)
+    lookups = tokens * L * K
+    h2d = st.uploaded_bytes / (st.copy_ms * 1e-3) / 1e9 if st.copy_ms > 0 else None
+    res = {
+        "workload": f"120B-shape MXFP4 stack, {n_slots} x {group_bytes} B HBM expert slots (16 GiB), rest in pinned "
+                    f"host RAM; {tokens} decode tokens, Zipf(1.1) routing with 0.6 reuse; classic causal admission",
+        "value": round(tokens / (ms.value * 1e-3), 2), "unit": "tok/s", "host_wall_s": round(wall, 2),
+        "hit_rate": round(st.hits / lookups, 4), "lookups": lookups, "admissions": int(st.admissions),
+        "evictions": int(st.evictions), "staged_misses": int(st.staged),
+        "uploaded_gb": round(st.uploaded_bytes / 1e9, 2), "h2d_gbs": round(h2d, 1) if h2d else None,
+        "copy_busy_ms": round(st.copy_ms, 1),
+    }
+    log(f"tier: {res['value']} tok/s, hit rate {res['hit_rate']}, {res['uploaded_gb']} GB uploaded at "
+        f"{res['h2d_gbs']} GB/s copy-busy")
+    return res
+
+
 def read_traffic(path: Path):
     """Measured HBM bytes per gate_up launch from the committed rocprofv3 PMC summary, if any."""
     if not path.exists():
@@ -227,6 +300,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the Q8_0 prefill GEMM measurement")
     ap.add_argument("--prefill-reps", type=int, default=5)
+    ap.add_argument("--no-tier", action="store_true",
+                    help="skip the host-RAM tier workload (it pins 61 GB of host memory)")
+    ap.add_argument("--tier-tokens", type=int, default=512)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="after the run, launch a plain device copy of BYTES three times (a known-traffic "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -344,6 +420,7 @@ def main() -> int:
     traffic = read_traffic(REPO / "profiles" / "decode_gate_up_120b_bs1_pmc.md")
 
     prefill = None if args.no_prefill else prefill_measure(args)
+    tier = None if args.no_tier else tier_measure(args, stack)
 
     cpu = None
     if not args.no_cpu and T == 1:
@@ -387,6 +464,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "tier": tier,
     }
     print(json.dumps(result), flush=True)
     if args.copy_probe > 0:
