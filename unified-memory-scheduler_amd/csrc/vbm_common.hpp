@@ -49,6 +49,9 @@ VBM_HD void synth_mxfp4_block(uint64_t key, uint64_t j, int exp_lo, int exp_hi, 
 
 // ---------------------------------------------------------------- fp16 (IEEE binary16)
 VBM_HD float half_bits_to_float(uint16_t h) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));   // v_cvt_f32_f16, exact
+#else
     const uint32_t sign = static_cast<uint32_t>(h & 0x8000u) << 16;
     uint32_t exponent = (h >> 10) & 0x1Fu, mantissa = h & 0x3FFu, bits;
     if (exponent == 0x1F) {
@@ -65,6 +68,7 @@ VBM_HD float half_bits_to_float(uint16_t h) {
     float f;
     __builtin_memcpy(&f, &bits, 4);
     return f;
+#endif
 }
 
 // Round-to-nearest-even float -> binary16 (the F16C _cvtss_sh(x, 0) result).

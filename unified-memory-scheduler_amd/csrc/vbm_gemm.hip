@@ -20,6 +20,8 @@
 //
 // A workgroup (4 waves) computes 64 bank rows (a tile pair) x 64 jobs of one expert; wave w owns
 // bank tile 2p + (w & 1) and jobs 32(w >> 1)..+31 as a 2x2 grid of 16x16 fragments.
+#include <type_traits>
+
 #include "vbm_device.hpp"
 #include "vbm_internal.hpp"
 
@@ -62,6 +64,7 @@ struct GemmArgs {
     const int32_t * n_tiles;
     const float * bias;        // [n_expert][rows] in ggml row order, or null
     float * dst;               // epilogue 0: [job][rows]
+    int row_pairs;             // 64-row tile pairs of the bank
     uint8_t * rows_out;        // epilogue 1: GLU output rows for the down projection (out_lay)
     GemmRowLayout out_lay;
     int activation;
@@ -78,53 +81,83 @@ __device__ __forceinline__ half2_g fp4x2(unsigned dw, int sel) {
     }
 }
 
-// Weight operand of block b (index within its group, compile-time) from the two slice entries
-// of the group: MXFP4 bytes 2b, 2b+1 of each 16-byte entry hold the slice's 4 nibbles.
-template <int B>
-__device__ __forceinline__ half8_t mx_a_operand(const u32x4g & s0, const u32x4g & s1) {
-    const unsigned w0 = s0[B / 2], w1 = s1[B / 2];
-    constexpr int sel = (B & 1) * 2;
-    const half2_g p0 = fp4x2(w0, sel), p1 = fp4x2(w0, sel + 1), p2 = fp4x2(w1, sel), p3 = fp4x2(w1, sel + 1);
+// Weight operand of one block from the dwords w0, w1 of slices 2q, 2q+1 that hold it: MXFP4
+// bytes 2b, 2b+1 of a 16-byte slice entry carry the slice's 4 nibbles of block b, so block b is
+// half (b & 1) of dword b / 2.
+__device__ __forceinline__ half8_t mx_a_operand(unsigned w0, unsigned w1, int odd) {
+    half2_g p0, p1, p2, p3;
+    if (odd) {
+        p0 = fp4x2(w0, 2), p1 = fp4x2(w0, 3), p2 = fp4x2(w1, 2), p3 = fp4x2(w1, 3);
+    } else {
+        p0 = fp4x2(w0, 0), p1 = fp4x2(w0, 1), p2 = fp4x2(w1, 0), p3 = fp4x2(w1, 1);
+    }
     return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
 // Exact VPSIGNB correction of one fragment column: contract minus true product is 256 * w for
-// every element whose activation code is -128 and whose weight is negative. Computed with the
-// same MFMA on (min(w, 0), [a == -128]) operands; only for flagged rows.
+// every element whose activation code is -128 and whose weight is negative. Computed by a second
+// f16 MFMA on (min(w, 0), 256 [a == -128]) operands accumulating into the block dot (all partial
+// sums stay integers below 2^24); only for waves holding flagged rows. Q8_0 takes the same route
+// with its int8 codes widened to f16.
 __device__ __forceinline__ half8_t neg_part(half8_t w) {
     half8_t r;
 #pragma unroll
     for (int i = 0; i < 8; ++i) r[i] = w[i] < static_cast<_Float16>(0.0f) ? w[i] : static_cast<_Float16>(0.0f);
     return r;
 }
-__device__ __forceinline__ half8_t is_neg128(half8_t a) {
+__device__ __forceinline__ half8_t is_neg128_x256(half8_t a) {
     half8_t r;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = a[i] == static_cast<_Float16>(-128.0f) ? static_cast<_Float16>(1.0f) : static_cast<_Float16>(0.0f);
-    return r;
-}
-__device__ __forceinline__ long neg_part_i8(long w) {
-    long r = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const signed char v = static_cast<signed char>(w >> (8 * i));
-        r |= static_cast<long>(static_cast<uint8_t>(v < 0 ? v : 0)) << (8 * i);
-    }
-    return r;
-}
-__device__ __forceinline__ long is_neg128_i8(long a) {
-    long r = 0;
-#pragma unroll
     for (int i = 0; i < 8; ++i)
-        r |= static_cast<long>(static_cast<signed char>(a >> (8 * i)) == -128 ? 1 : 0) << (8 * i);
+        r[i] = a[i] == static_cast<_Float16>(-128.0f) ? static_cast<_Float16>(256.0f) : static_cast<_Float16>(0.0f);
     return r;
 }
+__device__ __forceinline__ half8_t i8_to_f16(long v) {
+    half8_t r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = static_cast<_Float16>(static_cast<signed char>(v >> (8 * i)));
+    return r;
+}
+// Pipeline stages. Activations: chunks of CB blocks of the 64 jobs' codes (rows padded
+// by 16 bytes against bank conflicts) and their block scales. Weights: one bank group of both
+// tiles of the pair (8 slices x 32 rows x 16 bytes each) and its exponent / scale bytes. Both are
+// double-buffered in LDS; the next stage's global loads are in flight while the current one
+// computes, and one barrier per chunk separates them.
+template <int TYPE>
+struct GemmStage {
+    static constexpr int EB = TYPE == 39 ? 2 : 1;                       // bytes per activation code
+    static constexpr int GB = TYPE == 39 ? 8 : 4;                       // blocks per bank group
+    static constexpr int CB = 2;                                        // blocks per chunk
+    static constexpr int CPG = GB / CB;                                 // chunks per group
+    static constexpr int RB = CB * 32 * EB + 16;                        // LDS bytes per job row
+    static constexpr int ACT = kJobTile * RB;
+    static constexpr int DA = kJobTile * CB * 4;
+    static constexpr int W = 2 * 4096;
+    static constexpr int M = 2 * 256;
+    static constexpr int ACT_PIECES = kJobTile * CB * 32 * EB / 16 / kGemmThreads;   // per thread
+    static constexpr int W_PIECES = W / 16 / kGemmThreads;
+    static constexpr int OFF_DA = 2 * ACT, OFF_W = OFF_DA + 2 * DA, OFF_M = OFF_W + 2 * W;
+    static constexpr int BYTES = OFF_M + 2 * M;
+};
 
-template <int TYPE, int EPI>
+template <int TYPE, int EPI, bool FLAGGED>
 __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) {
-    __shared__ float tile_vals[kJobTile][64 + 1];   // epilogue 1: [job][bank row of the pair]
-    const int ti = blockIdx.y;
-    if (ti >= *cst<int32_t>(A.n_tiles)) return;
+    using G = GemmStage<TYPE>;
+    constexpr int EB = G::EB, RB = G::RB, CB = G::CB;
+    static_assert(G::BYTES >= kJobTile * 65 * 4, "epilogue tile must fit the stage buffers");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[G::BYTES];
+    float (*tile_vals)[65] = reinterpret_cast<float (*)[65]>(lds);    // epilogue 1, after the K loop
+
+    // XCD-aware order: workgroup i runs on XCD i % 8, so hand each XCD a contiguous range of
+    // (tile, pair) items; the pairs of one job tile then share its activation rows in one L2 and
+    // consecutive tiles of an expert share its weights.
+    const int n_items = *cst<int32_t>(A.n_tiles) * A.row_pairs;
+    const int per_xcd = (n_items + 7) >> 3;
+    const int slot8 = static_cast<int>(blockIdx.x >> 3);
+    const int item = static_cast<int>(blockIdx.x & 7) * per_xcd + slot8;
+    if (slot8 >= per_xcd || item >= n_items) return;
+    const int ti = item / A.row_pairs;
+    const int pair = item - ti * A.row_pairs;
     const int expert = cst<int32_t>(A.tile_expert)[ti];
     const int j0 = cst<int32_t>(A.tile_start)[ti];
     const int count = cst<int32_t>(A.counts)[expert];
@@ -135,31 +168,98 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int lr = lane & 15, q = lane >> 4;
-    const int pair = blockIdx.x;
     const int tile = pair * 2 + (wave & 1);
     const bool tile_live = tile * 32 < S.rows;
     const int nb = S.nb;
-    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
-    const int groups = nb / kGroupBlocks, tail = nb % kGroupBlocks;
+    const int groups = nb / G::GB, tail = nb % G::GB;
+    constexpr int kCodeRow = TYPE == 39 ? 16 : 32;     // code bytes per row and block
+    constexpr int kMetaRow = TYPE == 39 ? 1 : 2;       // exponent / scale bytes per row and block
     const uint8_t * slot_base = A.bank + static_cast<size_t>(slot) * S.slot_bytes;
-    const uint8_t * codes = slot_base + static_cast<size_t>(tile_live ? tile : 0) * 32 * nb * (TYPE == 39 ? 16 : 32);
-    const uint8_t * meta = slot_base + S.codes_bytes + static_cast<size_t>(tile_live ? tile : 0) * 32 * nb * (TYPE == 39 ? 1 : 2);
+    const uint8_t * codes = slot_base + static_cast<size_t>(tile_live ? tile : 0) * 32 * nb * kCodeRow;
+    const uint8_t * meta = slot_base + S.codes_bytes + static_cast<size_t>(tile_live ? tile : 0) * 32 * nb * kMetaRow;
+    auto row_of = [&](int jl) -> const uint8_t * {   // activation row of local job jl (must be live)
+        const int jb = A.jobs[joff + j0 + jl];
+        const int64_t row_index = A.b_ne1 == 1 ? jb / A.n_ids : jb;
+        return A.rows_in + row_index * A.lay.stride();
+    };
 
-    // The two job columns of this lane (fragment column lr of job halves 0 and 1).
-    const uint8_t * brow[2];
+    // This lane's fragment columns (jobs 32(w>>1) + 16jh + lr) and the -128 flags of the wave.
+    // Rows converted from caller-quantized Q8_0 data (FLAGGED) may hold -128 codes.
     bool jlive[2];
     int job[2];
     int flagged = 0;
 #pragma unroll
     for (int jh = 0; jh < 2; ++jh) {
-        const int jj = j0 + 32 * (wave >> 1) + 16 * jh + lr;
-        jlive[jh] = jj < count;
-        job[jh] = jlive[jh] ? A.jobs[joff + jj] : 0;
-        const int64_t row_index = A.b_ne1 == 1 ? job[jh] / A.n_ids : job[jh];
-        brow[jh] = A.rows_in + row_index * A.lay.stride();
-        if (jlive[jh]) flagged |= *reinterpret_cast<const int *>(brow[jh] + A.lay.flag_offset());
+        const int jl = 32 * (wave >> 1) + 16 * jh + lr;
+        jlive[jh] = j0 + jl < count;
+        job[jh] = jlive[jh] ? A.jobs[joff + j0 + jl] : 0;
+        if (FLAGGED && jlive[jh]) flagged |= *reinterpret_cast<const int *>(row_of(jl) + A.lay.flag_offset());
     }
-    const bool slow = __any(flagged != 0);   // wave-uniform: any flagged activation row in the wave
+    const bool slow = FLAGGED && __any(flagged != 0);   // wave-uniform
+
+    // Cooperative stage loaders. Activation piece i of this thread: job (t + 256i) / P, 16-byte
+    // part (t + 256i) % P, P = pieces per job row; block scale: job t / 4, block t % 4. Weight
+    // piece i: byte 16(t + 256i) of the pair's 8 KiB group; exponent / scale piece: threads
+    // 0..31, byte 16t of the pair's 512-byte group meta.
+    constexpr int P = CB * 32 * EB / 16;
+    const uint8_t * ld_row[G::ACT_PIECES];
+#pragma unroll
+    for (int i = 0; i < G::ACT_PIECES; ++i) {
+        const int jl = (threadIdx.x + i * kGemmThreads) / P;
+        ld_row[i] = j0 + jl < count ? row_of(jl) + ((threadIdx.x + i * kGemmThreads) % P) * 16 : nullptr;
+    }
+    const int sd_job = threadIdx.x / CB;
+    const float * sd_row = sd_job < kJobTile && j0 + sd_job < count
+                               ? reinterpret_cast<const float *>(row_of(sd_job) + A.lay.da_offset()) + threadIdx.x % CB
+                               : nullptr;
+    const uint8_t * w_src[G::W_PIECES];
+#pragma unroll
+    for (int i = 0; i < G::W_PIECES; ++i) {
+        const int byte = 16 * (threadIdx.x + i * kGemmThreads);
+        const int t = pair * 2 + byte / 4096;
+        w_src[i] = t * 32 < S.rows ? slot_base + static_cast<size_t>(t) * 32 * nb * kCodeRow + byte % 4096 : nullptr;
+    }
+    const uint8_t * m_src = nullptr;
+    if (threadIdx.x < 32) {
+        const int t = pair * 2 + static_cast<int>(threadIdx.x) / 16;
+        if (t * 32 < S.rows)
+            m_src = slot_base + S.codes_bytes + static_cast<size_t>(t) * 32 * nb * kMetaRow + (threadIdx.x % 16) * 16;
+    }
+
+    u32x4g st_act[G::ACT_PIECES];
+    float st_da = 0.0f;
+    u32x4g st_w[G::W_PIECES];
+    u32x4g st_m = u32x4g{0u, 0u, 0u, 0u};
+    auto load_act = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < G::ACT_PIECES; ++i) {
+            st_act[i] = u32x4g{0u, 0u, 0u, 0u};
+            if (ld_row[i]) st_act[i] = *reinterpret_cast<const u32x4g *>(ld_row[i] + static_cast<int64_t>(c) * CB * 32 * EB);
+        }
+        st_da = sd_row ? sd_row[c * CB] : 0.0f;
+    };
+    auto store_act = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < G::ACT_PIECES; ++i) {
+            const int piece = threadIdx.x + i * kGemmThreads;
+            *reinterpret_cast<u32x4g *>(lds + buf * G::ACT + (piece / P) * RB + (piece % P) * 16) = st_act[i];
+        }
+        if (threadIdx.x < kJobTile * CB) reinterpret_cast<float *>(lds + G::OFF_DA + buf * G::DA)[threadIdx.x] = st_da;
+    };
+    auto load_w = [&](int g) {
+#pragma unroll
+        for (int i = 0; i < G::W_PIECES; ++i) {
+            st_w[i] = u32x4g{0u, 0u, 0u, 0u};
+            if (w_src[i]) st_w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4g *>(w_src[i] + static_cast<size_t>(g) * 4096));
+        }
+        if (m_src) st_m = *reinterpret_cast<const u32x4g *>(m_src + static_cast<size_t>(g) * 256);
+    };
+    auto store_w = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < G::W_PIECES; ++i)
+            *reinterpret_cast<u32x4g *>(lds + G::OFF_W + buf * G::W + 16 * (threadIdx.x + i * kGemmThreads)) = st_w[i];
+        if (threadIdx.x < 32) *reinterpret_cast<u32x4g *>(lds + G::OFF_M + buf * G::M + 16 * threadIdx.x) = st_m;
+    };
 
     f32x4 acc[2][2];
 #pragma unroll
@@ -167,140 +267,197 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
 #pragma unroll
         for (int jh = 0; jh < 2; ++jh) acc[i][jh] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Output rows of this lane's fragments: in-tile rows 16i + 4q + j.
-    auto block_step = [&](int b, const auto & a_op, const u32x2g (&m)[2][4], int mb) {
-        // b: block index; a_op[i]: weight operand of row half i; m[i][j]: meta word pair of output
-        // row 16i + 4q + j; mb: position of block b inside the meta words.
+    // One block: weight operands a_op[i] (row halves i), activation operand and scale of job half
+    // jh from bsrc(jh) / dsrc(jh); mscale(i, j) is the weight exponent (MXFP4, signed) or fp16
+    // scale (Q8_0) of output row 16i + 4q + j. SLOW adds the exact -128 correction, accumulated
+    // into the same MFMA result (its operands scaled by 256 are exact in fp16).
+    auto block_step = [&](auto slow_c, const auto & a_op, auto && mscale, auto && bsrc, auto && dsrc) {
+        constexpr bool SLOW = decltype(slow_c)::value;
+        decltype(mscale(0, 0)) ms[2][4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ms[i][j] = mscale(i, j);
 #pragma unroll
         for (int jh = 0; jh < 2; ++jh) {
-            float da = 0.0f;
-            if constexpr (TYPE == 39) {
-                half8_t bv = half8_t{};
-                if (jlive[jh]) bv = *reinterpret_cast<const half8_t *>(brow[jh] + (static_cast<int64_t>(b) * 32 + 8 * q) * 2);
-                if (jlive[jh]) da = reinterpret_cast<const float *>(brow[jh] + A.lay.da_offset())[b];
+            const float da = dsrc(jh);
+            const auto bv = bsrc(jh);
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_op[i], bv, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                    if (slow) {
-                        const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(neg_part(a_op[i]), is_neg128(bv),
-                                                                               f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                        d = d + c * 256.0f;
-                    }
+            for (int i = 0; i < 2; ++i) {
+                f32x4 d;
+                if constexpr (TYPE == 39) {
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_op[i], bv, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    if constexpr (SLOW) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(neg_part(a_op[i]), is_neg128_x256(bv), d, 0, 0, 0);
+                } else if constexpr (!SLOW) {
+                    const i32x4 di = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_op[i], bv, i32x4{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const unsigned w = m[i][j][mb >> 2];
-                        const int e = static_cast<signed char>(w >> ((mb & 3) * 8));
-                        const float s = __builtin_amdgcn_ldexpf(da, e);
-                        acc[i][jh][j] = __builtin_fmaf(s, d[j], acc[i][jh][j]);
-                    }
+                    for (int j = 0; j < 4; ++j) d[j] = static_cast<float>(di[j]);
+                } else {
+                    const half8_t a16 = i8_to_f16(a_op[i]), b16 = i8_to_f16(bv);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a16, b16, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(neg_part(a16), is_neg128_x256(b16), d, 0, 0, 0);
                 }
-            } else {
-                long bv = 0;
-                if (jlive[jh]) bv = *reinterpret_cast<const long *>(brow[jh] + static_cast<int64_t>(b) * 32 + 8 * q);
-                if (jlive[jh]) da = reinterpret_cast<const float *>(brow[jh] + A.lay.da_offset())[b];
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_op[i], bv, i32x4{0, 0, 0, 0}, 0, 0, 0);
-                    if (slow) {
-                        const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(neg_part_i8(a_op[i]), is_neg128_i8(bv),
-                                                                              i32x4{0, 0, 0, 0}, 0, 0, 0);
-                        d = d + c * 256;
-                    }
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const unsigned w = m[i][j][mb >> 1];
-                        const float dw = half_bits_to_float(static_cast<uint16_t>(w >> ((mb & 1) * 16)));
-                        const float s = dw * da;
-                        acc[i][jh][j] = __builtin_fmaf(s, static_cast<float>(d[j]), acc[i][jh][j]);
-                    }
+                for (int j = 0; j < 4; ++j) {
+                    if constexpr (TYPE == 39)
+                        acc[i][jh][j] = __builtin_fmaf(__builtin_amdgcn_ldexpf(da, ms[i][j]), d[j], acc[i][jh][j]);
+                    else
+                        acc[i][jh][j] = __builtin_fmaf(ms[i][j] * da, d[j], acc[i][jh][j]);
                 }
             }
         }
     };
 
-    for (int g = 0; g < groups; ++g) {
-        // weight entries of slices 2q, 2q+1 for in-tile rows lr and 16 + lr
-        u32x4g s0[2], s1[2];
-        u32x2g m[2][4];
+    // The K loop, instantiated with and without the -128 correction (wave-uniform choice).
+    const int n_chunks = groups * G::CPG;
+    auto k_loop = [&](auto slow_c) {
+        const uint8_t * w_lds = lds + G::OFF_W + (wave & 1) * 4096 + (2 * q * 32 + lr) * 16;
+        const uint8_t * m_lds = lds + G::OFF_M + (wave & 1) * 256 + 4 * q * 8;
+        const uint8_t * b_lds = lds + (32 * (wave >> 1) + lr) * RB + 8 * q * EB;
+        const float * d_lds = reinterpret_cast<const float *>(lds + G::OFF_DA) + (32 * (wave >> 1) + lr) * CB;
+        for (int g = 0; g < groups; ++g) {
+            const int wb = g & 1;
+#pragma clang loop unroll(disable)
+            for (int sub = 0; sub < G::CPG; ++sub) {
+                const int c = g * G::CPG + sub;
+                const bool next_act = c + 1 < n_chunks, next_w = sub == 0 && g + 1 < groups;
+                if (next_act) load_act(c + 1);
+                if (next_w) load_w(g + 1);
+                const int ab = c & 1;
+                // This chunk's blocks 2sub, 2sub+1 in the group: weight dwords of slices 2q, 2q+1
+                // (MXFP4: one dword holds both blocks; Q8_0: one dword each) and the exponent /
+                // scale bytes of output rows 16i + 4q + j (MXFP4 one byte, Q8_0 two per block).
+                unsigned w0[2][2], w1[2][2], mw[2][4];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int r = 16 * i + lr;
-            s0[i] = u32x4g{0u, 0u, 0u, 0u};
-            s1[i] = u32x4g{0u, 0u, 0u, 0u};
-            if (tile_live) {
-                s0[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4g *>(codes + g * 4096 + ((2 * q) * 32 + r) * 16));
-                s1[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4g *>(codes + g * 4096 + ((2 * q + 1) * 32 + r) * 16));
-            }
+                for (int i = 0; i < 2; ++i) {
+                    const uint8_t * w = w_lds + wb * G::W + i * 16 * 16;
+                    if constexpr (TYPE == 39) {
+                        w0[i][0] = w0[i][1] = *reinterpret_cast<const unsigned *>(w + sub * 4);
+                        w1[i][0] = w1[i][1] = *reinterpret_cast<const unsigned *>(w + 32 * 16 + sub * 4);
+                    } else {
+                        const u32x2g v0 = *reinterpret_cast<const u32x2g *>(w + sub * 8);
+                        const u32x2g v1 = *reinterpret_cast<const u32x2g *>(w + 32 * 16 + sub * 8);
+                        w0[i][0] = v0[0], w0[i][1] = v0[1], w1[i][0] = v1[0], w1[i][1] = v1[1];
+                    }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int orow = 16 * i + 4 * q + j;
-                m[i][j] = tile_live ? *reinterpret_cast<const u32x2g *>(meta + g * 256 + orow * 8) : u32x2g{0u, 0u};
+                    for (int j = 0; j < 4; ++j) {
+                        const uint8_t * m = m_lds + wb * G::M + (16 * i + j) * 8;
+                        if constexpr (TYPE == 39) mw[i][j] = *reinterpret_cast<const uint16_t *>(m + sub * 2);
+                        else mw[i][j] = *reinterpret_cast<const unsigned *>(m + sub * 4);
+                    }
+                }
+                auto do_block = [&](int bb) {
+                    auto bsrc = [&](int jh) {
+                        const uint8_t * p = b_lds + ab * G::ACT + 16 * jh * RB + bb * 32 * EB;
+                        if constexpr (TYPE == 39) return *reinterpret_cast<const half8_t *>(p);
+                        else return *reinterpret_cast<const long *>(p);
+                    };
+                    auto dsrc = [&](int jh) { return d_lds[ab * (G::DA / 4) + 16 * jh * CB + bb]; };
+                    if constexpr (TYPE == 39) {
+                        auto mscale = [&](int i, int j) { return static_cast<int>(static_cast<signed char>(mw[i][j] >> (8 * bb))); };
+                        half8_t a_op[2];
+#pragma unroll
+                        for (int i = 0; i < 2; ++i) a_op[i] = mx_a_operand(w0[i][bb], w1[i][bb], bb);
+                        block_step(slow_c, a_op, mscale, bsrc, dsrc);
+                    } else {
+                        auto mscale = [&](int i, int j) { return half_bits_to_float(static_cast<uint16_t>(mw[i][j] >> (16 * bb))); };
+                        long a_op[2];
+#pragma unroll
+                        for (int i = 0; i < 2; ++i)
+                            a_op[i] = static_cast<long>(static_cast<uint64_t>(w0[i][bb]) | (static_cast<uint64_t>(w1[i][bb]) << 32));
+                        block_step(slow_c, a_op, mscale, bsrc, dsrc);
+                    }
+                };
+                if constexpr (decltype(slow_c)::value) {
+#pragma clang loop unroll(disable)
+                    for (int bb = 0; bb < CB; ++bb) do_block(bb);
+                } else {
+#pragma unroll
+                    for (int bb = 0; bb < CB; ++bb) do_block(bb);
+                }
+                if (next_act) store_act((c + 1) & 1);
+                if (next_w) store_w((g + 1) & 1);
+                __syncthreads();
             }
         }
-        if constexpr (TYPE == 39) {
-            half8_t a[2];
-#define VBM_MX_STEP(BB)                                                       \
-            a[0] = mx_a_operand<BB>(s0[0], s1[0]);                            \
-            a[1] = mx_a_operand<BB>(s0[1], s1[1]);                            \
-            block_step(g * 8 + BB, a, m, BB);
-            VBM_MX_STEP(0) VBM_MX_STEP(1) VBM_MX_STEP(2) VBM_MX_STEP(3)
-            VBM_MX_STEP(4) VBM_MX_STEP(5) VBM_MX_STEP(6) VBM_MX_STEP(7)
-#undef VBM_MX_STEP
-        } else {
-            long a[2];
+
+        // Tail blocks (nb even: MXFP4 tail in {0,2,4,6}, Q8_0 tail in {0,2}), per-row packed, read
+        // straight from global memory.
+        for (int bt = 0; bt < tail; ++bt) {
+            const int b = groups * G::GB + bt;
+            unsigned m[2][4];
 #pragma unroll
-            for (int bb = 0; bb < 4; ++bb) {
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    a[i] = static_cast<long>(static_cast<uint64_t>(s0[i][bb]) | (static_cast<uint64_t>(s1[i][bb]) << 32));
-                block_step(g * 4 + bb, a, m, bb);
+                for (int j = 0; j < 4; ++j) {
+                    const int orow = 16 * i + 4 * q + j;
+                    m[i][j] = 0;
+                    if (tile_live) {
+                        if constexpr (TYPE == 39) m[i][j] = meta[groups * 256 + orow * tail + bt];
+                        else m[i][j] = *reinterpret_cast<const uint16_t *>(meta + groups * 256 + (orow * tail + bt) * 2);
+                    }
+                }
+            auto mscale = [&](int i, int j) {
+                if constexpr (TYPE == 39) return static_cast<int>(static_cast<signed char>(m[i][j]));
+                else return half_bits_to_float(static_cast<uint16_t>(m[i][j]));
+            };
+            const uint8_t * brow[2];
+#pragma unroll
+            for (int jh = 0; jh < 2; ++jh) brow[jh] = jlive[jh] ? row_of(32 * (wave >> 1) + 16 * jh + lr) : nullptr;
+            auto bsrc = [&](int jh) {
+                if constexpr (TYPE == 39) {
+                    half8_t v = half8_t{};
+                    if (brow[jh]) v = *reinterpret_cast<const half8_t *>(brow[jh] + (static_cast<int64_t>(b) * 32 + 8 * q) * 2);
+                    return v;
+                } else {
+                    long v = 0;
+                    if (brow[jh]) v = *reinterpret_cast<const long *>(brow[jh] + static_cast<int64_t>(b) * 32 + 8 * q);
+                    return v;
+                }
+            };
+            auto dsrc = [&](int jh) { return brow[jh] ? reinterpret_cast<const float *>(brow[jh] + A.lay.da_offset())[b] : 0.0f; };
+            if constexpr (TYPE == 39) {
+                half8_t a[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int r = 16 * i + lr;
+                    unsigned w0 = 0, w1 = 0;
+                    if (tile_live) {
+                        w0 = *reinterpret_cast<const uint16_t *>(codes + groups * 4096 + ((2 * q) * 32 + r) * (tail * 2) + bt * 2);
+                        w1 = *reinterpret_cast<const uint16_t *>(codes + groups * 4096 + ((2 * q + 1) * 32 + r) * (tail * 2) + bt * 2);
+                    }
+                    const half2_g p0 = fp4x2(w0, 0), p1 = fp4x2(w0, 1), p2 = fp4x2(w1, 0), p3 = fp4x2(w1, 1);
+                    a[i] = half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+                }
+                block_step(slow_c, a, mscale, bsrc, dsrc);
+            } else {
+                long a[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int r = 16 * i + lr;
+                    uint64_t w0 = 0, w1 = 0;
+                    if (tile_live) {
+                        w0 = *reinterpret_cast<const unsigned *>(codes + groups * 4096 + ((2 * q) * 32 + r) * (tail * 4) + bt * 4);
+                        w1 = *reinterpret_cast<const unsigned *>(codes + groups * 4096 + ((2 * q + 1) * 32 + r) * (tail * 4) + bt * 4);
+                    }
+                    a[i] = static_cast<long>(w0 | (w1 << 32));
+                }
+                block_step(slow_c, a, mscale, bsrc, dsrc);
             }
         }
+    };
+    if (groups > 0) {
+        load_act(0);
+        load_w(0);
+        store_act(0);
+        store_w(0);
     }
-    // Tail blocks (nb even: MXFP4 tail in {0,2,4,6}, Q8_0 tail in {0,2}), per-row packed.
-    for (int bt = 0; bt < tail; ++bt) {
-        const int b = groups * kGroupBlocks + bt;
-        u32x2g m[2][4];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int orow = 16 * i + 4 * q + j;
-                unsigned w = 0;
-                if (tile_live) {
-                    if constexpr (TYPE == 39) w = meta[groups * 256 + orow * tail + bt];
-                    else w = *reinterpret_cast<const uint16_t *>(meta + groups * 256 + (orow * tail + bt) * 2);
-                }
-                m[i][j] = u32x2g{w, 0u};
-            }
-        if constexpr (TYPE == 39) {
-            half8_t a[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int r = 16 * i + lr;
-                unsigned w0 = 0, w1 = 0;
-                if (tile_live) {
-                    w0 = *reinterpret_cast<const uint16_t *>(codes + groups * 4096 + ((2 * q) * 32 + r) * (tail * 2) + bt * 2);
-                    w1 = *reinterpret_cast<const uint16_t *>(codes + groups * 4096 + ((2 * q + 1) * 32 + r) * (tail * 2) + bt * 2);
-                }
-                const half2_g p0 = fp4x2(w0, 0), p1 = fp4x2(w0, 1), p2 = fp4x2(w1, 0), p3 = fp4x2(w1, 1);
-                a[i] = half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-            }
-            block_step(b, a, m, 0);
-        } else {
-            long a[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int r = 16 * i + lr;
-                uint64_t w0 = 0, w1 = 0;
-                if (tile_live) {
-                    w0 = *reinterpret_cast<const unsigned *>(codes + groups * 4096 + ((2 * q) * 32 + r) * (tail * 4) + bt * 4);
-                    w1 = *reinterpret_cast<const unsigned *>(codes + groups * 4096 + ((2 * q + 1) * 32 + r) * (tail * 4) + bt * 4);
-                }
-                a[i] = static_cast<long>(w0 | (w1 << 32));
-            }
-            block_step(b, a, m, 0);
-        }
+    __syncthreads();
+    if constexpr (FLAGGED) {
+        if (slow) k_loop(std::true_type{});
+        else k_loop(std::false_type{});
+    } else {
+        k_loop(std::false_type{});
     }
 
     // Epilogue: biases (ggml row order), then either fp32 rows or GLU + Q8_0 requantization.
@@ -481,10 +638,13 @@ __global__ __launch_bounds__(256) void gemm_rows_from_q8_kernel(const uint8_t * 
     if (threadIdx.x == 0) *reinterpret_cast<int *>(o + L.flag_offset()) = s_flag;
 }
 
-template <int TYPE, int EPI>
+template <int TYPE, int EPI, bool FLAGGED>
 void launch_gemm_typed(const GemmArgs & a, int row_pairs, int max_tiles, hipStream_t stream) {
-    hipLaunchKernelGGL((grouped_gemm_kernel<TYPE, EPI>), dim3(static_cast<unsigned>(row_pairs), static_cast<unsigned>(max_tiles)),
-                       dim3(kGemmThreads), 0, stream, a);
+    GemmArgs b = a;
+    b.row_pairs = row_pairs;
+    const int64_t items = static_cast<int64_t>(row_pairs) * max_tiles;
+    hipLaunchKernelGGL((grouped_gemm_kernel<TYPE, EPI, FLAGGED>), dim3(static_cast<unsigned>((items + 7) / 8 * 8)),
+                       dim3(kGemmThreads), 0, stream, b);
     check_hip(hipGetLastError(), "grouped GEMM launch");
 }
 
@@ -554,12 +714,16 @@ void launch_grouped_gemm(const GemmParams & p, hipStream_t stream) {
     a.alpha = p.alpha;
     a.limit = p.limit;
     const int row_pairs = static_cast<int>((bank.rows + 63) / 64);
+    require(!p.flagged_rows || p.epilogue == 0, "flagged activation rows only with the plain epilogue");
+    const int mt = static_cast<int>(max_tiles);
     if (bank.type == VBM_TYPE_MXFP4) {
-        if (p.epilogue == 0) launch_gemm_typed<39, 0>(a, row_pairs, static_cast<int>(max_tiles), stream);
-        else launch_gemm_typed<39, 1>(a, row_pairs, static_cast<int>(max_tiles), stream);
+        if (p.flagged_rows) launch_gemm_typed<39, 0, true>(a, row_pairs, mt, stream);
+        else if (p.epilogue == 0) launch_gemm_typed<39, 0, false>(a, row_pairs, mt, stream);
+        else launch_gemm_typed<39, 1, false>(a, row_pairs, mt, stream);
     } else {
-        if (p.epilogue == 0) launch_gemm_typed<8, 0>(a, row_pairs, static_cast<int>(max_tiles), stream);
-        else launch_gemm_typed<8, 1>(a, row_pairs, static_cast<int>(max_tiles), stream);
+        if (p.flagged_rows) launch_gemm_typed<8, 0, true>(a, row_pairs, mt, stream);
+        else if (p.epilogue == 0) launch_gemm_typed<8, 0, false>(a, row_pairs, mt, stream);
+        else launch_gemm_typed<8, 1, false>(a, row_pairs, mt, stream);
     }
 }
 

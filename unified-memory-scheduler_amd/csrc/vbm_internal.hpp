@@ -173,6 +173,7 @@ struct GemmParams {
     GemmRowLayout out_layout;
     int epilogue, activation;
     float alpha, limit;
+    bool flagged_rows;                // rows_in may hold -128 codes (converted from caller Q8_0)
 };
 int64_t gemm_max_tiles(int64_t n_as, int64_t n_entries);
 size_t gemm_tiles_bytes(int64_t n_as, int64_t n_entries);

@@ -285,6 +285,7 @@ vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot,
             p.bias = bias;
             p.dst = dst;
             p.epilogue = 0;
+            p.flagged_rows = b_type != VBM_TYPE_F32;
             launch_grouped_gemm(p, s);
             check_hip(hipFreeAsync(scratch, s), "mul_mat_id scratch free");
             return;
