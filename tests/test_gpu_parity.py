@@ -167,21 +167,45 @@ def test_mul_mat_id_slot_map_and_residency_errors(gpu, orc):
     bank.destroy()
 
 
+def _group_on_gpu(gpu, ids, n_ids, tokens, stride, n_as):
+    d_ids = gpu.DeviceBuffer.from_array(np.ascontiguousarray(ids, np.int32))
+    counts, offsets, rows = (gpu.DeviceBuffer(4 * n) for n in (n_as, n_as + 1, n_ids * tokens))
+    err = gpu.DeviceBuffer(4)
+    gpu.call("vbm_group_by_expert", d_ids.ptr, n_ids, tokens, stride, n_as, counts.ptr, offsets.ptr, rows.ptr,
+             err.ptr, None)
+    o = offsets.download(np.int32, n_as + 1)
+    return (counts.download(np.int32, n_as), o, rows.download(np.int32, n_ids * tokens)[: o[-1]],
+            int(err.download(np.int32, 1)[0]))
+
+
 def test_grouping_exact(gpu, orc):
     rng = np.random.default_rng(12)
-    for n_as, n_ids, tokens in [(32, 4, 1), (32, 4, 64), (128, 4, 32), (128, 8, 2048), (7, 3, 5)]:
+    for n_as, n_ids, tokens in [(32, 4, 1), (32, 4, 64), (128, 4, 32), (128, 8, 2048), (7, 3, 5), (1024, 6, 700)]:
         ids = np.stack([rng.choice(n_as, n_ids, replace=False) for _ in range(tokens)]).astype(np.int32)
         ids[rng.random(ids.shape) < 0.05] = -1
-        d_ids = gpu.DeviceBuffer.from_array(ids)
-        counts, offsets, rows = (gpu.DeviceBuffer(4 * n) for n in (n_as, n_as + 1, n_ids * tokens))
-        err = gpu.DeviceBuffer(4)
-        gpu.call("vbm_group_by_expert", d_ids.ptr, n_ids, tokens, n_ids, n_as, counts.ptr, offsets.ptr, rows.ptr,
-                 err.ptr, None)
-        c, o, r = orc.group_by_expert(ids, n_ids, tokens, n_ids, n_as)
-        assert np.array_equal(counts.download(np.int32, n_as), c)
-        assert np.array_equal(offsets.download(np.int32, n_as + 1), o)
-        assert np.array_equal(rows.download(np.int32, n_ids * tokens)[: o[-1]], r)
-        assert err.download(np.int32, 1)[0] == 0
+        c, o, r, err = _group_on_gpu(gpu, ids, n_ids, tokens, n_ids, n_as)
+        rc, ro, rr = orc.group_by_expert(ids, n_ids, tokens, n_ids, n_as)
+        assert np.array_equal(c, rc) and np.array_equal(o, ro) and np.array_equal(r, rr) and err == 0
+
+
+def test_grouping_duplicates_strides_single_expert_and_bad_ids(gpu, orc):
+    """Entries in (token, rank) order whatever the ids hold: repeated experts within a token, a
+    token stride wider than n_ids, one expert only, chunk boundaries (1024 entries) cut inside
+    a token; ids outside [-1, n_as) set the error flag and are skipped."""
+    rng = np.random.default_rng(13)
+    for n_as, n_ids, tokens, stride in [(16, 5, 999, 7), (1, 3, 1500, 3), (300, 8, 1029, 8), (2, 1, 4099, 1)]:
+        full = rng.integers(-1, n_as, size=(tokens, stride)).astype(np.int32)
+        full[:, n_ids:] = 10**6                   # columns beyond n_ids are never read
+        c, o, r, err = _group_on_gpu(gpu, full, n_ids, tokens, stride, n_as)
+        rc, ro, rr = orc.group_by_expert(full, n_ids, tokens, stride, n_as)
+        assert np.array_equal(c, rc) and np.array_equal(o, ro) and np.array_equal(r, rr) and err == 0
+    ids = rng.integers(0, 64, size=(3000, 4)).astype(np.int32)
+    bad = rng.random(ids.shape) < 0.01
+    ids[bad] = np.where(rng.random(bad.sum()) < 0.5, 64, -5)
+    c, o, r, err = _group_on_gpu(gpu, ids, 4, 3000, 4, 64)
+    clean = np.where(bad, -1, ids).astype(np.int32)
+    rc, ro, rr = orc.group_by_expert(clean, 4, 3000, 4, 64)
+    assert err == 1 and np.array_equal(c, rc) and np.array_equal(o, ro) and np.array_equal(r, rr)
 
 
 def test_router_ids_exact(gpu, orc):

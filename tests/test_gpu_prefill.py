@@ -59,6 +59,28 @@ def test_gemm_integer_block_dots_exact(gpu, orc, type_id):
     bank.destroy()
 
 
+def test_gemm_mxfp4_exponent_ranges_exact(gpu, orc):
+    """Row tiles whose block exponents sit inside the range folded into the f16 weight operand
+    (e in [-14, 12]: bytes 114, 127, 140) and outside it (bytes 141 and 113, the ldexp path),
+    mixed within one workgroup's tile pair; every fp32 sum stays an exact multiple of its block
+    scale, so the result must match the oracle bit for bit."""
+    rng = np.random.default_rng(73)
+    experts, rows, k, n_ids, tokens = 4, 320, 512, 2, 48
+    blk = unit_scale_mxfp4(experts, rows, k, rng).reshape(experts, rows, k // 32, 17)
+    pattern = np.array([141, 127, 114, 140, 113], np.uint8)
+    blk[:, :, :, 0] = pattern[(np.arange(rows) // 32) % len(pattern)][None, :, None]
+    blk[:, 224:256, :, 0] = 140          # one out-of-range block inside an otherwise folded tile
+    blk[:, 224:256, 3, 0] = 141          # (scales 2^12 and 2^13 keep every sum exact)
+    w = blk.reshape(-1)
+    bank = H.make_bank(H.MX, w, experts, rows, k)
+    ids = np.stack([rng.choice(experts, n_ids, replace=False) for _ in range(tokens)]).astype(np.int32)
+    x = unit_scale_activations(tokens, k, rng).reshape(tokens, 1, k)
+    got = H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, ids, n_ids, order=gpu.ORDER_FAST)
+    ref = orc.mul_mat_id(H.MX, w, k, rows, experts, 0, x, 1, ids, n_ids, tokens, n_ids, threads=8)
+    assert H.bits_equal(got, ref), H.diff_report(got, ref)
+    bank.destroy()
+
+
 def test_gemm_mul_mat_id_fast_within_tolerance_and_broadcast(gpu, orc):
     """Config 0/1 gate_up shape (5760 x 2880, interleaved) with biases, T = 64, broadcast and
     per-rank activations."""

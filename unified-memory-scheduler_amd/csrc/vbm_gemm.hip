@@ -71,25 +71,26 @@ struct GemmArgs {
     float alpha, limit;
 };
 
-__device__ __forceinline__ half2_g fp4x2(unsigned dw, int sel) {
+__device__ __forceinline__ half2_g fp4x2(unsigned dw, int sel, float scale = 2.0f) {
     // sel is a compile-time constant at every call site after unrolling
     switch (sel) {
-        case 0: return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, 0);
-        case 1: return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, 1);
-        case 2: return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, 2);
-        default: return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, 3);
+        case 0: return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, scale, 0);
+        case 1: return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, scale, 1);
+        case 2: return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, scale, 2);
+        default: return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, scale, 3);
     }
 }
 
 // Weight operand of one block from the dwords w0, w1 of slices 2q, 2q+1 that hold it: MXFP4
 // bytes 2b, 2b+1 of a 16-byte slice entry carry the slice's 4 nibbles of block b, so block b is
-// half (b & 1) of dword b / 2.
-__device__ __forceinline__ half8_t mx_a_operand(unsigned w0, unsigned w1, int odd) {
+// half (b & 1) of dword b / 2. The e2m1 values come out multiplied by `scale` (a power of two):
+// 2 gives the doubled-table integers; 2^(e+1) folds the block exponent e in as well.
+__device__ __forceinline__ half8_t mx_a_operand(unsigned w0, unsigned w1, int odd, float scale = 2.0f) {
     half2_g p0, p1, p2, p3;
     if (odd) {
-        p0 = fp4x2(w0, 2), p1 = fp4x2(w0, 3), p2 = fp4x2(w1, 2), p3 = fp4x2(w1, 3);
+        p0 = fp4x2(w0, 2, scale), p1 = fp4x2(w0, 3, scale), p2 = fp4x2(w1, 2, scale), p3 = fp4x2(w1, 3, scale);
     } else {
-        p0 = fp4x2(w0, 0), p1 = fp4x2(w0, 1), p2 = fp4x2(w1, 0), p3 = fp4x2(w1, 1);
+        p0 = fp4x2(w0, 0, scale), p1 = fp4x2(w0, 1, scale), p2 = fp4x2(w1, 0, scale), p3 = fp4x2(w1, 1, scale);
     }
     return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
@@ -312,7 +313,8 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
     const int n_chunks = groups * G::CPG;
     auto k_loop = [&](auto slow_c) {
         const uint8_t * w_lds = lds + G::OFF_W + (wave & 1) * 4096 + (2 * q * 32 + lr) * 16;
-        const uint8_t * m_lds = lds + G::OFF_M + (wave & 1) * 256 + 4 * q * 8;
+        const uint8_t * m_lds = lds + G::OFF_M + (wave & 1) * 256 + 4 * q * 8;    // output rows 4q + j
+        const uint8_t * ma_lds = lds + G::OFF_M + (wave & 1) * 256 + lr * 8;      // A rows lr (+16i)
         const uint8_t * b_lds = lds + (32 * (wave >> 1) + lr) * RB + 8 * q * EB;
         const float * d_lds = reinterpret_cast<const float *>(lds + G::OFF_DA) + (32 * (wave >> 1) + lr) * CB;
         for (int g = 0; g < groups; ++g) {
@@ -325,9 +327,8 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                 if (next_w) load_w(g + 1);
                 const int ab = c & 1;
                 // This chunk's blocks 2sub, 2sub+1 in the group: weight dwords of slices 2q, 2q+1
-                // (MXFP4: one dword holds both blocks; Q8_0: one dword each) and the exponent /
-                // scale bytes of output rows 16i + 4q + j (MXFP4 one byte, Q8_0 two per block).
-                unsigned w0[2][2], w1[2][2], mw[2][4];
+                // (MXFP4: one dword holds both blocks; Q8_0: one dword each).
+                unsigned w0[2][2], w1[2][2];
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
                     const uint8_t * w = w_lds + wb * G::W + i * 16 * 16;
@@ -339,41 +340,85 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                         const u32x2g v1 = *reinterpret_cast<const u32x2g *>(w + 32 * 16 + sub * 8);
                         w0[i][0] = v0[0], w0[i][1] = v0[1], w1[i][0] = v1[0], w1[i][1] = v1[1];
                     }
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint8_t * m = m_lds + wb * G::M + (16 * i + j) * 8;
-                        if constexpr (TYPE == 39) mw[i][j] = *reinterpret_cast<const uint16_t *>(m + sub * 2);
-                        else mw[i][j] = *reinterpret_cast<const unsigned *>(m + sub * 4);
-                    }
                 }
-                auto do_block = [&](int bb) {
-                    auto bsrc = [&](int jh) {
-                        const uint8_t * p = b_lds + ab * G::ACT + 16 * jh * RB + bb * 32 * EB;
-                        if constexpr (TYPE == 39) return *reinterpret_cast<const half8_t *>(p);
-                        else return *reinterpret_cast<const long *>(p);
-                    };
-                    auto dsrc = [&](int jh) { return d_lds[ab * (G::DA / 4) + 16 * jh * CB + bb]; };
-                    if constexpr (TYPE == 39) {
-                        auto mscale = [&](int i, int j) { return static_cast<int>(static_cast<signed char>(mw[i][j] >> (8 * bb))); };
+                // MXFP4 fast path: when every exponent e of the wave's A rows (16i + lr) lies in
+                // [-14, 12], 2^(e+1) times the e2m1 values is an exact normal f16, so the exponent
+                // rides in the A operand and the block result needs one FMA with d_act:
+                // da * (2^e * dot) rounds the same product as ldexp(da, e) * dot.
+                bool folded = false;
+                float fsc[2][2];
+                if constexpr (TYPE == 39 && !decltype(slow_c)::value) {
+                    bool ok = true;
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const unsigned ea = *reinterpret_cast<const uint16_t *>(ma_lds + wb * G::M + i * 16 * 8 + sub * 2);
+#pragma unroll
+                        for (int bb = 0; bb < 2; ++bb) {
+                            const int e = static_cast<signed char>(ea >> (8 * bb));
+                            ok = ok && e >= -14 && e <= 12;
+                            fsc[i][bb] = __builtin_bit_cast(float, static_cast<unsigned>(e + 128) << 23);
+                        }
+                    }
+                    folded = __all(ok);
+                }
+                if (folded) {
+#pragma unroll
+                    for (int bb = 0; bb < CB; ++bb) {
                         half8_t a_op[2];
 #pragma unroll
-                        for (int i = 0; i < 2; ++i) a_op[i] = mx_a_operand(w0[i][bb], w1[i][bb], bb);
-                        block_step(slow_c, a_op, mscale, bsrc, dsrc);
-                    } else {
-                        auto mscale = [&](int i, int j) { return half_bits_to_float(static_cast<uint16_t>(mw[i][j] >> (16 * bb))); };
-                        long a_op[2];
+                        for (int i = 0; i < 2; ++i) a_op[i] = mx_a_operand(w0[i][bb], w1[i][bb], bb, fsc[i][bb]);
 #pragma unroll
-                        for (int i = 0; i < 2; ++i)
-                            a_op[i] = static_cast<long>(static_cast<uint64_t>(w0[i][bb]) | (static_cast<uint64_t>(w1[i][bb]) << 32));
-                        block_step(slow_c, a_op, mscale, bsrc, dsrc);
+                        for (int jh = 0; jh < 2; ++jh) {
+                            const float da = d_lds[ab * (G::DA / 4) + 16 * jh * CB + bb];
+                            const half8_t bv = *reinterpret_cast<const half8_t *>(b_lds + ab * G::ACT + 16 * jh * RB + bb * 32 * EB);
+#pragma unroll
+                            for (int i = 0; i < 2; ++i) {
+                                const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_op[i], bv, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                                for (int j = 0; j < 4; ++j) acc[i][jh][j] = __builtin_fmaf(da, d[j], acc[i][jh][j]);
+                            }
+                        }
                     }
-                };
-                if constexpr (decltype(slow_c)::value) {
-#pragma clang loop unroll(disable)
-                    for (int bb = 0; bb < CB; ++bb) do_block(bb);
                 } else {
+                    // exponent / scale bytes of output rows 16i + 4q + j (MXFP4 one byte, Q8_0 two per block)
+                    unsigned mw[2][4];
 #pragma unroll
-                    for (int bb = 0; bb < CB; ++bb) do_block(bb);
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const uint8_t * m = m_lds + wb * G::M + (16 * i + j) * 8;
+                            if constexpr (TYPE == 39) mw[i][j] = *reinterpret_cast<const uint16_t *>(m + sub * 2);
+                            else mw[i][j] = *reinterpret_cast<const unsigned *>(m + sub * 4);
+                        }
+                    auto do_block = [&](int bb) {
+                        auto bsrc = [&](int jh) {
+                            const uint8_t * p = b_lds + ab * G::ACT + 16 * jh * RB + bb * 32 * EB;
+                            if constexpr (TYPE == 39) return *reinterpret_cast<const half8_t *>(p);
+                            else return *reinterpret_cast<const long *>(p);
+                        };
+                        auto dsrc = [&](int jh) { return d_lds[ab * (G::DA / 4) + 16 * jh * CB + bb]; };
+                        if constexpr (TYPE == 39) {
+                            auto mscale = [&](int i, int j) { return static_cast<int>(static_cast<signed char>(mw[i][j] >> (8 * bb))); };
+                            half8_t a_op[2];
+#pragma unroll
+                            for (int i = 0; i < 2; ++i) a_op[i] = mx_a_operand(w0[i][bb], w1[i][bb], bb);
+                            block_step(slow_c, a_op, mscale, bsrc, dsrc);
+                        } else {
+                            auto mscale = [&](int i, int j) { return half_bits_to_float(static_cast<uint16_t>(mw[i][j] >> (16 * bb))); };
+                            long a_op[2];
+#pragma unroll
+                            for (int i = 0; i < 2; ++i)
+                                a_op[i] = static_cast<long>(static_cast<uint64_t>(w0[i][bb]) | (static_cast<uint64_t>(w1[i][bb]) << 32));
+                            block_step(slow_c, a_op, mscale, bsrc, dsrc);
+                        }
+                    };
+                    if constexpr (decltype(slow_c)::value) {
+#pragma clang loop unroll(disable)
+                        for (int bb = 0; bb < CB; ++bb) do_block(bb);
+                    } else {
+#pragma unroll
+                        for (int bb = 0; bb < CB; ++bb) do_block(bb);
+                    }
                 }
                 if (next_act) store_act((c + 1) & 1);
                 if (next_w) store_w((g + 1) & 1);

@@ -80,7 +80,9 @@ struct GroupBuffers {
     int32_t * active;    // [n_as] experts with count > 0, ascending
     int32_t * n_active;  // [1]
     int32_t * error;     // [1]
+    int32_t * chunk_counts;  // [group_chunk_ints]: per-chunk histograms, then chunk bases
 };
+int64_t group_chunk_ints(int64_t n_as, int64_t n_entries);
 size_t group_workspace_bytes(int64_t n_as, int64_t n_entries);
 GroupBuffers carve_group(void * base, int64_t n_as, int64_t n_entries);
 void launch_group(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride, int64_t n_as,

@@ -228,13 +228,16 @@ vbm_status vbm_group_by_expert(const int32_t * ids, int64_t n_ids, int64_t n_tok
         require(ids && counts && offsets && rows, "null buffer");
         const hipStream_t s = as_stream(stream);
         void * scratch = nullptr;
-        check_hip(hipMallocAsync(&scratch, sizeof(int32_t) * (n_as + 2 + 8), s), "group scratch");
+        require(n_as > 0 && n_ids > 0 && n_tokens > 0, "grouping sizes must be positive");
+        const int64_t chunk_ints = group_chunk_ints(n_as, n_ids * n_tokens);
+        check_hip(hipMallocAsync(&scratch, sizeof(int32_t) * (n_as + 2 + chunk_ints + 8), s), "group scratch");
         GroupBuffers g{};
         g.counts = counts;
         g.offsets = offsets;
         g.rows = rows;
         g.active = static_cast<int32_t *>(scratch);
         g.n_active = g.active + n_as;
+        g.chunk_counts = g.n_active + 2;
         g.error = error_flag ? error_flag : g.n_active + 1;
         launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
         check_hip(hipFreeAsync(scratch, s), "group scratch free");

@@ -9,39 +9,69 @@ namespace {
 constexpr int kGroupThreads = 1024;
 constexpr int kMaxExperts = 1024;
 
-constexpr int kMaxStagedIds = 16384;
-
-// One workgroup. Counting sort of entries i = token * n_ids + rank by expert, stable in i
+// Token->expert grouping: a stable counting sort of entries i = token * n_ids + rank by expert
 // (the (token outer, rank inner) append order of ggml's MMID row mapping). Entries with id -1
-// are skipped; ids outside [-1, n_as) raise the error flag and are skipped.
-//   1. ids -> LDS, per-expert counts with LDS atomics (order-independent);
-//   2. exclusive scans of counts (offsets) and of (count > 0) (active list) in parallel;
-//   3. stable placement: each wave owns experts w, w + 16, ... and ranks its matches over the
-//      entries in order, 64 at a time, with a ballot.
-__global__ __launch_bounds__(kGroupThreads) void group_kernel(const int32_t * __restrict__ ids, int n_ids,
-                                                               int n_tokens, int64_t ids_stride, int n_as,
-                                                               int32_t * counts, int32_t * offsets, int32_t * rows,
-                                                               int32_t * active, int32_t * n_active, int32_t * error) {
-    __shared__ int s_count[kMaxExperts];
-    __shared__ int s_offset[kMaxExperts];
-    __shared__ int s_wave_sum[2][kGroupThreads / 64];
-    __shared__ int s_ids[kMaxStagedIds];
-    __shared__ int s_error;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int n = n_ids * n_tokens;
-    const bool staged = n <= kMaxStagedIds;
-    for (int e = t; e < n_as; e += kGroupThreads) s_count[e] = 0;
-    if (t == 0) s_error = 0;
+// are skipped; ids outside [-1, n_as) raise the error flag and are skipped. Three launches over
+// chunks of 1024 entries:
+//   count: per-chunk expert histograms (LDS atomics, order-free) and per-chunk error flags;
+//   scan:  one workgroup turns the histograms into per-(chunk, expert) bases, then scans the
+//          expert totals into counts / offsets and the active-expert list;
+//   place: each wave finds, for every lane, the lanes holding the same expert with one ballot
+//          per id bit, ranks its entry among them, and adds the counts of the same expert in
+//          the chunk's earlier waves and the chunk base: positions follow i exactly.
+constexpr int kGroupChunk = kGroupThreads;
+
+__device__ __forceinline__ int group_id(const int32_t * __restrict__ ids, int64_t i, int n_ids, int64_t ids_stride,
+                                        int n_as, bool & bad) {
+    int id = ids[(i / n_ids) * ids_stride + i % n_ids];
+    bad = id != -1 && (id < 0 || id >= n_as);
+    return bad ? -2 : id;
+}
+
+__global__ __launch_bounds__(kGroupThreads) void group_count_kernel(const int32_t * __restrict__ ids, int n_ids,
+                                                                     int64_t n, int64_t ids_stride, int n_as,
+                                                                     int32_t * __restrict__ chunk_counts) {
+    __shared__ int s_hist[kMaxExperts];
+    __shared__ int s_bad;
+    const int t = threadIdx.x;
+    for (int e = t; e < n_as; e += kGroupThreads) s_hist[e] = 0;
+    if (t == 0) s_bad = 0;
     __syncthreads();
-    for (int i = t; i < n; i += kGroupThreads) {
-        int id = ids[static_cast<int64_t>(i / n_ids) * ids_stride + i % n_ids];
-        if (id != -1 && (id < 0 || id >= n_as)) { s_error = 1; id = -2; }
-        if (staged) s_ids[i] = id;
-        if (id >= 0) atomicAdd(&s_count[id], 1);
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kGroupChunk + t;
+    if (i < n) {
+        bool bad;
+        const int id = group_id(ids, i, n_ids, ids_stride, n_as, bad);
+        if (bad) s_bad = 1;
+        if (id >= 0) atomicAdd(&s_hist[id], 1);
     }
     __syncthreads();
-    // Two-level exclusive scans over experts e = t (n_as <= 1024 = one expert per thread).
-    const int c = t < n_as ? s_count[t] : 0;
+    int32_t * row = chunk_counts + static_cast<int64_t>(blockIdx.x) * (n_as + 1);
+    for (int e = t; e < n_as; e += kGroupThreads) row[e] = s_hist[e];
+    if (t == 0) row[n_as] = s_bad;
+}
+
+__global__ __launch_bounds__(kGroupThreads) void group_scan_kernel(int n_chunks, int n_as, int32_t * chunk_counts,
+                                                                    int32_t * counts, int32_t * offsets,
+                                                                    int32_t * active, int32_t * n_active,
+                                                                    int32_t * error) {
+    __shared__ int s_wave_sum[2][kGroupThreads / 64];
+    __shared__ int s_bad;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    if (t == 0) s_bad = 0;
+    __syncthreads();
+    // expert e = t: chunk bases (exclusive prefix over chunks) and the total
+    int c = 0;
+    if (t < n_as) {
+        for (int k = 0; k < n_chunks; ++k) {
+            int32_t * cell = chunk_counts + static_cast<int64_t>(k) * (n_as + 1) + t;
+            const int v = *cell;
+            *cell = c;
+            c += v;
+        }
+    }
+    for (int k = t; k < n_chunks; k += kGroupThreads)
+        if (chunk_counts[static_cast<int64_t>(k) * (n_as + 1) + n_as]) s_bad = 1;
+    // two-level exclusive scans of the totals and of (total > 0)
     const int live = c > 0 ? 1 : 0;
     int inc_c = c, inc_l = live;
     for (int off = 1; off < 64; off <<= 1) {
@@ -54,7 +84,6 @@ __global__ __launch_bounds__(kGroupThreads) void group_kernel(const int32_t * __
     for (int w = 0; w < wave; ++w) { base_c += s_wave_sum[0][w]; base_l += s_wave_sum[1][w]; }
     const int ex_c = base_c + inc_c - c, ex_l = base_l + inc_l - live;
     if (t < n_as) {
-        s_offset[t] = ex_c;
         counts[t] = c;
         offsets[t] = ex_c;
         if (live) active[ex_l] = t;
@@ -63,22 +92,40 @@ __global__ __launch_bounds__(kGroupThreads) void group_kernel(const int32_t * __
             *n_active = ex_l + live;
         }
     }
-    if (t == 0) *error = s_error;
-    __syncthreads();
-    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    for (int e = wave; e < n_as; e += kGroupThreads / 64) {
-        if (s_count[e] == 0) continue;
-        int running = s_offset[e];
-        for (int base = 0; base < n; base += 64) {
-            const int i = base + lane;
-            int id = -2;
-            if (i < n) id = staged ? s_ids[i] : ids[static_cast<int64_t>(i / n_ids) * ids_stride + i % n_ids];
-            const uint64_t mask = __ballot(id == e);
-            if (id == e) rows[running + __popcll(mask & below)] = i;
-            running += __popcll(mask);
-            if (running == s_offset[e] + s_count[e]) break;
-        }
+    if (t == 0) *error = s_bad;
+}
+
+__global__ __launch_bounds__(kGroupThreads) void group_place_kernel(const int32_t * __restrict__ ids, int n_ids,
+                                                                     int64_t n, int64_t ids_stride, int n_as, int id_bits,
+                                                                     const int32_t * __restrict__ chunk_counts,
+                                                                     const int32_t * __restrict__ offsets,
+                                                                     int32_t * __restrict__ rows) {
+    constexpr int kWaves = kGroupThreads / 64;
+    __shared__ int16_t s_wave_count[kWaves][kMaxExperts];   // counts <= 64
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    for (int k = t; k < kWaves * n_as; k += kGroupThreads) s_wave_count[k / n_as][k % n_as] = 0;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kGroupChunk + t;
+    int id = -2;
+    if (i < n) {
+        bool bad;
+        id = group_id(ids, i, n_ids, ids_stride, n_as, bad);
     }
+    const bool valid = id >= 0;
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < id_bits; ++b) {
+        const bool bit = valid && ((id >> b) & 1);
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+    }
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    const int rank = __popcll(peers & below);
+    __syncthreads();   // zeroed counts visible
+    if (valid && rank == 0) s_wave_count[wave][id] = static_cast<int16_t>(__popcll(peers));
+    __syncthreads();
+    if (!valid) return;
+    int pos = offsets[id] + chunk_counts[static_cast<int64_t>(blockIdx.x) * (n_as + 1) + id] + rank;
+    for (int w = 0; w < wave; ++w) pos += s_wave_count[w][id];
+    rows[pos] = static_cast<int32_t>(i);
 }
 
 // x86 quantize_row_q8_0: one 32-lane group per block.
@@ -193,8 +240,13 @@ unsigned blocks_for(int64_t n, int threads) { return static_cast<unsigned>((n + 
 
 }  // namespace
 
+int64_t group_chunk_ints(int64_t n_as, int64_t n_entries) {
+    return (n_entries + kGroupChunk - 1) / kGroupChunk * (n_as + 1);
+}
+
 size_t group_workspace_bytes(int64_t n_as, int64_t n_entries) {
-    return static_cast<size_t>(n_as + (n_as + 1) + n_entries + n_as + 1 + 1 + 8) * sizeof(int32_t);
+    return static_cast<size_t>(n_as + (n_as + 1) + n_entries + n_as + 1 + 1 + group_chunk_ints(n_as, n_entries) + 8) *
+           sizeof(int32_t);
 }
 
 GroupBuffers carve_group(void * base, int64_t n_as, int64_t n_entries) {
@@ -205,7 +257,8 @@ GroupBuffers carve_group(void * base, int64_t n_as, int64_t n_entries) {
     g.rows = p; p += n_entries;
     g.active = p; p += n_as;
     g.n_active = p; p += 1;
-    g.error = p;
+    g.error = p; p += 1;
+    g.chunk_counts = p;
     return g;
 }
 
@@ -214,10 +267,20 @@ void launch_group(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t 
     require(n_as > 0 && n_as <= kMaxExperts, "grouping supports 1..1024 experts");
     require(n_ids > 0 && n_tokens > 0 && n_ids * n_tokens <= (1ll << 24), "grouping entry count out of range");
     require(ids_stride >= n_ids, "ids token stride must be >= n_ids");
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(kGroupThreads), 0, stream, ids, static_cast<int>(n_ids),
-                       static_cast<int>(n_tokens), ids_stride, static_cast<int>(n_as), g.counts, g.offsets, g.rows,
-                       g.active, g.n_active, g.error);
-    check_hip(hipGetLastError(), "grouping launch");
+    require(g.chunk_counts != nullptr, "grouping needs its chunk-count scratch");
+    const int64_t n = n_ids * n_tokens;
+    const int n_chunks = static_cast<int>((n + kGroupChunk - 1) / kGroupChunk);
+    int id_bits = 0;
+    while ((1ll << id_bits) < n_as) ++id_bits;
+    hipLaunchKernelGGL(group_count_kernel, dim3(n_chunks), dim3(kGroupThreads), 0, stream, ids, static_cast<int>(n_ids), n,
+                       ids_stride, static_cast<int>(n_as), g.chunk_counts);
+    check_hip(hipGetLastError(), "grouping count launch");
+    hipLaunchKernelGGL(group_scan_kernel, dim3(1), dim3(kGroupThreads), 0, stream, n_chunks, static_cast<int>(n_as),
+                       g.chunk_counts, g.counts, g.offsets, g.active, g.n_active, g.error);
+    check_hip(hipGetLastError(), "grouping scan launch");
+    hipLaunchKernelGGL(group_place_kernel, dim3(n_chunks), dim3(kGroupThreads), 0, stream, ids, static_cast<int>(n_ids), n,
+                       ids_stride, static_cast<int>(n_as), id_bits, g.chunk_counts, g.offsets, g.rows);
+    check_hip(hipGetLastError(), "grouping place launch");
 }
 
 void launch_quantize_q8_0(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, uint8_t * dst,
