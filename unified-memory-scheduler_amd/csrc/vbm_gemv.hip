@@ -611,200 +611,279 @@ struct DecodeArgs {
     const float * prev_y;      // [top_k][hidden] previous layer's biased down outputs
     const float * prev_w;      // [top_k] previous layer's routing weights
     const float * bias;        // gate_up bias [n_expert][rows] (ggml row order) or null
-    uint8_t * act_rows;        // [top_k] down activation rows
-    XrowLayout act_lay;
+    float * act_f;             // [top_k][intermediate] GLU outputs (fp32)
     int32_t * route_ids;       // [top_k] this layer's routing
     float * route_w;           // [top_k]
+    int32_t * route_slots;     // [top_k] bank slot of each pick (expert_to_slot applied), or null
     int activation;
     float alpha, limit;
 };
 
 constexpr int kDownThreads = 256;
 
-// The layer input into `xs` (fp32, LDS): x, or the previous layer's combine (ggml MUL by the
-// routing weight, then ADD in rank order), eight elements per thread with the loads of up to four
-// ranks in flight together.
-__device__ __forceinline__ void combine_input(const DecodeArgs & A, float * xs, int H) {
-    for (int e0 = threadIdx.x * 8; e0 < H; e0 += kThreads * 8) {
-        float x[8];
-        if (A.x_in) {
-            const float4 lo = *reinterpret_cast<const float4 *>(A.x_in + e0);
-            const float4 hi = *reinterpret_cast<const float4 *>(A.x_in + e0 + 4);
-            x[0] = lo.x; x[1] = lo.y; x[2] = lo.z; x[3] = lo.w;
-            x[4] = hi.x; x[5] = hi.y; x[6] = hi.z; x[7] = hi.w;
+// x86 quantize_row_q8_0 of eight elements (part p of block b, thread t = 4b + p) of the layer input
+// into the activation row `act` (codes + block scales); block maximum over the thread quad (DPP),
+// so all four threads of a quad must call it together.
+template <int TYPE>
+__device__ __forceinline__ void quantize_x8(const float (&x)[8], int t, uint8_t * act, const XrowLayout & L, int nb) {
+    const int b = t >> 2, part = t & 3;
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    amax = quad_max(amax);
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    float q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float v = rintf(x[i] * id);
+        q[i] = v > 127.0f ? 127.0f : (v < -128.0f ? -128.0f : v);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int64_t sk = 2 * part + h;
+        if (TYPE == 39) {
+            half2_t p0, p1;
+            p0.x = static_cast<_Float16>(q[4 * h]); p0.y = static_cast<_Float16>(q[4 * h + 1]);
+            p1.x = static_cast<_Float16>(q[4 * h + 2]); p1.y = static_cast<_Float16>(q[4 * h + 3]);
+            u32x2 v;
+            v.x = __builtin_bit_cast(unsigned, p0);
+            v.y = __builtin_bit_cast(unsigned, p1);
+            *reinterpret_cast<u32x2 *>(act + (sk * nb + b) * 8) = v;
         } else {
-            for (int q0 = 0; q0 < A.top_k; q0 += 4) {
-                float4 lo[4], hi[4];
-                float w[4];
+            unsigned v = 0;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (q0 + j < A.top_k) {
-                        const float * y = A.prev_y + static_cast<int64_t>(q0 + j) * H + e0;
-                        lo[j] = *reinterpret_cast<const float4 *>(y);
-                        hi[j] = *reinterpret_cast<const float4 *>(y + 4);
-                        w[j] = A.prev_w[q0 + j];
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (q0 + j < A.top_k) {
-                        const float y[8] = {lo[j].x, lo[j].y, lo[j].z, lo[j].w, hi[j].x, hi[j].y, hi[j].z, hi[j].w};
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) {
-                            const float term = y[i] * w[j];
-                            x[i] = q0 + j == 0 ? term : x[i] + term;
-                        }
-                    }
-                }
-            }
+            for (int i = 0; i < 4; ++i)
+                v |= static_cast<unsigned>(static_cast<uint8_t>(static_cast<signed char>(q[4 * h + i]))) << (8 * i);
+            *reinterpret_cast<unsigned *>(act + (sk * nb + b) * 4) = v;
         }
-        *reinterpret_cast<float4 *>(xs + e0) = make_float4(x[0], x[1], x[2], x[3]);
-        *reinterpret_cast<float4 *>(xs + e0 + 4) = make_float4(x[4], x[5], x[6], x[7]);
+    }
+    if (part == 0) reinterpret_cast<float *>(act + L.da_offset())[b] = static_cast<float>(static_cast<_Float16>(d));
+}
+
+// One wavefront's top-k over n <= 64 NPL routing keys held in registers (lg[i]: expert lane + 64 i,
+// already route_key'd, so never NaN), in the total order (value desc, then lower index;
+// tools/trace/topk-tie-probe.cpp:111-113): pick j is the best element strictly after pick j - 1.
+// Each round takes the wave maximum of the lanes' best remaining candidates (DPP and a swizzle,
+// no LDS traffic), then the lowest expert index holding it with one ballot per register row.
+// Lane j < k returns pick j in (sel_v, sel_i). No barrier: every wave can route for itself.
+template <int NPL>
+__device__ __forceinline__ void wave_topk_regs(const float (&lg)[NPL], int n, int k, float & sel_v, int & sel_i) {
+    const int lane = threadIdx.x & 63;
+    float prev_v = INFINITY;
+    int prev_i = -1;
+    sel_v = 0.0f;
+    sel_i = -1;
+    for (int j = 0; j < k; ++j) {
+        float best = -INFINITY;
+        int best_i = -1;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            const int c = lane + 64 * i;
+            const float v = lg[i];
+            const bool after_prev = v < prev_v || (v == prev_v && c > prev_i);
+            if (c < n && after_prev && (best_i < 0 || v > best)) { best = v; best_i = c; }
+        }
+        const float h = half_wave_max(best);
+        const float m0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, h), 0));
+        const float m1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, h), 32));
+        const float top = m0 > m1 ? m0 : m1;
+        int pick = -1;
+#pragma unroll
+        for (int i = NPL - 1; i >= 0; --i) {
+            const uint64_t m = __ballot(best_i >= 0 && best == top && (best_i >> 6) == i);
+            if (m) pick = 64 * i + __builtin_ctzll(m);
+        }
+        if (lane == j) { sel_v = top; sel_i = pick; }
+        prev_v = top;
+        prev_i = pick;
     }
 }
 
-// x86 quantize_row_q8_0 of `xs` into the activation row `act` (codes + block scales): four
-// threads per 32-element block, eight elements each, block maximum over the quad (DPP).
-template <int TYPE>
-__device__ __forceinline__ void quantize_input(const float * xs, uint8_t * act, const XrowLayout & L, int nb) {
-    for (int t = threadIdx.x; t < 4 * nb; t += kThreads) {
-        const int b = t >> 2, part = t & 3;
-        const int e0 = b * 32 + part * 8;
-        const float4 lo = *reinterpret_cast<const float4 *>(xs + e0);
-        const float4 hi = *reinterpret_cast<const float4 *>(xs + e0 + 4);
-        const float x[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-        float amax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
-        amax = quad_max(amax);
-        const float d = amax / 127.0f;
-        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-        float q[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float v = rintf(x[i] * id);
-            q[i] = v > 127.0f ? 127.0f : (v < -128.0f ? -128.0f : v);
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int64_t sk = 2 * part + h;
-            if (TYPE == 39) {
-                half2_t p0, p1;
-                p0.x = static_cast<_Float16>(q[4 * h]); p0.y = static_cast<_Float16>(q[4 * h + 1]);
-                p1.x = static_cast<_Float16>(q[4 * h + 2]); p1.y = static_cast<_Float16>(q[4 * h + 3]);
-                u32x2 v;
-                v.x = __builtin_bit_cast(unsigned, p0);
-                v.y = __builtin_bit_cast(unsigned, p1);
-                *reinterpret_cast<u32x2 *>(act + (sk * nb + b) * 8) = v;
-            } else {
-                unsigned v = 0;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    v |= static_cast<unsigned>(static_cast<uint8_t>(static_cast<signed char>(q[4 * h + i]))) << (8 * i);
-                *reinterpret_cast<unsigned *>(act + (sk * nb + b) * 4) = v;
-            }
-        }
-        if (part == 0) reinterpret_cast<float *>(act + L.da_offset())[b] = static_cast<float>(static_cast<_Float16>(d));
+// ggml soft_max over the k picks held by lanes 0..k-1 (expf(v - max), sum in double in pick order,
+// scale by (float)(1/sum)); returns the weight of pick `lane` (lane < k).
+__device__ __forceinline__ float wave_pick_softmax(float sel_v, int k) {
+    const int lane = threadIdx.x & 63;
+    float max = -INFINITY;
+    for (int j = 0; j < k; ++j) {
+        const float v = __shfl(sel_v, j);
+        max = v > max ? v : max;
     }
+    const float e = lane < k ? expf_rn(sel_v - max) : 0.0f;
+    double sum = 0.0;
+    for (int j = 0; j < k; ++j) sum += static_cast<double>(__shfl(e, j));
+    return e * static_cast<float>(1.0 / sum);
 }
 
-// Dynamic LDS of kernel A: [xs: hidden fp32][meta of 2 tiles][activation row][scale table].
+// Dynamic LDS of kernels A and B: [meta of 1 tile][activation row][scale table of 1 tile].
 template <int TYPE>
-size_t gate_up_lds_bytes(int nb) {
-    return static_cast<size_t>(nb) * 128 + 2 * 32 * static_cast<size_t>(nb) * (TYPE == 39 ? 1 : 2) +
-           ((static_cast<size_t>(nb) * (TYPE == 39 ? 68 : 36) + 15) & ~static_cast<size_t>(15)) +
-           static_cast<size_t>((nb + 3) / 4) * 1024;
-}
-// Dynamic LDS of kernel B: [meta of 1 tile][activation row][scale table of 1 tile].
-template <int TYPE>
-size_t down_lds_bytes(int nb) {
+size_t decode_lds_bytes(int nb) {
     return 32 * static_cast<size_t>(nb) * (TYPE == 39 ? 1 : 2) +
            ((static_cast<size_t>(nb) * (TYPE == 39 ? 68 : 36) + 15) & ~static_cast<size_t>(15)) +
            static_cast<size_t>((nb + 3) / 4) * 512;
 }
 
-template <int TYPE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void decode_gate_up_kernel(DecodeArgs A) {
+// Kernel A: one 32-row bank tile (16 gate + 16 up rows) of one rank per workgroup, wave w holding
+// lane slices 2w (lanes 0..31) and 2w + 1 (lanes 32..63); 2 x hidden / 32 small workgroups spread
+// evenly over the CUs. Prologue order is what sets its latency: the routing logits, this wave's
+// share of the expert->slot map and the layer-input loads go out first; each wave routes on its
+// own registers (no barrier), and the expert's weight stream is issued as soon as the logits are
+// in, while the layer-input loads are still landing. Only then the input is combined (ggml MUL by
+// the routing weight, then ADD in rank order) and quantized, thread t owning elements 8t..8t+7
+// and 8(t + 256).., straight from registers into the activation row. The tile's 16 GLU outputs
+// go out as fp32; kernel B quantizes each 32-element block of them (the pair of tiles).
+template <int TYPE, int NPL>
+__global__ __launch_bounds__(kDownThreads) __attribute__((amdgpu_waves_per_eu(3))) void decode_gate_up_kernel(DecodeArgs A) {
     constexpr int D = gate_up_depth<TYPE>();
-    __shared__ float red[8][64];
-    __shared__ float vals[64];
-    __shared__ __attribute__((aligned(16))) float s_val[kMaxRouteExperts];
-    __shared__ int s_rank[kMaxRouteExperts];
-    __shared__ int32_t s_ids[64];
+    constexpr int kChunks = 2;                     // 8-element input chunks per thread (hidden <= 4096)
+    __shared__ float red[8][32];
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
     const Shape S = A.shape;
     const int nb = S.nb;
-    float * xs = reinterpret_cast<float *>(lds_dyn);
-    uint8_t * lmeta = lds_dyn + nb * 128;
-    uint8_t * act = lmeta + 2 * meta_tile_bytes<TYPE>(nb);
+    uint8_t * lmeta = lds_dyn;
+    uint8_t * act = lmeta + meta_tile_bytes<TYPE>(nb);
     float * lscale = reinterpret_cast<float *>(act + ((A.lay.flag_offset() + 15) & ~15ll));
-    const int k = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, r = lane & 31;
-    const int pair = blockIdx.x, rank = blockIdx.y;
-
-    // The routing logits and the layer input are loaded together; only then the routing decides
-    // which weights to stream.
+    const int k = (threadIdx.x >> 6) * 2 + (lane >> 5);
+    const int tile = blockIdx.x, rank = blockIdx.y;
     const int n = A.n_expert;
-    float lg[kMaxRouteExperts / kThreads];
+
+    // 1. routing keys and slots of experts lane + 64 i; the first four ranks of the layer input.
+    // Every load below is unconditional (clamped indices), so the compiler's in-order wait
+    // counts stay exact: the top-k waits for the logits only, the slot for the map only, and the
+    // input loads are still in flight when the weight stream goes out.
+    float lg[NPL];
+    int sl[NPL];
+    const int32_t * map = A.expert_to_slot;
 #pragma unroll
-    for (int i = 0; i < kMaxRouteExperts / kThreads; ++i) {
-        const int c = threadIdx.x + i * kThreads;
-        lg[i] = c < n ? A.logits[c] : 0.0f;
+    for (int i = 0; i < NPL; ++i) {
+        const int c = lane + 64 * i;
+        lg[i] = A.logits[c < n ? c : 0];
     }
-    combine_input(A, xs, nb * 32);
 #pragma unroll
-    for (int i = 0; i < kMaxRouteExperts / kThreads; ++i) {
-        const int c = threadIdx.x + i * kThreads;
-        if (c < n) {
-            s_val[c] = route_key(lg[i]);
-            s_rank[c] = 0;
+    for (int i = 0; i < NPL; ++i) {
+        const int c = lane + 64 * i;
+        sl[i] = map ? map[c < n ? c : 0] : c;
+    }
+    const int k0 = A.x_in ? 1 : (A.top_k < 4 ? A.top_k : 4);
+    float yv[kChunks][4][8];
+#pragma unroll
+    for (int h = 0; h < kChunks; ++h) {
+        const int e0 = (threadIdx.x + h * kDownThreads) * 8;
+        const int ec = e0 < nb * 32 ? e0 : 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int jj = j < k0 ? j : 0;
+            const float * src = A.x_in ? A.x_in + ec : A.prev_y + static_cast<int64_t>(jj) * nb * 32 + ec;
+            const float4 lo = *reinterpret_cast<const float4 *>(src);
+            const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
+            yv[h][j][0] = lo.x; yv[h][j][1] = lo.y; yv[h][j][2] = lo.z; yv[h][j][3] = lo.w;
+            yv[h][j][4] = hi.x; yv[h][j][5] = hi.y; yv[h][j][6] = hi.z; yv[h][j][7] = hi.w;
         }
     }
-    block_topk<kThreads>(n, A.top_k, s_val, s_rank, s_ids);
-    const int expert = s_ids[rank];
-    const int slot = A.expert_to_slot ? A.expert_to_slot[expert] : expert;
+
+    // 2. this wave's routing; the slot of the pick at `rank`
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) lg[i] = route_key(lg[i]);
+    float sel_v;
+    int sel_i;
+    wave_topk_regs<NPL>(lg, n, A.top_k, sel_v, sel_i);
+    const int expert = __builtin_amdgcn_readlane(sel_i, rank);
+    int sv = sl[0];
+#pragma unroll
+    for (int i = 1; i < NPL; ++i)
+        if ((expert >> 6) == i) sv = sl[i];
+    const int slot = __builtin_amdgcn_readlane(sv, expert & 63);
+
+    // 3. the weight stream: tile meta, the ring, the tail, the bias
     const bool slot_ok = slot >= 0 && slot < S.n_slots;
-    const int tile = pair * 2 + (lane >> 5);
-    const bool live = slot_ok && tile * 32 < S.rows;
     const uint8_t * slot_base = A.bank + static_cast<size_t>(slot_ok ? slot : 0) * S.slot_bytes;
-    const uint8_t * codes_tile = slot_base + static_cast<size_t>(live ? tile : 0) * 32 * nb * (TYPE == 39 ? 16 : 32);
+    const uint8_t * codes_tile = slot_base + static_cast<size_t>(tile) * 32 * nb * (TYPE == 39 ? 16 : 32);
     const int mbytes = meta_tile_bytes<TYPE>(nb);
     u32x4 mst[2];
-    load_meta<kThreads>(mst, slot_base + S.codes_bytes + static_cast<size_t>(pair) * 2 * mbytes, slot_ok ? 2 * mbytes : 0);
+    load_meta<kDownThreads>(mst, slot_base + S.codes_bytes + static_cast<size_t>(tile) * mbytes, slot_ok ? mbytes : 0);
     Group ring[D];
     Tail tl;
-    preload_ring<TYPE, D, true>(ring, codes_tile, nullptr, k, r, nb, live);
-    preload_tail<TYPE, true>(tl, codes_tile, nullptr, k, r, nb, live);
+    preload_ring<TYPE, D, true>(ring, codes_tile, nullptr, k, r, nb, slot_ok);
+    preload_tail<TYPE, true>(tl, codes_tile, nullptr, k, r, nb, slot_ok);
     const int grow = static_cast<int>(ggml_row(static_cast<int64_t>(tile) * 32 + r, S.rows, S.interleave));
     float bias_v = 0.0f;
-    if (k == 0 && live && A.bias) bias_v = A.bias[static_cast<size_t>(expert) * S.rows + grow];
+    if (k == 0 && slot_ok && A.bias) bias_v = A.bias[static_cast<size_t>(expert) * S.rows + grow];
 
-    quantize_input<TYPE>(xs, act, A.lay, nb);
-    store_meta<kThreads>(mst, lmeta, 2 * mbytes);
+    // 4. the layer input, combined in rank order, quantized into the activation row (the routing
+    // weights are read only now: their scalar loads would otherwise hold up the routing's waits)
+    float wv[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if (!A.x_in) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (j < k0) wv[j] = A.prev_w[j];
+    }
+#pragma unroll
+    for (int h = 0; h < kChunks; ++h) {
+        const int t = threadIdx.x + h * kDownThreads;
+        const int e0 = t * 8;
+        if (e0 < nb * 32) {
+            float x[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = yv[h][0][i];
+            if (!A.x_in) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (j < k0) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            const float term = yv[h][j][i] * wv[j];
+                            x[i] = j == 0 ? term : x[i] + term;
+                        }
+                    }
+                for (int j = 4; j < A.top_k; ++j) {
+                    const float * src = A.prev_y + static_cast<int64_t>(j) * nb * 32 + e0;
+                    const float w = A.prev_w[j];
+                    const float4 lo = *reinterpret_cast<const float4 *>(src);
+                    const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
+                    const float y[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) x[i] = x[i] + y[i] * w;
+                }
+            }
+            quantize_x8<TYPE>(x, t, act, A.lay, nb);
+        }
+    }
+    store_meta<kDownThreads>(mst, lmeta, mbytes);
     __syncthreads();
-    build_scales<TYPE, kThreads, 2>(lscale, lmeta, reinterpret_cast<const float *>(act + A.lay.da_offset()), nb, mbytes);
+    build_scales<TYPE, kDownThreads, 1>(lscale, lmeta, reinterpret_cast<const float *>(act + A.lay.da_offset()), nb, mbytes);
     __syncthreads();
     float acc[2] = {0.0f, 0.0f};
-    decode_stream<TYPE, D>(ring, tl, codes_tile, k, r, nb, live, act + static_cast<int64_t>(k) * nb * A.lay.code_entry(),
-                           lscale + ((lane >> 5) * ((nb + 3) / 4) * 32 + r) * 4, acc);
-    red[k][lane] = acc[0] + acc[1];
+    decode_stream<TYPE, D>(ring, tl, codes_tile, k, r, nb, slot_ok, act + static_cast<int64_t>(k) * nb * A.lay.code_entry(),
+                           lscale + r * 4, acc);
+    red[k][r] = acc[0] + acc[1];
     __syncthreads();
-    if (k == 0) {
-        float v = lane_tree(&red[0][lane]);
+    if (threadIdx.x < 32) {
+        const float * l = &red[0][r];
+        const float s0 = l[4 * 32] + l[0], s1 = l[5 * 32] + l[1 * 32];
+        const float s2 = l[6 * 32] + l[2 * 32], s3 = l[7 * 32] + l[3 * 32];
+        float v = (s0 + s2) + (s1 + s3);           // lane_tree over slices 32 floats apart
         if (A.bias) v = v + bias_v;
-        vals[lane] = v;
+        red[0][r] = v;                              // rows r: 0..15 gate, 16..31 up
     }
     __syncthreads();
-    if (k == 0) {
-        if (lane < 32 && slot_ok)
-            glu_requant_block(vals, lane, pair, A.act_rows + static_cast<size_t>(rank) * A.act_lay.stride(), A.act_lay,
-                              A.activation, A.alpha, A.limit);
-        if (pair == 0 && rank == 0) {
-            const float w = route_softmax(s_val, s_ids, A.top_k, lane);
-            if (lane < A.top_k) {
-                A.route_ids[lane] = s_ids[lane];
-                A.route_w[lane] = w;
-            }
+    if (threadIdx.x < 16) {
+        float g = glu(A.activation, red[0][threadIdx.x], red[0][threadIdx.x + 16], A.alpha, A.limit);
+        if (!slot_ok) g = __builtin_nanf("");      // expert not resident in this bank: loud output
+        A.act_f[static_cast<size_t>(rank) * (S.rows / 2) + tile * 16 + threadIdx.x] = g;
+    }
+    if (threadIdx.x < 64 && tile == 0 && rank == 0) {
+        const float w = wave_pick_softmax(sel_v, A.top_k);
+        int ps = 0;                               // lane j: slot of pick j
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            const int v = __shfl(sl[i], sel_i & 63);
+            if ((sel_i >> 6) == i) ps = v;
+        }
+        if (lane < A.top_k) {
+            A.route_ids[lane] = sel_i;
+            A.route_w[lane] = w;
+            if (A.route_slots) A.route_slots[lane] = ps;
         }
     }
 }
@@ -814,14 +893,17 @@ struct DecodeDownArgs {
     Shape shape;
     const int32_t * expert_to_slot;
     XrowLayout lay;            // down activation format (nb = intermediate / 32)
-    const uint8_t * act_rows;  // [top_k] activation rows written by kernel A
+    const float * act_f;       // [top_k][intermediate] GLU outputs written by kernel A
     const int32_t * route_ids; // [top_k]
+    const int32_t * route_slots;  // [top_k] slots written by kernel A (same map), or null
     const float * bias;        // down bias [n_expert][rows] or null
     float * y;                 // [top_k][rows]
 };
 
 // Kernel B: one 32-row tile of one rank; wave w holds lane slices 2w (lanes 0..31) and 2w + 1
-// (lanes 32..63) of the tile's rows.
+// (lanes 32..63) of the tile's rows. Its prologue requantizes the rank's GLU outputs (x86
+// quantize_row_q8_0 per 32-element block, the arithmetic of the reference's activation
+// quantization) into the LDS activation row while its weight stream is in flight.
 template <int TYPE>
 __global__ __launch_bounds__(kDownThreads) void decode_down_kernel(DecodeDownArgs A) {
     constexpr int D = down_depth<TYPE>();
@@ -835,19 +917,22 @@ __global__ __launch_bounds__(kDownThreads) void decode_down_kernel(DecodeDownArg
     const int lane = threadIdx.x & 63, r = lane & 31;
     const int k = (threadIdx.x >> 6) * 2 + (lane >> 5);
     const int tile = blockIdx.x, rank = blockIdx.y;
-    // The activation row (independent of the routing) is loaded together with the expert id.
-    const int copy_bytes = static_cast<int>(A.lay.flag_offset());   // codes + block scales
-    const uint8_t * xr = A.act_rows + static_cast<size_t>(rank) * A.lay.stride();
-    u32x4 stage[3];
+    // The GLU outputs (independent of the routing) are loaded together with the expert id.
+    constexpr int kChunks = 2;                     // 8-element chunks per thread (intermediate <= 4096)
+    const float * xf = A.act_f + static_cast<size_t>(rank) * nb * 32;
+    float xq[kChunks][8];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        const int off = (threadIdx.x + i * kDownThreads) * 16;
-        stage[i] = u32x4{0u, 0u, 0u, 0u};
-        if (off + 16 <= copy_bytes) stage[i] = *reinterpret_cast<const u32x4 *>(xr + off);
-        else if (off < copy_bytes) stage[i].xy = *reinterpret_cast<const u32x2 *>(xr + off);   // 8-byte remainder
+    for (int h = 0; h < kChunks; ++h) {
+        const int e0 = (threadIdx.x + h * kDownThreads) * 8;
+        const int ec = e0 < nb * 32 ? e0 : 0;
+        const float4 lo = *reinterpret_cast<const float4 *>(xf + ec);
+        const float4 hi = *reinterpret_cast<const float4 *>(xf + ec + 4);
+        xq[h][0] = lo.x; xq[h][1] = lo.y; xq[h][2] = lo.z; xq[h][3] = lo.w;
+        xq[h][4] = hi.x; xq[h][5] = hi.y; xq[h][6] = hi.z; xq[h][7] = hi.w;
     }
     const int expert = as_const<int32_t>(A.route_ids)[rank];
-    const int slot = A.expert_to_slot ? as_const<int32_t>(A.expert_to_slot)[expert] : expert;
+    const int slot = A.route_slots ? as_const<int32_t>(A.route_slots)[rank]
+                                   : (A.expert_to_slot ? as_const<int32_t>(A.expert_to_slot)[expert] : expert);
     const bool slot_ok = slot >= 0 && slot < S.n_slots;
     const uint8_t * slot_base = A.bank + static_cast<size_t>(slot_ok ? slot : 0) * S.slot_bytes;
     const uint8_t * codes_tile = slot_base + static_cast<size_t>(tile) * 32 * nb * (TYPE == 39 ? 16 : 32);
@@ -862,10 +947,9 @@ __global__ __launch_bounds__(kDownThreads) void decode_down_kernel(DecodeDownArg
     float bias_v = 0.0f;
     if (k == 0 && slot_ok && A.bias) bias_v = A.bias[static_cast<size_t>(expert) * S.rows + row];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        const int off = (threadIdx.x + i * kDownThreads) * 16;
-        if (off + 16 <= copy_bytes) *reinterpret_cast<u32x4 *>(act + off) = stage[i];
-        else if (off < copy_bytes) *reinterpret_cast<u32x2 *>(act + off) = stage[i].xy;
+    for (int h = 0; h < kChunks; ++h) {
+        const int t = threadIdx.x + h * kDownThreads;
+        if (t * 8 < nb * 32) quantize_x8<TYPE>(xq[h], t, act, A.lay, nb);
     }
     store_meta<kDownThreads>(mst, lmeta, mbytes);
     __syncthreads();
@@ -888,21 +972,28 @@ __global__ __launch_bounds__(kDownThreads) void decode_down_kernel(DecodeDownArg
     }
 }
 
-template <int TYPE>
-void launch_decode_typed(const DecodeArgs & a, hipStream_t stream) {
-    const size_t lds = gate_up_lds_bytes<TYPE>(a.shape.nb);
+template <int TYPE, int NPL>
+void launch_gate_up_npl(const DecodeArgs & a, dim3 grid, size_t lds, hipStream_t stream) {
     if (lds > 65536)
-        check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_gate_up_kernel<TYPE>),
+        check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_gate_up_kernel<TYPE, NPL>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)),
                   "decode gate_up LDS attribute");
-    const dim3 grid(static_cast<unsigned>(a.shape.rows / 64), static_cast<unsigned>(a.top_k));
-    hipLaunchKernelGGL((decode_gate_up_kernel<TYPE>), grid, dim3(kThreads), lds, stream, a);
+    hipLaunchKernelGGL((decode_gate_up_kernel<TYPE, NPL>), grid, dim3(kDownThreads), lds, stream, a);
+}
+
+template <int TYPE>
+void launch_decode_typed(const DecodeArgs & a, hipStream_t stream) {
+    const size_t lds = decode_lds_bytes<TYPE>(a.shape.nb);
+    const dim3 grid(static_cast<unsigned>(a.shape.rows / 32), static_cast<unsigned>(a.top_k));
+    if (a.n_expert <= 128) launch_gate_up_npl<TYPE, 2>(a, grid, lds, stream);
+    else if (a.n_expert <= 256) launch_gate_up_npl<TYPE, 4>(a, grid, lds, stream);
+    else launch_gate_up_npl<TYPE, 16>(a, grid, lds, stream);
     check_hip(hipGetLastError(), "decode gate_up launch");
 }
 
 template <int TYPE>
 void launch_decode_down_typed(const DecodeDownArgs & a, int top_k, hipStream_t stream) {
-    const size_t lds = down_lds_bytes<TYPE>(a.shape.nb);
+    const size_t lds = decode_lds_bytes<TYPE>(a.shape.nb);
     const dim3 grid(static_cast<unsigned>(a.shape.rows / 32), static_cast<unsigned>(top_k));
     hipLaunchKernelGGL((decode_down_kernel<TYPE>), grid, dim3(kDownThreads), lds, stream, a);
     check_hip(hipGetLastError(), "decode down launch");
@@ -1052,8 +1143,6 @@ void launch_decode_gate_up(const DecodeGateUpArgs & d, hipStream_t stream) {
     require(d.top_k >= 1 && d.top_k <= 64 && d.n_expert >= d.top_k && d.n_expert <= kMaxRouteExperts,
             "routing shape out of range");
     require(d.hidden == bank.k && d.hidden <= 4096, "hidden size mismatch");
-    require(d.act_layout.nb == bank.rows / 64 && d.act_layout.weight_type == bank.type,
-            "down activation layout does not match the gate_up bank");
     require(d.x_in != nullptr || (d.prev_y != nullptr && d.prev_w != nullptr), "decode layer input missing");
     DecodeArgs a{};
     a.bank = bank.base;
@@ -1068,10 +1157,10 @@ void launch_decode_gate_up(const DecodeGateUpArgs & d, hipStream_t stream) {
     a.prev_y = d.prev_y;
     a.prev_w = d.prev_w;
     a.bias = d.bias;
-    a.act_rows = d.act_rows;
-    a.act_lay = d.act_layout;
+    a.act_f = d.act_f;
     a.route_ids = d.route_ids;
     a.route_w = d.route_w;
+    a.route_slots = d.route_slots;
     a.activation = d.activation;
     a.alpha = d.alpha;
     a.limit = d.limit;
@@ -1090,8 +1179,9 @@ void launch_decode_down(const DecodeDownParams & d, hipStream_t stream) {
                     bank.geometry().codes_bytes(), bank.n_slots};
     a.expert_to_slot = d.expert_to_slot;
     a.lay = d.act_layout;
-    a.act_rows = d.act_rows;
+    a.act_f = d.act_f;
     a.route_ids = d.route_ids;
+    a.route_slots = d.route_slots;
     a.bias = d.bias;
     a.y = d.y;
     if (bank.type == VBM_TYPE_MXFP4) launch_decode_down_typed<39>(a, static_cast<int>(d.top_k), stream);

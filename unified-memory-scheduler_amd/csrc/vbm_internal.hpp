@@ -192,10 +192,10 @@ struct DecodeGateUpArgs {
     const float * prev_y;
     const float * prev_w;
     const float * bias;
-    uint8_t * act_rows;
-    XrowLayout act_layout;
+    float * act_f;                    // [top_k][intermediate] GLU outputs for kernel B
     int32_t * route_ids;
     float * route_w;
+    int32_t * route_slots;            // [top_k] slots of the picks for kernel B, or null
     int activation;
     float alpha, limit;
 };
@@ -205,9 +205,10 @@ void launch_decode_gate_up(const DecodeGateUpArgs & d, hipStream_t stream);
 struct DecodeDownParams {
     const vbm_bank * bank;
     const int32_t * expert_to_slot;
-    const uint8_t * act_rows;         // [top_k] activation rows from kernel A
+    const float * act_f;              // [top_k][intermediate] GLU outputs from kernel A
     XrowLayout act_layout;
     const int32_t * route_ids;        // [top_k]
+    const int32_t * route_slots;      // [top_k] from kernel A with the same expert_to_slot, or null
     int64_t top_k;
     const float * bias;               // [n_expert][hidden] or null
     float * y;                        // [top_k][hidden]

@@ -14,7 +14,8 @@ struct vbm_decode_plan {
     uint8_t * workspace = nullptr;
     int32_t * route_ids = nullptr;   // [L][K]
     float * route_w = nullptr;       // [L][K]
-    uint8_t * act_rows = nullptr;    // [K] down activation rows
+    int32_t * route_slots = nullptr; // [L][K] bank slots of the picks (kernel A -> kernel B)
+    float * act_f = nullptr;         // [K][I] GLU outputs (kernel A -> kernel B)
     XrowLayout act_layout{};
     float * y = nullptr;             // [K][H]
 };
@@ -452,14 +453,15 @@ vbm_status vbm_decode_plan_create(const vbm_moe_layer_desc * layers, int64_t n_l
         plan->act_layout = XrowLayout{plan->I / 32, layers[0].down->type};
         const size_t route = align_up(sizeof(int32_t) * plan->L * plan->K);
         const size_t weights = align_up(sizeof(float) * plan->L * plan->K);
-        const size_t act = align_up(static_cast<size_t>(plan->K * plan->act_layout.stride()));
+        const size_t act = align_up(sizeof(float) * plan->K * plan->I);
         const size_t y = align_up(sizeof(float) * plan->K * plan->H);
-        check_hip(hipMalloc(reinterpret_cast<void **>(&plan->workspace), route + weights + act + y),
+        check_hip(hipMalloc(reinterpret_cast<void **>(&plan->workspace), 2 * route + weights + act + y),
                   "decode plan workspace");
         uint8_t * p = plan->workspace;
         plan->route_ids = reinterpret_cast<int32_t *>(p); p += route;
+        plan->route_slots = reinterpret_cast<int32_t *>(p); p += route;
         plan->route_w = reinterpret_cast<float *>(p); p += weights;
-        plan->act_rows = p; p += act;
+        plan->act_f = reinterpret_cast<float *>(p); p += act;
         plan->y = reinterpret_cast<float *>(p);
         *out = plan.release();
     });
@@ -492,10 +494,10 @@ void decode_launch_a(const vbm_decode_plan * plan, int64_t l, const float * x, c
     a.prev_y = plan->y;
     a.prev_w = l == 0 ? nullptr : plan->route_w + (l - 1) * K;
     a.bias = d.gate_up_bias;
-    a.act_rows = plan->act_rows;
-    a.act_layout = plan->act_layout;
+    a.act_f = plan->act_f;
     a.route_ids = plan->route_ids + l * K;
     a.route_w = plan->route_w + l * K;
+    a.route_slots = plan->route_slots + l * K;
     a.activation = d.activation;
     a.alpha = 1.702f;
     a.limit = 7.0f;
@@ -507,9 +509,10 @@ void decode_launch_b(const vbm_decode_plan * plan, int64_t l, hipStream_t s) {
     DecodeDownParams b{};
     b.bank = d.down;
     b.expert_to_slot = d.expert_to_slot;
-    b.act_rows = plan->act_rows;
+    b.act_f = plan->act_f;
     b.act_layout = plan->act_layout;
     b.route_ids = plan->route_ids + l * plan->K;
+    b.route_slots = plan->route_slots + l * plan->K;
     b.top_k = plan->K;
     b.bias = d.down_bias;
     b.y = plan->y;

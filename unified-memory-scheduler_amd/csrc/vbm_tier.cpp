@@ -39,7 +39,7 @@ struct vbm_tier {
     uint8_t * workspace = nullptr;
     int32_t * route_ids = nullptr;    // [L][K]
     float * route_w = nullptr;        // [L][K]
-    uint8_t * act_rows = nullptr;
+    float * act_f = nullptr;          // [K][I] GLU outputs (kernel A -> kernel B)
     XrowLayout act_layout{};
     float * y = nullptr;
     std::vector<const float *> gu_bias, dn_bias;
@@ -125,13 +125,13 @@ vbm_status vbm_tier_create(const vbm_tier_desc * d, vbm_tier ** out) {
         check_hip(hipEventCreate(&t->copy_end), "tier event");
         t->act_layout = XrowLayout{I / 32, d->type};
         const size_t route = align_up(sizeof(int32_t) * L * K), wts = align_up(sizeof(float) * L * K);
-        const size_t act = align_up(static_cast<size_t>(K * t->act_layout.stride()));
+        const size_t act = align_up(sizeof(float) * K * I);
         const size_t y = align_up(sizeof(float) * K * H);
         check_hip(hipMalloc(reinterpret_cast<void **>(&t->workspace), route + wts + act + y), "tier workspace");
         uint8_t * p = t->workspace;
         t->route_ids = reinterpret_cast<int32_t *>(p); p += route;
         t->route_w = reinterpret_cast<float *>(p); p += wts;
-        t->act_rows = p; p += act;
+        t->act_f = reinterpret_cast<float *>(p); p += act;
         t->y = reinterpret_cast<float *>(p);
         t->gu_bias.assign(static_cast<size_t>(L), nullptr);
         t->dn_bias.assign(static_cast<size_t>(L), nullptr);
@@ -263,8 +263,7 @@ vbm_status vbm_tier_step(vbm_tier * t, const float * x, const float * logits, fl
             a.prev_y = t->y;
             a.prev_w = l == 0 ? nullptr : t->route_w + (l - 1) * K;
             a.bias = t->gu_bias[l];
-            a.act_rows = t->act_rows;
-            a.act_layout = t->act_layout;
+            a.act_f = t->act_f;
             a.route_ids = t->route_ids + l * K;
             a.route_w = t->route_w + l * K;
             a.activation = d.activation;
@@ -274,7 +273,7 @@ vbm_status vbm_tier_step(vbm_tier * t, const float * x, const float * logits, fl
             DecodeDownParams b{};
             b.bank = t->down;
             b.expert_to_slot = t->dev_map;
-            b.act_rows = t->act_rows;
+            b.act_f = t->act_f;
             b.act_layout = t->act_layout;
             b.route_ids = t->route_ids + l * K;
             b.top_k = K;
