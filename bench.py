@@ -404,12 +404,12 @@ def main() -> int:
         gu_avg_us = dn_avg_us = float("nan")
     last_ids = np.stack([np.lexsort((np.arange(E), -logits_host[n_steps - 1, l, 0]))[:K] for l in range(L)])
     # Algorithmic bytes per launch of kernel A: K experts x (5760 rows x 1530 B + 5760 fp32 biases)
-    # + logits (E x 4 B) + previous layer outputs (K x 2880 x 4 B) + Q8_0 down activations out
-    # (K x 3060 B). Kernel B: K experts x (2880 x 1530 B + 2880 x 4 B) + activations in (K x 3060 B)
+    # + logits (E x 4 B) + previous layer outputs (K x 2880 x 4 B) + fp32 GLU outputs (K x 2880 x
+    # 4 B). Kernel B: K experts x (2880 x 1530 B + 2880 x 4 B) + GLU outputs in (K x 2880 x 4 B)
     # + outputs (K x 2880 x 4 B).
     mean_distinct = distinct_experts(last_ids.reshape(L, K)) / L
-    gu_bytes = mean_distinct * (2 * I * MXFP4_ROW_BYTES + 2 * I * 4) + E * 4 + K * H * 4 + K * (I // 32) * 34
-    dn_bytes = mean_distinct * (H * MXFP4_ROW_BYTES + H * 4) + K * (I // 32) * 34 + K * H * 4
+    gu_bytes = mean_distinct * (2 * I * MXFP4_ROW_BYTES + 2 * I * 4) + E * 4 + K * H * 4 + K * I * 4
+    dn_bytes = mean_distinct * (H * MXFP4_ROW_BYTES + H * 4) + K * I * 4 + K * H * 4
     gu_gbs = gu_bytes / (gu_avg_us * 1e-6) / 1e9
     dn_gbs = dn_bytes / (dn_avg_us * 1e-6) / 1e9
 
@@ -451,7 +451,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_gate_up_kernel<MXFP4> (routing + combine + Q8_0 + gate_up GEMV + bias + SwiGLU-OAI + requant)",
+            "kernel": "decode_gate_up_kernel<MXFP4> (routing + combine + Q8_0 + gate_up GEMV + bias + SwiGLU-OAI)",
             "achieved": num(gu_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

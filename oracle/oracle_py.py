@@ -37,6 +37,9 @@ def load() -> C.CDLL:
             "orc_quantize_row_q8_0": ([vp, vp, i64], None),
             "orc_vec_dot_mxfp4_q8_0": ([C.c_int, vp, vp], C.c_float),
             "orc_mxfp4_block_lanes": ([vp, vp, vp], C.c_int32),
+            "orc_pack_mxfp4x8": ([vp, i64, i64, vp], None),
+            "orc_unpack_mxfp4x8": ([vp, i64, i64, vp], None),
+            "orc_gemv_mxfp4x8_q8_0": ([C.c_int, vp, vp, vp, C.c_int], C.c_int),
             "orc_vec_dot_q8_0_q8_0": ([C.c_int, vp, vp], C.c_float),
             "orc_q8_block_lanes": ([vp, vp, vp], C.c_int32),
             "orc_vec_dot_f32": ([C.c_int, vp, vp], C.c_float),
@@ -82,6 +85,31 @@ def mul_mat_id(type_id, as_bytes, k, rows, n_as, b_type, b, b_ne1, ids, n_ids, n
     if status != 0:
         raise ValueError("oracle mul_mat_id rejected its inputs")
     return dst
+
+
+def pack_mxfp4x8(raw: np.ndarray, rows: int, blocks: int) -> np.ndarray:
+    """block_mxfp4 rows [rows][blocks] (17 B each) -> block_mxfp4x8 groups (136 B each)."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.empty(rows // 8 * blocks * 136, np.uint8)
+    load().orc_pack_mxfp4x8(_p(raw), rows, blocks, _p(out))
+    return out
+
+
+def unpack_mxfp4x8(packed: np.ndarray, rows: int, blocks: int) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    out = np.empty(rows * blocks * 17, np.uint8)
+    load().orc_unpack_mxfp4x8(_p(packed), rows, blocks, _p(out))
+    return out
+
+
+def gemv_mxfp4x8(packed: np.ndarray, act_q8: np.ndarray, k: int, rows: int) -> np.ndarray:
+    """Repacked 8x8 contract: one Q8_0 activation row against `rows` packed rows."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    act_q8 = np.ascontiguousarray(act_q8, dtype=np.uint8)
+    out = np.empty(rows, np.float32)
+    if load().orc_gemv_mxfp4x8_q8_0(k, _p(out), _p(packed), _p(act_q8), rows) != 0:
+        raise ValueError("repacked GEMV needs k % 64 == 0 and rows % 8 == 0")
+    return out
 
 
 def group_by_expert(ids: np.ndarray, n_ids: int, n_tokens: int, ids_stride: int, n_as: int):

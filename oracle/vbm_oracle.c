@@ -150,6 +150,101 @@ float orc_vec_dot_mxfp4_q8_0(int n, const void * vx, const void * vy) {
     return hsum8(lanes);
 }
 
+/* ------------------------------------------------------------------ repacked 8x8 contract (a8) */
+/* block_mxfp4x8 {u8 e[8]; u8 qs[128]} for eight consecutive rows: e[r] is row r's exponent and
+ * qs[(c*8 + r)*8 + j] is row r's qs[c*8 + j] (c = 0, 1). orc_unpack_mxfp4x8 restates the expert
+ * export at HP:751-762; orc_pack_mxfp4x8 is its inverse. Rows must be a multiple of 8. */
+void orc_unpack_mxfp4x8(const void * vpacked, int64_t rows, int64_t blocks, void * vraw) {
+    const uint8_t * packed = (const uint8_t *)vpacked;
+    uint8_t * raw = (uint8_t *)vraw;
+    for (int64_t row = 0; row < rows; row += 8)
+        for (int64_t block = 0; block < blocks; ++block) {
+            const uint8_t * group = packed + ((row / 8) * blocks + block) * 136;
+            for (int r = 0; r < 8; ++r) {
+                uint8_t * result = raw + ((row + r) * blocks + block) * 17;
+                result[0] = group[r];
+                for (int chunk = 0; chunk < 2; ++chunk) memcpy(result + 1 + chunk * 8, group + 8 + (chunk * 8 + r) * 8, 8);
+            }
+        }
+}
+
+void orc_pack_mxfp4x8(const void * vraw, int64_t rows, int64_t blocks, void * vpacked) {
+    const uint8_t * raw = (const uint8_t *)vraw;
+    uint8_t * packed = (uint8_t *)vpacked;
+    for (int64_t row = 0; row < rows; row += 8)
+        for (int64_t block = 0; block < blocks; ++block) {
+            uint8_t * group = packed + ((row / 8) * blocks + block) * 136;
+            for (int r = 0; r < 8; ++r) {
+                const uint8_t * src = raw + ((row + r) * blocks + block) * 17;
+                group[r] = src[0];
+                for (int chunk = 0; chunk < 2; ++chunk) memcpy(group + 8 + (chunk * 8 + r) * 8, src + 1 + chunk * 8, 8);
+            }
+        }
+}
+
+/* One dword lane of tools/trace/exact_packed_cpu.h:33-50 for row r: the four bytes j0..j0+3 of the
+ * row's 8-byte chunk `c` (low or high nibbles) against activation codes act[a0..a0+3]: dpbusd of
+ * |w| with the activation negated where w < 0 (byte wrap keeps -(-128) == -128, :34-39). */
+static int32_t packed_lane(const uint8_t * group, int r, int chunk, int high, int j0, const int8_t * act) {
+    int32_t sum = 0;
+    for (int j = 0; j < 4; ++j) {
+        const uint8_t byte = group[8 + (chunk * 8 + r) * 8 + j0 + j];
+        const int w = kMxfp4Values[high ? byte >> 4 : byte & 15];
+        int a = act[j];
+        if (w < 0) a = a == -128 ? -128 : -a;
+        sum += abs(w) * a;
+    }
+    return sum;
+}
+
+/* ggml_gemv_mxfp4_8x8_q8_0 as restated at tools/trace/exact_packed_cpu.h:52-88: one Q8_0
+ * activation row against eight-row tiles. Vector v of a tile carries, per row r, two dword lanes
+ * h = 0, 1 (activation codes 8v' + 4h.. with v' the activation octet of :56-57): v = 0 the low
+ * nibbles of chunk 0 against codes 0..7, v = 1 chunk 1 low against 8..15, v = 2 chunk 0 high
+ * against 16..23, v = 3 chunk 1 high against 24..31; per block s = fp16(d_a) * E8M0_HALF(e_r)
+ * (:14-24); even/odd block FMA chains e_v / o_v (:58-70); a..d = e_v + o_v; pairs = (c + a) +
+ * (d + b); output row r = pairs[2r] + pairs[2r + 1] (:71-76). n % 64 == 0, nc % 8 == 0 (:80). */
+int orc_gemv_mxfp4x8_q8_0(int n, float * out, const void * vpacked, const void * vact, int nc) {
+    if (n <= 0 || n % 64 || nc <= 0 || nc % 8) return -1;
+    const uint8_t * packed = (const uint8_t *)vpacked;
+    const uint8_t * act = (const uint8_t *)vact;
+    const int blocks = n / 32;
+    static const int kChunk[4] = {0, 1, 0, 1}, kHigh[4] = {0, 0, 1, 1}, kAct[4] = {0, 8, 16, 24};
+    for (int column = 0; column < nc; column += 8) {
+        float e[4][16], o[4][16];
+        memset(e, 0, sizeof(e));
+        memset(o, 0, sizeof(o));
+        for (int block = 0; block < blocks; block += 2) {
+            for (int par = 0; par < 2; ++par) {
+                const uint8_t * group = packed + ((size_t)(column / 8) * blocks + block + par) * 136;
+                const uint8_t * y = act + (size_t)(block + par) * 34;
+                const float da = orc_fp16_to_fp32((uint16_t)(y[0] | (y[1] << 8)));
+                const int8_t * q = (const int8_t *)(y + 2);
+                for (int v = 0; v < 4; ++v)
+                    for (int r = 0; r < 8; ++r) {
+                        const float d = da * orc_e8m0_half(group[r]);
+                        for (int h = 0; h < 2; ++h) {
+                            const int32_t lane = packed_lane(group, r, kChunk[v], kHigh[v], 4 * h, q + kAct[v] + 4 * h);
+                            float * acc = par ? &o[v][2 * r + h] : &e[v][2 * r + h];
+                            *acc = fmaf(d, (float)lane, *acc);
+                        }
+                    }
+            }
+        }
+        for (int r = 0; r < 8; ++r) {
+            float pairs[2];
+            for (int h = 0; h < 2; ++h) {
+                const int i = 2 * r + h;
+                const float a = e[0][i] + o[0][i], b = e[1][i] + o[1][i];
+                const float c = e[2][i] + o[2][i], d = e[3][i] + o[3][i];
+                pairs[h] = (c + a) + (d + b);
+            }
+            out[column + r] = pairs[0] + pairs[1];
+        }
+    }
+    return 0;
+}
+
 /* ------------------------------------------------------------------ Q8_0 x Q8_0 */
 /* Integer part of ggml_vec_dot_q8_0_q8_0 on x86 (mul_sum_i8_pairs: |x| times VPSIGNB(y, x),
  * pairwise maddubs then madd, i.e. lane l = elements 4l..4l+3; no saturation is reachable since

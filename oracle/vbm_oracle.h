@@ -100,6 +100,13 @@ int orc_moe_layer(const orc_layer * layer, const float * x, float * logits, int6
                   float * out, int32_t * ids, float * weights, float * act_out, float * y_out,
                   int threads);
 
+/* Secondary CPU contract (repacked 8x8, tools/trace/exact_packed_cpu.h:52-88): block_mxfp4x8
+ * packing of 8-row groups (inverse of the export at HP:751-762) and the one-row GEMV over it.
+ * out[nc] for nc rows (nc % 8 == 0); returns -1 on shapes the reference rejects (:80). */
+void orc_pack_mxfp4x8(const void * raw_rows, int64_t rows, int64_t blocks, void * packed);
+void orc_unpack_mxfp4x8(const void * packed, int64_t rows, int64_t blocks, void * raw_rows);
+int orc_gemv_mxfp4x8_q8_0(int n, float * out, const void * packed, const void * act, int nc);
+
 /* Fast (bit-identical) single-row dots used by orc_mul_mat_id when threads > 0. */
 int orc_fast_isa(void);  /* 0 scalar, 2 AVX2, 3 AVX-512 VNNI */
 

@@ -113,6 +113,34 @@ def test_mul_mat_id_mxfp4_adversarial_and_neg128(gpu, orc):
     bank.destroy()
 
 
+def test_mul_mat_id_mxfp4_matches_repacked_8x8_contract(gpu, orc):
+    """Row a8: the GPU's exact-order GEMV against the oracle's restatement of the repacked 8x8 CPU
+    contract (tools/trace/exact_packed_cpu.h:52-88) on block_mxfp4x8-packed copies of the same
+    experts (the packing the expert export at HP:751-762 inverts): bit-identical per row, with
+    the recipe of tests/test_exact_packed_cpu.cpp:55-72 (exponents 96 + r % 40, two rows at 0/1,
+    one activation code -128), for one and for several tokens."""
+    rng = np.random.default_rng(417)
+    experts, rows, n = 4, 64, 2880
+    blocks = n // 32
+    w = np.zeros((experts, rows, blocks, 17), np.uint8)
+    w[..., 0] = 96 + rng.integers(0, 40, (experts, rows, blocks))
+    w[..., 1:] = rng.integers(0, 256, (experts, rows, blocks, 16))
+    w[:, 0, 0, 0], w[:, 0, 1, 0] = 0, 1
+    bank = H.make_bank(H.MX, w.reshape(-1), experts, rows, n)
+    for tokens in (1, 3):
+        x = rng.uniform(-8, 8, (tokens, n)).astype(np.float32)
+        q = orc.quantize_q8_0(x).reshape(tokens, 1, -1)
+        q.reshape(-1)[2] = 0x80                                   # one activation code -128
+        ids = np.stack([rng.choice(experts, 2, replace=False) for _ in range(tokens)]).astype(np.int32)
+        got = H.mul_mat_id(bank, experts, q, gpu.TYPE_Q8_0, 1, ids, 2)
+        for t in range(tokens):
+            for r, e in enumerate(ids[t]):
+                packed = orc.pack_mxfp4x8(w[e].reshape(-1), rows, blocks)
+                ref = orc.gemv_mxfp4x8(packed, q[t, 0], n, rows)
+                assert H.bits_equal(got[t, r], ref), (tokens, t, r, H.diff_report(got[t, r], ref))
+    bank.destroy()
+
+
 @pytest.mark.parametrize("tokens", [1, 8, 64])
 def test_mul_mat_id_mxfp4_bitwise_config_shapes(gpu, orc, tokens):
     """Config 0/1 shapes: E=32, top-4, H=I=2880, down (2880 x 2880) and fused gate_up (5760 x 2880)."""

@@ -106,6 +106,68 @@ def test_mxfp4_dot_matches_reference_restatement_bits(orc):
     assert compared == 240
 
 
+def test_repacked_8x8_contract_equals_standard_bits(orc):
+    """Row a8. The reference's own tests/test_exact_packed_cpu.cpp:55-85 asserts that the repacked
+    8x8 GEMV (tools/trace/exact_packed_cpu.h:52-88) reproduces ggml_vec_dot_mxfp4_q8_0 bit for bit;
+    the same recipe here (n in {64, 256, 2880}, 8/16/64 rows, exponents 96 + r % 40 with rows 0/1
+    at exponents 0/1, Q8_0 activations of U(-8, 8) with one code -128) checks the oracle's
+    restatement of the repacked layout and tile against the reference's standard contract compiled
+    from cpu_mxfp4_vnni.cpp (oracle/_ref), or against the oracle's restatement of it when the
+    reference sources are absent. A lane-map, chunk or tree mistake in the repacked restatement
+    changes bits here."""
+    lib = orc.load()
+    native = None
+    if orc.REF_VNNI.exists():
+        ref = C.CDLL(str(orc.REF_VNNI))
+        native = ref.ggml_vec_dot_mxfp4_q8_0
+        native.argtypes = [C.c_int, C.POINTER(C.c_float), C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p,
+                           C.c_size_t, C.c_int]
+        native.restype = None
+    rng = np.random.default_rng(417)
+    checks = 0
+    for n in (64, 256, 2880):
+        blocks = n // 32
+        for columns in (8, 16, 64):
+            w = np.zeros((columns, blocks, 17), np.uint8)
+            w[:, :, 0] = 96 + rng.integers(0, 40, (columns, blocks))
+            w[:, :, 1:] = rng.integers(0, 256, (columns, blocks, 16))
+            w[0, 0, 0], w[0, 1, 0] = 0, 1
+            x = rng.uniform(-8, 8, n).astype(np.float32)
+            act = orc.quantize_q8_0(x.reshape(1, n)).reshape(-1).copy()
+            act[2] = 0x80                                       # activations[0].qs[0] = -128
+            packed = orc.pack_mxfp4x8(w.reshape(-1), columns, blocks)
+            actual = orc.gemv_mxfp4x8(packed, act, n, columns)
+            expected = np.empty(columns, np.float32)
+            for c in range(columns):
+                row = np.ascontiguousarray(w[c].reshape(-1))
+                if native is not None:
+                    out = C.c_float()
+                    native(n, C.byref(out), 0, row.ctypes.data, 0, act.ctypes.data, 0, 1)
+                    expected[c] = out.value
+                else:
+                    expected[c] = lib.orc_vec_dot_mxfp4_q8_0(n, row.ctypes.data, act.ctypes.data)
+            assert expected.tobytes() == actual.tobytes(), (n, columns)
+            checks += 1
+    assert checks == 9
+
+
+def test_repacked_layout_round_trip_and_shapes(orc):
+    """orc_unpack_mxfp4x8 restates the expert export of HP:751-762; packing then exporting is the
+    identity on raw block_mxfp4 rows, and the GEMV rejects what exact_packed_cpu.h:80 rejects."""
+    rng = np.random.default_rng(5)
+    raw = rng.integers(0, 256, 24 * 7 * 17).astype(np.uint8)
+    packed = orc.pack_mxfp4x8(raw, 24, 7)
+    assert packed.size == 3 * 7 * 136
+    assert np.array_equal(orc.unpack_mxfp4x8(packed, 24, 7), raw)
+    group = packed[:136]                                    # rows 0..7, block 0
+    assert list(group[:8]) == [raw[r * 7 * 17] for r in range(8)]
+    assert bytes(group[8 + (1 * 8 + 3) * 8: 8 + (1 * 8 + 3) * 8 + 8]) == bytes(raw[3 * 7 * 17 + 1 + 8: 3 * 7 * 17 + 17])
+    act = np.zeros(2 * 34, np.uint8)
+    for n, rows in ((32, 8), (64, 12)):
+        with pytest.raises(ValueError):
+            orc.gemv_mxfp4x8(np.zeros(136 * 4, np.uint8), act, n, rows)
+
+
 def test_mxfp4_block_lanes_brute_force(orc):
     lib = orc.load()
     rng = np.random.default_rng(5)

@@ -133,8 +133,9 @@ struct GemmStage {
     static constexpr int RB = CB * 32 * EB + 16;                        // LDS bytes per job row
     static constexpr int ACT = kJobTile * RB;
     static constexpr int DA = kJobTile * CB * 4;
-    static constexpr int W = 2 * 4096;
-    static constexpr int M = 2 * 256;
+    static constexpr int WT = 8 * (512 + 16);                          // one tile's group, slices padded
+    static constexpr int W = 2 * WT;
+    static constexpr int M = TYPE == 39 ? 2 * 256 : 2 * 32 * 4 * 4;    // exponents, or fp32 Q8_0 scales
     static constexpr int ACT_PIECES = kJobTile * CB * 32 * EB / 16 / kGemmThreads;   // per thread
     static constexpr int W_PIECES = W / 16 / kGemmThreads;
     static constexpr int OFF_DA = 2 * ACT, OFF_W = OFF_DA + 2 * DA, OFF_M = OFF_W + 2 * W;
@@ -257,9 +258,32 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
     };
     auto store_w = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < G::W_PIECES; ++i)
-            *reinterpret_cast<u32x4g *>(lds + G::OFF_W + buf * G::W + 16 * (threadIdx.x + i * kGemmThreads)) = st_w[i];
-        if (threadIdx.x < 32) *reinterpret_cast<u32x4g *>(lds + G::OFF_M + buf * G::M + 16 * threadIdx.x) = st_m;
+        for (int i = 0; i < G::W_PIECES; ++i) {
+            const int off = 16 * (threadIdx.x + i * kGemmThreads);    // byte of the pair's 8 KiB group
+            const int t = off >> 12, o = off & 4095;
+            if constexpr (TYPE == 39) {
+                *reinterpret_cast<u32x4g *>(lds + G::OFF_W + buf * G::W + t * G::WT + o + (o >> 9) * 16) = st_w[i];
+            } else {
+                // Q8_0: [slice pair q][block pair][row][16 B = (2q, b), (2q+1, b), (2q, b+1), (2q+1, b+1)],
+                // so one 16-byte read brings both int8 operands of a two-block chunk
+                const int k = o >> 9, r = (o >> 4) & 31;
+                uint8_t * base = lds + G::OFF_W + buf * G::W + t * G::WT + ((k >> 1) * 2 * 32 + r) * 16 + (k & 1) * 4;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) *reinterpret_cast<unsigned *>(base + (d >> 1) * 32 * 16 + (d & 1) * 8) = st_w[i][d];
+            }
+        }
+        if (threadIdx.x < 32) {
+            if constexpr (TYPE == 39) {
+                *reinterpret_cast<u32x4g *>(lds + G::OFF_M + buf * G::M + 16 * threadIdx.x) = st_m;
+            } else {   // rows 2p, 2p + 1 of tile t: four fp16 scales each, widened once here
+                float f[8];
+#pragma unroll
+                for (int h = 0; h < 8; ++h) f[h] = half_bits_to_float(static_cast<uint16_t>(st_m[h >> 1] >> ((h & 1) * 16)));
+                float * dstm = reinterpret_cast<float *>(lds + G::OFF_M + buf * G::M) + threadIdx.x * 8;
+                *reinterpret_cast<f32x4 *>(dstm) = f32x4{f[0], f[1], f[2], f[3]};
+                *reinterpret_cast<f32x4 *>(dstm + 4) = f32x4{f[4], f[5], f[6], f[7]};
+            }
+        }
     };
 
     f32x4 acc[2][2];
@@ -312,8 +336,8 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
     // The K loop, instantiated with and without the -128 correction (wave-uniform choice).
     const int n_chunks = groups * G::CPG;
     auto k_loop = [&](auto slow_c) {
-        const uint8_t * w_lds = lds + G::OFF_W + (wave & 1) * 4096 + (2 * q * 32 + lr) * 16;
-        const uint8_t * m_lds = lds + G::OFF_M + (wave & 1) * 256 + 4 * q * 8;    // output rows 4q + j
+        const uint8_t * w_lds = lds + G::OFF_W + (wave & 1) * G::WT + (TYPE == 39 ? 2 * q * 528 : q * 2 * 32 * 16) + lr * 16;
+        const uint8_t * m_lds = lds + G::OFF_M + (wave & 1) * (G::M / 2) + 4 * q * (TYPE == 39 ? 8 : 16);   // output rows 4q + j
         const uint8_t * ma_lds = lds + G::OFF_M + (wave & 1) * 256 + lr * 8;      // A rows lr (+16i)
         const uint8_t * b_lds = lds + (32 * (wave >> 1) + lr) * RB + 8 * q * EB;
         const float * d_lds = reinterpret_cast<const float *>(lds + G::OFF_DA) + (32 * (wave >> 1) + lr) * CB;
@@ -334,11 +358,10 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                     const uint8_t * w = w_lds + wb * G::W + i * 16 * 16;
                     if constexpr (TYPE == 39) {
                         w0[i][0] = w0[i][1] = *reinterpret_cast<const unsigned *>(w + sub * 4);
-                        w1[i][0] = w1[i][1] = *reinterpret_cast<const unsigned *>(w + 32 * 16 + sub * 4);
+                        w1[i][0] = w1[i][1] = *reinterpret_cast<const unsigned *>(w + 528 + sub * 4);
                     } else {
-                        const u32x2g v0 = *reinterpret_cast<const u32x2g *>(w + sub * 8);
-                        const u32x2g v1 = *reinterpret_cast<const u32x2g *>(w + 32 * 16 + sub * 8);
-                        w0[i][0] = v0[0], w0[i][1] = v0[1], w1[i][0] = v1[0], w1[i][1] = v1[1];
+                        const u32x4g v = *reinterpret_cast<const u32x4g *>(w + sub * 32 * 16);
+                        w0[i][0] = v[0], w1[i][0] = v[1], w0[i][1] = v[2], w1[i][1] = v[3];
                     }
                 }
                 // MXFP4 fast path: when every exponent e of the wave's A rows (16i + lr) lies in
@@ -382,13 +405,18 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                 } else {
                     // exponent / scale bytes of output rows 16i + 4q + j (MXFP4 one byte, Q8_0 two per block)
                     unsigned mw[2][4];
+                    float mf[2][4][2];
 #pragma unroll
                     for (int i = 0; i < 2; ++i)
 #pragma unroll
                         for (int j = 0; j < 4; ++j) {
-                            const uint8_t * m = m_lds + wb * G::M + (16 * i + j) * 8;
-                            if constexpr (TYPE == 39) mw[i][j] = *reinterpret_cast<const uint16_t *>(m + sub * 2);
-                            else mw[i][j] = *reinterpret_cast<const unsigned *>(m + sub * 4);
+                            if constexpr (TYPE == 39) {
+                                mw[i][j] = *reinterpret_cast<const uint16_t *>(m_lds + wb * G::M + (16 * i + j) * 8 + sub * 2);
+                            } else {
+                                const float * m = reinterpret_cast<const float *>(m_lds + wb * G::M + (16 * i + j) * 16) + sub * 2;
+                                mf[i][j][0] = m[0];
+                                mf[i][j][1] = m[1];
+                            }
                         }
                     auto do_block = [&](int bb) {
                         auto bsrc = [&](int jh) {
@@ -404,7 +432,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                             for (int i = 0; i < 2; ++i) a_op[i] = mx_a_operand(w0[i][bb], w1[i][bb], bb);
                             block_step(slow_c, a_op, mscale, bsrc, dsrc);
                         } else {
-                            auto mscale = [&](int i, int j) { return half_bits_to_float(static_cast<uint16_t>(mw[i][j] >> (16 * bb))); };
+                            auto mscale = [&](int i, int j) { return mf[i][j][bb]; };
                             long a_op[2];
 #pragma unroll
                             for (int i = 0; i < 2; ++i)
