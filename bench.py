@@ -39,17 +39,18 @@ def log(msg: str) -> None:
 class Stack:
     """36 seeded 120B-shape layers resident on the device."""
 
-    def __init__(self, layers: int, experts: int, hidden: int, inter: int, top_k: int, tokens: int):
+    def __init__(self, layers: int, experts: int, hidden: int, inter: int, top_k: int, tokens: int, seed_base: int = 0):
         self.L, self.E, self.H, self.I, self.K, self.T = layers, experts, hidden, inter, top_k, tokens
         self.gate_up, self.down, self.gu_bias, self.dn_bias, self.descs = [], [], [], [], []
         t0 = time.time()
         for l in range(layers):
             gu = vb.Bank(vb.TYPE_MXFP4, 2 * inter, hidden, experts, True)
             dn = vb.Bank(vb.TYPE_MXFP4, hidden, inter, experts, False)
-            gu.generate(0, experts, SEED, 16 * l + 1, 0, -8, -3)
-            dn.generate(0, experts, SEED, 16 * l + 2, 0, -8, -3)
-            gub = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 16 * l + 3, 0, experts * 2 * inter, 0.0, 0.02))
-            dnb = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 16 * l + 4, 0, experts * hidden, 0.0, 0.02))
+            sb = seed_base + 16 * l
+            gu.generate(0, experts, SEED, sb + 1, 0, -8, -3)
+            dn.generate(0, experts, SEED, sb + 2, 0, -8, -3)
+            gub = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, sb + 3, 0, experts * 2 * inter, 0.0, 0.02))
+            dnb = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, sb + 4, 0, experts * hidden, 0.0, 0.02))
             self.gate_up.append(gu)
             self.down.append(dn)
             self.gu_bias.append(gub)
@@ -69,6 +70,11 @@ class Stack:
         self.out = vb.DeviceBuffer(4 * tokens * hidden)
         self.logits_cur = vb.DeviceBuffer(4 * layers * tokens * experts)
         self.ids = vb.DeviceBuffer(4 * layers * tokens * top_k)
+
+    def destroy(self) -> None:
+        vb.call("vbm_decode_plan_destroy", self.plan)
+        for b in self.gate_up + self.down:
+            b.destroy()
 
     def step_logits_bytes(self) -> int:
         return 4 * self.L * self.T * self.E
@@ -199,6 +205,130 @@ def prefill_measure(args) -> dict:
     }
 
 
+def graph_layers(descs, T: int, x0, logits, ids, reps: int) -> float:
+    """One step = the layers chained through vbm_moe_layer_forward at T tokens, captured as a HIP
+    graph; returns the average step time (ms) over `reps` replays (inputs resident, events on the
+    launch stream)."""
+    L = len(descs)
+    H = descs[0].hidden
+    ws = C.c_size_t()
+    vb.call("vbm_moe_layer_workspace", C.byref(descs[0]), T, C.byref(ws))
+    work = vb.DeviceBuffer(ws.value)
+    bufs = [vb.DeviceBuffer(4 * T * H), vb.DeviceBuffer(4 * T * H)]
+    stream = C.c_void_p()
+    vb.call("vbm_stream_create", C.byref(stream))
+    stream = stream.value
+    E, K = descs[0].n_expert, descs[0].top_k
+
+    def enqueue():
+        x = x0.ptr
+        for l, d in enumerate(descs):
+            out = bufs[l & 1].ptr
+            vb.call("vbm_moe_layer_forward", C.byref(d), x, logits.ptr + 4 * l * T * E, T, out,
+                    ids.ptr + 4 * l * T * K, None, work.ptr, ws.value, stream)
+            x = out
+
+    g = C.c_void_p()
+    vb.call("vbm_graph_begin_capture", stream)
+    enqueue()
+    vb.call("vbm_graph_end_capture", stream, C.byref(g))
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    vb.call("vbm_event_create", C.byref(e0))
+    vb.call("vbm_event_create", C.byref(e1))
+    for _ in range(2):
+        vb.call("vbm_graph_launch", g.value, stream)
+    vb.call("vbm_event_record", e0.value, stream)
+    for _ in range(reps):
+        vb.call("vbm_graph_launch", g.value, stream)
+    vb.call("vbm_event_record", e1.value, stream)
+    vb.call("vbm_stream_synchronize", stream)
+    t = C.c_float()
+    vb.call("vbm_event_elapsed_ms", e0.value, e1.value, C.byref(t))
+    vb.call("vbm_graph_destroy", g.value)
+    return t.value / reps
+
+
+def batch_line(descs, T: int, order: int, reps: int, seed_stream: int, slot_bytes: int) -> dict:
+    """Decode of T tokens per step through the stack `descs` in accumulation order `order`:
+    tok/s, step time and the expert bytes the step streams (distinct experts per layer x slot
+    bytes of gate_up + down)."""
+    L = len(descs)
+    E, K, H = descs[0].n_expert, descs[0].top_k, descs[0].hidden
+    ordered = []
+    for d in descs:
+        c = vb.MoeLayerDesc()
+        C.pointer(c)[0] = d
+        c.order = order
+        ordered.append(c)
+    x0 = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, seed_stream, 0, T * H))
+    logits = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, seed_stream + 1, 0, L * T * E))
+    ids = vb.DeviceBuffer(4 * L * T * K)
+    ms = graph_layers(ordered, T, x0, logits, ids, reps)
+    ids_host = ids.download(np.int32, (L, T, K))
+    distinct = distinct_experts(ids_host)
+    step_bytes = distinct * slot_bytes
+    return {"tokens": T, "order": "exact" if order == vb.ORDER_EXACT else "fast",
+            "path": "MFMA grouped GEMM" if (order == vb.ORDER_FAST and T >= 16) else "batched GEMV",
+            "tok_s": round(T / (ms / 1e3), 1), "ms_per_step": round(ms, 4),
+            "distinct_experts_per_layer": round(distinct / L, 2),
+            "expert_bytes_per_step": int(step_bytes), "expert_gbs": round(step_bytes / (ms / 1e3) / 1e9, 1)}
+
+
+def batched_measure(args, stack) -> dict:
+    """Config 2 at batch 32 on the resident stack (exact GEMV order and the fast MFMA order)."""
+    slot = stack.gate_up[0].slot_bytes + stack.down[0].slot_bytes
+    lines = [batch_line(stack.descs, 32, order, args.batch_reps, 910, slot) for order in (vb.ORDER_EXACT, vb.ORDER_FAST)]
+    for r in lines:
+        log(f"config 2 batch {r['tokens']} ({r['order']}, {r['path']}): {r['tok_s']} tok/s, {r['ms_per_step']} ms/step, "
+            f"{r['distinct_experts_per_layer']} experts/layer -> {r['expert_gbs']} GB/s")
+    return {"workload": "120B-shape MXFP4 stack (36 layers x 128 experts, top-4), decode batch 32", "lines": lines}
+
+
+def config1_measure(args) -> dict:
+    """Config 1: the 32-expert / top-4 / 2880 MXFP4 layer stacked 24 deep (seeded per layer),
+    decode batches 1, 8 and 64; batch 1 through the fused decode plan, 8 and 64 through the
+    layer forward (batched GEMV; at 64 also the MFMA grouped GEMM)."""
+    L, E, H, I, K = 24, 32, 2880, 2880, 4
+    st = Stack(L, E, H, I, K, 1, seed_base=1000)
+    slot = st.gate_up[0].slot_bytes + st.down[0].slot_bytes
+    # batch 1: the fused decode plan
+    logits = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 930, 0, L * E))
+    vb.call("vbm_memcpy_d2d", st.logits_cur.ptr, logits.ptr, 4 * L * E, None)
+    s = C.c_void_p()
+    vb.call("vbm_stream_create", C.byref(s))
+    s = s.value
+    g = C.c_void_p()
+    vb.call("vbm_graph_begin_capture", s)
+    st.enqueue_step(s)
+    vb.call("vbm_graph_end_capture", s, C.byref(g))
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    vb.call("vbm_event_create", C.byref(e0))
+    vb.call("vbm_event_create", C.byref(e1))
+    for _ in range(3):
+        vb.call("vbm_graph_launch", g.value, s)
+    vb.call("vbm_event_record", e0.value, s)
+    for _ in range(args.batch_reps * 4):
+        vb.call("vbm_graph_launch", g.value, s)
+    vb.call("vbm_event_record", e1.value, s)
+    vb.call("vbm_stream_synchronize", s)
+    t = C.c_float()
+    vb.call("vbm_event_elapsed_ms", e0.value, e1.value, C.byref(t))
+    vb.call("vbm_graph_destroy", g.value)
+    ms1 = t.value / (args.batch_reps * 4)
+    ids1 = st.ids.download(np.int32, (L, 1, K))
+    b1 = {"tokens": 1, "order": "exact", "path": "fused decode plan (2 kernels per layer)", "tok_s": round(1 / (ms1 / 1e3), 1),
+          "ms_per_step": round(ms1, 4), "distinct_experts_per_layer": K,
+          "expert_bytes_per_step": int(L * K * slot), "expert_gbs": round(L * K * slot / (ms1 / 1e3) / 1e9, 1)}
+    lines = [b1]
+    for T, order in ((8, vb.ORDER_EXACT), (64, vb.ORDER_EXACT), (64, vb.ORDER_FAST)):
+        lines.append(batch_line(st.descs, T, order, args.batch_reps, 940 + T, slot))
+    for r in lines:
+        log(f"config 1 batch {r['tokens']} ({r['order']}, {r['path']}): {r['tok_s']} tok/s, {r['ms_per_step']} ms/step, "
+            f"{r['distinct_experts_per_layer']} experts/layer -> {r['expert_gbs']} GB/s")
+    st.destroy()
+    return {"workload": "MXFP4 MoE stack: 24 layers x 32 experts, top-4, hidden 2880, intermediate 2880", "lines": lines}
+
+
 def tier_measure(args, stack) -> dict:
     """Host-RAM tiered experts on one GPU: the same 36-layer 120B-shape stack with every expert in
     pinned host memory, an HBM pool of 16 GiB of expert groups (1296 x 13,253,760 B) under causal
@@ -299,6 +429,9 @@ def main() -> int:
     ap.add_argument("--cpu-layers", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the Q8_0 prefill GEMM measurement")
+    ap.add_argument("--no-batched", action="store_true",
+                    help="skip the batched decode lines (config 2 at batch 32, config 1 at batches 1/8/64)")
+    ap.add_argument("--batch-reps", type=int, default=5, help="graph replays per batched decode line")
     ap.add_argument("--prefill-reps", type=int, default=5)
     ap.add_argument("--no-tier", action="store_true",
                     help="skip the host-RAM tier workload (it pins 61 GB of host memory)")
@@ -419,6 +552,8 @@ def main() -> int:
         f"{gu_gbs:.0f} GB/s; kernel B (down GEMV): {dn_avg_us:.2f} us -> {dn_gbs:.0f} GB/s")
     traffic = read_traffic(REPO / "profiles" / "decode_gate_up_120b_bs1_pmc.md")
 
+    batched = None if args.no_batched else batched_measure(args, stack)
+    config1 = None if args.no_batched else config1_measure(args)
     prefill = None if args.no_prefill else prefill_measure(args)
     tier = None if args.no_tier else tier_measure(args, stack)
 
@@ -463,6 +598,8 @@ def main() -> int:
                             "bytes_per_launch": round(dn_bytes)},
         },
         "cpu_baseline": cpu,
+        "batched": batched,
+        "config1": config1,
         "prefill": prefill,
         "tier": tier,
     }
