@@ -294,6 +294,9 @@ vbm_status vbm_decode_kernel(vbm_decode_plan * plan, int64_t layer, int which, c
 #define VBM_ADMIT_CLASSIC 0  /* recent-frequency margin, lowest-recent victim (the default)   */
 #define VBM_ADMIT_LRU 1      /* free slot or least recently seen; the reference uses margin 1   */
 #define VBM_ADMIT_RANKED 2   /* classic with seed-priority / recency tie-breaks                 */
+#define VBM_ADMIT_PROBATION 3 /* classic; margin 4 + (3 - reuse) after an unreused lifetime   */
+#define VBM_ADMIT_ANCHORED 4 /* classic above a floor protecting up to 1/4 of the pool for seeds */
+#define VBM_ADMIT_LFU 5      /* capped demand counts, periodic halving, LRU victim              */
 
 typedef struct vbm_admission vbm_admission;
 
@@ -321,6 +324,14 @@ vbm_status vbm_admission_write_dispatch(const vbm_admission * a, int64_t layer, 
 vbm_status vbm_admission_slot_map(const vbm_admission * a, int64_t layer, int32_t * map);
 /* stats[4] = dispatch calls, hits before admission, admissions, evictions. */
 vbm_status vbm_admission_stats(const vbm_admission * a, uint64_t * stats);
+
+/* LFU thresholds (llama-b11669-hybrid-experts.patch:2199-2200, :2398-2413): demands before an
+ * expert may replace a cached one (default 6) / take a free slot (default 1), each in 1..15. */
+vbm_status vbm_admission_set_lfu(vbm_admission * a, int32_t admit_after, int32_t fill_after);
+
+/* LFU demand counts [n_layers * n_expert] (may be NULL) and the number of halvings so far
+ * (:2191-2195); for inspection and tests. No reference counterpart beyond those fields. */
+vbm_status vbm_admission_lfu_state(const vbm_admission * a, uint16_t * counts, uint64_t * halvings);
 /* llama_moe_colder_admission / probation_margin / anchor_slots / cold_gpu_budget /
  * gpu_slot_limit; -1 where the reference asserts. */
 int vbm_moe_colder_admission(int candidate_frequency, int candidate_seed_priority,

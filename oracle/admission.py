@@ -2,7 +2,9 @@
 
 Only tests/ may import this module, as the checker of the library's host-side admission state
 (vbm_admission_*). It follows third_party/patches/llama-b11669-hybrid-experts.patch:
-  admit            :3087-3242 (classic, lru and ranked branches; adaptive mode)
+  admit            :3087-3242 (classic, lru, ranked, probation, anchored and lfu branches;
+                   adaptive mode); policy switch :2375-2391, lfu state :2188-2201, lifetimes
+                   :2214-2218 and :3300-3305, anchored floor :2686-2692
   write_dispatch   :3059-3084
   helpers          :3543-3574
   frozen-plan seed :2659-2680 (slots from n_expert_used upward, priority INT32_MAX - count)
@@ -12,7 +14,8 @@ from __future__ import annotations
 from collections import deque
 
 INT32_MAX = 2**31 - 1
-CLASSIC, LRU, RANKED = 0, 1, 2
+CLASSIC, LRU, RANKED, PROBATION, ANCHORED, LFU = 0, 1, 2, 3, 4, 5
+LFU_CAP, LFU_INSERTS_PER_LAYER = 15, 4
 
 
 def colder_admission(candidate, current) -> bool:
@@ -66,6 +69,12 @@ class Admission:
         self.history = deque()
         self.next_seed = n_used
         self.seeds = 0
+        self.floor_fixed = False
+        self.lfu_count = [0] * (n_layers * n_expert)
+        self.lfu_demands = self.lfu_renewed = self.lfu_entries = self.lfu_halvings = 0
+        self.lfu_admit_after, self.lfu_fill_after = 6, 1
+        # lifetimes: [future_hits, bytes, dynamic]
+        self.life = [[0, 0, False] for _ in range(n_layers * n_expert)]
 
     def seed(self, layer, expert):
         key = layer * self.E + expert
@@ -80,12 +89,33 @@ class Admission:
     def admit(self, layer, selected):
         """Returns (hits, [(slot, expert, evicted_key)])."""
         keys = [layer * self.E + e for e in selected]
+        if not self.floor_fixed:
+            if self.policy == ANCHORED:
+                self.floor = self.K + anchor_slots(self.S, self.K, self.next_seed - self.K)
+            self.lfu_entries = self.S - self.floor
+            self.floor_fixed = True
         self.dispatch_calls += 1
-        if self.policy in (LRU, RANKED):
+        if self.policy in (LRU, RANKED, LFU):
             for k in keys:
                 self.last_seen[k] = self.dispatch_calls
+        if self.policy == LFU:
+            for k in keys:
+                self.lfu_count[k] += 1 if self.lfu_count[k] < LFU_CAP else 0
+            self.lfu_demands += len(keys)
+            self.lfu_renewed += len(keys)
+            entries = float(max(self.lfu_entries, 1))
+            window = min(5.0, 2.0 + 3.0 * self.lfu_renewed / (20.0 * entries))
+            if self.lfu_demands >= window * entries:
+                self.lfu_demands = 0
+                self.lfu_halvings += 1
+                self.lfu_count = [c >> 1 for c in self.lfu_count]
+        lfu_inserts = 0
         hits = [1 if self.slot_map[k] >= 0 else 0 for k in keys]
         self.hits += sum(hits)
+        if self.policy == PROBATION:
+            for k, h in zip(keys, hits):
+                if h and self.life[k][2]:
+                    self.life[k][0] += 1
         self.history.append(keys)
         for k in keys:
             self.recent[k] += 1
@@ -94,10 +124,16 @@ class Admission:
                 self.recent[k] -= 1
         made = []
         for key in keys:
-            if self.slot_map[key] >= 0 or self.recent[key] < self.margin:
+            margin = probation_margin(self.life[key][1] > 0, self.life[key][0]) if self.policy == PROBATION else self.margin
+            if self.slot_map[key] >= 0:
+                continue
+            if self.policy == LFU:
+                if self.lfu_count[key] < min(self.lfu_fill_after, self.lfu_admit_after) or lfu_inserts >= LFU_INSERTS_PER_LAYER:
+                    continue
+            elif self.recent[key] < margin:
                 continue
             victim_slot, victim_frequency = -1, 0
-            if self.policy == LRU:
+            if self.policy in (LRU, LFU):
                 oldest = None
                 for slot in range(self.floor, self.S):
                     victim = self.key_of[slot]
@@ -108,6 +144,15 @@ class Admission:
                         continue
                     if oldest is None or self.last_seen[victim] < oldest:
                         oldest, victim_slot = self.last_seen[victim], slot
+                if self.policy == LFU:
+                    if victim_slot < 0:
+                        continue
+                    victim = self.key_of[victim_slot]
+                    if self.lfu_count[key] < (self.lfu_fill_after if victim < 0 else self.lfu_admit_after):
+                        continue
+                    if victim >= 0 and self.lfu_count[victim] >= self.lfu_count[key]:
+                        continue
+                    lfu_inserts += 1
             else:
                 for slot in range(self.floor, self.S):
                     victim = self.key_of[slot]
@@ -123,15 +168,17 @@ class Admission:
                         victim_slot, victim_frequency = slot, frequency
                         if victim < 0:
                             break
-            if victim_slot < 0 or (self.policy != LRU and self.recent[key] < victim_frequency + self.margin):
+            if victim_slot < 0 or (self.policy not in (LRU, LFU) and self.recent[key] < victim_frequency + margin):
                 continue
             victim = self.key_of[victim_slot]
             if victim >= 0:
+                self.life[victim][2] = False
                 self.slot_map[victim] = -1
                 self.evictions += 1
             self.key_of[victim_slot] = key
             self.slot_map[key] = victim_slot
             self.admissions += 1
+            self.life[key] = [0, 1, True]
             made.append((victim_slot, key % self.E, victim))
         return hits, made
 

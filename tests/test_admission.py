@@ -48,7 +48,7 @@ def test_helper_known_answers_oracle():
 # ------------------------------------------------------------------ library wrapper
 class LibAdmission:
     def __init__(self, vb, L, E, K, S, window=64, margin=4, policy=0):
-        self.vb, self.K, self.E = vb, K, E
+        self.vb, self.K, self.E, self.L = vb, K, E, L
         h = C.c_void_p()
         vb.call("vbm_admission_create", L, E, K, S, window, margin, policy, C.byref(h))
         self.h = h.value
@@ -85,6 +85,15 @@ class LibAdmission:
                      cold_rank, out.ctypes.data)
         return out
 
+    def set_lfu(self, admit_after, fill_after):
+        self.vb.call("vbm_admission_set_lfu", self.h, admit_after, fill_after)
+
+    def lfu_state(self):
+        counts = np.zeros(self.L * self.E, np.uint16)
+        halvings = C.c_uint64()
+        self.vb.call("vbm_admission_lfu_state", self.h, counts.ctypes.data, C.byref(halvings))
+        return counts.tolist(), halvings.value
+
     def close(self):
         self.vb.call("vbm_admission_destroy", self.h)
 
@@ -118,6 +127,90 @@ def test_hand_worked_classic_trace(vb, impl):
         a.close()
 
 
+# Worked by hand from :3091-3137 (lfu): one layer, 8 experts, top-2, 5 slots, admit after 2
+# demands, fill after 1. lfu_entries = 3, so the halving threshold is (2 + renewed / 20) x 3.
+LFU_TRACE = [
+    ([0, 1], [0, 0], [(2, 0, -1), (3, 1, -1)]),   # free slots fill after one demand
+    ([2, 3], [0, 0], [(4, 2, -1)]),               # 3 would replace the LRU entry 0: count 1 < 2
+    ([3, 0], [0, 1], [(3, 3, 1)]),                # count 2 >= 2 and the LRU victim (1) has count 1
+    ([1, 5], [0, 0], []),                         # 8 demands >= 7.2: counts halve first
+    ([5, 1], [0, 0], [(4, 1, 2)]),                # 1 (count 2) replaces 2 (count 0)
+]
+
+
+@pytest.mark.parametrize("impl", ["library", "oracle"])
+def test_hand_worked_lfu_trace(vb, impl):
+    if impl == "library":
+        a = LibAdmission(vb, 1, 8, 2, 5, window=8, margin=4, policy=ref.LFU)
+        a.set_lfu(2, 1)
+    else:
+        a = ref.Admission(1, 8, 2, 5, 8, 4, ref.LFU)
+        a.lfu_admit_after, a.lfu_fill_after = 2, 1
+    for selected, hits, made in LFU_TRACE:
+        assert a.admit(0, selected) == (hits, made), selected
+    got_map = a.slot_map(0) if impl == "library" else a.slot_map[:8]
+    assert got_map == [2, 4, -1, 3, -1, -1, -1, -1]
+    counts, halvings = a.lfu_state() if impl == "library" else (a.lfu_count, a.lfu_halvings)
+    assert counts == [1, 2, 0, 1, 0, 1, 0, 0] and halvings == 1
+    if impl == "library":
+        assert a.stats() == [5, 1, 5, 2]
+        a.close()
+
+
+def _admissions_by_dispatch(a, seq):
+    out = []
+    for d, sel in enumerate(seq, 1):
+        _, made = a.admit(0, sel)
+        if made:
+            out.append((d, made))
+    return out
+
+
+@pytest.mark.parametrize("impl", ["library", "oracle"])
+def test_probation_delays_readmission_after_unreused_lifetime(vb, impl):
+    """Top-1, one layer, 6 experts, 2 dynamic slots, window 8. Expert 0 is admitted at the 4th
+    selection, evicted at dispatch 12 without a single hit while resident; its readmission then
+    needs margin 4 + 3 = 7 recent selections (dispatch 19), where classic readmits at 16."""
+    seq = [[0]] * 4 + [[1]] * 4 + [[2]] * 4 + [[0]] * 7
+    expected = {ref.PROBATION: [(4, [(1, 0, -1)]), (8, [(2, 1, -1)]), (12, [(1, 2, 0)]), (19, [(2, 0, 1)])],
+                ref.CLASSIC: [(4, [(1, 0, -1)]), (8, [(2, 1, -1)]), (12, [(1, 2, 0)]), (16, [(2, 0, 1)])]}
+    for policy, want in expected.items():
+        a = LibAdmission(vb, 1, 6, 1, 3, window=8, margin=4, policy=policy) if impl == "library" \
+            else ref.Admission(1, 6, 1, 3, 8, 4, policy)
+        assert _admissions_by_dispatch(a, seq) == want, policy
+        if impl == "library":
+            a.close()
+
+
+@pytest.mark.parametrize("impl", ["library", "oracle"])
+def test_anchored_floor_protects_the_first_seeds(vb, impl):
+    """Ten slots, top-2, five seeded experts: anchor_slots(10, 2, 5) = 2 protects the seeds in slots
+    2 and 3, so the first admissions evict the seeds in slots 4 and 5; classic evicts slots 2, 3."""
+    for policy, evict in ((ref.ANCHORED, [(4, 6, 2), (5, 7, 3)]), (ref.CLASSIC, [(2, 6, 0), (3, 7, 1)])):
+        a = LibAdmission(vb, 1, 8, 2, 10, window=8, margin=2, policy=policy) if impl == "library" \
+            else ref.Admission(1, 8, 2, 10, 8, 2, policy)
+        for e in range(5):
+            a.seed(0, e)
+        assert _admissions_by_dispatch(a, [[6, 7]] * 3) == [(2, evict)], policy
+        if impl == "library":
+            with pytest.raises(vb.VbmError):
+                a.seed(0, 5)                              # seeding after a dispatch
+            a.close()
+
+
+def test_lfu_thresholds_are_validated(vb):
+    a = LibAdmission(vb, 1, 8, 2, 5, policy=ref.LFU)
+    for admit, fill in ((0, 1), (16, 1), (6, 0), (6, 16)):
+        with pytest.raises(vb.VbmError):
+            a.set_lfu(admit, fill)
+    a.set_lfu(15, 15)
+    a.close()
+    b = LibAdmission(vb, 1, 8, 2, 10, policy=ref.ANCHORED)
+    with pytest.raises(vb.VbmError):
+        vb.call("vbm_admission_set_anchors", b.h, 1)      # anchored derives its floor from the seeds
+    b.close()
+
+
 def zipf_trace(rng, L, E, K, tokens, s=1.1, reuse=0.6):
     """Per layer a seeded permutation; Zipf(s) popularity; with p=reuse keep the previous set."""
     perms = [rng.permutation(E) for _ in range(L)]
@@ -138,11 +231,15 @@ def zipf_trace(rng, L, E, K, tokens, s=1.1, reuse=0.6):
     return out
 
 
-@pytest.mark.parametrize("policy,margin", [(ref.CLASSIC, 4), (ref.LRU, 1), (ref.RANKED, 4)])
+@pytest.mark.parametrize("policy,margin", [(ref.CLASSIC, 4), (ref.LRU, 1), (ref.RANKED, 4), (ref.PROBATION, 4),
+                                           (ref.ANCHORED, 4), (ref.LFU, 4)])
 def test_library_matches_restatement_on_zipf_traces(vb, policy, margin):
     L, E, K, S = 4, 32, 4, 4 + 40
     rng = np.random.default_rng(policy + 5)
     lib, py = LibAdmission(vb, L, E, K, S, window=16, margin=margin, policy=policy), ref.Admission(L, E, K, S, 16, margin, policy)
+    if policy == ref.LFU:                                 # thresholds that admit within a 200-token trace
+        lib.set_lfu(3, 1)
+        py.lfu_admit_after, py.lfu_fill_after = 3, 1
     for l in range(L):                                   # a frozen plan seeds a few experts per layer
         for e in range(3):
             assert lib.seed(l, (5 * l + 7 * e) % E) == py.seed(l, (5 * l + 7 * e) % E)
@@ -153,6 +250,8 @@ def test_library_matches_restatement_on_zipf_traces(vb, policy, margin):
         assert lib.slot_map(l) == py.slot_map[l * E:(l + 1) * E]
     assert lib.stats() == [py.dispatch_calls, py.hits, py.admissions, py.evictions]
     assert py.admissions > 0 and (policy == ref.LRU or py.evictions > 0)
+    if policy == ref.LFU:
+        assert lib.lfu_state() == (py.lfu_count, py.lfu_halvings) and py.lfu_halvings > 0
     ids = np.array([[3, 9, 1, 30], [4, 5, 6, 7]])
     w = np.array([[0.4, 0.3, 0.2, 0.1], [0.25, 0.25, 0.25, 0.25]])
     for cold in (-1, 2):

@@ -4,9 +4,13 @@
 //   write_dispatch llama-b11669-hybrid-experts.patch:3059-3084
 //   helpers        llama-b11669-hybrid-experts.patch:3543-3574
 //   frozen-plan seeding and the admission floor  llama-b11669-hybrid-experts.patch:2650-2695
-// Policies: classic (recent-frequency margin), lru (free slot or least recently seen), ranked
-// (classic with cold-start seed priority and recency tie-breaks). Slots [0, n_used) are the
-// reserved per-rank zero slots of misses; anchors (anchored plans) follow them.
+// Policies (llama-b11669-hybrid-experts.patch:2375-2391): classic (recent-frequency margin), lru
+// (free slot or least recently seen), ranked (classic with cold-start seed priority and recency
+// tie-breaks), probation (classic whose margin grows after an admitted lifetime without reuse,
+// :3116-3119), anchored (classic above a floor protecting up to a quarter of the dynamic slots
+// for frozen-plan seeds, :2689-2691) and lfu (capped demand counts with periodic halving,
+// :3092-3102, :3121-3137). Slots [0, n_used) are the reserved per-rank zero slots of misses;
+// anchors follow them.
 #include "vbm_internal.hpp"
 
 #include <algorithm>
@@ -32,7 +36,22 @@ struct vbm_admission {
     std::vector<uint64_t> last_seen;    // [keys] dispatch call of the last selection
     std::vector<int32_t> seed_priority; // [keys] frozen-plan order, 0 when not seeded
     std::deque<std::vector<int32_t>> history;
+    bool floor_fixed = false;           // the floor (and LFU's entry count) is set at the first dispatch
+    // lfu (:2188-2201)
+    std::vector<uint16_t> lfu_count;    // [keys]
+    uint64_t lfu_demands = 0, lfu_renewed = 0, lfu_entries = 0, lfu_halvings = 0;
+    int lfu_admit_after = 6, lfu_fill_after = 1;
+    // probation (:2214-2218): a key's last admitted lifetime
+    struct Lifetime {
+        uint64_t future_hits = 0;
+        uint64_t bytes = 0;             // > 0 once the key was admitted dynamically
+        bool dynamic = false;
+    };
+    std::vector<Lifetime> life;         // [keys]
 };
+
+constexpr uint16_t kLfuCap = 15;                 // :2196
+constexpr int kLfuInsertsPerLayer = 4;           // :2201
 
 namespace {
 
@@ -81,7 +100,7 @@ vbm_status vbm_admission_create(int64_t n_layers, int64_t n_expert, int64_t n_us
         require(n_layers * n_expert < INT32_MAX, "too many expert keys");
         require(recent_window >= 8 && recent_window <= 256, "recent window must be in 8..256");
         require(margin >= 1, "margin must be positive");
-        require(policy == VBM_ADMIT_CLASSIC || policy == VBM_ADMIT_LRU || policy == VBM_ADMIT_RANKED, "unknown policy");
+        require(policy >= VBM_ADMIT_CLASSIC && policy <= VBM_ADMIT_LFU, "unknown policy");
         auto a = std::make_unique<vbm_admission>();
         a->n_layers = n_layers;
         a->n_expert = n_expert;
@@ -97,6 +116,8 @@ vbm_status vbm_admission_create(int64_t n_layers, int64_t n_expert, int64_t n_us
         a->recent.assign(static_cast<size_t>(n_layers * n_expert), 0);
         a->last_seen.assign(static_cast<size_t>(n_layers * n_expert), 0);
         a->seed_priority.assign(static_cast<size_t>(n_layers * n_expert), 0);
+        a->lfu_count.assign(static_cast<size_t>(n_layers * n_expert), 0);
+        a->life.assign(static_cast<size_t>(n_layers * n_expert), vbm_admission::Lifetime{});
         *out = a.release();
     });
 }
@@ -125,8 +146,20 @@ vbm_status vbm_admission_seed(vbm_admission * a, int64_t layer, int64_t expert, 
 vbm_status vbm_admission_set_anchors(vbm_admission * a, int32_t anchors) {
     return guarded([&] {
         require(a != nullptr, "null admission state");
+        require(a->dispatch_calls == 0, "anchors must be set before the first dispatch");
+        require(a->policy != VBM_ADMIT_ANCHORED, "the anchored policy derives its anchors from the seeds");
         require(anchors >= 0 && a->n_used + anchors < a->n_slots, "anchors exceed the pool");
         a->admission_floor = a->n_used + anchors;
+    });
+}
+
+vbm_status vbm_admission_set_lfu(vbm_admission * a, int32_t admit_after, int32_t fill_after) {
+    return guarded([&] {
+        require(a != nullptr, "null admission state");
+        require(admit_after >= 1 && admit_after <= kLfuCap, "LFU admission threshold must be in 1..15");   // :2403
+        require(fill_after >= 1 && fill_after <= kLfuCap, "LFU fill threshold must be in 1..15");          // :2410
+        a->lfu_admit_after = admit_after;
+        a->lfu_fill_after = fill_after;
     });
 }
 
@@ -142,13 +175,36 @@ vbm_status vbm_admission_admit(vbm_admission * a, int64_t layer, const int32_t *
             require(selected[r] >= 0 && selected[r] < E, "selected expert out of range");
             keys[r] = static_cast<int32_t>(layer * E + selected[r]);
         }
+        const bool lru = a->policy == VBM_ADMIT_LRU, lfu = a->policy == VBM_ADMIT_LFU;
+        const bool probation = a->policy == VBM_ADMIT_PROBATION;
+        if (!a->floor_fixed) {   // :2686-2692, once the frozen plan's seeds are in place
+            if (a->policy == VBM_ADMIT_ANCHORED)
+                a->admission_floor = a->n_used + vbm_moe_anchor_slots(static_cast<int>(a->n_slots), static_cast<int>(a->n_used),
+                                                                      static_cast<int>(a->next_seed_slot - a->n_used));
+            a->lfu_entries = static_cast<uint64_t>(a->n_slots - a->admission_floor);
+            a->floor_fixed = true;
+        }
         ++a->dispatch_calls;
-        if (a->policy == VBM_ADMIT_LRU || a->policy == VBM_ADMIT_RANKED)
+        if (a->policy == VBM_ADMIT_RANKED || lru || lfu)
             for (int32_t key : keys) a->last_seen[key] = a->dispatch_calls;
+        if (lfu) {   // :3091-3102
+            for (int32_t key : keys) a->lfu_count[key] += a->lfu_count[key] < kLfuCap;
+            a->lfu_demands += static_cast<uint64_t>(K);
+            a->lfu_renewed += static_cast<uint64_t>(K);
+            const double entries = static_cast<double>(std::max<uint64_t>(a->lfu_entries, 1));
+            const double window = std::min(5.0, 2.0 + 3.0 * static_cast<double>(a->lfu_renewed) / (20.0 * entries));
+            if (static_cast<double>(a->lfu_demands) >= window * entries) {
+                a->lfu_demands = 0;
+                ++a->lfu_halvings;
+                for (auto & c : a->lfu_count) c >>= 1;
+            }
+        }
+        int lfu_inserts = 0;
         for (int64_t r = 0; r < K; ++r) {
             const bool hit = a->slot_map[keys[r]] >= 0;
             a->pre_admission_hits += hit;
             if (hits) hits[r] = hit ? 1 : 0;
+            if (probation && hit && a->life[keys[r]].dynamic) ++a->life[keys[r]].future_hits;   // :3300-3305
         }
         a->history.push_back(keys);
         for (int32_t key : keys) ++a->recent[key];
@@ -159,17 +215,28 @@ vbm_status vbm_admission_admit(vbm_admission * a, int64_t layer, const int32_t *
         int64_t n = 0;
         for (int64_t r = 0; r < K; ++r) {
             const int32_t key = keys[r];
+            const vbm_admission::Lifetime & lk = a->life[key];
+            const int margin = probation ? vbm_moe_probation_margin(lk.bytes > 0, lk.future_hits) : a->margin;
             if (a->slot_map[key] >= 0) continue;
-            if (a->recent[key] < a->margin) continue;
+            if (lfu ? (a->lfu_count[key] < std::min(a->lfu_fill_after, a->lfu_admit_after) || lfu_inserts >= kLfuInsertsPerLayer)
+                    : a->recent[key] < margin)
+                continue;
             int32_t victim_slot = -1;
             int victim_frequency = 0;
-            if (a->policy == VBM_ADMIT_LRU) {
+            if (lru || lfu) {
                 uint64_t oldest = UINT64_MAX;
                 for (int64_t slot = a->admission_floor; slot < a->n_slots; ++slot) {
                     const int32_t victim = a->key_of[slot];
                     if (victim < 0) { victim_slot = static_cast<int32_t>(slot); break; }
                     if (a->last_seen[victim] >= a->dispatch_calls) continue;   // selected by this dispatch
                     if (a->last_seen[victim] < oldest) { oldest = a->last_seen[victim]; victim_slot = static_cast<int32_t>(slot); }
+                }
+                if (lfu) {   // :3131-3137
+                    if (victim_slot < 0) continue;
+                    const int32_t victim = a->key_of[victim_slot];
+                    if (a->lfu_count[key] < (victim < 0 ? a->lfu_fill_after : a->lfu_admit_after)) continue;
+                    if (victim >= 0 && a->lfu_count[victim] >= a->lfu_count[key]) continue;
+                    ++lfu_inserts;
                 }
             } else {
                 for (int64_t slot = a->admission_floor; slot < a->n_slots; ++slot) {
@@ -189,15 +256,17 @@ vbm_status vbm_admission_admit(vbm_admission * a, int64_t layer, const int32_t *
                     }
                 }
             }
-            if (victim_slot < 0 || (a->policy != VBM_ADMIT_LRU && a->recent[key] < victim_frequency + a->margin)) continue;
+            if (victim_slot < 0 || (!lru && !lfu && a->recent[key] < victim_frequency + margin)) continue;
             const int32_t victim = a->key_of[victim_slot];
             if (victim >= 0) {
+                a->life[victim].dynamic = false;   // :3208-3216 (the lifetime's record stays)
                 a->slot_map[victim] = -1;
                 ++a->evictions;
             }
             a->key_of[victim_slot] = key;
             a->slot_map[key] = victim_slot;
             ++a->admissions;
+            a->life[key] = vbm_admission::Lifetime{0, 1, true};   // :3229-3238 (only bytes > 0 is read)
             if (admitted_slots) admitted_slots[n] = victim_slot;
             if (admitted_experts) admitted_experts[n] = static_cast<int32_t>(key % E);
             if (evicted_keys) evicted_keys[n] = victim;
@@ -243,6 +312,14 @@ vbm_status vbm_admission_stats(const vbm_admission * a, uint64_t * stats) {
         stats[1] = a->pre_admission_hits;
         stats[2] = a->admissions;
         stats[3] = a->evictions;
+    });
+}
+
+vbm_status vbm_admission_lfu_state(const vbm_admission * a, uint16_t * counts, uint64_t * halvings) {
+    return guarded([&] {
+        require(a != nullptr, "invalid argument");
+        if (counts) std::copy(a->lfu_count.begin(), a->lfu_count.end(), counts);
+        if (halvings) *halvings = a->lfu_halvings;
     });
 }
 

@@ -107,6 +107,8 @@ SIGNATURES = {
     "vbm_admission_write_dispatch": [vp, i64, vp, vp, i64, C.c_int32, vp],
     "vbm_admission_slot_map": [vp, i64, vp],
     "vbm_admission_stats": [vp, vp],
+    "vbm_admission_set_lfu": [vp, C.c_int32, C.c_int32],
+    "vbm_admission_lfu_state": [vp, vp, vp],
     "vbm_tier_create": [C.POINTER(TierDesc), C.POINTER(vp)],
     "vbm_tier_destroy": [vp],
     "vbm_tier_host_bytes": [vp, C.POINTER(sz)],
@@ -125,7 +127,7 @@ OTHER = {
     "vbm_moe_cold_gpu_budget": ([C.c_int], C.c_int),
     "vbm_moe_gpu_slot_limit": ([C.c_int32, C.c_int], C.c_int32),
 }
-ADMIT_CLASSIC, ADMIT_LRU, ADMIT_RANKED = 0, 1, 2
+ADMIT_CLASSIC, ADMIT_LRU, ADMIT_RANKED, ADMIT_PROBATION, ADMIT_ANCHORED, ADMIT_LFU = 0, 1, 2, 3, 4, 5
 
 _lib = None
 
