@@ -331,10 +331,12 @@ def config1_measure(args) -> dict:
 
 def tier_measure(args, stack) -> dict:
     """Host-RAM tiered experts on one GPU: the same 36-layer 120B-shape stack with every expert in
-    pinned host memory, an HBM pool of 16 GiB of expert groups (1296 x 13,253,760 B) under causal
-    (classic) admission, misses staged with hipMemcpyAsync on a side stream. Trace: 512 decode
-    tokens; per layer a seeded permutation of the experts with Zipf(1.1) popularity, and with
-    probability 0.6 the previous token's set is reused."""
+    pinned host memory, an HBM pool of 16 GiB of expert groups under causal (classic) admission,
+    misses staged with hipMemcpyAsync on a side stream. The pool is first seeded with the trained
+    gpt-oss-120b plan of 944 expert groups (plans/gpt120-trained-hot944.txt, in file order, as the
+    frozen-plan loader seeds it), unless --tier-plan none. Trace: 512 decode tokens; per layer a
+    seeded permutation of the experts with Zipf(1.1) popularity, and with probability 0.6 the
+    previous token's set is reused."""
     L, E, K, H, I = stack.L, stack.E, stack.K, stack.H, stack.I
     group_bytes = stack.gate_up[0].slot_bytes + stack.down[0].slot_bytes
     n_slots = (16 << 30) // group_bytes
@@ -348,8 +350,14 @@ def tier_measure(args, stack) -> dict:
     vb.call("vbm_tier_generate", tier.value, SEED, 16, 1, 2, -8.0, -3.0, None)
     host = C.c_size_t()
     vb.call("vbm_tier_host_bytes", tier.value, C.byref(host))
+    plan = []
+    if args.tier_plan != "none":
+        from vbmoe.routing_trace import read_plan
+        plan = read_plan(args.tier_plan, L, E)
+        for layer, expert in plan:
+            vb.call("vbm_tier_seed", tier.value, layer, expert)
     log(f"tier: {host.value / 1e9:.1f} GB of experts in pinned host memory, {n_slots} device slots "
-        f"({n_slots * group_bytes / 2**30:.1f} GiB), ready in {time.time() - t0:.1f} s")
+        f"({n_slots * group_bytes / 2**30:.1f} GiB), {len(plan)} seeded, ready in {time.time() - t0:.1f} s")
     rng = np.random.default_rng(SEED)
     tokens = args.tier_tokens
     p = 1.0 / np.arange(1, E + 1) ** 1.1
@@ -390,12 +398,13 @@ def tier_measure(args, stack) -> dict:
     h2d = st.uploaded_bytes / (st.copy_ms * 1e-3) / 1e9 if st.copy_ms > 0 else None
     res = {
         "workload": f"120B-shape MXFP4 stack, {n_slots} x {group_bytes} B HBM expert slots (16 GiB), rest in pinned "
-                    f"host RAM; {tokens} decode tokens, Zipf(1.1) routing with 0.6 reuse; classic causal admission",
+                    f"host RAM; {tokens} decode tokens, Zipf(1.1) routing with 0.6 reuse; classic causal admission"
+                    + (f"; seeded with {Path(args.tier_plan).name} ({len(plan)} expert groups)" if plan else ""),
         "value": round(tokens / (ms.value * 1e-3), 2), "unit": "tok/s", "host_wall_s": round(wall, 2),
         "hit_rate": round(st.hits / lookups, 4), "lookups": lookups, "admissions": int(st.admissions),
         "evictions": int(st.evictions), "staged_misses": int(st.staged),
         "uploaded_gb": round(st.uploaded_bytes / 1e9, 2), "h2d_gbs": round(h2d, 1) if h2d else None,
-        "copy_busy_ms": round(st.copy_ms, 1),
+        "copy_busy_ms": round(st.copy_ms, 1), "seeded": len(plan),
     }
     log(f"tier: {res['value']} tok/s, hit rate {res['hit_rate']}, {res['uploaded_gb']} GB uploaded at "
         f"{res['h2d_gbs']} GB/s copy-busy")
@@ -436,6 +445,8 @@ def main() -> int:
     ap.add_argument("--no-tier", action="store_true",
                     help="skip the host-RAM tier workload (it pins 61 GB of host memory)")
     ap.add_argument("--tier-tokens", type=int, default=512)
+    ap.add_argument("--tier-plan", default=str(REPO / "unified-memory-scheduler_amd" / "plans" / "gpt120-trained-hot944.txt"),
+                    help="frozen plan seeding the tier's pool ('layer expert' lines), or 'none'")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="after the run, launch a plain device copy of BYTES three times (a known-traffic "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")

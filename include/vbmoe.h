@@ -343,6 +343,51 @@ int vbm_moe_cold_gpu_budget(int cold_experts);
 int32_t vbm_moe_gpu_slot_limit(int32_t resident_slots, int cold_gpu);
 
 /* ----------------------------------------------------------------------------------------------
+ * Decode routing traces in the reference's JSONL schema (benchmarks/schema/
+ * vrambridge-routing-trace.schema.json), written like its collector tools/trace/routing_trace.cpp:
+ * metadata (:701-728), request_start (:501-503), one route per routed layer and decoded token
+ * (:206-216), request_end (:566-569), trace_end (:744). Records are compact JSON lines with keys in
+ * ascending order; the file is written as "<path>.part" (created exclusively) and hard-linked to
+ * `path` by vbm_trace_close (:632-634, :745-749). Host-side; no device calls.
+ * -------------------------------------------------------------------------------------------- */
+typedef struct {
+    int64_t id;                              /* model layer number                               */
+    int64_t experts, active;                 /* experts in the layer, experts routed per token   */
+    uint64_t bytes_per_expert;               /* all expert tensors of the layer, per expert      */
+    uint64_t static_host_bytes_per_expert;   /* of which statically held in host memory          */
+    const char * tensor_types;               /* comma-separated ggml type names, or NULL         */
+} vbm_trace_layer;
+
+typedef struct vbm_trace vbm_trace;
+
+/* model and token_equivalence_check may be NULL (omitted). Refuses an existing path or partial. */
+vbm_status vbm_trace_open(const char * path, const char * architecture, const char * backend_commit,
+                          const char * model, int64_t context_tokens, const vbm_trace_layer * layers,
+                          int64_t n_layers, const char * token_equivalence_check, vbm_trace ** trace);
+/* split "train" or "test"; prompt_tokens + max_tokens <= context_tokens; ids unique. */
+vbm_status vbm_trace_request_start(vbm_trace * trace, const char * id, const char * split,
+                                   const char * category, int64_t prompt_tokens, int64_t max_tokens);
+/* One layer's routed experts (rank order) for the current token; layers in ascending id order. */
+vbm_status vbm_trace_route(vbm_trace * trace, int64_t layer_id, const int32_t * experts, int64_t n_active);
+/* All layers of one token: ids [n_layers][stride] (stride 0 = each layer's active count), e.g. the
+ * ids output of vbm_decode_step or vbm_tier_step copied to the host. */
+vbm_status vbm_trace_token(vbm_trace * trace, const int32_t * ids, int64_t stride);
+/* stop_reason "limit" (exactly max_tokens decoded) or "eos" (fewer); token_sequence_equivalent
+ * non-zero records the observer-equivalence claim, zero omits it. */
+vbm_status vbm_trace_request_end(vbm_trace * trace, const char * stop_reason, int token_sequence_equivalent);
+/* Writes trace_end and publishes the file. Consumes the handle, also on failure. */
+vbm_status vbm_trace_close(vbm_trace * trace);
+/* Discards the partial file and the handle. */
+vbm_status vbm_trace_abort(vbm_trace * trace);
+/* Layer `index` in ascending id order; any output may be NULL. */
+vbm_status vbm_trace_layer_info(const vbm_trace * trace, int64_t index, int64_t * id, int64_t * experts,
+                                int64_t * active);
+/* Routed layers, requests started, complete tokens of the open request (-1: none open), next
+ * layer index within the current token. */
+vbm_status vbm_trace_position(const vbm_trace * trace, int64_t * n_layers, int64_t * requests,
+                              int64_t * token, int64_t * layer_index);
+
+/* ----------------------------------------------------------------------------------------------
  * Single-GPU host-RAM expert tier for single-token decode (the cold-expert path of the reference's
  * llama_moe_cache: admission, staged uploads and publish-after-event,
  * llama-b11669-hybrid-experts.patch:2727-3298). Every expert of every layer is kept in pinned
@@ -390,6 +435,12 @@ vbm_status vbm_tier_seed(vbm_tier * tier, int64_t layer, int64_t expert);
 vbm_status vbm_tier_step(vbm_tier * tier, const float * x, const float * logits, float * out, int32_t * ids,
                          void * stream);
 vbm_status vbm_tier_get_stats(const vbm_tier * tier, vbm_tier_stats * stats);
+
+/* Attach a routing trace (or NULL to detach): every vbm_tier_step then records each layer's
+ * routed experts, as they reach the host for admission, as one route record (tier layer l is the
+ * trace's l-th layer in ascending id order; counts and top_k must match). The trace stays owned
+ * by the caller and must outlive the attachment. */
+vbm_status vbm_tier_set_trace(vbm_tier * tier, vbm_trace * trace);
 
 /* ----------------------------------------------------------------------------------------------
  * HIP graph capture of stream-ordered work (per-token layer chains replay without host launch

@@ -107,3 +107,68 @@ def test_tier_matches_resident_plan(gpu, type_id, policy, margin):
     for gu, dn in banks:
         gu.destroy()
         dn.destroy()
+
+
+def test_tier_routing_trace_replays_to_the_same_decisions(gpu, tmp_path):
+    """A routing trace recorded by the tier (vbm_tier_set_trace) holds exactly the routed experts,
+    the tier's outputs are bit-identical with and without it attached, and replaying the trace
+    through the admission alone reproduces the tier's counters."""
+    from vbmoe import routing_trace as rt
+    vb = gpu
+    L, E, K, H, I, slots, policy, margin = 3, 16, 4, 256, 256, 4 + 9, vb.ADMIT_LFU, 4
+    biases = [(vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 16 * l + 3, 0, E * 2 * I, 0.0, 0.02)),
+               vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 16 * l + 4, 0, E * H, 0.0, 0.02))) for l in range(L)]
+    gub = (C.c_void_p * L)(*[b[0].ptr for b in biases])
+    dnb = (C.c_void_p * L)(*[b[1].ptr for b in biases])
+    desc = vb.TierDesc(39, H, I, L, E, K, vb.ACT_SWIGLU_OAI, slots, 8, margin, policy,
+                       C.cast(gub, C.POINTER(C.c_void_p)), C.cast(dnb, C.POINTER(C.c_void_p)))
+    tiers = []
+    for _ in range(2):
+        tier = C.c_void_p()
+        vb.call("vbm_tier_create", C.byref(desc), C.byref(tier))
+        vb.call("vbm_tier_generate", tier.value, SEED, 16, 1, 2, -8.0, -3.0, None)
+        for l, e in ((0, 3), (2, 5)):
+            vb.call("vbm_tier_seed", tier.value, l, e)
+        tiers.append(tier.value)
+    ids = [3, 7, 11]
+    expert_bytes = 2 * I * (H // 32) * 17 + H * (I // 32) * 17 + 4 * (2 * I + H)   # MXFP4 weights + fp32 biases
+    layers = [{"id": i, "experts": E, "active": K, "bytes_per_expert": expert_bytes,
+               "static_host_bytes_per_expert": expert_bytes, "tensor_types": ["f32", "mxfp4"]} for i in ids]
+    path = tmp_path / "tier.jsonl"
+    writer = rt.TraceWriter(path, layers, "gpt-oss", "vbmoe-test", 64, model="synthetic",
+                            token_equivalence_check="tier outputs with and without the trace attached")
+    rng = np.random.default_rng(77)
+    x = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 6, 0, H))
+    dl = vb.DeviceBuffer(4 * L * E)
+    outs = [vb.DeviceBuffer(4 * H), vb.DeviceBuffer(4 * H)]
+    vb.call("vbm_tier_set_trace", tiers[0], writer.handle)
+    with pytest.raises(vb.VbmError, match="no open request"):
+        vb.call("vbm_tier_step", tiers[0], x.ptr, dl.ptr, outs[0].ptr, None, None)   # rejected before any work
+    routed = []
+    for name, split, tokens in (("warm", "train", 14), ("held-out", "test", 9)):
+        logits, chosen = routed_logits(rng, L, E, K, tokens)
+        routed += chosen
+        writer.request_start(name, split, "coding", 3, tokens)
+        for t in range(tokens):
+            dl.upload(logits[t])
+            for tier, o in zip(tiers, outs):
+                vb.call("vbm_tier_step", tier, x.ptr, dl.ptr, o.ptr, None, None)
+            vb.call("vbm_stream_synchronize", None)
+            a, b = (o.download(np.float32, H) for o in outs)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (name, t)
+        writer.request_end("limit", True)
+    vb.call("vbm_tier_set_trace", tiers[0], None)
+    writer.close()
+    data = rt.read_trace(path)
+    assert [list(e.experts) for e in data.events] == [sel for row in routed for sel in row]
+    assert [e.layer for e in data.events] == ids * len(routed)
+    stats = rt.replay_admission(data, slots, policy, recent_window=8, margin=margin, plan=[(0, 3), (2, 5)])
+    for tier in tiers:
+        st = vb.TierStats()
+        vb.call("vbm_tier_get_stats", tier, C.byref(st))
+        a = stats["all"]
+        assert (st.dispatches, st.hits, st.admissions, st.evictions, st.staged) == \
+            (a.dispatches, a.hits, a.admissions, a.evictions, a.staged)
+        vb.call("vbm_tier_destroy", tier)
+    print(f"[tier trace] {len(data.events)} routes, hit rate {stats['all'].hit_rate:.3f} "
+          f"(train {stats['train'].hit_rate:.3f}, test {stats['test'].hit_rate:.3f})", flush=True)

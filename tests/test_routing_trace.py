@@ -1,0 +1,364 @@
+"""Routing traces (writer in libvbmoe, reader and replays in vbmoe.routing_trace) and frozen plans.
+
+Pinned by: the reference analyzer's own reader cases (tests/test_routing_analysis.py:37-144 of the
+reference, restated below), the reference analyzer's reading of a trace written by this library
+(tests/golden/routing_trace_small_report.json, made by tests/golden/make_routing_trace_golden.py),
+Python's JSON serializer as an independent rendering of the same compact sorted-key records, and
+the admission restatement (oracle/admission.py) for replays.
+"""
+import copy
+import hashlib
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+REPO = Path(__file__).resolve().parents[1]
+GOLDEN = REPO / "tests" / "golden"
+PLAN = REPO / "unified-memory-scheduler_amd" / "plans" / "gpt120-trained-hot944.txt"
+sys.path.insert(0, str(GOLDEN))
+
+
+@pytest.fixture(scope="module")
+def rt(vb):
+    from vbmoe import routing_trace
+    return routing_trace
+
+
+def small_layers(host=(0, 10)):
+    return [{"id": 0, "experts": 3, "active": 1, "bytes_per_expert": 10, "static_host_bytes_per_expert": host[0]},
+            {"id": 1, "experts": 3, "active": 1, "bytes_per_expert": 10, "static_host_bytes_per_expert": host[1]}]
+
+
+def records(layers=None, training=None, testing=None):
+    """The reference analyzer tests' trace builder (tests/test_routing_analysis.py:37-61)."""
+    layers = layers or small_layers()
+    training = training or [(0, 0), (0, 1), (1, 0)]
+    testing = testing or [(0, 2), (1, 0), (2, 1)]
+    out = [{"type": "metadata", "schema_version": 1, "instrumented": True, "capture_scope": "decode_only",
+            "context_tokens": 256, "backend_commit": "test", "architecture": "test-moe", "model": "test.gguf",
+            "static_device_expert_bytes": sum((l["bytes_per_expert"] - l["static_host_bytes_per_expert"])
+                                              * l["experts"] for l in layers),
+            "layers": layers}]
+    for split, sequence in (("train", training), ("test", testing)):
+        out.append({"type": "request_start", "id": split, "split": split, "category": "reasoning",
+                    "prompt_tokens": 4, "max_tokens": len(sequence)})
+        for token, selected in enumerate(sequence):
+            for layer, expert in zip(layers, selected):
+                out.append({"type": "route", "request": split, "phase": "decode", "token": token,
+                            "layer": layer["id"], "experts": expert if isinstance(expert, list) else [expert]})
+        out.append({"type": "request_end", "id": split, "decode_tokens": len(sequence), "stop_reason": "limit",
+                    "token_sequence_equivalent": True})
+    out.append({"type": "trace_end", "requests": 2, "complete": True})
+    return out
+
+
+def dump(tmp_path, values, name="trace.jsonl"):
+    path = tmp_path / name
+    path.write_text("".join(json.dumps(v) + "\n" for v in values), encoding="utf-8")
+    return path
+
+
+def write_small(rt, path, layers=None, training=((0, 0), (0, 1), (1, 0)), testing=((0, 2), (1, 0), (2, 1))):
+    with rt.TraceWriter(path, layers or small_layers(), "test-moe", "test", 256, model="test.gguf") as w:
+        for split, seq in (("train", training), ("test", testing)):
+            w.request_start(split, split, "reasoning", 4, len(seq))
+            for pair in seq:
+                for lid, e in zip((0, 1), pair):
+                    w.route(lid, [e])
+            w.request_end("limit", True)
+    return path
+
+
+# ------------------------------------------------------------------------------------------------
+# writer format
+
+
+def test_writer_emits_compact_sorted_records(rt, tmp_path):
+    path = write_small(rt, tmp_path / "t.jsonl")
+    lines = path.read_text().splitlines()
+    assert lines[0] == (
+        '{"architecture":"test-moe","backend_commit":"test","capture_scope":"decode_only","context_tokens":256,'
+        '"instrumented":true,"layers":[{"active":1,"bytes_per_expert":10,"experts":3,"id":0,'
+        '"static_host_bytes_per_expert":0,"tensor_types":[]},{"active":1,"bytes_per_expert":10,"experts":3,"id":1,'
+        '"static_host_bytes_per_expert":10,"tensor_types":[]}],"model":"test.gguf","schema_version":1,'
+        '"static_device_expert_bytes":30,"type":"metadata"}')
+    assert lines[1] == ('{"category":"reasoning","id":"train","max_tokens":3,"prompt_tokens":4,"split":"train",'
+                        '"type":"request_start"}')
+    assert lines[2] == '{"experts":[0],"layer":0,"phase":"decode","request":"train","token":0,"type":"route"}'
+    assert lines[8] == ('{"decode_tokens":3,"id":"train","stop_reason":"limit","token_sequence_equivalent":true,'
+                        '"type":"request_end"}')
+    assert lines[-1] == '{"complete":true,"requests":2,"type":"trace_end"}'
+    # the same records, as the reference test builds them, read back identically
+    ours = [json.loads(line) for line in lines]
+    theirs = records()
+    for mine, ref in zip(ours, theirs):
+        if mine["type"] == "metadata":
+            for layer in mine["layers"]:
+                assert layer.pop("tensor_types") == []
+        assert mine == ref
+    for line in lines:
+        assert line == json.dumps(json.loads(line), sort_keys=True, separators=(",", ":"), ensure_ascii=False)
+    assert not Path(str(path) + ".part").exists()
+
+
+def test_writer_string_escapes_and_utf8(rt, vb, tmp_path):
+    tricky = 'a"b\\c\nd\te\x01f\x1f\x7f-é-€-😀'
+    path = tmp_path / "s.jsonl"
+    with rt.TraceWriter(path, small_layers(), "arch\u2028x", "c0mmit", 256, model="m\x08.gguf",
+                        token_equivalence_check="ctl\x0c\r") as w:
+        for split in ("train", "test"):
+            w.request_start(tricky + split, split, "cat/é", 4, 1)
+            w.route(0, [2])
+            w.route(1, [1])
+            w.request_end("limit")
+    lines = path.read_text(encoding="utf-8").split("\n")[:-1]   # U+2028 is data, not a line break
+    for line in lines:
+        assert line == json.dumps(json.loads(line), sort_keys=True, separators=(",", ":"), ensure_ascii=False)
+    assert json.loads(lines[0])["architecture"] == "arch\u2028x"
+    first = json.loads(lines[1])
+    assert first["id"] == tricky + "train" and first["category"] == "cat/é"
+    assert '\\u0001' in path.read_text(encoding="utf-8")          # lower-case hex control escapes
+    # invalid UTF-8 is rejected, not written
+    w = rt.TraceWriter(tmp_path / "u.jsonl", small_layers(), "a", "b", 256)
+    for bad in (b"\xff", b"a\xc3", b"\xc0\xaf", b"\xed\xa0\x80"):
+        with pytest.raises(vb.VbmError, match="UTF-8"):
+            vb.call("vbm_trace_request_start", w.handle, bad, b"train", b"c", 1, 1)
+    w.abort()
+    assert not (tmp_path / "u.jsonl").exists() and not (tmp_path / "u.jsonl.part").exists()
+
+
+def test_writer_rejections(rt, vb, tmp_path):
+    path = tmp_path / "r.jsonl"
+    w = rt.TraceWriter(path, small_layers(), "a", "b", 16)
+    assert Path(str(path) + ".part").exists() and not path.exists()
+    with pytest.raises(vb.VbmError, match="outside"):
+        w.route(0, [0])                                     # no open request
+    with pytest.raises(vb.VbmError, match="context"):
+        w.request_start("x", "train", "c", 10, 7)            # 10 + 7 > 16
+    with pytest.raises(vb.VbmError, match="split"):
+        w.request_start("x", "dev", "c", 1, 1)
+    w.request_start("x", "train", "c", 4, 2)
+    with pytest.raises(vb.VbmError, match="nested"):
+        w.request_start("y", "train", "c", 4, 2)
+    with pytest.raises(vb.VbmError, match="out-of-order"):
+        w.route(1, [0])                                     # layer 0 comes first
+    with pytest.raises(vb.VbmError, match="Out-of-range or duplicate"):
+        w.route(0, [3])
+    with pytest.raises(vb.VbmError, match="active"):
+        w.route(0, [0, 1])
+    with pytest.raises(vb.VbmError, match="not a routed layer"):
+        w.route(5, [0])
+    w.route(0, [1])
+    with pytest.raises(vb.VbmError, match="Missing or duplicate routing observations in layer 1"):
+        w.request_end("eos")
+    w.route(1, [2])
+    assert w.position() == (2, 1, 1, 0)
+    with pytest.raises(vb.VbmError, match="stop reason"):
+        w.request_end("limit")                              # 1 of 2 tokens
+    w.token(np.array([[0], [1]]))
+    with pytest.raises(vb.VbmError, match="max_tokens"):
+        w.route(0, [0])
+    with pytest.raises(vb.VbmError, match="stop reason"):
+        w.request_end("eos")                                # 2 of 2 tokens is the limit
+    w.request_end("limit")
+    with pytest.raises(vb.VbmError, match="duplicate request"):
+        w.request_start("x", "test", "c", 4, 2)
+    w.request_start("z", "test", "c", 4, 2)
+    with pytest.raises(vb.VbmError, match="incomplete"):
+        w.close()                                           # consumes the handle, drops the partial
+    assert not path.exists() and not Path(str(path) + ".part").exists()
+    # refuses to overwrite a published trace or a partial
+    write_small(rt, tmp_path / "done.jsonl")
+    with pytest.raises(vb.VbmError, match="overwrite"):
+        rt.TraceWriter(tmp_path / "done.jsonl", small_layers(), "a", "b", 16)
+    (tmp_path / "p.jsonl.part").write_text("")
+    with pytest.raises(vb.VbmError, match="overwrite"):
+        rt.TraceWriter(tmp_path / "p.jsonl", small_layers(), "a", "b", 16)
+    bad_layers = small_layers()
+    bad_layers[0]["active"] = 4
+    with pytest.raises(vb.VbmError, match="expert counts"):
+        rt.TraceWriter(tmp_path / "q.jsonl", bad_layers, "a", "b", 16)
+    bad_layers = small_layers(host=(11, 0))
+    with pytest.raises(vb.VbmError, match="byte accounting"):
+        rt.TraceWriter(tmp_path / "q.jsonl", bad_layers, "a", "b", 16)
+
+
+def test_writer_sorts_layers_and_token_strides(rt, tmp_path):
+    layers = [{"id": 7, "experts": 3, "active": 1, "bytes_per_expert": 20, "static_host_bytes_per_expert": 20},
+              {"id": 2, "experts": 4, "active": 2, "bytes_per_expert": 12, "static_host_bytes_per_expert": 6,
+               "tensor_types": ["q8_0", "f32", "q8_0"]}]
+    path = tmp_path / "v.jsonl"
+    with rt.TraceWriter(path, layers, "a", "b", 64) as w:
+        for split, toks in (("train", [[[0, 1], [0, 9]], [[1, 2], [1, 9]]]), ("test", [[[1, 3], [2, 9]]])):
+            w.request_start(split, split, "c", 1, len(toks))
+            for ids in toks:
+                # layer 2 (two experts) first, then layer 7 (one): rows of stride 2, padding ignored
+                w.token(np.array(ids, np.int32))
+            w.request_end("limit")
+    meta = json.loads(path.read_text().splitlines()[0])
+    assert [l["id"] for l in meta["layers"]] == [2, 7]
+    assert meta["layers"][0]["tensor_types"] == ["f32", "q8_0"]
+    assert meta["static_device_expert_bytes"] == 24
+    data = rt.read_trace(path)
+    assert [e.experts for e in data.events] == [(0, 1), (0,), (1, 2), (1,), (1, 3), (2,)]
+    # the reference analyzer test of the same shape: 3 calls, 32 cold bytes, gpu fraction 12/44
+    test_calls = sum(len(e.experts) for e in data.events_for("test"))
+    cold = sum(len(e.experts) * data.layers[e.layer].host_size for e in data.events_for("test"))
+    total = sum(len(e.experts) * data.layers[e.layer].size for e in data.events_for("test"))
+    assert (test_calls, cold) == (3, 32) and abs(1 - cold / total - 12 / 44) < 1e-12
+
+
+# ------------------------------------------------------------------------------------------------
+# reader: the reference analyzer's own cases
+
+
+def test_reader_counts(rt, tmp_path):
+    data = rt.read_trace(dump(tmp_path, records()))
+    assert data.tokens_for("train") == 3 and data.tokens_for("test") == 3
+    assert len(data.events) == 12 and len(data.sha256) == 64
+    assert all(r.verified for r in data.requests.values())
+
+
+def test_reader_rejects_incomplete_or_reordered(rt, tmp_path):
+    original = records()
+    bad = [original[:-1], original + [original[-1]], original[1:]]
+    changed = copy.deepcopy(original)
+    del changed[3]
+    bad.append(changed)
+    changed = copy.deepcopy(original)
+    changed[2], changed[3] = changed[3], changed[2]
+    bad.append(changed)
+    for values in bad:
+        with pytest.raises(ValueError):
+            rt.read_trace(dump(tmp_path, values))
+
+
+@pytest.mark.parametrize("changes", [{"experts": [True]}, {"experts": [-1]}, {"experts": [3]}, {"experts": [0, 0]},
+                                     {"token": True}, {"phase": "prefill"}, {"request": "unknown"}, {"layer": 99}])
+def test_reader_rejects_invalid_route(rt, tmp_path, changes):
+    values = records()
+    values[2].update(changes)
+    with pytest.raises(ValueError):
+        rt.read_trace(dump(tmp_path, values))
+
+
+@pytest.mark.parametrize("case", range(10))
+def test_reader_rejects_inconsistent_metadata_and_stops(rt, tmp_path, case):
+    values = records()
+    [lambda v: v[0].update(schema_version=True),
+     lambda v: v[0].update(static_device_expert_bytes=29),
+     lambda v: v[0]["layers"][0].update(static_host_bytes_per_expert=11),
+     lambda v: v[0]["layers"].append(v[0]["layers"][0]),
+     lambda v: v[8].update(decode_tokens=2),
+     lambda v: v[8].update(stop_reason="eos"),
+     lambda v: v[8].update(token_sequence_equivalent=False),
+     lambda v: v[8].update(token_sequence_equivalent="true"),
+     lambda v: v[-1].update(complete=False),
+     lambda v: [r.update(split="test") for r in v if r["type"] == "request_start"]][case](values)
+    with pytest.raises(ValueError):
+        rt.read_trace(dump(tmp_path, values))
+
+
+def test_reader_legacy_trace_is_not_verified(rt, tmp_path):
+    values = records()
+    for v in values:
+        v.pop("token_sequence_equivalent", None)
+    data = rt.read_trace(dump(tmp_path, values))
+    assert not any(r.verified for r in data.requests.values())
+
+
+def test_hotset_uses_training_counts_only(rt):
+    layers = {0: rt.Layer(3, 1, 10, 10)}
+    assert rt.hotset(rt.Counter({(0, 0): 10, (0, 1): 2}), layers, 10) == [(0, 0)]
+    layers = {0: rt.Layer(3, 1, 10, 10), 1: rt.Layer(3, 1, 25, 25)}
+    counts = rt.Counter({(1, 0): 5, (0, 2): 5, (0, 1): 4, (1, 1): 9})
+    # budget 40: (1,1) 25 B; then count 5 ties by size: (0,2) 10 B; (1,0) no longer fits; (0,1) does not
+    assert rt.hotset(counts, layers, 40) == [(1, 1), (0, 2)]
+
+
+# ------------------------------------------------------------------------------------------------
+# golden: the reference analyzer reading a trace written by this library
+
+
+def test_golden_trace_bytes_and_reference_reading(rt, tmp_path):
+    import make_routing_trace_golden as mk
+    report = json.loads((GOLDEN / "routing_trace_small_report.json").read_text())
+    path = mk.write_trace(tmp_path / "small.jsonl")
+    assert path.read_bytes() == (GOLDEN / "routing_trace_small.jsonl").read_bytes()
+    assert hashlib.sha256(path.read_bytes()).hexdigest() == report["trace_sha256"]
+    data = rt.read_trace(path)
+    assert data.sha256 == report["trace_sha256"]
+    assert len(data.events) == report["events"]
+    assert {"train": data.tokens_for("train"), "test": data.tokens_for("test")} == report["tokens"]
+    assert report["counts"] == {"layers": len(data.layers), "requests": len(data.requests),
+                                "train_tokens": data.tokens_for("train"), "test_tokens": data.tokens_for("test")}
+    assert report["observation_equivalence"]["all_requests_verified"] is True
+    plan = rt.plan_from_trace(data, mk.CAPACITY_EXPERTS)
+    assert len(plan) == mk.CAPACITY_EXPERTS
+    by_layer = {entry["layer"]: entry["experts"] for entry in report["trained_residency_plan"]["layers"]}
+    assert {l: sorted(e for ll, e in plan if ll == l) for l in range(4)} == by_layer
+    assert report["trained_residency_plan"]["used_bytes"] == len(plan) * mk.EXPERT_BYTES
+
+
+# ------------------------------------------------------------------------------------------------
+# frozen plans and the admission replay
+
+
+def test_trained_hot944_plan(rt):
+    assert hashlib.sha256(PLAN.read_bytes()).hexdigest() == \
+        "6a679bec76f1a410ed65fa79c186d164a388fc76419d96dcad5978782343949c"
+    plan = rt.read_plan(PLAN, 36, 128)
+    assert len(plan) == 944 and len(set(plan)) == 944
+    assert plan[:3] == [(26, 38), (30, 116), (35, 117)]
+    assert {l for l, _ in plan} == set(range(36))
+    with pytest.raises(ValueError):
+        rt.read_plan(PLAN, 35, 128)                         # layer 35 out of range
+    with pytest.raises(ValueError):
+        rt.read_plan(PLAN, 36, 127)                         # expert 127 out of range
+
+
+@pytest.mark.parametrize("text", ["0 1\n0 1\n", "0\n", "0 1 2\n", "a b\n", "-1 0\n", "0 8\n", "2 0\n"])
+def test_plan_rejections(rt, tmp_path, text):
+    p = tmp_path / "plan.txt"
+    p.write_text(text)
+    with pytest.raises(ValueError, match="frozen hybrid plan"):
+        rt.read_plan(p, 2, 8)
+
+
+def test_plan_comments_and_round_trip(rt, tmp_path):
+    p = tmp_path / "plan.txt"
+    p.write_text("# trained\n\n1 7\n0 3\n")
+    assert rt.read_plan(p, 2, 8) == [(1, 7), (0, 3)]
+    q = rt.write_plan(tmp_path / "q.txt", [(1, 7), (0, 3)])
+    assert rt.read_plan(q, 2, 8) == [(1, 7), (0, 3)]
+
+
+@pytest.mark.parametrize("policy", [0, 1, 3, 5])
+def test_replay_admission_matches_restatement(rt, tmp_path, policy):
+    import admission as ref
+    data = rt.read_trace(GOLDEN / "routing_trace_small.jsonl")
+    plan = rt.plan_from_trace(data, 6)
+    margin = 1 if policy == ref.LRU else 2
+    stats = rt.replay_admission(data, 2 + 10, policy, recent_window=8, margin=margin, plan=plan,
+                                lfu=(2, 1) if policy == ref.LFU else None)
+    py = ref.Admission(4, 16, 2, 12, 8, margin, policy)
+    if policy == ref.LFU:
+        py.lfu_admit_after, py.lfu_fill_after = 2, 1
+    for layer, expert in plan:
+        py.seed(layer, expert)
+    hits = admissions = evictions = staged = 0
+    for event in data.events:
+        h, adm = py.admit(event.layer, list(event.experts))
+        hits += sum(h)
+        admissions += len(adm)
+        evictions += sum(1 for _, _, ev in adm if ev >= 0)
+        staged += sum(1 for e in event.experts if py.slot_map[event.layer * 16 + e] < 0)
+    a = stats["all"]
+    assert (a.dispatches, a.hits, a.admissions, a.evictions, a.staged) == \
+        (len(data.events), hits, admissions, evictions, staged)
+    assert a.lookups == 2 * len(data.events) and a.admissions > 0
+    assert stats["train"].dispatches + stats["test"].dispatches == a.dispatches
+    assert stats["train"].hits + stats["test"].hits == a.hits

@@ -44,6 +44,8 @@ struct vbm_tier {
     float * y = nullptr;
     std::vector<const float *> gu_bias, dn_bias;
     vbm_tier_stats stats{};
+    vbm_trace * trace = nullptr;      // optional routing trace (caller-owned)
+    std::vector<int64_t> trace_layer_ids;
     bool started = false;             // seeded or stepped: the pool's slots are live
 
     ~vbm_tier() {
@@ -217,6 +219,11 @@ vbm_status vbm_tier_step(vbm_tier * t, const float * x, const float * logits, fl
         const hipStream_t s = as_stream(stream);
         const vbm_tier_desc & d = t->desc;
         const int64_t L = d.n_layers, E = d.n_expert, K = d.top_k, H = d.hidden;
+        if (t->trace) {
+            int64_t token = -1, next_layer = -1;
+            check_status(vbm_trace_position(t->trace, nullptr, nullptr, &token, &next_layer), "tier trace");
+            require(token >= 0 && next_layer == 0, "the attached trace has no open request at a token boundary");
+        }
         t->started = true;
         std::vector<int32_t> hits(static_cast<size_t>(K)), slots(static_cast<size_t>(K)),
             experts(static_cast<size_t>(K)), evicted(static_cast<size_t>(K));
@@ -227,6 +234,9 @@ vbm_status vbm_tier_step(vbm_tier * t, const float * x, const float * logits, fl
             check_hip(hipMemcpyAsync(t->host_ids, t->route_ids + l * K, sizeof(int32_t) * K, hipMemcpyDeviceToHost, s),
                       "tier ids");
             check_hip(hipStreamSynchronize(s), "tier ids synchronize");
+            if (t->trace)
+                check_status(vbm_trace_route(t->trace, t->trace_layer_ids[static_cast<size_t>(l)], t->host_ids, K),
+                             "tier trace");
             // 2. admission, then copies of admitted experts and staged misses
             int64_t n_admitted = 0;
             check_status(vbm_admission_admit(t->admission, l, t->host_ids, hits.data(), slots.data(), experts.data(),
@@ -289,6 +299,27 @@ vbm_status vbm_tier_step(vbm_tier * t, const float * x, const float * logits, fl
         }
         launch_combine(t->y, t->route_w + (L - 1) * K, H, K, 1, out, s);
         if (ids) check_hip(hipMemcpyAsync(ids, t->route_ids, sizeof(int32_t) * L * K, hipMemcpyDeviceToDevice, s), "ids copy");
+    });
+}
+
+vbm_status vbm_tier_set_trace(vbm_tier * t, vbm_trace * trace) {
+    return guarded([&] {
+        require(t != nullptr, "null tier");
+        std::vector<int64_t> ids;
+        if (trace) {
+            int64_t n = 0;
+            check_status(vbm_trace_position(trace, &n, nullptr, nullptr, nullptr), "tier trace");
+            require(n == t->desc.n_layers, "trace layer count does not match the tier");
+            for (int64_t l = 0; l < n; ++l) {
+                int64_t id = 0, experts = 0, active = 0;
+                check_status(vbm_trace_layer_info(trace, l, &id, &experts, &active), "tier trace");
+                require(experts == t->desc.n_expert && active == t->desc.top_k,
+                        "trace layer expert counts do not match the tier");
+                ids.push_back(id);
+            }
+        }
+        t->trace = trace;
+        t->trace_layer_ids = std::move(ids);
     });
 }
 

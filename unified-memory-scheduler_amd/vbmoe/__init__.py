@@ -38,6 +38,13 @@ class TierStats(C.Structure):
     ]
 
 
+class TraceLayer(C.Structure):
+    _fields_ = [
+        ("id", i64), ("experts", i64), ("active", i64), ("bytes_per_expert", u64),
+        ("static_host_bytes_per_expert", u64), ("tensor_types", C.c_char_p),
+    ]
+
+
 class MoeLayerDesc(C.Structure):
     _fields_ = [
         ("gate_up", vp), ("down", vp), ("gate_up_bias", vp), ("down_bias", vp), ("expert_to_slot", vp),
@@ -117,6 +124,17 @@ SIGNATURES = {
     "vbm_tier_seed": [vp, i64, i64],
     "vbm_tier_step": [vp, vp, vp, vp, vp, vp],
     "vbm_tier_get_stats": [vp, C.POINTER(TierStats)],
+    "vbm_tier_set_trace": [vp, vp],
+    "vbm_trace_open": [C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, i64, C.POINTER(TraceLayer), i64,
+                       C.c_char_p, C.POINTER(vp)],
+    "vbm_trace_request_start": [vp, C.c_char_p, C.c_char_p, C.c_char_p, i64, i64],
+    "vbm_trace_route": [vp, i64, vp, i64],
+    "vbm_trace_token": [vp, vp, i64],
+    "vbm_trace_request_end": [vp, C.c_char_p, C.c_int],
+    "vbm_trace_close": [vp],
+    "vbm_trace_abort": [vp],
+    "vbm_trace_layer_info": [vp, i64, C.POINTER(i64), C.POINTER(i64), C.POINTER(i64)],
+    "vbm_trace_position": [vp, C.POINTER(i64), C.POINTER(i64), C.POINTER(i64), C.POINTER(i64)],
 }
 OTHER = {
     "vbm_last_error": ([], C.c_char_p),
