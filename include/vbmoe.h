@@ -220,8 +220,8 @@ vbm_status vbm_weighted_combine(const float * y, const float * weights, int64_t 
 typedef struct vbm_moe_layer_desc {
     const vbm_bank * gate_up;      /* fused 2*I-row bank, interleave = 1                        */
     const vbm_bank * down;         /* H-row bank, k = I                                         */
-    const float * gate_up_bias;    /* device, [n_slots][2*I] in ggml row order (gate | up), or NULL */
-    const float * down_bias;       /* device, [n_slots][H], or NULL                              */
+    const float * gate_up_bias;    /* device, [n_expert][2*I] by expert id, gate | up, or NULL   */
+    const float * down_bias;       /* device, [n_expert][H] by expert id, or NULL                */
     const int32_t * expert_to_slot;/* device [n_expert] or NULL (identity)                       */
     const float * router_w;        /* device fp32 [n_expert][H] or NULL (logits given)           */
     const float * router_b;        /* device fp32 [n_expert] or NULL                             */
@@ -343,6 +343,46 @@ int vbm_moe_cold_gpu_budget(int cold_experts);
 int32_t vbm_moe_gpu_slot_limit(int32_t resident_slots, int cold_gpu);
 
 /* ----------------------------------------------------------------------------------------------
+ * GGUF expert tensors (tools/engine/gguf_experts.cpp:27-140): blk.L.ffn_{gate,up,down}_exps.
+ * {weight,bias} (or the fused blk.L.ffn_gate_up_exps.weight) of a GGUF file and its
+ * "-0000k-of-0000N.gguf" shards, read one expert slice at a time. Headers are parsed at open;
+ * tensor data is read on demand with pread. Weights must be MXFP4 or Q8_0, biases F32.
+ * -------------------------------------------------------------------------------------------- */
+typedef struct vbm_gguf vbm_gguf;
+
+typedef struct {
+    int64_t hidden, intermediate, n_expert;
+    int gate_up_type, down_type;             /* ggml type ids                                    */
+    int fused_gate_up;                       /* ffn_gate_up_exps instead of separate gate / up   */
+    int has_bias;
+    uint64_t gate_up_bytes, down_bytes;      /* ggml bytes of one expert (gate rows then up rows) */
+} vbm_gguf_expert_info;
+
+/* path: a single .gguf or the first shard "<stem>-00001-of-NNNNN.gguf" (then all NNNNN are read). */
+vbm_status vbm_gguf_open(const char * path, vbm_gguf ** gguf);
+vbm_status vbm_gguf_close(vbm_gguf * gguf);
+vbm_status vbm_gguf_shards(const vbm_gguf * gguf, int64_t * shards, int64_t * tensors);
+/* Metadata of integer (or bool) / string keys. found == NULL makes a missing key an error. */
+vbm_status vbm_gguf_get_u64(const vbm_gguf * gguf, const char * key, uint64_t * value, int * found);
+vbm_status vbm_gguf_get_string(const vbm_gguf * gguf, const char * key, char * dst, size_t capacity, int * found);
+/* ne[4] ggml dimensions; nbytes 0 for types of unknown block size. */
+vbm_status vbm_gguf_tensor_info(const vbm_gguf * gguf, const char * name, int * type, int64_t * ne,
+                                uint64_t * nbytes, int * found);
+vbm_status vbm_gguf_expert_layer_info(const vbm_gguf * gguf, int64_t layer, vbm_gguf_expert_info * info);
+/* Host copies of one expert: ggml bytes of gate|up (gate_up_bytes) and down (down_bytes), fp32
+ * biases gate|up [2I] and down [H] (zeros when the file has none). Any output may be NULL. */
+vbm_status vbm_gguf_read_expert(const vbm_gguf * gguf, int64_t layer, int64_t expert, void * gate_up,
+                                void * down, float * gate_up_bias, float * down_bias);
+/* experts[n] of `layer` into bank slots[n] (NULL: slot = expert id) of a fused interleaved gate_up
+ * bank and a down bank, plus every expert's biases into device arrays indexed by expert id
+ * (either may be NULL). Synchronous on `stream` for the biases. */
+vbm_status vbm_gguf_load_layer(const vbm_gguf * gguf, int64_t layer, const int32_t * experts,
+                               const int32_t * slots, int64_t n, vbm_bank * gate_up, vbm_bank * down,
+                               float * gate_up_bias, float * down_bias, void * stream);
+vbm_status vbm_gguf_load_biases(const vbm_gguf * gguf, int64_t layer, float * gate_up_bias,
+                                float * down_bias, void * stream);
+
+/* ----------------------------------------------------------------------------------------------
  * Decode routing traces in the reference's JSONL schema (benchmarks/schema/
  * vrambridge-routing-trace.schema.json), written like its collector tools/trace/routing_trace.cpp:
  * metadata (:701-728), request_start (:501-503), one route per routed layer and decoded token
@@ -428,6 +468,9 @@ vbm_status vbm_tier_set_expert(vbm_tier * tier, int64_t layer, int64_t expert, c
  * Both stores must precede seeding and stepping. */
 vbm_status vbm_tier_generate(vbm_tier * tier, uint64_t seed, uint64_t layer_stride, uint64_t gate_up_stream,
                              uint64_t down_stream, float p0, float p1, void * stream);
+/* Store every expert of GGUF layers layer_ids[n_layers] (tier layer l <- GGUF layer layer_ids[l]);
+ * shapes and types must match the tier. Biases stay the caller's (vbm_gguf_load_biases). */
+vbm_status vbm_tier_load_gguf(vbm_tier * tier, const vbm_gguf * gguf, const int64_t * layer_ids, void * stream);
 /* Frozen-plan seed: admit (layer, expert) into the next slot and copy it there. */
 vbm_status vbm_tier_seed(vbm_tier * tier, int64_t layer, int64_t expert);
 /* x [hidden] (16-byte aligned) -> out [hidden]; logits [n_layers][n_expert]; ids optional

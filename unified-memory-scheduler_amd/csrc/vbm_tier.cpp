@@ -201,6 +201,29 @@ vbm_status vbm_tier_generate(vbm_tier * t, uint64_t seed, uint64_t layer_stride,
     });
 }
 
+vbm_status vbm_tier_load_gguf(vbm_tier * t, const vbm_gguf * g, const int64_t * layer_ids, void * stream) {
+    return guarded([&] {
+        require(t != nullptr && g != nullptr && layer_ids != nullptr, "null argument");
+        require(!t->started, "experts must be stored before the tier is seeded or stepped");
+        const vbm_tier_desc & d = t->desc;
+        std::vector<uint8_t> gu, dn;
+        for (int64_t l = 0; l < d.n_layers; ++l) {
+            vbm_gguf_expert_info info{};
+            check_status(vbm_gguf_expert_layer_info(g, layer_ids[l], &info), "tier gguf layer");
+            require(info.gate_up_type == d.type && info.down_type == d.type && info.hidden == d.hidden &&
+                        info.intermediate == d.intermediate && info.n_expert == d.n_expert,
+                    "GGUF layer " + std::to_string(layer_ids[l]) + " does not match the tier's shape and type");
+            gu.resize(info.gate_up_bytes);
+            dn.resize(info.down_bytes);
+            for (int64_t e = 0; e < d.n_expert; ++e) {
+                check_status(vbm_gguf_read_expert(g, layer_ids[l], e, gu.data(), dn.data(), nullptr, nullptr),
+                             "tier gguf read");
+                check_status(vbm_tier_set_expert(t, l, e, gu.data(), dn.data(), stream), "tier gguf store");
+            }
+        }
+    });
+}
+
 vbm_status vbm_tier_seed(vbm_tier * t, int64_t layer, int64_t expert) {
     return guarded([&] {
         require(t != nullptr, "null tier");

@@ -45,6 +45,13 @@ class TraceLayer(C.Structure):
     ]
 
 
+class GgufExpertInfo(C.Structure):
+    _fields_ = [
+        ("hidden", i64), ("intermediate", i64), ("n_expert", i64), ("gate_up_type", C.c_int), ("down_type", C.c_int),
+        ("fused_gate_up", C.c_int), ("has_bias", C.c_int), ("gate_up_bytes", u64), ("down_bytes", u64),
+    ]
+
+
 class MoeLayerDesc(C.Structure):
     _fields_ = [
         ("gate_up", vp), ("down", vp), ("gate_up_bias", vp), ("down_bias", vp), ("expert_to_slot", vp),
@@ -125,6 +132,17 @@ SIGNATURES = {
     "vbm_tier_step": [vp, vp, vp, vp, vp, vp],
     "vbm_tier_get_stats": [vp, C.POINTER(TierStats)],
     "vbm_tier_set_trace": [vp, vp],
+    "vbm_tier_load_gguf": [vp, vp, vp, vp],
+    "vbm_gguf_open": [C.c_char_p, C.POINTER(vp)],
+    "vbm_gguf_close": [vp],
+    "vbm_gguf_shards": [vp, C.POINTER(i64), C.POINTER(i64)],
+    "vbm_gguf_get_u64": [vp, C.c_char_p, C.POINTER(u64), C.POINTER(C.c_int)],
+    "vbm_gguf_get_string": [vp, C.c_char_p, C.c_char_p, sz, C.POINTER(C.c_int)],
+    "vbm_gguf_tensor_info": [vp, C.c_char_p, C.POINTER(C.c_int), C.POINTER(i64), C.POINTER(u64), C.POINTER(C.c_int)],
+    "vbm_gguf_expert_layer_info": [vp, i64, C.POINTER(GgufExpertInfo)],
+    "vbm_gguf_read_expert": [vp, i64, i64, vp, vp, vp, vp],
+    "vbm_gguf_load_layer": [vp, i64, vp, vp, i64, vp, vp, vp, vp, vp],
+    "vbm_gguf_load_biases": [vp, i64, vp, vp, vp],
     "vbm_trace_open": [C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, i64, C.POINTER(TraceLayer), i64,
                        C.c_char_p, C.POINTER(vp)],
     "vbm_trace_request_start": [vp, C.c_char_p, C.c_char_p, C.c_char_p, i64, i64],
