@@ -452,6 +452,9 @@ typedef struct {
 typedef struct {
     uint64_t dispatches, hits, admissions, evictions, staged, uploaded_bytes;
     double copy_ms;                      /* copy-stream busy time (events around each layer's copies) */
+    uint64_t prefill_tokens;             /* tokens through vbm_tier_prefill                       */
+    uint64_t prefill_resident;           /* routed experts computed from resident slots (per call) */
+    uint64_t prefill_streamed;           /* routed experts streamed through the reserved slots    */
 } vbm_tier_stats;
 
 typedef struct vbm_tier vbm_tier;
@@ -477,6 +480,18 @@ vbm_status vbm_tier_seed(vbm_tier * tier, int64_t layer, int64_t expert);
  * [n_layers][top_k]. Bit-identical to vbm_decode_step on resident banks holding the same experts. */
 vbm_status vbm_tier_step(vbm_tier * tier, const float * x, const float * logits, float * out, int32_t * ids,
                          void * stream);
+/* Multi-token prefill of one layer (16..65536 tokens; the MFMA grouped GEMM, VBM_ORDER_FAST):
+ * x [T][hidden] (16-byte aligned) -> out [T][hidden]; logits [T][n_expert]; ids / weights optional
+ * [T][top_k]. Residency is frozen for the batch (no admission; the reference freezes it for
+ * multi-position dispatch, llama-b11669-hybrid-experts.patch:3252-3257): the routed experts
+ * resident in the pool are computed from their slots in one pass, and the others stream through
+ * the reserved slots in chunks of top_k / 2, each chunk's copies on the side stream overlapping
+ * the previous chunk's GEMMs. This is the device-side counterpart of the reference's
+ * resident-down prefill split (llama-b11669-resident-down-prefill-experimental.patch:192-283),
+ * which runs cold experts on the CPU instead. Outputs are bit-identical to
+ * vbm_moe_layer_forward (VBM_ORDER_FAST) over banks holding every expert. */
+vbm_status vbm_tier_prefill(vbm_tier * tier, int64_t layer, const float * x, const float * logits,
+                            int64_t n_tokens, float * out, int32_t * ids, float * weights, void * stream);
 vbm_status vbm_tier_get_stats(const vbm_tier * tier, vbm_tier_stats * stats);
 
 /* Attach a routing trace (or NULL to detach): every vbm_tier_step then records each layer's

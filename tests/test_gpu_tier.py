@@ -172,3 +172,75 @@ def test_tier_routing_trace_replays_to_the_same_decisions(gpu, tmp_path):
         vb.call("vbm_tier_destroy", tier)
     print(f"[tier trace] {len(data.events)} routes, hit rate {stats['all'].hit_rate:.3f} "
           f"(train {stats['train'].hit_rate:.3f}, test {stats['test'].hit_rate:.3f})", flush=True)
+
+
+@pytest.mark.parametrize("type_id", [39, 8])
+def test_tier_prefill_matches_resident_layer(gpu, type_id):
+    """Multi-token prefill through the tier (resident experts in one pass, the others streamed
+    through the reserved slots in chunks) is bit-identical to the fused layer forward over banks
+    holding every expert (both in the fast accumulation order), before and after decode steps
+    have changed the pool."""
+    vb = gpu
+    L, E, K, H, I, slots, T = 2, 16, 4, 256, 256, 4 + 6, 48
+    act = vb.ACT_SWIGLU_OAI if type_id == 39 else vb.ACT_SILU
+    p0, p1 = (-8, -3) if type_id == 39 else (1e-4, 5e-4)
+    biases = [(vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 16 * l + 3, 0, E * 2 * I, 0.0, 0.02)),
+               vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 16 * l + 4, 0, E * H, 0.0, 0.02))) for l in range(L)]
+    banks, descs = [], []
+    for l in range(L):
+        gu, dn = vb.Bank(type_id, 2 * I, H, E, True), vb.Bank(type_id, H, I, E, False)
+        gu.generate(0, E, SEED, 16 * l + 1, 0, p0, p1)
+        dn.generate(0, E, SEED, 16 * l + 2, 0, p0, p1)
+        banks.append((gu, dn))
+        descs.append(vb.MoeLayerDesc(gu.handle, dn.handle, biases[l][0].ptr, biases[l][1].ptr, None, None, None,
+                                     H, I, E, K, act, vb.ORDER_FAST))
+    gub = (C.c_void_p * L)(*[b[0].ptr for b in biases])
+    dnb = (C.c_void_p * L)(*[b[1].ptr for b in biases])
+    desc = vb.TierDesc(type_id, H, I, L, E, K, act, slots, 8, 2, vb.ADMIT_CLASSIC,
+                       C.cast(gub, C.POINTER(C.c_void_p)), C.cast(dnb, C.POINTER(C.c_void_p)))
+    tier = C.c_void_p()
+    vb.call("vbm_tier_create", C.byref(desc), C.byref(tier))
+    vb.call("vbm_tier_generate", tier.value, SEED, 16, 1, 2, p0, p1, None)
+    for l, e in ((0, 3), (0, 5), (0, 7), (1, 2)):
+        vb.call("vbm_tier_seed", tier.value, l, e)
+    rng = np.random.default_rng(type_id)
+    out1, out2 = vb.DeviceBuffer(4 * T * H), vb.DeviceBuffer(4 * T * H)
+    i1, i2 = vb.DeviceBuffer(4 * T * K), vb.DeviceBuffer(4 * T * K)
+    w1, w2 = vb.DeviceBuffer(4 * T * K), vb.DeviceBuffer(4 * T * K)
+
+    def compare(tag):
+        for l in range(L):
+            x = vb.DeviceBuffer.from_array(rng.standard_normal((T, H)).astype(np.float32))
+            lg = vb.DeviceBuffer.from_array(rng.standard_normal((T, E)).astype(np.float32))
+            ws = C.c_size_t()
+            vb.call("vbm_moe_layer_workspace", C.byref(descs[l]), T, C.byref(ws))
+            work = vb.DeviceBuffer(ws.value)
+            vb.call("vbm_moe_layer_forward", C.byref(descs[l]), x.ptr, lg.ptr, T, out1.ptr, i1.ptr, w1.ptr, work.ptr,
+                    ws.value, None)
+            vb.call("vbm_tier_prefill", tier.value, l, x.ptr, lg.ptr, T, out2.ptr, i2.ptr, w2.ptr, None)
+            vb.call("vbm_stream_synchronize", None)
+            assert np.array_equal(i1.download(np.int32, (T, K)), i2.download(np.int32, (T, K))), (tag, l)
+            assert np.array_equal(w1.download(np.uint32, (T, K)), w2.download(np.uint32, (T, K))), (tag, l)
+            a, b = out1.download(np.uint32, (T, H)), out2.download(np.uint32, (T, H))
+            assert np.array_equal(a, b), (tag, l, int(np.count_nonzero(a != b)))
+
+    compare("seeded")
+    # decode steps admit experts into the pool and stage misses in the reserved slots
+    logits, _ = routed_logits(np.random.default_rng(4), L, E, K, 8)
+    x1 = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 6, 0, H))
+    dl, o = vb.DeviceBuffer(logits[0].nbytes), vb.DeviceBuffer(4 * H)
+    for t in range(8):
+        dl.upload(logits[t])
+        vb.call("vbm_tier_step", tier.value, x1.ptr, dl.ptr, o.ptr, None, None)
+    compare("after decode")
+    with pytest.raises(vb.VbmError, match="16"):
+        vb.call("vbm_tier_prefill", tier.value, 0, x1.ptr, dl.ptr, 8, out2.ptr, None, None, None)
+    st = vb.TierStats()
+    vb.call("vbm_tier_get_stats", tier.value, C.byref(st))
+    print(f"[tier prefill type={type_id}] tokens={st.prefill_tokens} resident={st.prefill_resident} "
+          f"streamed={st.prefill_streamed} admissions={st.admissions}", flush=True)
+    assert st.prefill_tokens == 4 * T and st.prefill_resident > 0 and st.prefill_streamed > 0
+    vb.call("vbm_tier_destroy", tier.value)
+    for gu, dn in banks:
+        gu.destroy()
+        dn.destroy()

@@ -181,6 +181,32 @@ int64_t gemm_max_tiles(int64_t n_as, int64_t n_entries);
 size_t gemm_tiles_bytes(int64_t n_as, int64_t n_entries);
 void launch_grouped_gemm(const GemmParams & p, hipStream_t stream);
 
+// Device workspace of one fused layer forward (vbm_moe_layer_forward), carved from `base` (NULL:
+// sizes only).
+struct LayerWorkspace {
+    int32_t * ids;
+    float * weights;
+    float * logits;
+    uint8_t * xrows_x;     // [T] activation rows of the layer input (gate_up format)
+    void * group;
+    uint8_t * xrows_act;   // [T*K] requantized GLU outputs (down format)
+    void * tiles;          // GEMM tile lists (fast order only)
+    float * y;             // [T*K][H] down outputs per (token, rank)
+    size_t total;
+};
+constexpr int64_t kGemmMinTokens = 16;
+bool use_gemm(const vbm_moe_layer_desc & d, int64_t n_tokens);
+LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint8_t * base);
+// Prefill through the grouped GEMM in steps: the input rows and the token->expert grouping once,
+// then one or more passes over disjoint expert subsets (experts whose expert_to_slot entry is
+// -1 are skipped: their workgroups exit without writing), each writing the down outputs y of its
+// entries; the combine of y runs once all entries are written. events (optional) [4]: around the
+// pass's gate_up and down GEMMs.
+void prefill_prepare(const vbm_moe_layer_desc & d, const float * x, const int32_t * ids, int64_t n_tokens,
+                     const LayerWorkspace & w, hipStream_t s);
+void prefill_pass(const vbm_moe_layer_desc & d, const int32_t * expert_to_slot, int64_t n_tokens,
+                  const LayerWorkspace & w, void * const * events, hipStream_t s);
+
 // Kernel A of the fused single-token decode: routing, input combine + Q8_0, gate_up GEMV, GLU,
 // requantization into the down activation rows.
 struct DecodeGateUpArgs {

@@ -52,25 +52,15 @@ void validate_ids_on_host(const int32_t * ids, int64_t n_ids, int64_t n_tokens, 
         }
 }
 
-// Layers of at least this many tokens use the MFMA grouped GEMM when the caller asks for the fast
-// accumulation order; below it the exact GEMV path is used (its results satisfy either order).
-constexpr int64_t kGemmMinTokens = 16;
+}  // namespace
 
+namespace vbm {
+
+// Layers of at least kGemmMinTokens tokens use the MFMA grouped GEMM when the caller asks for the
+// fast accumulation order; below it the exact GEMV path is used (its results satisfy either order).
 bool use_gemm(const vbm_moe_layer_desc & d, int64_t n_tokens) {
     return d.order == VBM_ORDER_FAST && n_tokens >= kGemmMinTokens;
 }
-
-struct LayerWorkspace {
-    int32_t * ids;
-    float * weights;
-    float * logits;
-    uint8_t * xrows_x;     // [T] activation rows of the layer input (gate_up format)
-    void * group;
-    uint8_t * xrows_act;   // [T*K] requantized GLU outputs (down format)
-    void * tiles;          // GEMM tile lists (fast order only)
-    float * y;
-    size_t total;
-};
 
 LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint8_t * base) {
     LayerWorkspace w{};
@@ -94,6 +84,56 @@ LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint
     w.total = off;
     return w;
 }
+
+void prefill_prepare(const vbm_moe_layer_desc & d, const float * x, const int32_t * ids, int64_t n_tokens,
+                     const LayerWorkspace & w, hipStream_t s) {
+    const GemmRowLayout gx{d.hidden / 32, d.gate_up->type};
+    launch_gemm_rows_from_f32(x, n_tokens, d.hidden, d.hidden, gx, w.xrows_x, s);
+    const GroupBuffers g = carve_group(w.group, d.n_expert, n_tokens * d.top_k);
+    launch_group(ids, d.top_k, n_tokens, d.top_k, d.n_expert, g, s);
+}
+
+void prefill_pass(const vbm_moe_layer_desc & d, const int32_t * expert_to_slot, int64_t n_tokens,
+                  const LayerWorkspace & w, void * const * events, hipStream_t s) {
+    const int64_t K = d.top_k;
+    const GemmRowLayout gx{d.hidden / 32, d.gate_up->type}, ga{d.intermediate / 32, d.down->type};
+    GemmParams p{};
+    p.expert_to_slot = expert_to_slot;
+    p.n_ids = K;
+    p.n_as = d.n_expert;
+    p.n_entries = n_tokens * K;
+    p.group = carve_group(w.group, d.n_expert, n_tokens * K);
+    p.tiles = w.tiles;
+    p.activation = d.activation;
+    p.alpha = 1.702f;
+    p.limit = 7.0f;
+    p.bank = d.gate_up;
+    p.rows_in = w.xrows_x;
+    p.lay = gx;
+    p.b_ne1 = 1;
+    p.bias = d.gate_up_bias;
+    p.rows_out = w.xrows_act;
+    p.out_layout = ga;
+    p.epilogue = 1;
+    if (events) check_hip(hipEventRecord(static_cast<hipEvent_t>(events[0]), s), "hipEventRecord");
+    launch_grouped_gemm(p, s);
+    if (events) check_hip(hipEventRecord(static_cast<hipEvent_t>(events[1]), s), "hipEventRecord");
+    p.bank = d.down;
+    p.rows_in = w.xrows_act;
+    p.lay = ga;
+    p.b_ne1 = K;
+    p.bias = d.down_bias;
+    p.dst = w.y;
+    p.rows_out = nullptr;
+    p.epilogue = 0;
+    if (events) check_hip(hipEventRecord(static_cast<hipEvent_t>(events[2]), s), "hipEventRecord");
+    launch_grouped_gemm(p, s);
+    if (events) check_hip(hipEventRecord(static_cast<hipEvent_t>(events[3]), s), "hipEventRecord");
+}
+
+}  // namespace vbm
+
+namespace {
 
 void validate_layer(const vbm_moe_layer_desc * d) {
     require(d != nullptr && d->gate_up != nullptr && d->down != nullptr, "layer needs gate_up and down banks");
@@ -137,41 +177,8 @@ void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits
     const GroupBuffers g = carve_group(w.group, d->n_expert, entries);
     if (use_gemm(*d, n_tokens)) {
         // Prefill-sized groups: MFMA grouped GEMM (exact block dots, fp32 accumulation order).
-        const GemmRowLayout gx{H / 32, d->gate_up->type}, ga{I / 32, d->down->type};
-        launch_gemm_rows_from_f32(x, n_tokens, H, H, gx, w.xrows_x, s);
-        launch_group(ids_d, K, n_tokens, K, d->n_expert, g, s);
-        GemmParams p{};
-        p.expert_to_slot = d->expert_to_slot;
-        p.n_ids = K;
-        p.n_as = d->n_expert;
-        p.n_entries = entries;
-        p.group = g;
-        p.tiles = w.tiles;
-        p.activation = d->activation;
-        p.alpha = 1.702f;
-        p.limit = 7.0f;
-        p.bank = d->gate_up;
-        p.rows_in = w.xrows_x;
-        p.lay = gx;
-        p.b_ne1 = 1;
-        p.bias = d->gate_up_bias;
-        p.rows_out = w.xrows_act;
-        p.out_layout = ga;
-        p.epilogue = 1;
-        record(events, 0, s);
-        launch_grouped_gemm(p, s);
-        record(events, 1, s);
-        p.bank = d->down;
-        p.rows_in = w.xrows_act;
-        p.lay = ga;
-        p.b_ne1 = K;
-        p.bias = d->down_bias;
-        p.dst = w.y;
-        p.rows_out = nullptr;
-        p.epilogue = 0;
-        record(events, 2, s);
-        launch_grouped_gemm(p, s);
-        record(events, 3, s);
+        prefill_prepare(*d, x, ids_d, n_tokens, w, s);
+        prefill_pass(*d, d->expert_to_slot, n_tokens, w, events, s);
         launch_combine(w.y, w_d, H, K, n_tokens, out, s);
         return;
     }

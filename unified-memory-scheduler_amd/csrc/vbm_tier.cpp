@@ -44,6 +44,16 @@ struct vbm_tier {
     float * y = nullptr;
     std::vector<const float *> gu_bias, dn_bias;
     vbm_tier_stats stats{};
+    hipEvent_t last_use = nullptr;    // end of the previous step / prefill on its stream
+    bool used = false;
+    // prefill (vbm_tier_prefill): layer workspace, per-pass expert->slot maps, ping-pong events
+    uint8_t * pf_work = nullptr;
+    size_t pf_work_bytes = 0;
+    int32_t * pf_maps = nullptr;      // device [passes][n_expert]
+    int32_t * pf_maps_host = nullptr; // pinned mirror
+    int32_t * pf_ids_host = nullptr;  // pinned [max tokens][top_k]
+    int64_t pf_tokens = 0;            // capacity of pf_work / pf_ids_host in tokens
+    hipEvent_t pf_ready[2] = {nullptr, nullptr}, pf_done[2] = {nullptr, nullptr};
     vbm_trace * trace = nullptr;      // optional routing trace (caller-owned)
     std::vector<int64_t> trace_layer_ids;
     bool started = false;             // seeded or stepped: the pool's slots are live
@@ -62,6 +72,15 @@ struct vbm_tier {
         if (copy_begin) (void)hipEventDestroy(copy_begin);
         if (copy_end) (void)hipEventDestroy(copy_end);
         if (copy_stream) (void)hipStreamDestroy(copy_stream);
+        if (last_use) (void)hipEventDestroy(last_use);
+        for (int i = 0; i < 2; ++i) {
+            if (pf_ready[i]) (void)hipEventDestroy(pf_ready[i]);
+            if (pf_done[i]) (void)hipEventDestroy(pf_done[i]);
+        }
+        if (pf_work) (void)hipFree(pf_work);
+        if (pf_maps) (void)hipFree(pf_maps);
+        if (pf_maps_host) (void)hipHostFree(pf_maps_host);
+        if (pf_ids_host) (void)hipHostFree(pf_ids_host);
     }
 
     uint8_t * host_expert(int64_t layer, int64_t expert) const {
@@ -125,6 +144,14 @@ vbm_status vbm_tier_create(const vbm_tier_desc * d, vbm_tier ** out) {
         check_hip(hipStreamCreateWithFlags(&t->copy_stream, hipStreamNonBlocking), "tier copy stream");
         check_hip(hipEventCreate(&t->copy_begin), "tier event");
         check_hip(hipEventCreate(&t->copy_end), "tier event");
+        check_hip(hipEventCreateWithFlags(&t->last_use, hipEventDisableTiming), "tier event");
+        for (int i = 0; i < 2; ++i) {
+            check_hip(hipEventCreateWithFlags(&t->pf_ready[i], hipEventDisableTiming), "tier event");
+            check_hip(hipEventCreateWithFlags(&t->pf_done[i], hipEventDisableTiming), "tier event");
+        }
+        check_hip(hipMalloc(reinterpret_cast<void **>(&t->pf_maps), sizeof(int32_t) * E * (E + 1)), "tier prefill maps");
+        check_hip(hipHostMalloc(reinterpret_cast<void **>(&t->pf_maps_host), sizeof(int32_t) * E * (E + 1),
+                                hipHostMallocDefault), "tier prefill maps");
         t->act_layout = XrowLayout{I / 32, d->type};
         const size_t route = align_up(sizeof(int32_t) * L * K), wts = align_up(sizeof(float) * L * K);
         const size_t act = align_up(sizeof(float) * K * I);
@@ -265,6 +292,8 @@ vbm_status vbm_tier_step(vbm_tier * t, const float * x, const float * logits, fl
             check_status(vbm_admission_admit(t->admission, l, t->host_ids, hits.data(), slots.data(), experts.data(),
                                              evicted.data(), &n_admitted), "tier admission");
             ++t->stats.dispatches;
+            if (l == 0 && t->used)   // slots the previous call's kernels read may be restaged now
+                check_hip(hipStreamWaitEvent(t->copy_stream, t->last_use, 0), "tier reuse wait");
             check_hip(hipEventRecord(t->copy_begin, t->copy_stream), "tier copy event");
             const uint64_t before = t->stats.uploaded_bytes;
             for (int64_t i = 0; i < n_admitted; ++i) stage(*t, l, experts[i], slots[i]);
@@ -322,6 +351,102 @@ vbm_status vbm_tier_step(vbm_tier * t, const float * x, const float * logits, fl
         }
         launch_combine(t->y, t->route_w + (L - 1) * K, H, K, 1, out, s);
         if (ids) check_hip(hipMemcpyAsync(ids, t->route_ids, sizeof(int32_t) * L * K, hipMemcpyDeviceToDevice, s), "ids copy");
+        check_hip(hipEventRecord(t->last_use, s), "tier last use");
+        t->used = true;
+    });
+}
+
+vbm_status vbm_tier_prefill(vbm_tier * t, int64_t layer, const float * x, const float * logits, int64_t n_tokens,
+                            float * out, int32_t * ids, float * weights, void * stream) {
+    return guarded([&] {
+        require(t != nullptr && x && logits && out, "null buffer");
+        const vbm_tier_desc & d = t->desc;
+        require(layer >= 0 && layer < d.n_layers, "layer out of range");
+        require(n_tokens >= kGemmMinTokens && n_tokens <= 65536,
+                "tier prefill takes 16..65536 tokens (single tokens: vbm_tier_step)");
+        const hipStream_t s = as_stream(stream);
+        const int64_t E = d.n_expert, K = d.top_k, H = d.hidden, T = n_tokens;
+        vbm_moe_layer_desc desc{};
+        desc.gate_up = t->gate_up;
+        desc.down = t->down;
+        desc.gate_up_bias = t->gu_bias[layer];
+        desc.down_bias = t->dn_bias[layer];
+        desc.hidden = H;
+        desc.intermediate = d.intermediate;
+        desc.n_expert = E;
+        desc.top_k = K;
+        desc.activation = d.activation;
+        desc.order = VBM_ORDER_FAST;
+        if (T > t->pf_tokens) {           // grow the workspace (rare: a larger batch than before)
+            check_hip(hipStreamSynchronize(s), "tier prefill grow");
+            if (t->used) check_hip(hipEventSynchronize(t->last_use), "tier prefill grow");
+            if (t->pf_work) check_hip(hipFree(t->pf_work), "tier prefill grow");
+            if (t->pf_ids_host) check_hip(hipHostFree(t->pf_ids_host), "tier prefill grow");
+            t->pf_work = nullptr;
+            t->pf_ids_host = nullptr;
+            t->pf_tokens = 0;
+            const size_t bytes = plan_layer(desc, T, nullptr).total;
+            check_hip(hipMalloc(reinterpret_cast<void **>(&t->pf_work), bytes), "tier prefill workspace");
+            check_hip(hipHostMalloc(reinterpret_cast<void **>(&t->pf_ids_host), sizeof(int32_t) * T * K,
+                                    hipHostMallocDefault), "tier prefill ids");
+            t->pf_work_bytes = bytes;
+            t->pf_tokens = T;
+        }
+        const LayerWorkspace w = plan_layer(desc, T, t->pf_work);
+        // 1. routing, input rows and grouping; the routed ids come to the host
+        launch_router(nullptr, nullptr, nullptr, H, const_cast<float *>(logits), E, T, K, w.ids, w.weights, s);
+        prefill_prepare(desc, x, w.ids, T, w, s);
+        check_hip(hipMemcpyAsync(t->pf_ids_host, w.ids, sizeof(int32_t) * T * K, hipMemcpyDeviceToHost, s), "prefill ids");
+        check_hip(hipStreamSynchronize(s), "prefill ids synchronize");
+        if (t->used) check_hip(hipStreamWaitEvent(t->copy_stream, t->last_use, 0), "tier reuse wait");
+        t->started = true;
+        // 2. residency is frozen for multi-token batches: pass 0 covers the resident experts, then
+        //    the remaining routed experts stream through the reserved slots in chunks
+        int32_t * maps = t->pf_maps_host;
+        check_status(vbm_admission_slot_map(t->admission, layer, maps), "prefill slot map");
+        std::vector<char> routed(static_cast<size_t>(E), 0);
+        for (int64_t i = 0; i < T * K; ++i) routed[static_cast<size_t>(t->pf_ids_host[i])] = 1;
+        std::vector<int32_t> cold;
+        uint64_t resident_hits = 0;
+        for (int64_t e = 0; e < E; ++e) {
+            if (!routed[static_cast<size_t>(e)]) continue;
+            if (maps[e] >= 0) ++resident_hits;
+            else cold.push_back(static_cast<int32_t>(e));
+        }
+        const int64_t chunk = std::max<int64_t>(1, K / 2);       // two halves of the reserved slots
+        const int64_t n_chunks = (static_cast<int64_t>(cold.size()) + chunk - 1) / chunk;
+        for (int64_t j = 0; j < n_chunks; ++j) {
+            int32_t * m = maps + (j + 1) * E;
+            std::fill(m, m + E, -1);
+            const int64_t half = K >= 2 ? (j % 2) * chunk : 0;
+            for (int64_t i = 0; i < chunk && j * chunk + i < static_cast<int64_t>(cold.size()); ++i)
+                m[cold[static_cast<size_t>(j * chunk + i)]] = static_cast<int32_t>(half + i);
+        }
+        check_hip(hipMemcpyAsync(t->pf_maps, maps, sizeof(int32_t) * E * (n_chunks + 1), hipMemcpyHostToDevice, s),
+                  "prefill maps");
+        if (resident_hits) prefill_pass(desc, t->pf_maps, T, w, nullptr, s);
+        for (int64_t j = 0; j < n_chunks; ++j) {
+            const int b = K >= 2 ? static_cast<int>(j % 2) : 0;
+            if (j >= (K >= 2 ? 2 : 1))    // the half's previous chunk must be consumed first
+                check_hip(hipStreamWaitEvent(t->copy_stream, t->pf_done[b], 0), "prefill reuse wait");
+            const int64_t half = K >= 2 ? (j % 2) * chunk : 0;
+            for (int64_t i = 0; i < chunk && j * chunk + i < static_cast<int64_t>(cold.size()); ++i)
+                stage(*t, layer, cold[static_cast<size_t>(j * chunk + i)], half + i);
+            check_hip(hipEventRecord(t->pf_ready[b], t->copy_stream), "prefill ready");
+            check_hip(hipStreamWaitEvent(s, t->pf_ready[b], 0), "prefill publish");
+            prefill_pass(desc, t->pf_maps + (j + 1) * E, T, w, nullptr, s);
+            check_hip(hipEventRecord(t->pf_done[b], s), "prefill done");
+        }
+        // 3. rank-ordered weighted combine of every (token, rank) down output
+        launch_combine(w.y, w.weights, H, K, T, out, s);
+        if (ids) check_hip(hipMemcpyAsync(ids, w.ids, sizeof(int32_t) * T * K, hipMemcpyDeviceToDevice, s), "ids copy");
+        if (weights) check_hip(hipMemcpyAsync(weights, w.weights, sizeof(float) * T * K, hipMemcpyDeviceToDevice, s),
+                               "weights copy");
+        check_hip(hipEventRecord(t->last_use, s), "tier last use");
+        t->used = true;
+        t->stats.prefill_tokens += static_cast<uint64_t>(T);
+        t->stats.prefill_resident += resident_hits;
+        t->stats.prefill_streamed += cold.size();
     });
 }
 

@@ -34,7 +34,8 @@ class TierDesc(C.Structure):
 class TierStats(C.Structure):
     _fields_ = [
         ("dispatches", u64), ("hits", u64), ("admissions", u64), ("evictions", u64), ("staged", u64),
-        ("uploaded_bytes", u64), ("copy_ms", C.c_double),
+        ("uploaded_bytes", u64), ("copy_ms", C.c_double), ("prefill_tokens", u64), ("prefill_resident", u64),
+        ("prefill_streamed", u64),
     ]
 
 
@@ -133,6 +134,7 @@ SIGNATURES = {
     "vbm_tier_get_stats": [vp, C.POINTER(TierStats)],
     "vbm_tier_set_trace": [vp, vp],
     "vbm_tier_load_gguf": [vp, vp, vp, vp],
+    "vbm_tier_prefill": [vp, i64, vp, vp, i64, vp, vp, vp, vp],
     "vbm_gguf_open": [C.c_char_p, C.POINTER(vp)],
     "vbm_gguf_close": [vp],
     "vbm_gguf_shards": [vp, C.POINTER(i64), C.POINTER(i64)],
