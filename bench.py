@@ -393,6 +393,37 @@ def tier_measure(args, stack) -> dict:
     vb.call("vbm_event_elapsed_ms", ev0.value, ev1.value, C.byref(ms))
     st = vb.TierStats()
     vb.call("vbm_tier_get_stats", tier.value, C.byref(st))
+    prefill = None
+    if args.tier_prefill_tokens >= 16:
+        # multi-token prefill through the same pool: every layer of one batch, residency frozen
+        T = args.tier_prefill_tokens
+        px = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 900, 0, T * H))
+        plg = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 901, 0, L * T * E))
+        pout = vb.DeviceBuffer(4 * T * H)
+        vb.call("vbm_tier_prefill", tier.value, 0, px.ptr, plg.ptr, T, pout.ptr, None, None, stream)  # warm-up
+        vb.call("vbm_stream_synchronize", stream)
+        before = vb.TierStats()
+        vb.call("vbm_tier_get_stats", tier.value, C.byref(before))
+        vb.call("vbm_event_record", ev0.value, stream)
+        for l in range(L):
+            vb.call("vbm_tier_prefill", tier.value, l, px.ptr, plg.ptr + l * T * E * 4, T, pout.ptr, None, None, stream)
+        vb.call("vbm_event_record", ev1.value, stream)
+        vb.call("vbm_stream_synchronize", stream)
+        pms = C.c_float()
+        vb.call("vbm_event_elapsed_ms", ev0.value, ev1.value, C.byref(pms))
+        after = vb.TierStats()
+        vb.call("vbm_tier_get_stats", tier.value, C.byref(after))
+        up = after.uploaded_bytes - before.uploaded_bytes
+        prefill = {
+            "tokens": T, "layers": L, "ms": round(pms.value, 2), "value": round(T / (pms.value * 1e-3), 1),
+            "unit": "prefill tok/s through all layers",
+            "resident_experts": int(after.prefill_resident - before.prefill_resident),
+            "streamed_experts": int(after.prefill_streamed - before.prefill_streamed),
+            "uploaded_gb": round(up / 1e9, 2), "h2d_gbs_overall": round(up / (pms.value * 1e-3) / 1e9, 1),
+        }
+        log(f"tier prefill: {T} tokens x {L} layers in {pms.value:.1f} ms ({prefill['value']} tok/s); "
+            f"{prefill['streamed_experts']} experts streamed, {prefill['resident_experts']} resident; "
+            f"{prefill['h2d_gbs_overall']} GB/s of expert copies overall")
     vb.call("vbm_tier_destroy", tier.value)
     lookups = tokens * L * K
     h2d = st.uploaded_bytes / (st.copy_ms * 1e-3) / 1e9 if st.copy_ms > 0 else None
@@ -404,7 +435,7 @@ def tier_measure(args, stack) -> dict:
         "hit_rate": round(st.hits / lookups, 4), "lookups": lookups, "admissions": int(st.admissions),
         "evictions": int(st.evictions), "staged_misses": int(st.staged),
         "uploaded_gb": round(st.uploaded_bytes / 1e9, 2), "h2d_gbs": round(h2d, 1) if h2d else None,
-        "copy_busy_ms": round(st.copy_ms, 1), "seeded": len(plan),
+        "copy_busy_ms": round(st.copy_ms, 1), "seeded": len(plan), "prefill": prefill,
     }
     log(f"tier: {res['value']} tok/s, hit rate {res['hit_rate']}, {res['uploaded_gb']} GB uploaded at "
         f"{res['h2d_gbs']} GB/s copy-busy")
@@ -445,6 +476,8 @@ def main() -> int:
     ap.add_argument("--no-tier", action="store_true",
                     help="skip the host-RAM tier workload (it pins 61 GB of host memory)")
     ap.add_argument("--tier-tokens", type=int, default=512)
+    ap.add_argument("--tier-prefill-tokens", type=int, default=2048,
+                    help="prefill batch through the tier's pool after the decode trace (0: skip)")
     ap.add_argument("--tier-plan", default=str(REPO / "unified-memory-scheduler_amd" / "plans" / "gpt120-trained-hot944.txt"),
                     help="frozen plan seeding the tier's pool ('layer expert' lines), or 'none'")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
