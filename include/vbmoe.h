@@ -501,6 +501,68 @@ vbm_status vbm_tier_get_stats(const vbm_tier * tier, vbm_tier_stats * stats);
 vbm_status vbm_tier_set_trace(vbm_tier * tier, vbm_trace * trace);
 
 /* ----------------------------------------------------------------------------------------------
+ * Stream-ordered host calls: the HIP side of the reference's GGML_OP_CUSTOM host-call node
+ * (struct ggml_host_call, third_party/patches/llama-b11669-hybrid-experts.patch:82-101, and the
+ * CUDA backend's handling of it, :800-1054). vbm_host_call has ggml_host_call's layout (with
+ * VBM_HOST_MAX_SRC equal to GGML_MAX_SRC), so a ggml HIP backend passes the node's userdata
+ * straight through. fn runs on a host thread and must not call device APIs; src_host[i] and
+ * dst_host are pinned host buffers (vbm_host_alloc) of the input and output sizes.
+ * -------------------------------------------------------------------------------------------- */
+#define VBM_HOST_CALL_MAGIC 0x56424843414c4c31ULL /* "VBHCALL1" */
+#define VBM_HOST_JOIN_MAGIC 0x5642484a4f494e31ULL /* "VBHJOIN1" */
+#define VBM_HOST_MAX_SRC 10
+#define VBM_HOST_CALL_FUNC 0      /* hipLaunchHostFunc on the side stream                        */
+#define VBM_HOST_CALL_MAILBOX 1   /* device-posted request to a persistent host worker (bounded) */
+
+typedef struct vbm_host_call {
+    uint64_t magic;
+    void (*fn)(void * ctx);
+    void * ctx;
+    void * src_host[VBM_HOST_MAX_SRC];
+    void * dst_host;
+    void * backend_state;           /* owned by the library once the call has been enqueued      */
+    struct vbm_host_call * call;    /* join nodes: the call they wait for                        */
+    int32_t miss_src;               /* ggml's field; the miss ids are passed to the enqueue here */
+} vbm_host_call;
+
+/* Creates the call's events, the device's side stream and (mailbox) its worker: do it before
+ * capturing a graph that enqueues the call. */
+vbm_status vbm_host_call_prepare(vbm_host_call * call, int mode);
+/* On a side stream forked from `stream`: device srcs[i] (src_bytes[i]) -> call->src_host[i],
+ * fn(ctx), call->dst_host -> device dst (dst_bytes). miss (mailbox mode, optional): device int32
+ * [n_miss]; when none of them is 0 the call is posted for bookkeeping only, not waited for, and dst
+ * is zero-filled (fn still runs before vbm_host_mailbox_drain returns). The call runs on the side
+ * stream: work that needs its output, or a synchronize meant to cover it, must follow a
+ * vbm_host_join or vbm_host_call_wait on `stream`. */
+vbm_status vbm_host_call_enqueue(vbm_host_call * call, const void * const * srcs, const size_t * src_bytes,
+                                 int n_src, void * dst, size_t dst_bytes, const int32_t * miss, int64_t n_miss,
+                                 int mode, void * stream);
+/* Join node: dst = a + b (fp32, n) on `stream` once the call has completed. */
+vbm_status vbm_host_join(vbm_host_call * call, const float * a, const float * b, float * dst, int64_t n,
+                         void * stream);
+/* Makes `stream` wait for the call's completion without a join. */
+vbm_status vbm_host_call_wait(vbm_host_call * call, void * stream);
+/* Waits for the call's last enqueue and frees what the library attached to it. */
+vbm_status vbm_host_call_release(vbm_host_call * call);
+/* Returns once the device's worker has handled every posted request (call after the stream is idle). */
+vbm_status vbm_host_mailbox_drain(int device, double timeout_s);
+/* Requests posted and handled, and waited posts whose bounded wait expired (output zero-filled). */
+vbm_status vbm_host_mailbox_stats(int device, uint64_t * posted, uint64_t * done, uint32_t * timeouts);
+/* Polls (~1 us each) a waited post makes before it expires; default 2^21. */
+vbm_status vbm_host_mailbox_set_spin_limit(uint32_t polls);
+
+/* supports_op for a ggml HIP backend: 1 when the node can run here. ne0 / ne1: ggml ne[4] of the
+ * node's first and second operand (MUL_MAT_ID: as, b; ADD_ID: y, bias; GLU: gate, up; host join:
+ * a, b); type0 / type1: their ggml types. Host-call nodes are supported whenever their inputs and
+ * output are contiguous and have host buffers (checked by vbm_host_call_enqueue). */
+#define VBM_OP_MUL_MAT_ID 0
+#define VBM_OP_ADD_ID 1
+#define VBM_OP_GLU_SWIGLU 2
+#define VBM_OP_GLU_SWIGLU_OAI 3
+#define VBM_OP_HOST_JOIN 4
+int vbm_op_supported(int op, int type0, int type1, const int64_t * ne0, const int64_t * ne1);
+
+/* ----------------------------------------------------------------------------------------------
  * HIP graph capture of stream-ordered work (per-token layer chains replay without host launch
  * overhead). Only entry points that do not allocate (the layer forward with a caller workspace,
  * the router, combine, quantize and device copies) may be captured.

@@ -53,6 +53,22 @@ class GgufExpertInfo(C.Structure):
     ]
 
 
+HOST_CALL_MAGIC, HOST_JOIN_MAGIC, HOST_MAX_SRC = 0x56424843414C4C31, 0x5642484A4F494E31, 10
+HOST_CALL_FUNC, HOST_CALL_MAILBOX = 0, 1
+OP_MUL_MAT_ID, OP_ADD_ID, OP_GLU_SWIGLU, OP_GLU_SWIGLU_OAI, OP_HOST_JOIN = 0, 1, 2, 3, 4
+HOST_FN = C.CFUNCTYPE(None, C.c_void_p)
+
+
+class HostCall(C.Structure):
+    pass
+
+
+HostCall._fields_ = [
+    ("magic", u64), ("fn", HOST_FN), ("ctx", vp), ("src_host", vp * HOST_MAX_SRC), ("dst_host", vp),
+    ("backend_state", vp), ("call", C.POINTER(HostCall)), ("miss_src", C.c_int32),
+]
+
+
 class MoeLayerDesc(C.Structure):
     _fields_ = [
         ("gate_up", vp), ("down", vp), ("gate_up_bias", vp), ("down_bias", vp), ("expert_to_slot", vp),
@@ -134,6 +150,14 @@ SIGNATURES = {
     "vbm_tier_get_stats": [vp, C.POINTER(TierStats)],
     "vbm_tier_set_trace": [vp, vp],
     "vbm_tier_load_gguf": [vp, vp, vp, vp],
+    "vbm_host_call_prepare": [C.POINTER(HostCall), C.c_int],
+    "vbm_host_call_enqueue": [C.POINTER(HostCall), vp, vp, C.c_int, vp, sz, vp, i64, C.c_int, vp],
+    "vbm_host_join": [C.POINTER(HostCall), vp, vp, vp, i64, vp],
+    "vbm_host_call_wait": [C.POINTER(HostCall), vp],
+    "vbm_host_call_release": [C.POINTER(HostCall)],
+    "vbm_host_mailbox_drain": [C.c_int, C.c_double],
+    "vbm_host_mailbox_stats": [C.c_int, C.POINTER(u64), C.POINTER(u64), C.POINTER(C.c_uint32)],
+    "vbm_host_mailbox_set_spin_limit": [C.c_uint32],
     "vbm_tier_prefill": [vp, i64, vp, vp, i64, vp, vp, vp, vp],
     "vbm_gguf_open": [C.c_char_p, C.POINTER(vp)],
     "vbm_gguf_close": [vp],
@@ -164,6 +188,7 @@ OTHER = {
     "vbm_moe_anchor_slots": ([C.c_int, C.c_int, C.c_int], C.c_int),
     "vbm_moe_cold_gpu_budget": ([C.c_int], C.c_int),
     "vbm_moe_gpu_slot_limit": ([C.c_int32, C.c_int], C.c_int32),
+    "vbm_op_supported": ([C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_int64)], C.c_int),
 }
 ADMIT_CLASSIC, ADMIT_LRU, ADMIT_RANKED, ADMIT_PROBATION, ADMIT_ANCHORED, ADMIT_LFU = 0, 1, 2, 3, 4, 5
 
