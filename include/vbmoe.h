@@ -342,6 +342,45 @@ int vbm_moe_anchor_slots(int capacity, int reserved, int seeds);
 int vbm_moe_cold_gpu_budget(int cold_experts);
 int32_t vbm_moe_gpu_slot_limit(int32_t resident_slots, int cold_gpu);
 
+/* Offline residency replay of a decode routing trace under the expert-cache cost models of the
+ * reference's analyzer (tools/benchmark/vrambridge-routing.py:191-512): events in trace order,
+ * layer indices in ascending layer-id order, experts of event i at [event_offsets[i],
+ * event_offsets[i + 1]); event_split 0 = training request (warms the cache), 1 = held-out
+ * request (totalled). Host-side. */
+#define VBM_RESIDENCY_MEASURED_STATIC 0
+#define VBM_RESIDENCY_TRAIN_STATIC 1
+#define VBM_RESIDENCY_LRU 2
+#define VBM_RESIDENCY_LFU 3
+#define VBM_RESIDENCY_BELADY_HITS 4
+#define VBM_RESIDENCY_COST_AWARE 5
+
+typedef struct {
+    int64_t experts;
+    uint64_t bytes_per_expert, static_host_bytes_per_expert;
+} vbm_residency_layer;
+
+typedef struct {
+    int policy;                              /* VBM_RESIDENCY_*                                  */
+    uint64_t capacity_bytes;
+    int admit_after;                         /* references before admission (>= 1)             */
+    int64_t payback_tokens;                  /* cost-aware window in generated tokens (>= 1)   */
+    int cold_cache;                          /* clear the cache before the first held-out event */
+    double ram_gbps, pcie_gbps, gpu_expert_us, layer_sync_us;
+    int staging_ram_passes;                  /* 0 or 2                                          */
+    uint64_t static_device_expert_bytes;     /* the trace metadata's (measured_static)          */
+} vbm_residency_params;
+
+typedef struct {
+    int supported;                           /* 0: belady_hits over unequal expert sizes        */
+    uint64_t expert_calls, full_hits, bytes, cold_bytes, upload_bytes, evictions;
+    double serial_s, optimistic_s, shared_ram_bytes;   /* latency-model sums over held-out layers */
+    uint64_t warmup_upload_bytes, initial_bytes, rejected, warmup_rejected;
+} vbm_residency_totals;
+
+vbm_status vbm_residency_replay(const vbm_residency_layer * layers, int64_t n_layers, const int32_t * event_layer,
+                                const int32_t * event_split, const int64_t * event_offsets, const int32_t * experts,
+                                int64_t n_events, const vbm_residency_params * params, vbm_residency_totals * totals);
+
 /* ----------------------------------------------------------------------------------------------
  * GGUF expert tensors (tools/engine/gguf_experts.cpp:27-140): blk.L.ffn_{gate,up,down}_exps.
  * {weight,bias} (or the fused blk.L.ffn_gate_up_exps.weight) of a GGUF file and its

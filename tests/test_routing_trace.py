@@ -362,3 +362,52 @@ def test_replay_admission_matches_restatement(rt, tmp_path, policy):
     assert a.lookups == 2 * len(data.events) and a.admissions > 0
     assert stats["train"].dispatches + stats["test"].dispatches == a.dispatches
     assert stats["train"].hits + stats["test"].hits == a.hits
+
+
+# ------------------------------------------------------------------------------------------------
+# residency replays against the reference analyzer's own replays of the same traces
+
+
+@pytest.mark.parametrize("trace_name", ["small", "mixed"])
+def test_residency_replays_match_reference_analyzer(rt, trace_name):
+    import make_routing_trace_golden as mk
+    report = json.loads((GOLDEN / "routing_trace_small_report.json").read_text())
+    golden = report["replays"][trace_name]
+    params = report["replay_parameters"]
+    path = GOLDEN / f"routing_trace_{trace_name}.jsonl"
+    data = rt.read_trace(path)
+    assert data.sha256 == golden["trace_sha256"]
+    costs = params["costs"]
+    checked = 0
+    for name, want in golden.items():
+        if name == "trace_sha256":
+            continue
+        cold = name.startswith("cold:")
+        policy = name.split(":")[-1]
+        got = rt.replay_residency(data, policy, params["capacity"][trace_name], costs["ram_gbps"], costs["pcie_gbps"],
+                                  costs["gpu_expert_us"], costs["layer_sync_us"], costs["staging_ram_passes"],
+                                  admit_after=params["admit_after"], payback_tokens=params["payback_tokens"],
+                                  cold_cache=cold)
+        assert got["supported"] == want["supported"], name
+        if not want["supported"]:
+            continue
+        for key in mk.KEEP:
+            w, g = want[key], got[key]
+            if isinstance(w, float):
+                assert g == pytest.approx(w, rel=1e-12, abs=0), (name, key, g, w)
+            else:
+                assert g == w, (name, key, g, w)
+        checked += 1
+    assert checked >= 10                                    # belady needs equal sizes (mixed: unsupported)
+
+
+def test_residency_replay_rejects_bad_parameters(rt, vb):
+    data = rt.read_trace(GOLDEN / "routing_trace_small.jsonl")
+    with pytest.raises(ValueError, match="Unknown residency"):
+        rt.replay_residency(data, "unknown", 10, 1.0, 1.0)
+    with pytest.raises(vb.VbmError, match="finite and positive"):
+        rt.replay_residency(data, "lru", 10, 0.0, 1.0)
+    with pytest.raises(vb.VbmError, match="staging"):
+        rt.replay_residency(data, "lru", 10, 1.0, 1.0, staging_ram_passes=1)
+    with pytest.raises(vb.VbmError, match=">= 1"):
+        rt.replay_residency(data, "cost_aware", 10, 1.0, 1.0, payback_tokens=0)

@@ -69,6 +69,27 @@ HostCall._fields_ = [
 ]
 
 
+class ResidencyLayer(C.Structure):
+    _fields_ = [("experts", i64), ("bytes_per_expert", u64), ("static_host_bytes_per_expert", u64)]
+
+
+class ResidencyParams(C.Structure):
+    _fields_ = [
+        ("policy", C.c_int), ("capacity_bytes", u64), ("admit_after", C.c_int), ("payback_tokens", i64),
+        ("cold_cache", C.c_int), ("ram_gbps", C.c_double), ("pcie_gbps", C.c_double), ("gpu_expert_us", C.c_double),
+        ("layer_sync_us", C.c_double), ("staging_ram_passes", C.c_int), ("static_device_expert_bytes", u64),
+    ]
+
+
+class ResidencyTotals(C.Structure):
+    _fields_ = [
+        ("supported", C.c_int), ("expert_calls", u64), ("full_hits", u64), ("bytes", u64), ("cold_bytes", u64),
+        ("upload_bytes", u64), ("evictions", u64), ("serial_s", C.c_double), ("optimistic_s", C.c_double),
+        ("shared_ram_bytes", C.c_double), ("warmup_upload_bytes", u64), ("initial_bytes", u64), ("rejected", u64),
+        ("warmup_rejected", u64),
+    ]
+
+
 class MoeLayerDesc(C.Structure):
     _fields_ = [
         ("gate_up", vp), ("down", vp), ("gate_up_bias", vp), ("down_bias", vp), ("expert_to_slot", vp),
@@ -150,6 +171,8 @@ SIGNATURES = {
     "vbm_tier_get_stats": [vp, C.POINTER(TierStats)],
     "vbm_tier_set_trace": [vp, vp],
     "vbm_tier_load_gguf": [vp, vp, vp, vp],
+    "vbm_residency_replay": [C.POINTER(ResidencyLayer), i64, vp, vp, vp, vp, i64, C.POINTER(ResidencyParams),
+                             C.POINTER(ResidencyTotals)],
     "vbm_host_call_prepare": [C.POINTER(HostCall), C.c_int],
     "vbm_host_call_enqueue": [C.POINTER(HostCall), vp, vp, C.c_int, vp, sz, vp, i64, C.c_int, vp],
     "vbm_host_join": [C.POINTER(HostCall), vp, vp, vp, i64, vp],
