@@ -608,13 +608,15 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
 // Tiles of kJobTile jobs per active expert, in active order: one workgroup, wave scans plus a
 // scan of the 16 wave totals.
 __global__ __launch_bounds__(1024) void gemm_tiles_kernel(const int32_t * counts, const int32_t * active,
-                                                          const int32_t * n_active, int max_tiles, int32_t * tile_expert,
-                                                          int32_t * tile_start, int32_t * n_tiles, int32_t * error) {
+                                                          const int32_t * n_active, const int32_t * filter, int max_tiles,
+                                                          int32_t * tile_expert, int32_t * tile_start, int32_t * n_tiles,
+                                                          int32_t * error) {
     __shared__ int s_wave[16];
     const int na = *n_active;
     const int a = threadIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int e = a < na ? active[a] : 0;
-    const int nt = a < na ? (counts[e] + kJobTile - 1) / kJobTile : 0;
+    const bool kept = a < na && (filter == nullptr || filter[e] >= 0);   // filtered experts get no tiles
+    const int nt = kept ? (counts[e] + kJobTile - 1) / kJobTile : 0;
     int incl = nt;
     for (int off = 1; off < 64; off <<= 1) {
         const int v = __shfl_up(incl, off);
@@ -762,7 +764,8 @@ void launch_grouped_gemm(const GemmParams & p, hipStream_t stream) {
     int32_t * tile_start = tile_expert + max_tiles;
     int32_t * n_tiles = tile_start + max_tiles;
     hipLaunchKernelGGL(gemm_tiles_kernel, dim3(1), dim3(1024), 0, stream, p.group.counts, p.group.active,
-                       p.group.n_active, static_cast<int>(max_tiles), tile_expert, tile_start, n_tiles, p.group.error);
+                       p.group.n_active, p.tile_filter, static_cast<int>(max_tiles), tile_expert, tile_start, n_tiles,
+                       p.group.error);
     check_hip(hipGetLastError(), "GEMM tile list launch");
     GemmArgs a{};
     a.bank = bank.base;
@@ -788,7 +791,10 @@ void launch_grouped_gemm(const GemmParams & p, hipStream_t stream) {
     a.limit = p.limit;
     const int row_pairs = static_cast<int>((bank.rows + 63) / 64);
     require(!p.flagged_rows || p.epilogue == 0, "flagged activation rows only with the plain epilogue");
-    const int mt = static_cast<int>(max_tiles);
+    // the launch covers max_tiles tiles, or the caller's bound on this call's tiles (its tile filter
+    // leaves only the experts whose tiles it counted)
+    require(p.grid_tiles >= 0 && (p.grid_tiles == 0 || p.tile_filter != nullptr), "grid tile bound needs a tile filter");
+    const int mt = static_cast<int>(p.grid_tiles > 0 ? std::min<int64_t>(p.grid_tiles, max_tiles) : max_tiles);
     if (bank.type == VBM_TYPE_MXFP4) {
         if (p.flagged_rows) launch_gemm_typed<39, 0, true>(a, row_pairs, mt, stream);
         else if (p.epilogue == 0) launch_gemm_typed<39, 0, false>(a, row_pairs, mt, stream);

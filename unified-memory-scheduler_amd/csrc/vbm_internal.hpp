@@ -176,6 +176,8 @@ struct GemmParams {
     int epilogue, activation;
     float alpha, limit;
     bool flagged_rows;                // rows_in may hold -128 codes (converted from caller Q8_0)
+    const int32_t * tile_filter;      // device [n_as]: experts with a negative entry get no tiles, or null
+    int64_t grid_tiles;               // > 0: bound on the tiles left by tile_filter (launch size), else 0
 };
 int64_t gemm_max_tiles(int64_t n_as, int64_t n_entries);
 size_t gemm_tiles_bytes(int64_t n_as, int64_t n_entries);
@@ -201,11 +203,13 @@ LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint
 // then one or more passes over disjoint expert subsets (experts whose expert_to_slot entry is
 // -1 are skipped: their workgroups exit without writing), each writing the down outputs y of its
 // entries; the combine of y runs once all entries are written. events (optional) [4]: around the
-// pass's gate_up and down GEMMs.
+// pass's gate_up and down GEMMs. grid_tiles > 0: the pass's expert->slot map also filters the tile
+// list, and grid_tiles bounds its tiles (sum over its experts of ceil(count / 64)), so a pass over a
+// few experts launches only their workgroups.
 void prefill_prepare(const vbm_moe_layer_desc & d, const float * x, const int32_t * ids, int64_t n_tokens,
                      const LayerWorkspace & w, hipStream_t s);
 void prefill_pass(const vbm_moe_layer_desc & d, const int32_t * expert_to_slot, int64_t n_tokens,
-                  const LayerWorkspace & w, void * const * events, hipStream_t s);
+                  const LayerWorkspace & w, void * const * events, hipStream_t s, int64_t grid_tiles = 0);
 
 // Kernel A of the fused single-token decode: routing, input combine + Q8_0, gate_up GEMV, GLU,
 // requantization into the down activation rows.

@@ -94,7 +94,7 @@ void prefill_prepare(const vbm_moe_layer_desc & d, const float * x, const int32_
 }
 
 void prefill_pass(const vbm_moe_layer_desc & d, const int32_t * expert_to_slot, int64_t n_tokens,
-                  const LayerWorkspace & w, void * const * events, hipStream_t s) {
+                  const LayerWorkspace & w, void * const * events, hipStream_t s, int64_t grid_tiles) {
     const int64_t K = d.top_k;
     const GemmRowLayout gx{d.hidden / 32, d.gate_up->type}, ga{d.intermediate / 32, d.down->type};
     GemmParams p{};
@@ -107,6 +107,10 @@ void prefill_pass(const vbm_moe_layer_desc & d, const int32_t * expert_to_slot, 
     p.activation = d.activation;
     p.alpha = 1.702f;
     p.limit = 7.0f;
+    if (grid_tiles > 0) {
+        p.tile_filter = expert_to_slot;
+        p.grid_tiles = grid_tiles;
+    }
     p.bank = d.gate_up;
     p.rows_in = w.xrows_x;
     p.lay = gx;

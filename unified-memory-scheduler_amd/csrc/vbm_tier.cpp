@@ -404,14 +404,22 @@ vbm_status vbm_tier_prefill(vbm_tier * t, int64_t layer, const float * x, const 
         //    the remaining routed experts stream through the reserved slots in chunks
         int32_t * maps = t->pf_maps_host;
         check_status(vbm_admission_slot_map(t->admission, layer, maps), "prefill slot map");
+        std::vector<int64_t> count(static_cast<size_t>(E), 0);
+        for (int64_t i = 0; i < T * K; ++i) ++count[static_cast<size_t>(t->pf_ids_host[i])];
+        auto tiles_of = [&](int64_t e) { return (count[static_cast<size_t>(e)] + 63) / 64; };   // GEMM job tiles
         std::vector<char> routed(static_cast<size_t>(E), 0);
-        for (int64_t i = 0; i < T * K; ++i) routed[static_cast<size_t>(t->pf_ids_host[i])] = 1;
+        for (int64_t e = 0; e < E; ++e) routed[static_cast<size_t>(e)] = count[static_cast<size_t>(e)] > 0;
         std::vector<int32_t> cold;
         uint64_t resident_hits = 0;
+        int64_t resident_tiles = 0;
         for (int64_t e = 0; e < E; ++e) {
             if (!routed[static_cast<size_t>(e)]) continue;
-            if (maps[e] >= 0) ++resident_hits;
-            else cold.push_back(static_cast<int32_t>(e));
+            if (maps[e] >= 0) {
+                ++resident_hits;
+                resident_tiles += tiles_of(e);
+            } else {
+                cold.push_back(static_cast<int32_t>(e));
+            }
         }
         const int64_t chunk = std::max<int64_t>(1, K / 2);       // two halves of the reserved slots
         const int64_t n_chunks = (static_cast<int64_t>(cold.size()) + chunk - 1) / chunk;
@@ -424,17 +432,20 @@ vbm_status vbm_tier_prefill(vbm_tier * t, int64_t layer, const float * x, const 
         }
         check_hip(hipMemcpyAsync(t->pf_maps, maps, sizeof(int32_t) * E * (n_chunks + 1), hipMemcpyHostToDevice, s),
                   "prefill maps");
-        if (resident_hits) prefill_pass(desc, t->pf_maps, T, w, nullptr, s);
+        if (resident_hits) prefill_pass(desc, t->pf_maps, T, w, nullptr, s, resident_tiles);
         for (int64_t j = 0; j < n_chunks; ++j) {
             const int b = K >= 2 ? static_cast<int>(j % 2) : 0;
             if (j >= (K >= 2 ? 2 : 1))    // the half's previous chunk must be consumed first
                 check_hip(hipStreamWaitEvent(t->copy_stream, t->pf_done[b], 0), "prefill reuse wait");
             const int64_t half = K >= 2 ? (j % 2) * chunk : 0;
-            for (int64_t i = 0; i < chunk && j * chunk + i < static_cast<int64_t>(cold.size()); ++i)
+            int64_t chunk_tiles = 0;
+            for (int64_t i = 0; i < chunk && j * chunk + i < static_cast<int64_t>(cold.size()); ++i) {
                 stage(*t, layer, cold[static_cast<size_t>(j * chunk + i)], half + i);
+                chunk_tiles += tiles_of(cold[static_cast<size_t>(j * chunk + i)]);
+            }
             check_hip(hipEventRecord(t->pf_ready[b], t->copy_stream), "prefill ready");
             check_hip(hipStreamWaitEvent(s, t->pf_ready[b], 0), "prefill publish");
-            prefill_pass(desc, t->pf_maps + (j + 1) * E, T, w, nullptr, s);
+            prefill_pass(desc, t->pf_maps + (j + 1) * E, T, w, nullptr, s, chunk_tiles);
             check_hip(hipEventRecord(t->pf_done[b], s), "prefill done");
         }
         // 3. rank-ordered weighted combine of every (token, rank) down output
