@@ -69,7 +69,24 @@ def build(jobs: int = 8) -> Path:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed\n{' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
     os.replace(tmp, LIB)
+    build_host_tests()
     return LIB
+
+
+TEST_SRC = HERE.parent / "tests" / "cpp" / "test_native_hip_down.cpp"
+TEST_BIN = HERE.parent / "tests" / "cpp" / "bin" / "test_native_hip_down"
+
+
+def build_host_tests() -> Path:
+    """The C++ driver of the engine-level mirror's tests, linked against libvbmoe.so with a
+    relative rpath so it runs from any copy of the tree."""
+    TEST_BIN.parent.mkdir(parents=True, exist_ok=True)
+    cmd = ["g++", "-std=c++17", "-O2", f"-I{HOST}", f"-I{INCLUDE}", str(TEST_SRC), "-o", str(TEST_BIN),
+           f"-L{OUT_DIR}", "-lvbmoe", "-Wl,-rpath,$ORIGIN/../../../unified-memory-scheduler_amd/vbmoe"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"host test build failed\n{' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
+    return TEST_BIN
 
 
 if __name__ == "__main__":
