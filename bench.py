@@ -365,11 +365,13 @@ def tier_measure(args, stack) -> dict:
     perms = [rng.permutation(E) for _ in range(L)]
     prev = [None] * L
     logits = np.empty((tokens, L, E), np.float32)
+    routes = np.empty((tokens, L, K), np.int32)
     for t in range(tokens):
         for l in range(L):
             sel = prev[l] if prev[l] is not None and rng.random() < 0.6 else \
                 [int(perms[l][i]) for i in rng.choice(E, K, replace=False, p=p)]
             prev[l] = sel
+            routes[t, l] = sel
             lg = rng.standard_normal(E).astype(np.float32)
             lg[sel] = 10.0 - np.arange(K, dtype=np.float32)
             logits[t, l] = lg
@@ -425,6 +427,34 @@ def tier_measure(args, stack) -> dict:
             f"{prefill['streamed_experts']} experts streamed, {prefill['resident_experts']} resident; "
             f"{prefill['h2d_gbs_overall']} GB/s of expert copies overall")
     vb.call("vbm_tier_destroy", tier.value)
+    policies = policy_study(args, routes, n_slots, plan, group_bytes, st) if args.tier_policies else None
+    live_policy = None
+    if args.tier_live_policy != "none":
+        # the same trace through a second pool under another admission policy, live
+        names = ("classic", "lru", "ranked", "probation", "anchored", "lfu")
+        pol = names.index(args.tier_live_policy)
+        desc2 = vb.TierDesc(vb.TYPE_MXFP4, H, I, L, E, K, vb.ACT_SWIGLU_OAI, n_slots, 64,
+                            1 if args.tier_live_policy == "lru" else 4, pol,
+                            C.cast(gub, C.POINTER(C.c_void_p)), C.cast(dnb, C.POINTER(C.c_void_p)))
+        tier2 = C.c_void_p()
+        vb.call("vbm_tier_create", C.byref(desc2), C.byref(tier2))
+        vb.call("vbm_tier_generate", tier2.value, SEED, 16, 1, 2, -8.0, -3.0, None)
+        for layer, expert in plan:
+            vb.call("vbm_tier_seed", tier2.value, layer, expert)
+        vb.call("vbm_event_record", ev0.value, stream)
+        for t in range(tokens):
+            vb.call("vbm_tier_step", tier2.value, stack.x0.ptr, dl.ptr + t * step, out.ptr, None, stream)
+        vb.call("vbm_event_record", ev1.value, stream)
+        vb.call("vbm_stream_synchronize", stream)
+        ms2 = C.c_float()
+        vb.call("vbm_event_elapsed_ms", ev0.value, ev1.value, C.byref(ms2))
+        st2 = vb.TierStats()
+        vb.call("vbm_tier_get_stats", tier2.value, C.byref(st2))
+        vb.call("vbm_tier_destroy", tier2.value)
+        live_policy = {"policy": args.tier_live_policy, "value": round(tokens / (ms2.value * 1e-3), 2), "unit": "tok/s",
+                       "hit_rate": round(st2.hits / (tokens * L * K), 4), "uploaded_gb": round(st2.uploaded_bytes / 1e9, 2)}
+        log(f"tier ({args.tier_live_policy} admission, live): {live_policy['value']} tok/s, hit rate "
+            f"{live_policy['hit_rate']}, {live_policy['uploaded_gb']} GB uploaded")
     lookups = tokens * L * K
     h2d = st.uploaded_bytes / (st.copy_ms * 1e-3) / 1e9 if st.copy_ms > 0 else None
     res = {
@@ -435,11 +465,46 @@ def tier_measure(args, stack) -> dict:
         "hit_rate": round(st.hits / lookups, 4), "lookups": lookups, "admissions": int(st.admissions),
         "evictions": int(st.evictions), "staged_misses": int(st.staged),
         "uploaded_gb": round(st.uploaded_bytes / 1e9, 2), "h2d_gbs": round(h2d, 1) if h2d else None,
-        "copy_busy_ms": round(st.copy_ms, 1), "seeded": len(plan), "prefill": prefill,
+        "copy_busy_ms": round(st.copy_ms, 1), "seeded": len(plan), "prefill": prefill, "policies": policies,
+        "live_policy": live_policy,
     }
     log(f"tier: {res['value']} tok/s, hit rate {res['hit_rate']}, {res['uploaded_gb']} GB uploaded at "
         f"{res['h2d_gbs']} GB/s copy-busy")
     return res
+
+
+def policy_study(args, routes, n_slots, plan, group_bytes, live) -> dict:
+    """The tier's decode routing written as a routing trace (reference JSONL schema) and replayed
+    offline through every causal admission policy on the same pool and seed plan: hit rate and
+    expert groups copied per policy. The classic replay must reproduce the live tier's counters."""
+    import tempfile
+    from vbmoe import routing_trace as rt
+    tokens, L, K = routes.shape
+    E = args.experts
+    layers = [{"id": l, "experts": E, "active": K, "bytes_per_expert": group_bytes,
+               "static_host_bytes_per_expert": group_bytes, "tensor_types": ["f32", "mxfp4"]} for l in range(L)]
+    with tempfile.TemporaryDirectory() as tmp:
+        path = Path(tmp) / "tier_routing.jsonl"
+        half = tokens // 2
+        with rt.TraceWriter(path, layers, "gpt-oss", "vbmoe", tokens + 1, model="synthetic-120b-shape") as w:
+            for name, split, lo, hi in (("zipf-a", "train", 0, half), ("zipf-b", "test", half, tokens)):
+                w.request_start(name, split, "synthetic", 1, hi - lo)
+                for t in range(lo, hi):
+                    w.token(routes[t])
+                w.request_end("limit")
+        data = rt.read_trace(path)
+    out = {"trace_events": len(data.events)}
+    names = ("classic", "lru", "ranked", "probation", "anchored", "lfu")
+    for policy, name in enumerate(names):
+        r = rt.replay_admission(data, n_slots, policy, 64, 1 if name == "lru" else 4, plan=plan)["all"]
+        out[name] = {"hit_rate": round(r.hit_rate, 4), "admissions": r.admissions, "staged": r.staged,
+                     "copied_groups": r.admissions + r.staged}
+    c = out["classic"]
+    out["classic_replay_matches_live"] = (c["admissions"], c["staged"]) == (int(live.admissions), int(live.staged)) \
+        and abs(c["hit_rate"] - round(live.hits / (tokens * L * K), 4)) < 1e-9
+    log("tier policies (offline replay of the tier's trace): " +
+        ", ".join(f"{n} {out[n]['hit_rate']}" for n in names) + f"; classic matches live: {out['classic_replay_matches_live']}")
+    return out
 
 
 def read_traffic(path: Path):
@@ -476,6 +541,11 @@ def main() -> int:
     ap.add_argument("--no-tier", action="store_true",
                     help="skip the host-RAM tier workload (it pins 61 GB of host memory)")
     ap.add_argument("--tier-tokens", type=int, default=512)
+    ap.add_argument("--tier-live-policy", default="lru",
+                    choices=("none", "classic", "lru", "ranked", "probation", "anchored", "lfu"),
+                    help="run the tier trace a second time live under this admission policy")
+    ap.add_argument("--no-tier-policies", dest="tier_policies", action="store_false",
+                    help="skip the offline admission-policy replay of the tier's routing trace")
     ap.add_argument("--tier-prefill-tokens", type=int, default=2048,
                     help="prefill batch through the tier's pool after the decode trace (0: skip)")
     ap.add_argument("--tier-plan", default=str(REPO / "unified-memory-scheduler_amd" / "plans" / "gpt120-trained-hot944.txt"),
