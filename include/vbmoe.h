@@ -439,10 +439,24 @@ typedef struct {
 
 typedef struct vbm_trace vbm_trace;
 
-/* model and token_equivalence_check may be NULL (omitted). Refuses an existing path or partial. */
+/* model, token_equivalence_check and collector_source_sha256 (64 lower-case hex digits) may be
+ * NULL (omitted). Refuses an existing path or partial. */
 vbm_status vbm_trace_open(const char * path, const char * architecture, const char * backend_commit,
                           const char * model, int64_t context_tokens, const vbm_trace_layer * layers,
-                          int64_t n_layers, const char * token_equivalence_check, vbm_trace ** trace);
+                          int64_t n_layers, const char * token_equivalence_check,
+                          const char * collector_source_sha256, vbm_trace ** trace);
+/* Also write the prefill summary of the reference collector's prefill mode (routing_trace.cpp:
+ * 750-769: "observed_prefill_expert_rows", pretty-printed, published like the trace) to
+ * summary_path at vbm_trace_close. Before the first request; needs collector_source_sha256. */
+vbm_status vbm_trace_enable_prefill(vbm_trace * trace, const char * summary_path, int64_t batch_size,
+                                    int64_t microbatch_size, int64_t cpu_threads, int64_t batch_threads);
+vbm_status vbm_trace_prefill_enabled(const vbm_trace * trace, int * enabled);
+/* One prompt batch of `layer_id` in the open request, before its decode routes: ids [rows][active]
+ * (0..32768 rows; 0 records an output-pruned batch), each row's experts in range and distinct;
+ * recorded as the batch's rows-per-expert histogram (routing_trace.cpp:180-225). Before the first
+ * decode route (or request end) every routed layer must have seen 1..prompt_tokens rows
+ * (routing_trace.cpp:510-519); the request's coverage is written at request end. */
+vbm_status vbm_trace_prefill_route(vbm_trace * trace, int64_t layer_id, const int32_t * ids, int64_t rows);
 /* split "train" or "test"; prompt_tokens + max_tokens <= context_tokens; ids unique. */
 vbm_status vbm_trace_request_start(vbm_trace * trace, const char * id, const char * split,
                                    const char * category, int64_t prompt_tokens, int64_t max_tokens);
@@ -535,8 +549,10 @@ vbm_status vbm_tier_get_stats(const vbm_tier * tier, vbm_tier_stats * stats);
 
 /* Attach a routing trace (or NULL to detach): every vbm_tier_step then records each layer's
  * routed experts, as they reach the host for admission, as one route record (tier layer l is the
- * trace's l-th layer in ascending id order; counts and top_k must match). The trace stays owned
- * by the caller and must outlive the attachment. */
+ * trace's l-th layer in ascending id order; counts and top_k must match). When the trace writes
+ * a prefill summary, every vbm_tier_prefill also records its routed ids as prompt batches of
+ * <= 32768 rows (vbm_trace_prefill_route). The trace stays owned by the caller and must outlive
+ * the attachment. */
 vbm_status vbm_tier_set_trace(vbm_tier * tier, vbm_trace * trace);
 
 /* ----------------------------------------------------------------------------------------------

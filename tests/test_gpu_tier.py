@@ -2,6 +2,7 @@
 fully resident decode plan holding the same experts, routing identical, and the tier's admission
 counters equal to the Python restatement fed with the same routes."""
 import ctypes as C
+import json
 import sys
 from pathlib import Path
 
@@ -244,3 +245,50 @@ def test_tier_prefill_matches_resident_layer(gpu, type_id):
     for gu, dn in banks:
         gu.destroy()
         dn.destroy()
+
+
+def test_tier_prefill_records_the_prefill_summary(gpu, tmp_path):
+    """With a trace that writes the prefill summary attached, each vbm_tier_prefill records its
+    routed ids as one prompt batch (rows per expert), and the following decode steps record routes
+    as before; the summary's histograms equal the counts of the ids the prefill returned."""
+    from vbmoe import routing_trace as rt
+    vb = gpu
+    L, E, K, H, I, slots, T = 2, 16, 4, 256, 256, 4 + 6, 40
+    desc = vb.TierDesc(39, H, I, L, E, K, vb.ACT_SWIGLU_OAI, slots, 8, 2, vb.ADMIT_CLASSIC, None, None)
+    tier = C.c_void_p()
+    vb.call("vbm_tier_create", C.byref(desc), C.byref(tier))
+    vb.call("vbm_tier_generate", tier.value, SEED, 16, 1, 2, -8.0, -3.0, None)
+    layers = [{"id": i, "experts": E, "active": K, "bytes_per_expert": 1000, "static_host_bytes_per_expert": 1000}
+              for i in (4, 9)]
+    path, summary = tmp_path / "p.jsonl", tmp_path / "p.json"
+    writer = rt.TraceWriter(path, layers, "gpt-oss", "vbmoe-test", 128, collector_source_sha256="ab" * 32)
+    writer.enable_prefill(summary, T, T)
+    vb.call("vbm_tier_set_trace", tier.value, writer.handle)
+    rng = np.random.default_rng(9)
+    out, ids = vb.DeviceBuffer(4 * T * H), vb.DeviceBuffer(4 * T * K)
+    expected = []
+    writer.request_start("r0", "test", "chat", T, 3)
+    for l in range(L):
+        x = vb.DeviceBuffer.from_array(rng.standard_normal((T, H)).astype(np.float32))
+        lg = vb.DeviceBuffer.from_array(rng.standard_normal((T, E)).astype(np.float32))
+        vb.call("vbm_tier_prefill", tier.value, l, x.ptr, lg.ptr, T, out.ptr, ids.ptr, None, None)
+        vb.call("vbm_stream_synchronize", None)
+        expected.append(np.bincount(ids.download(np.int32, (T, K)).ravel(), minlength=E).tolist())
+    logits, chosen = routed_logits(rng, L, E, K, 3)
+    x1 = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 6, 0, H))
+    dl, o = vb.DeviceBuffer(logits[0].nbytes), vb.DeviceBuffer(4 * H)
+    for t in range(3):
+        dl.upload(logits[t])
+        vb.call("vbm_tier_step", tier.value, x1.ptr, dl.ptr, o.ptr, None, None)
+    vb.call("vbm_stream_synchronize", None)
+    writer.request_end("limit", True)
+    vb.call("vbm_tier_set_trace", tier.value, None)
+    writer.close()
+    vb.call("vbm_tier_destroy", tier.value)
+    doc = json.loads(summary.read_text())
+    req = doc["requests"][0]
+    assert [(b["layer"], b["rows"]) for b in req["batches"]] == [(4, T), (9, T)]
+    assert [b["expert_row_counts"] for b in req["batches"]] == expected
+    assert all(c["covers_all_prompt_rows"] for c in req["coverage"])
+    routes = [r for r in map(json.loads, path.read_text().splitlines()) if r["type"] == "route"]
+    assert [r["experts"] for r in routes] == [sel for row in chosen for sel in row]

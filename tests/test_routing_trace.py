@@ -411,3 +411,128 @@ def test_residency_replay_rejects_bad_parameters(rt, vb):
         rt.replay_residency(data, "lru", 10, 1.0, 1.0, staging_ram_passes=1)
     with pytest.raises(vb.VbmError, match=">= 1"):
         rt.replay_residency(data, "cost_aware", 10, 1.0, 1.0, payback_tokens=0)
+
+
+# ------------------------------------------------------------------------------------------------
+# prefill summary (routing_trace.cpp:180-225, 500-519, 570-580, 750-769)
+
+SHA = "0123456789abcdef" * 4
+
+
+def write_prefill(rt, tmp_path, prefill_batches, name="p"):
+    """Two requests over small_layers(); prefill_batches(split) yields (layer, ids) per batch."""
+    trace, summary = tmp_path / f"{name}.jsonl", tmp_path / f"{name}.json"
+    with rt.TraceWriter(trace, small_layers(), "test-moe", "test", 256, model="test.gguf",
+                        collector_source_sha256=SHA) as w:
+        w.enable_prefill(summary, 512, 128, cpu_threads=8, batch_threads=16)
+        for split, seq in (("train", ((0, 0), (0, 1))), ("test", ((1, 2),))):
+            w.request_start(split, split, "code", 4, len(seq))
+            for layer, ids in prefill_batches(split):
+                w.prefill_route(layer, ids)
+            for pair in seq:
+                w.token(np.array(pair, np.int32).reshape(2, 1))
+            w.request_end("limit", True)
+    return trace, summary
+
+
+def test_prefill_summary_format_and_histograms(rt, tmp_path):
+    def batches(split):
+        yield 0, [[0], [2], [2]]
+        yield 1, [[1], [1], [0]]
+        yield 0, [[1]]                              # a second batch: layer 0 sees all 4 prompt rows
+        if split == "test":
+            yield 1, np.zeros((0, 1), np.int32)     # output-pruned batch: zero rows are recorded
+    trace, summary = write_prefill(rt, tmp_path, batches)
+    text = summary.read_text(encoding="utf-8")
+    doc = json.loads(text)
+    # nlohmann dump(2) of sorted keys is Python's indent-2 sorted rendering
+    assert text == json.dumps(doc, sort_keys=True, indent=2, ensure_ascii=False) + "\n"
+    assert {k: doc[k] for k in ("schema_version", "capture_scope", "instrumented", "performance_measurement",
+                                "full_model_acceleration_claim", "complete", "batch_size", "microbatch_size",
+                                "cpu_threads", "batch_threads", "context_tokens", "model", "architecture",
+                                "backend_commit", "collector_source_sha256")} == {
+        "schema_version": 1, "capture_scope": "observed_prefill_expert_rows", "instrumented": True,
+        "performance_measurement": False, "full_model_acceleration_claim": False, "complete": True,
+        "batch_size": 512, "microbatch_size": 128, "cpu_threads": 8, "batch_threads": 16, "context_tokens": 256,
+        "model": "test.gguf", "architecture": "test-moe", "backend_commit": "test", "collector_source_sha256": SHA}
+    meta = json.loads(trace.read_text().splitlines()[0])
+    assert meta["collector_source_sha256"] == SHA and doc["layers"] == meta["layers"]
+    assert doc["coverage_note"].startswith("Observed graph rows only")
+    train, test = doc["requests"]
+    assert train["id"] == "train" and train["split"] == "train" and train["category"] == "code"
+    assert train["prompt_tokens"] == 4 and train["token_sequence_equivalent"] is True
+    assert [b["expert_row_counts"] for b in train["batches"]] == [[1, 0, 2], [1, 2, 0], [0, 1, 0]]
+    assert [(b["layer"], b["rows"], b["active_experts_per_row"]) for b in test["batches"]] == \
+        [(0, 3, 1), (1, 3, 1), (0, 1, 1), (1, 0, 1)]
+    assert test["batches"][3]["expert_row_counts"] == [0, 0, 0]
+    assert train["coverage"] == [{"covers_all_prompt_rows": True, "layer": 0, "observed_rows": 4},
+                                 {"covers_all_prompt_rows": False, "layer": 1, "observed_rows": 3}]
+    assert not Path(str(summary) + ".part").exists()
+    # the decode trace itself is unchanged by the prefill capture
+    data = rt.read_trace(trace)
+    assert data.tokens_for("train") == 2 and data.tokens_for("test") == 1
+
+
+def test_prefill_histogram_of_random_batches(rt, tmp_path):
+    rng = np.random.default_rng(3)
+    layers = [{"id": 5, "experts": 32, "active": 4, "bytes_per_expert": 1, "static_host_bytes_per_expert": 0}]
+    ids = np.stack([rng.permutation(32)[:4] for _ in range(300)]).astype(np.int32)
+    summary = tmp_path / "r.json"
+    with rt.TraceWriter(tmp_path / "r.jsonl", layers, "a", "b", 4096, collector_source_sha256=SHA) as w:
+        w.enable_prefill(summary, 1, 1)
+        w.request_start("r", "train", "c", 300, 1)
+        w.prefill_route(5, ids[:100])
+        w.prefill_route(5, ids[100:])
+        w.token(np.array([[1, 2, 3, 4]], np.int32))
+        w.request_end("limit", True)
+    doc = json.loads(summary.read_text())
+    hists = [b["expert_row_counts"] for b in doc["requests"][0]["batches"]]
+    assert hists == [np.bincount(ids[:100].ravel(), minlength=32).tolist(),
+                     np.bincount(ids[100:].ravel(), minlength=32).tolist()]
+    assert "model" not in doc                                  # omitted like the trace metadata's
+
+
+def test_prefill_rejections(rt, vb, tmp_path):
+    layers = small_layers()
+    with pytest.raises(vb.VbmError, match="collector_source_sha256"):
+        with rt.TraceWriter(tmp_path / "a.jsonl", layers, "a", "b", 256) as w:
+            w.enable_prefill(tmp_path / "a.json", 1, 1)
+    with pytest.raises(vb.VbmError, match="64 lower-case hex"):
+        rt.TraceWriter(tmp_path / "h.jsonl", layers, "a", "b", 256, collector_source_sha256=SHA.upper())
+    (tmp_path / "exists.json").write_text("{}")
+    with pytest.raises(vb.VbmError, match="Refusing to overwrite"):
+        with rt.TraceWriter(tmp_path / "b.jsonl", layers, "a", "b", 256, collector_source_sha256=SHA) as w:
+            w.enable_prefill(tmp_path / "exists.json", 1, 1)
+    with pytest.raises(vb.VbmError, match="must not alias"):
+        with rt.TraceWriter(tmp_path / "c.jsonl", layers, "a", "b", 256, collector_source_sha256=SHA) as w:
+            w.enable_prefill(tmp_path / "c.jsonl.part", 1, 1)
+
+    def case(body, match, name):
+        with pytest.raises((vb.VbmError, ValueError), match=match):
+            with rt.TraceWriter(tmp_path / f"{name}.jsonl", layers, "a", "b", 256, collector_source_sha256=SHA) as w:
+                w.enable_prefill(tmp_path / f"{name}.json", 1, 1)
+                w.request_start("r", "train", "c", 4, 1)
+                body(w)
+        assert not (tmp_path / f"{name}.json").exists() and not (tmp_path / f"{name}.jsonl").exists()
+
+    case(lambda w: w.prefill_route(0, [[3]]), "Out-of-range", "range")
+    case(lambda w: w.prefill_route(0, [[-1]]), "Out-of-range", "negative")
+    case(lambda w: w.prefill_route(2, [[0]]), "layer", "unknown")
+    case(lambda w: w.prefill_route(0, [[0, 1]]), r"\[rows\]\[1\]", "shape")
+    case(lambda w: w.prefill_route(0, np.zeros((32769, 1), np.int32)), "0..32768", "rows")
+    # a layer without observed rows, or more rows than the prompt, stops decoding
+    case(lambda w: (w.prefill_route(0, [[0]]), w.route(0, [1])), "Missing or duplicate prefill", "missing")
+    case(lambda w: (w.prefill_route(0, [[0]] * 5), w.prefill_route(1, [[0]]), w.route(0, [1])),
+         "Missing or duplicate prefill", "excess")
+    case(lambda w: (w.prefill_route(0, [[0]]), w.prefill_route(1, [[0]]), w.route(0, [1]), w.prefill_route(0, [[1]])),
+         "precede", "late")
+    case(lambda w: w.request_end("eos", True), "Missing or duplicate prefill", "empty")
+
+
+def test_prefill_duplicate_expert_in_row(rt, vb, tmp_path):
+    layers = [{"id": 0, "experts": 8, "active": 2, "bytes_per_expert": 1, "static_host_bytes_per_expert": 0}]
+    with pytest.raises(vb.VbmError, match="duplicate routed expert"):
+        with rt.TraceWriter(tmp_path / "d.jsonl", layers, "a", "b", 256, collector_source_sha256=SHA) as w:
+            w.enable_prefill(tmp_path / "d.json", 1, 1)
+            w.request_start("r", "train", "c", 4, 1)
+            w.prefill_route(0, [[1, 2], [3, 3]])

@@ -398,6 +398,12 @@ vbm_status vbm_tier_prefill(vbm_tier * t, int64_t layer, const float * x, const 
         prefill_prepare(desc, x, w.ids, T, w, s);
         check_hip(hipMemcpyAsync(t->pf_ids_host, w.ids, sizeof(int32_t) * T * K, hipMemcpyDeviceToHost, s), "prefill ids");
         check_hip(hipStreamSynchronize(s), "prefill ids synchronize");
+        int prefill_summary = 0;
+        if (t->trace) check_status(vbm_trace_prefill_enabled(t->trace, &prefill_summary), "tier trace");
+        for (int64_t r = 0; prefill_summary && r < T; r += 32768)   // the summary's batches hold <= 32768 rows
+            check_status(vbm_trace_prefill_route(t->trace, t->trace_layer_ids[static_cast<size_t>(layer)],
+                                                 t->pf_ids_host + r * K, std::min<int64_t>(32768, T - r)),
+                         "tier trace");
         if (t->used) check_hip(hipStreamWaitEvent(t->copy_stream, t->last_use, 0), "tier reuse wait");
         t->started = true;
         // 2. residency is frozen for multi-token batches: pass 0 covers the resident experts, then

@@ -20,6 +20,8 @@
 #include <cerrno>
 #include <cstdio>
 #include <cstring>
+#include <iterator>
+#include <map>
 #include <memory>
 #include <set>
 #include <string>
@@ -91,6 +93,54 @@ struct Obj {
     std::string done() { return s + "}"; }
 };
 
+// A JSON value for the prefill summary, printed like the reference serializer's dump(2): keys in
+// ascending order, two-space indentation, one element per line, "key": value, [] and {} when empty.
+struct JVal {
+    enum Kind { Null, Bool, Int, Str, Arr, Obj } kind = Null;
+    bool b = false;
+    long long i = 0;
+    std::string s;
+    std::vector<JVal> arr;
+    std::map<std::string, JVal> obj;
+    static JVal boolean(bool v) { JVal j; j.kind = Bool; j.b = v; return j; }
+    static JVal integer(long long v) { JVal j; j.kind = Int; j.i = v; return j; }
+    static JVal string(const std::string & v) { JVal j; j.kind = Str; j.s = v; return j; }
+    static JVal array() { JVal j; j.kind = Arr; return j; }
+    static JVal object() { JVal j; j.kind = Obj; return j; }
+    JVal & set(const std::string & k, JVal v) { obj[k] = std::move(v); return *this; }
+    void pretty(std::string & out, int depth) const {
+        const std::string pad(static_cast<size_t>(2 * (depth + 1)), ' '), close(static_cast<size_t>(2 * depth), ' ');
+        switch (kind) {
+            case Null: out += "null"; break;
+            case Bool: out += b ? "true" : "false"; break;
+            case Int: out += std::to_string(i); break;
+            case Str: append_json_string(out, s); break;
+            case Arr:
+                if (arr.empty()) { out += "[]"; break; }
+                out += "[\n";
+                for (size_t k = 0; k < arr.size(); ++k) {
+                    out += pad;
+                    arr[k].pretty(out, depth + 1);
+                    out += k + 1 < arr.size() ? ",\n" : "\n";
+                }
+                out += close + "]";
+                break;
+            case Obj:
+                if (obj.empty()) { out += "{}"; break; }
+                out += "{\n";
+                for (auto it = obj.begin(); it != obj.end(); ++it) {
+                    out += pad;
+                    append_json_string(out, it->first);
+                    out += ": ";
+                    it->second.pretty(out, depth + 1);
+                    out += std::next(it) != obj.end() ? ",\n" : "\n";
+                }
+                out += close + "}";
+                break;
+        }
+    }
+};
+
 struct TraceLayer {
     int64_t id = 0, experts = 0, active = 0;
     uint64_t bytes = 0, host_bytes = 0;
@@ -112,6 +162,17 @@ struct vbm_trace {
     int64_t max_tokens = 0;
     int64_t token = 0;                // complete tokens of the open request
     size_t layer_index = 0;           // next layer expected within the current token
+    // prefill summary (optional): observed expert rows per routed layer and prompt batch
+    std::string architecture, backend_commit, model, collector_sha256;
+    std::string prefill_path;         // empty: no summary
+    int64_t batch_size = 0, microbatch_size = 0, cpu_threads = 0, batch_threads = 0;
+    std::string layers_json;          // the metadata layers array (compact)
+    JVal layers_val = JVal::array();
+    JVal prefill_requests = JVal::array();
+    JVal open_batches = JVal::array();
+    std::map<int64_t, int64_t> open_rows;   // layer id -> observed rows of the open request
+    std::string request_split, request_category;
+    int64_t prompt_tokens = 0;
 
     void emit(const std::string & line) {
         const std::string text = line + '\n';
@@ -123,8 +184,19 @@ struct vbm_trace {
             if (layers[i].id == id) return i;
         fail(VBM_ERR_INVALID_ARGUMENT, "route layer " + std::to_string(id) + " is not a routed layer of the trace");
     }
+    // With a prefill summary, every routed layer must have observed 1..prompt_tokens prompt rows
+    // before decoding starts (routing_trace.cpp:510-519).
+    void check_prefill_coverage() const {
+        if (prefill_path.empty()) return;
+        for (const TraceLayer & L : layers) {
+            const auto it = open_rows.find(L.id);
+            require(it != open_rows.end() && it->second > 0 && it->second <= prompt_tokens,
+                    "Missing or duplicate prefill layer observations.");
+        }
+    }
     void route(int64_t layer_id, const int32_t * experts, int64_t n) {
         require(in_request, "route is outside a decode request");
+        if (token == 0 && layer_index == 0) check_prefill_coverage();
         require(token < max_tokens, "route beyond the request's max_tokens");
         const size_t li = find_layer(layer_id);
         require(li == layer_index, "missing, duplicate, or out-of-order layer observation (expected layer " +
@@ -159,7 +231,8 @@ extern "C" {
 
 vbm_status vbm_trace_open(const char * path, const char * architecture, const char * backend_commit,
                           const char * model, int64_t context_tokens, const vbm_trace_layer * layers,
-                          int64_t n_layers, const char * token_equivalence_check, vbm_trace ** out) {
+                          int64_t n_layers, const char * token_equivalence_check,
+                          const char * collector_source_sha256, vbm_trace ** out) {
     return guarded([&] {
         require(path && *path && out, "null argument");
         require(architecture && *architecture, "architecture must be a nonempty string");
@@ -167,8 +240,17 @@ vbm_status vbm_trace_open(const char * path, const char * architecture, const ch
         require(context_tokens >= 1, "context_tokens must be >= 1");
         require(layers != nullptr && n_layers >= 1, "a trace needs at least one routed layer");
         *out = nullptr;
+        if (collector_source_sha256 && *collector_source_sha256) {
+            const std::string h = collector_source_sha256;
+            require(h.size() == 64 && h.find_first_not_of("0123456789abcdef") == std::string::npos,
+                    "collector_source_sha256 must be 64 lower-case hex digits");
+        }
         auto t = std::make_unique<vbm_trace>();
         t->destination = path;
+        t->architecture = architecture;
+        t->backend_commit = backend_commit;
+        t->model = model ? model : "";
+        t->collector_sha256 = collector_source_sha256 ? collector_source_sha256 : "";
         t->partial = t->destination + ".part";
         t->context_tokens = context_tokens;
         uint64_t device_bytes = 0;
@@ -215,6 +297,13 @@ vbm_status vbm_trace_open(const char * path, const char * architecture, const ch
                 append_json_string(types, L.types[k]);
             }
             types += ']';
+            JVal lv = JVal::object(), tv = JVal::array();
+            for (const auto & name : L.types) tv.arr.push_back(JVal::string(name));
+            lv.set("active", JVal::integer(L.active)).set("bytes_per_expert", JVal::integer(static_cast<long long>(L.bytes)))
+                .set("experts", JVal::integer(L.experts)).set("id", JVal::integer(L.id))
+                .set("static_host_bytes_per_expert", JVal::integer(static_cast<long long>(L.host_bytes)))
+                .set("tensor_types", tv);
+            t->layers_val.arr.push_back(lv);
             if (i) list += ',';
             list += Obj().num("active", L.active).unum("bytes_per_expert", L.bytes).num("experts", L.experts)
                         .num("id", L.id).unum("static_host_bytes_per_expert", L.host_bytes)
@@ -222,9 +311,11 @@ vbm_status vbm_trace_open(const char * path, const char * architecture, const ch
         }
         list += ']';
         Obj meta;
+        t->layers_json = list;
         meta.str("architecture", architecture).str("backend_commit", backend_commit)
-            .str("capture_scope", "decode_only").num("context_tokens", context_tokens).boolean("instrumented", true)
-            .raw("layers", list);
+            .str("capture_scope", "decode_only");
+        if (!t->collector_sha256.empty()) meta.str("collector_source_sha256", t->collector_sha256);
+        meta.num("context_tokens", context_tokens).boolean("instrumented", true).raw("layers", list);
         if (model && *model) meta.str("model", model);
         meta.num("schema_version", 1).unum("static_device_expert_bytes", device_bytes);
         if (token_equivalence_check && *token_equivalence_check)
@@ -257,6 +348,11 @@ vbm_status vbm_trace_request_start(vbm_trace * t, const char * id, const char * 
         t->max_tokens = max_tokens;
         t->token = 0;
         t->layer_index = 0;
+        t->request_split = split;
+        t->request_category = category;
+        t->prompt_tokens = prompt_tokens;
+        t->open_batches = JVal::array();
+        t->open_rows.clear();
         ++t->requests;
     });
 }
@@ -294,8 +390,24 @@ vbm_status vbm_trace_request_end(vbm_trace * t, const char * stop_reason, int to
         end.num("decode_tokens", t->token).str("id", t->request).str("stop_reason", stop_reason);
         if (token_sequence_equivalent) end.boolean("token_sequence_equivalent", true);
         end.str("type", "request_end");
+        if (t->token == 0) t->check_prefill_coverage();
         t->emit(end.done());
         t->in_request = false;
+        if (!t->prefill_path.empty()) {        // routing_trace.cpp:570-580
+            JVal cov = JVal::array();
+            for (const TraceLayer & L : t->layers) {
+                const int64_t rows = t->open_rows[L.id];
+                JVal c = JVal::object();
+                c.set("covers_all_prompt_rows", JVal::boolean(rows == t->prompt_tokens))
+                    .set("layer", JVal::integer(L.id)).set("observed_rows", JVal::integer(rows));
+                cov.arr.push_back(c);
+            }
+            JVal r = JVal::object();
+            r.set("batches", t->open_batches).set("category", JVal::string(t->request_category))
+                .set("coverage", cov).set("id", JVal::string(t->request)).set("prompt_tokens", JVal::integer(t->prompt_tokens))
+                .set("split", JVal::string(t->request_split)).set("token_sequence_equivalent", JVal::boolean(true));
+            t->prefill_requests.arr.push_back(r);
+        }
     });
 }
 
@@ -319,6 +431,96 @@ vbm_status vbm_trace_close(vbm_trace * t) {
             fail(VBM_ERR_RUNTIME, "Cannot publish the routing trace: " + why);
         }
         std::remove(t->partial.c_str());
+        if (!t->prefill_path.empty()) {        // routing_trace.cpp:750-769
+            JVal doc = JVal::object();
+            doc.set("schema_version", JVal::integer(1)).set("capture_scope", JVal::string("observed_prefill_expert_rows"))
+                .set("instrumented", JVal::boolean(true)).set("performance_measurement", JVal::boolean(false))
+                .set("full_model_acceleration_claim", JVal::boolean(false))
+                .set("backend_commit", JVal::string(t->backend_commit)).set("architecture", JVal::string(t->architecture))
+                .set("batch_size", JVal::integer(t->batch_size)).set("microbatch_size", JVal::integer(t->microbatch_size))
+                .set("cpu_threads", JVal::integer(t->cpu_threads)).set("batch_threads", JVal::integer(t->batch_threads))
+                .set("context_tokens", JVal::integer(t->context_tokens)).set("layers", t->layers_val)
+                .set("coverage_note", JVal::string("Observed graph rows only; final-layer output pruning can omit prompt positions."))
+                .set("requests", t->prefill_requests).set("complete", JVal::boolean(true));
+            if (!t->model.empty()) doc.set("model", JVal::string(t->model));
+            doc.set("collector_source_sha256", JVal::string(t->collector_sha256));
+            std::string text;
+            doc.pretty(text, 0);
+            text += '\n';
+            const std::string part = t->prefill_path + ".part";
+            FILE * f = std::fopen(part.c_str(), "wx");
+            if (!f) fail(VBM_ERR_RUNTIME, "Cannot exclusively create prefill summary.");
+            const bool ok = std::fwrite(text.data(), 1, text.size(), f) == text.size();
+            if (std::fclose(f) != 0 || !ok || link(part.c_str(), t->prefill_path.c_str()) != 0) {
+                std::remove(part.c_str());
+                fail(VBM_ERR_RUNTIME, "Failed to publish complete prefill summary.");
+            }
+            std::remove(part.c_str());
+        }
+    });
+}
+
+vbm_status vbm_trace_enable_prefill(vbm_trace * t, const char * summary_path, int64_t batch_size,
+                                    int64_t microbatch_size, int64_t cpu_threads, int64_t batch_threads) {
+    return guarded([&] {
+        require(t != nullptr && t->file != nullptr, "closed or null trace");
+        require(t->requests == 0, "the prefill summary must be enabled before the first request");
+        require(t->prefill_path.empty(), "the prefill summary is already enabled");
+        // the summary's reader matches it against the trace's collector hash (vrambridge-prefill-seed.py:37)
+        require(!t->collector_sha256.empty(), "the prefill summary needs collector_source_sha256 in the trace");
+        require(summary_path && *summary_path, "null summary path");
+        const std::string path = summary_path;
+        require(path != t->destination && path != t->partial && path + ".part" != t->destination &&
+                    path + ".part" != t->partial,
+                "Prefill output must not alias the trace or partial paths.");
+        require(access(path.c_str(), F_OK) != 0 && access((path + ".part").c_str(), F_OK) != 0,
+                "Refusing to overwrite an existing prefill summary or partial.");
+        require(batch_size >= 1 && microbatch_size >= 1 && cpu_threads >= 0 && batch_threads >= 0,
+                "batch sizes must be >= 1 and thread counts >= 0");
+        t->prefill_path = path;
+        t->batch_size = batch_size;
+        t->microbatch_size = microbatch_size;
+        t->cpu_threads = cpu_threads;
+        t->batch_threads = batch_threads;
+    });
+}
+
+vbm_status vbm_trace_prefill_enabled(const vbm_trace * t, int * enabled) {
+    return guarded([&] {
+        require(t != nullptr && enabled != nullptr, "null argument");
+        *enabled = t->prefill_path.empty() ? 0 : 1;
+    });
+}
+
+vbm_status vbm_trace_prefill_route(vbm_trace * t, int64_t layer_id, const int32_t * ids, int64_t rows) {
+    return guarded([&] {
+        require(t != nullptr && t->file != nullptr, "closed or null trace");
+        require(!t->prefill_path.empty(), "no prefill summary enabled");
+        require(t->in_request && t->token == 0 && t->layer_index == 0,
+                "prefill batches precede the request's decode routes");
+        require(rows >= 0 && rows <= 32768, "Unsupported routing tensor shape: prefill rows outside 0..32768");
+        require(rows == 0 || ids != nullptr, "null ids");
+        const TraceLayer & L = t->layers[t->find_layer(layer_id)];
+        // routing_trace.cpp:188-223: each row's experts in range and distinct; rows per expert
+        std::vector<int64_t> counts(static_cast<size_t>(L.experts), 0);
+        std::vector<char> seen(static_cast<size_t>(L.experts), 0);
+        for (int64_t r = 0; r < rows; ++r) {
+            const int32_t * row = ids + r * L.active;
+            for (int64_t k = 0; k < L.active; ++k) {
+                const int32_t e = row[k];
+                require(e >= 0 && e < L.experts && !seen[static_cast<size_t>(e)], "Out-of-range or duplicate routed expert.");
+                seen[static_cast<size_t>(e)] = 1;
+                ++counts[static_cast<size_t>(e)];
+            }
+            for (int64_t k = 0; k < L.active; ++k) seen[static_cast<size_t>(row[k])] = 0;
+        }
+        JVal hist = JVal::array();
+        for (int64_t c : counts) hist.arr.push_back(JVal::integer(c));
+        JVal b = JVal::object();
+        b.set("active_experts_per_row", JVal::integer(L.active)).set("expert_row_counts", hist)
+            .set("layer", JVal::integer(layer_id)).set("rows", JVal::integer(rows));
+        t->open_batches.arr.push_back(b);
+        t->open_rows[layer_id] += rows;
     });
 }
 

@@ -193,7 +193,10 @@ SIGNATURES = {
     "vbm_gguf_load_layer": [vp, i64, vp, vp, i64, vp, vp, vp, vp, vp],
     "vbm_gguf_load_biases": [vp, i64, vp, vp, vp],
     "vbm_trace_open": [C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, i64, C.POINTER(TraceLayer), i64,
-                       C.c_char_p, C.POINTER(vp)],
+                       C.c_char_p, C.c_char_p, C.POINTER(vp)],
+    "vbm_trace_enable_prefill": [vp, C.c_char_p, i64, i64, i64, i64],
+    "vbm_trace_prefill_enabled": [vp, C.POINTER(C.c_int)],
+    "vbm_trace_prefill_route": [vp, i64, vp, i64],
     "vbm_trace_request_start": [vp, C.c_char_p, C.c_char_p, C.c_char_p, i64, i64],
     "vbm_trace_route": [vp, i64, vp, i64],
     "vbm_trace_token": [vp, vp, i64],
