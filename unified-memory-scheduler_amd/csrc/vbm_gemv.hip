@@ -244,32 +244,6 @@ __device__ __forceinline__ void preload_ring(Group (&ring)[D], const uint8_t * c
     }
 }
 
-// Streams the full groups of one lane's row slice once through the D-deep register ring,
-// applying every staged token to each group as it arrives. With MLDS, `meta_tile` is the
-// lane's tile exponents / scales staged in LDS.
-template <int TYPE, int MT, bool SLOW, int D, bool MLDS>
-__device__ __forceinline__ void stream_groups(Group (&ring)[D], const uint8_t * codes_tile, const uint8_t * meta_tile,
-                                              int k, int r, int nb, bool live, const uint8_t * la, const float * lda,
-                                              int tok_bytes, int mcount, float (&acc)[MT][2]) {
-    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
-    const int groups = nb / kGroupBlocks;
-    const uint8_t * cp = codes_tile + (k * 32 + r) * 16;
-    const uint8_t * mp = meta_tile + r * 8;
-    for (int g0 = 0; g0 < groups; g0 += D) {
-#pragma unroll
-        for (int i = 0; i < D; ++i) {
-            const int g = g0 + i;
-            if (g < groups) {
-                const Group cur = ring[i];
-                if (live && g + D < groups) ring[i] = load_group<MLDS>(cp, mp, g + D);
-                const u32x2 m = MLDS ? *reinterpret_cast<const u32x2 *>(mp + g * 256) : cur.m;
-                if (TYPE == 39) mx_group<MT, SLOW>(cur.c, m, g * 8, la, lda, tok_bytes, mcount, acc);
-                else q8_group<MT, SLOW>(cur.c, m, g * 4, la, lda, tok_bytes, mcount, acc);
-            }
-        }
-    }
-}
-
 // The tail blocks of one lane's row slice (after its full groups: block order is chain order).
 // With MLDS the exponents / scales come from the lane's tile meta staged in LDS (`meta_lds`).
 template <int TYPE, int MT, bool SLOW, bool MLDS>
@@ -289,6 +263,94 @@ __device__ __forceinline__ void apply_tail(const Tail & tl, const uint8_t * meta
                 mx_block<MT, SLOW, 2, 1>(tl.c[i], static_cast<signed char>(m >> 8), b + 1, la, lda, tok_bytes, mcount, acc);
             } else {
                 q8_block<MT, SLOW>(tl.c[i], static_cast<unsigned short>(m), groups * 4 + i, la, lda, tok_bytes, mcount, acc);
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ buffer-descriptor weight stream
+// The batched kernel reads one expert slot through a buffer descriptor (SGPRs) with one VGPR
+// offset per lane and the group offsets as SGPR soffsets, so the ring costs no per-group address
+// registers and no per-lane exec masking (lanes of a half-live tile pair read tile 0 and drop it).
+// dword3 0x00020000 is the raw-buffer format word of the gfx9 family; aux 2 marks the loads
+// non-temporal, as the pointer loads above.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slot_rsrc(const uint8_t * base, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes < 0x7fffffffu ? bytes : 0x7fffffffu), 0x00020000);
+}
+
+struct BufLane {
+    __amdgpu_buffer_rsrc_t rsrc;
+    int code_off;   // byte offset of the lane's first group of codes in the slot
+    int meta_off;   // byte offset of the lane's first group of exponents / scales
+    int tail_code;  // byte offset of the lane's tail codes
+    int tail_meta;  // byte offset of the lane's tail exponents / scales
+};
+
+__device__ __forceinline__ Group load_group_buf(const BufLane & B, int g) {
+    Group r;
+    r.c = __builtin_amdgcn_raw_buffer_load_b128(B.rsrc, B.code_off, g * 4096, 2);
+    r.m = __builtin_amdgcn_raw_buffer_load_b64(B.rsrc, B.meta_off, g * 256, 2);
+    return r;
+}
+
+template <int TYPE>
+__device__ __forceinline__ BufLane buf_lane(const uint8_t * slot_base, size_t slot_bytes, int64_t codes_bytes, int tile,
+                                            int k, int r, int nb) {
+    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4, kCode = TYPE == 39 ? 2 : 4, kMeta = TYPE == 39 ? 1 : 2;
+    const int groups = nb / kGroupBlocks, tail = nb % kGroupBlocks;
+    BufLane B;
+    B.rsrc = slot_rsrc(slot_base, slot_bytes);
+    const int codes_tile = tile * 32 * nb * (TYPE == 39 ? 16 : 32);
+    const int meta_tile = static_cast<int>(codes_bytes) + tile * 32 * nb * kMeta;
+    B.code_off = codes_tile + (k * 32 + r) * 16;
+    B.meta_off = meta_tile + r * 8;
+    B.tail_code = codes_tile + groups * 4096 + (k * 32 + r) * (tail * kCode);
+    B.tail_meta = meta_tile + groups * 256 + r * tail * kMeta;
+    return B;
+}
+
+template <int TYPE, int D>
+__device__ __forceinline__ void preload_ring_buf(Group (&ring)[D], const BufLane & B, int nb) {
+    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
+    const int groups = nb / kGroupBlocks;
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+        ring[i] = Group{};
+        if (i < groups) ring[i] = load_group_buf(B, i);
+    }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void preload_tail_buf(Tail & t, const BufLane & B, int nb) {
+    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
+    const int tail = nb % kGroupBlocks;
+    const int n = TYPE == 39 ? tail / 2 : tail;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        t.c[i] = 0u;
+        t.m[i] = 0u;
+        if (i < n) {
+            t.c[i] = __builtin_amdgcn_raw_buffer_load_b32(B.rsrc, B.tail_code, 4 * i, 2);
+            t.m[i] = __builtin_amdgcn_raw_buffer_load_b16(B.rsrc, B.tail_meta, 2 * i, 0);
+        }
+    }
+}
+
+template <int TYPE, int MT, bool SLOW, int D>
+__device__ __forceinline__ void stream_groups_buf(Group (&ring)[D], const BufLane & B, int nb, const uint8_t * la,
+                                                  const float * lda, int tok_bytes, int mcount, float (&acc)[MT][2]) {
+    constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
+    const int groups = nb / kGroupBlocks;
+    for (int g0 = 0; g0 < groups; g0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const int g = g0 + i;
+            if (g < groups) {
+                const Group cur = ring[i];
+                if (g + D < groups) ring[i] = load_group_buf(B, g + D);
+                if (TYPE == 39) mx_group<MT, SLOW>(cur.c, cur.m, g * 8, la, lda, tok_bytes, mcount, acc);
+                else q8_group<MT, SLOW>(cur.c, cur.m, g * 4, la, lda, tok_bytes, mcount, acc);
             }
         }
     }
@@ -519,8 +581,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const int tile = blockIdx.x * 2 + (lane >> 5);
     const bool live = tile * 32 < S.rows;                              // the last tile pair may be half
     const uint8_t * slot_base = A.bank + static_cast<size_t>(slot) * S.slot_bytes;
-    const uint8_t * codes_tile = slot_base + static_cast<size_t>(live ? tile : 0) * 32 * nb * (TYPE == 39 ? 16 : 32);
-    const uint8_t * meta_tile = slot_base + S.codes_bytes + static_cast<size_t>(live ? tile : 0) * 32 * nb * (TYPE == 39 ? 1 : 2);
+    const BufLane B = buf_lane<TYPE>(slot_base, S.slot_bytes, S.codes_bytes, live ? tile : 0, k, r, nb);
     const int copy_bytes = static_cast<int>(A.lay.flag_offset());        // codes + scales of a row
     const int tok_bytes = (copy_bytes + 15) & ~15;
     const uint8_t * la = lds_tok + static_cast<int64_t>(k) * nb * A.lay.code_entry();
@@ -530,7 +591,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     for (int c0 = 0; c0 < count; c0 += MT) {
         const int mcount = count - c0 < MT ? count - c0 : MT;
         Group ring[D];
-        preload_ring<TYPE, D, false>(ring, codes_tile, meta_tile, k, r, nb, live);
+        preload_ring_buf<TYPE, D>(ring, B, nb);
         // Stage the chunk's activation rows (and their -128 flags) in LDS.
         if (threadIdx.x == 0) s_flag = 0;
         __syncthreads();
@@ -553,14 +614,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         for (int m = 0; m < MT; ++m) acc[m][0] = acc[m][1] = 0.0f;
         Tail tl;
         if (s_flag) {
-            stream_groups<TYPE, MT, true, D, false>(ring, codes_tile, meta_tile, k, r, nb, live, la, lda, tok_bytes, mcount,
-                                                    acc);
-            preload_tail<TYPE, false>(tl, codes_tile, meta_tile, k, r, nb, live);
+            stream_groups_buf<TYPE, MT, true, D>(ring, B, nb, la, lda, tok_bytes, mcount, acc);
+            preload_tail_buf<TYPE>(tl, B, nb);
             apply_tail<TYPE, MT, true, false>(tl, nullptr, r, nb, la, lda, tok_bytes, mcount, acc);
         } else {
-            stream_groups<TYPE, MT, false, D, false>(ring, codes_tile, meta_tile, k, r, nb, live, la, lda, tok_bytes, mcount,
-                                                     acc);
-            preload_tail<TYPE, false>(tl, codes_tile, meta_tile, k, r, nb, live);
+            stream_groups_buf<TYPE, MT, false, D>(ring, B, nb, la, lda, tok_bytes, mcount, acc);
+            preload_tail_buf<TYPE>(tl, B, nb);
             apply_tail<TYPE, MT, false, false>(tl, nullptr, r, nb, la, lda, tok_bytes, mcount, acc);
         }
 #pragma unroll
