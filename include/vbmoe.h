@@ -368,6 +368,14 @@ typedef struct {
     double ram_gbps, pcie_gbps, gpu_expert_us, layer_sync_us;
     int staging_ram_passes;                  /* 0 or 2                                          */
     uint64_t static_device_expert_bytes;     /* the trace metadata's (measured_static)          */
+    /* Seeded replay (vrambridge-prefill-seed.py:133-154; lru, lfu, cost_aware): at the first
+     * held-out event the cache holds exactly these n_seed (layer index, expert) keys, whose bytes
+     * must fit the capacity; `frozen` then keeps it fixed (no admission). NULL / 0: no seed. */
+    const int32_t * seed_layer;
+    const int32_t * seed_expert;
+    int64_t n_seed;
+    int seeded;
+    int frozen;
 } vbm_residency_params;
 
 typedef struct {
@@ -380,6 +388,11 @@ typedef struct {
 vbm_status vbm_residency_replay(const vbm_residency_layer * layers, int64_t n_layers, const int32_t * event_layer,
                                 const int32_t * event_split, const int64_t * event_offsets, const int32_t * experts,
                                 int64_t n_events, const vbm_residency_params * params, vbm_residency_totals * totals);
+/* The latency model alone (Costs.latency, vrambridge-routing.py:212-223) for one layer's cold
+ * bytes, GPU experts and uploads, with params' costs: serial, optimistic-overlap seconds and the
+ * shared RAM bytes. */
+vbm_status vbm_residency_latency(const vbm_residency_params * params, double cpu_bytes, double gpu_experts,
+                                 double upload_bytes, double * serial_s, double * optimistic_s, double * shared_ram_bytes);
 
 /* ----------------------------------------------------------------------------------------------
  * GGUF expert tensors (tools/engine/gguf_experts.cpp:27-140): blk.L.ffn_{gate,up,down}_exps.

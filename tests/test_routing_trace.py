@@ -3,8 +3,10 @@
 Pinned by: the reference analyzer's own reader cases (tests/test_routing_analysis.py:37-144 of the
 reference, restated below), the reference analyzer's reading of a trace written by this library
 (tests/golden/routing_trace_small_report.json, made by tests/golden/make_routing_trace_golden.py),
-Python's JSON serializer as an independent rendering of the same compact sorted-key records, and
-the admission restatement (oracle/admission.py) for replays.
+Python's JSON serializer as an independent rendering of the same compact sorted-key records, the
+admission restatement (oracle/admission.py) for replays, and the reference seed study's report of
+a trace and prefill summary written here (tests/golden/routing_trace_prefill_report.json, made by
+tests/golden/make_prefill_seed_golden.py).
 """
 import copy
 import hashlib
@@ -536,3 +538,89 @@ def test_prefill_duplicate_expert_in_row(rt, vb, tmp_path):
             w.enable_prefill(tmp_path / "d.json", 1, 1)
             w.request_start("r", "train", "c", 4, 1)
             w.prefill_route(0, [[1, 2], [3, 3]])
+
+
+# ------------------------------------------------------------------------------------------------
+# the prompt-conditioned seed study against the reference study's own report (committed fixture)
+
+
+def test_prefill_seed_study_matches_reference_report(rt, tmp_path):
+    import make_prefill_seed_golden as mk
+    report = json.loads((GOLDEN / "routing_trace_prefill_report.json").read_text())
+    trace, summary = mk.write_trace(tmp_path / "p.jsonl", tmp_path / "p.json")
+    assert trace.read_bytes() == (GOLDEN / "routing_trace_prefill.jsonl").read_bytes()
+    assert summary.read_bytes() == (GOLDEN / "routing_trace_prefill_summary.json").read_bytes()
+    data = rt.read_trace(GOLDEN / "routing_trace_prefill.jsonl")
+    prefill = rt.read_prefill(GOLDEN / "routing_trace_prefill_summary.json", data)
+    for ident, want in report["prefill_read"].items():
+        got = prefill[ident]
+        assert sorted([l, e, c] for (l, e), c in got["counts"].items() if c) == want["counts"]
+        assert sorted([l, r] for l, r in got["rows"].items()) == want["rows"]
+        assert sorted([l, c] for l, c in got["coverage"].items()) == want["coverage"]
+    baseline = rt.read_baseline_plan(GOLDEN / "routing_trace_prefill_plan.txt", data)
+    ours = rt.prefill_seed_study(data, prefill, baseline, mk.COSTS["ram_gbps"], mk.COSTS["pcie_gbps"],
+                                 mk.COSTS["gpu_expert_us"])
+    for key in ("schema_version", "study", "capacity_bytes", "train_tokens", "test_tokens", "trace_sha256", "model",
+                "blend_weight", "costs"):
+        assert ours[key] == report[key], key
+    assert [r["id"] for r in ours["requests"]] == [r["id"] for r in report["requests"]]
+    checked = 0
+    for mine, ref in zip(ours["requests"], report["requests"]):
+        assert mine["partial_prefill_layers_using_training_prior"] == ref["partial_prefill_layers_using_training_prior"]
+        assert mine["decode_tokens"] == ref["decode_tokens"]
+        for policy, seeds in ref["policies"].items():
+            for seed, want in seeds.items():
+                got = mine["policies"][policy][seed]
+                assert set(got) == set(want)
+                for key, w in want.items():
+                    if isinstance(w, float):
+                        assert got[key] == pytest.approx(w, rel=1e-12, abs=0), (mine["id"], policy, seed, key)
+                    else:
+                        assert got[key] == w, (mine["id"], policy, seed, key)
+                checked += 1
+    assert checked == 2 * 2 * 5
+    # the fixture exercises what it is for: a partial layer falls back to the prior, and the
+    # prompt-conditioned seed differs from the training hot set
+    assert report["requests"][1]["partial_prefill_layers_using_training_prior"] == [3]
+    seeds = rt.prefill_seeds(data, prefill, baseline)
+    assert seeds["test-a"]["prompt_only"] != seeds["test-a"]["train_only"]
+
+
+@pytest.mark.parametrize("edit,match", [
+    (lambda d: d.update(collector_source_sha256="0" * 64), "provenance"),
+    (lambda d: d["requests"][0]["batches"][0]["expert_row_counts"].__setitem__(0, 99), "exceeds observed rows"),
+    (lambda d: d["requests"][0]["coverage"].pop(), "Missing prefill layer coverage"),
+    (lambda d: d["requests"].pop(), "request count"),
+    (lambda d: d["requests"][3]["coverage"][3].__setitem__("covers_all_prompt_rows", True), "coverage inconsistent"),
+])
+def test_read_prefill_rejections(rt, tmp_path, edit, match):
+    data = rt.read_trace(GOLDEN / "routing_trace_prefill.jsonl")
+    doc = json.loads((GOLDEN / "routing_trace_prefill_summary.json").read_text())
+    edit(doc)                                   # request 3 (test-b) observes part of its prompt at layer 3
+    path = tmp_path / "s.json"
+    path.write_text(json.dumps(doc))
+    with pytest.raises(ValueError, match=match):
+        rt.read_prefill(path, data)
+
+
+def test_seeded_replay_rejections(rt, vb):
+    data = rt.read_trace(GOLDEN / "routing_trace_prefill.jsonl")
+    prefill = rt.read_prefill(GOLDEN / "routing_trace_prefill_summary.json", data)
+    baseline = rt.read_baseline_plan(GOLDEN / "routing_trace_prefill_plan.txt", data)
+    big = {(l, e) for l in range(4) for e in range(16)}
+    events = [e for e in data.events if e.request == "test-a"]
+    params = vb.ResidencyParams(rt.RESIDENCY_POLICIES.index("cost_aware"), 0, 3, 64, 0, 64.0, 50.0, 0.0, 0.0, 0,
+                                data.metadata["static_device_expert_bytes"])
+    capacity = 12 * 13_253_760
+    with pytest.raises(vb.VbmError, match="exceeds the cache capacity"):
+        rt._seed_replay(data, events, big, baseline, capacity, params, True)
+    params.policy = rt.RESIDENCY_POLICIES.index("belady_hits")
+    with pytest.raises(vb.VbmError, match="lru, lfu or cost_aware"):
+        rt._seed_replay(data, events, baseline, baseline, capacity, params, True)
+    # frozen from the baseline: hits are exactly the routed experts inside the plan
+    params.policy = rt.RESIDENCY_POLICIES.index("cost_aware")
+    got = rt._seed_replay(data, events, baseline, baseline, capacity, params, False)
+    hits = sum(k in baseline for e in events for k in e.keys())
+    assert got["hit_fraction"] == hits / sum(len(e.experts) for e in events)
+    assert got["decode_admission_bytes"] == 0 and got["evictions"] == 0 and got["seed_change_upload_bytes"] == 0
+    assert rt.read_prefill(GOLDEN / "routing_trace_prefill_summary.json", data).keys() == prefill.keys()

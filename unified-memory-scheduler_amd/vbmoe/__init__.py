@@ -78,6 +78,7 @@ class ResidencyParams(C.Structure):
         ("policy", C.c_int), ("capacity_bytes", u64), ("admit_after", C.c_int), ("payback_tokens", i64),
         ("cold_cache", C.c_int), ("ram_gbps", C.c_double), ("pcie_gbps", C.c_double), ("gpu_expert_us", C.c_double),
         ("layer_sync_us", C.c_double), ("staging_ram_passes", C.c_int), ("static_device_expert_bytes", u64),
+        ("seed_layer", vp), ("seed_expert", vp), ("n_seed", i64), ("seeded", C.c_int), ("frozen", C.c_int),
     ]
 
 
@@ -173,6 +174,8 @@ SIGNATURES = {
     "vbm_tier_load_gguf": [vp, vp, vp, vp],
     "vbm_residency_replay": [C.POINTER(ResidencyLayer), i64, vp, vp, vp, vp, i64, C.POINTER(ResidencyParams),
                              C.POINTER(ResidencyTotals)],
+    "vbm_residency_latency": [C.POINTER(ResidencyParams), C.c_double, C.c_double, C.c_double, C.POINTER(C.c_double),
+                              C.POINTER(C.c_double), C.POINTER(C.c_double)],
     "vbm_host_call_prepare": [C.POINTER(HostCall), C.c_int],
     "vbm_host_call_enqueue": [C.POINTER(HostCall), vp, vp, C.c_int, vp, sz, vp, i64, C.c_int, vp],
     "vbm_host_join": [C.POINTER(HostCall), vp, vp, vp, i64, vp],
