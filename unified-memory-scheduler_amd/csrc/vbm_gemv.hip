@@ -558,10 +558,84 @@ __device__ __forceinline__ void glu_requant_block(const float * vals, int lane, 
     }
 }
 
+// One chunk of mcount <= M tokens of the workgroup's tile pair: stage the activation rows in LDS,
+// stream every lane's row slice once applying each token, reduce the eight slices per token and
+// write the outputs (or the GLU block). M is the narrowest token width holding the chunk.
+template <int TYPE, int M>
+__device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane & B, const __attribute__((address_space(4))) int32_t * jobs,
+                                           int expert, int c0, int mcount, int k, int lane, int r, int tile, bool live,
+                                           uint8_t * lds_tok, float * red, float * vals, int * s_flag) {
+    const Shape S = A.shape;
+    const int nb = S.nb;
+    const int copy_bytes = static_cast<int>(A.lay.flag_offset());        // codes + scales of a row
+    const int tok_bytes = (copy_bytes + 15) & ~15;
+    const uint8_t * la = lds_tok + static_cast<int64_t>(k) * nb * A.lay.code_entry();
+    const float * lda = reinterpret_cast<const float *>(lds_tok + A.lay.da_offset());
+    constexpr int D = M == 1 ? 6 : kBatchDepth;
+    Group ring[D];
+    preload_ring_buf<TYPE, D>(ring, B, nb);
+    // Stage the chunk's activation rows (and their -128 flags) in LDS.
+    if (threadIdx.x == 0) *s_flag = 0;
+    __syncthreads();
+    int flag = 0;
+    for (int mi = 0; mi < mcount; ++mi) {
+        const int64_t j = jobs[c0 + mi];
+        const int64_t row = A.b_ne1 == 1 ? j / A.n_ids : j;
+        const uint8_t * xr = A.xrows + row * A.lay.stride();
+        uint8_t * dst = lds_tok + mi * tok_bytes;
+        for (int i = threadIdx.x; i * 16 < copy_bytes - 15; i += kThreads)
+            *reinterpret_cast<u32x4 *>(dst + i * 16) = *reinterpret_cast<const u32x4 *>(xr + i * 16);
+        for (int i = (copy_bytes & ~15) + threadIdx.x * 4; i < copy_bytes; i += kThreads * 4)
+            *reinterpret_cast<unsigned *>(dst + i) = *reinterpret_cast<const unsigned *>(xr + i);
+        if (threadIdx.x == 0) flag |= *reinterpret_cast<const int *>(xr + A.lay.flag_offset());
+    }
+    if (threadIdx.x == 0 && flag) *s_flag = 1;
+    __syncthreads();
+    float acc[M][2];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.0f;
+    // widths 1 and 2 only ever carry full chunks: a constant count drops the per-token checks
+    const int mc = M <= 2 ? M : mcount;
+    Tail tl;
+    if (*s_flag) {
+        stream_groups_buf<TYPE, M, true, D>(ring, B, nb, la, lda, tok_bytes, mc, acc);
+        preload_tail_buf<TYPE>(tl, B, nb);
+        apply_tail<TYPE, M, true, false>(tl, nullptr, r, nb, la, lda, tok_bytes, mc, acc);
+    } else {
+        stream_groups_buf<TYPE, M, false, D>(ring, B, nb, la, lda, tok_bytes, mc, acc);
+        preload_tail_buf<TYPE>(tl, B, nb);
+        apply_tail<TYPE, M, false, false>(tl, nullptr, r, nb, la, lda, tok_bytes, mc, acc);
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) red[(m * 8 + k) * 64 + lane] = acc[m][0] + acc[m][1];
+    __syncthreads();
+    for (int mi = k; mi < mcount; mi += 8) {                           // wave k reduces tokens k, k+8, ...
+        if (live) {
+            float v = lane_tree(&red[mi * 8 * 64 + lane]);
+            const int grow = static_cast<int>(ggml_row(static_cast<int64_t>(tile) * 32 + r, S.rows, S.interleave));
+            if (A.bias) v = v + A.bias[static_cast<size_t>(expert) * S.rows + grow];
+            if (A.epilogue == 0) A.dst[static_cast<size_t>(jobs[c0 + mi]) * S.rows + grow] = v;
+            else vals[mi * 64 + lane] = v;
+        }
+    }
+    if (A.epilogue == 1) {
+        __syncthreads();
+        for (int mi = k; mi < mcount; mi += 8)
+            if (lane < 32)
+                glu_requant_block(vals + mi * 64, lane, blockIdx.x, A.dst_xrows + static_cast<size_t>(jobs[c0 + mi]) * A.dst_lay.stride(),
+                                  A.dst_lay, A.activation, A.alpha, A.limit);
+    }
+    __syncthreads();
+}
+
+// Batched GEMV: one workgroup per (tile pair, active expert); the expert's jobs go through in
+// chunks of up to MT tokens, each chunk with the narrowest token width in {1, 2, 4, 8} that
+// holds it (a uniform branch: most experts of a small decode batch see one or two tokens, and a
+// narrow width keeps the per-block token loop short).
 template <int TYPE, int MT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void expert_gemv_kernel(KernelArgs A) {
-    __shared__ float red[MT][8][64];
-    __shared__ float vals[MT][64];
+    __shared__ float red[MT * 8 * 64];
+    __shared__ float vals[MT * 64];
     __shared__ int s_flag;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_tok[];   // MT activation rows
     // Per-expert metadata is read through the constant address space so it stays scalar.
@@ -574,74 +648,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     if (slot < 0 || slot >= A.shape.n_slots || count <= 0) return;
 
     const Shape S = A.shape;
-    const int nb = S.nb;
     const int k = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // lane slice, wave-uniform
     const int lane = threadIdx.x & 63;
     const int r = lane & 31;
     const int tile = blockIdx.x * 2 + (lane >> 5);
     const bool live = tile * 32 < S.rows;                              // the last tile pair may be half
     const uint8_t * slot_base = A.bank + static_cast<size_t>(slot) * S.slot_bytes;
-    const BufLane B = buf_lane<TYPE>(slot_base, S.slot_bytes, S.codes_bytes, live ? tile : 0, k, r, nb);
-    const int copy_bytes = static_cast<int>(A.lay.flag_offset());        // codes + scales of a row
-    const int tok_bytes = (copy_bytes + 15) & ~15;
-    const uint8_t * la = lds_tok + static_cast<int64_t>(k) * nb * A.lay.code_entry();
-    const float * lda = reinterpret_cast<const float *>(lds_tok + A.lay.da_offset());
-
-    constexpr int D = kBatchDepth;
+    const BufLane B = buf_lane<TYPE>(slot_base, S.slot_bytes, S.codes_bytes, live ? tile : 0, k, r, S.nb);
     for (int c0 = 0; c0 < count; c0 += MT) {
         const int mcount = count - c0 < MT ? count - c0 : MT;
-        Group ring[D];
-        preload_ring_buf<TYPE, D>(ring, B, nb);
-        // Stage the chunk's activation rows (and their -128 flags) in LDS.
-        if (threadIdx.x == 0) s_flag = 0;
-        __syncthreads();
-        int flag = 0;
-        for (int mi = 0; mi < mcount; ++mi) {
-            const int64_t j = jobs[c0 + mi];
-            const int64_t row = A.b_ne1 == 1 ? j / A.n_ids : j;
-            const uint8_t * xr = A.xrows + row * A.lay.stride();
-            uint8_t * dst = lds_tok + mi * tok_bytes;
-            for (int i = threadIdx.x; i * 16 < copy_bytes - 15; i += kThreads)
-                *reinterpret_cast<u32x4 *>(dst + i * 16) = *reinterpret_cast<const u32x4 *>(xr + i * 16);
-            for (int i = (copy_bytes & ~15) + threadIdx.x * 4; i < copy_bytes; i += kThreads * 4)
-                *reinterpret_cast<unsigned *>(dst + i) = *reinterpret_cast<const unsigned *>(xr + i);
-            if (threadIdx.x == 0) flag |= *reinterpret_cast<const int *>(xr + A.lay.flag_offset());
-        }
-        if (threadIdx.x == 0 && flag) s_flag = 1;
-        __syncthreads();
-        float acc[MT][2];
-#pragma unroll
-        for (int m = 0; m < MT; ++m) acc[m][0] = acc[m][1] = 0.0f;
-        Tail tl;
-        if (s_flag) {
-            stream_groups_buf<TYPE, MT, true, D>(ring, B, nb, la, lda, tok_bytes, mcount, acc);
-            preload_tail_buf<TYPE>(tl, B, nb);
-            apply_tail<TYPE, MT, true, false>(tl, nullptr, r, nb, la, lda, tok_bytes, mcount, acc);
-        } else {
-            stream_groups_buf<TYPE, MT, false, D>(ring, B, nb, la, lda, tok_bytes, mcount, acc);
-            preload_tail_buf<TYPE>(tl, B, nb);
-            apply_tail<TYPE, MT, false, false>(tl, nullptr, r, nb, la, lda, tok_bytes, mcount, acc);
-        }
-#pragma unroll
-        for (int m = 0; m < MT; ++m) red[m][k][lane] = acc[m][0] + acc[m][1];
-        __syncthreads();
-        for (int mi = k; mi < mcount; mi += 8) {                       // wave k reduces tokens k, k+8, ...
-            if (live) {
-                float v = lane_tree(&red[mi][0][lane]);
-                const int grow = static_cast<int>(ggml_row(static_cast<int64_t>(tile) * 32 + r, S.rows, S.interleave));
-                if (A.bias) v = v + A.bias[static_cast<size_t>(expert) * S.rows + grow];
-                if (A.epilogue == 0) A.dst[static_cast<size_t>(jobs[c0 + mi]) * S.rows + grow] = v;
-                else vals[mi][lane] = v;
-            }
-        }
-        if (A.epilogue == 1) {
-            __syncthreads();
-            for (int mi = k; mi < mcount; mi += 8)
-                if (lane < 32)
-                    glu_requant_block(vals[mi], lane, blockIdx.x, A.dst_xrows + static_cast<size_t>(jobs[c0 + mi]) * A.dst_lay.stride(),
-                                      A.dst_lay, A.activation, A.alpha, A.limit);
-        }
-        __syncthreads();
+        if (MT >= 8 && mcount > 4)
+            gemv_chunk<TYPE, (MT >= 8 ? 8 : 1)>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
+        else if (MT >= 4 && mcount > 2)
+            gemv_chunk<TYPE, (MT >= 4 ? 4 : 1)>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
+        else if (MT >= 2 && mcount > 1)
+            gemv_chunk<TYPE, (MT >= 2 ? 2 : 1)>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
+        else
+            gemv_chunk<TYPE, 1>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
     }
 }
 
