@@ -129,3 +129,22 @@ def test_prefill_layer_mxfp4_config1_shape(gpu, orc):
     print(f"[prefill config1 T={T}] max_rel={max_rel:.3e} cos={cos:.9f}", flush=True)
     assert max_rel <= 1e-3 and cos >= 0.99999
     layer.destroy()
+
+
+@pytest.mark.parametrize("experts,tokens", [(128, 32), (32, 24)])
+def test_fast_order_small_groups_take_the_exact_gemv(gpu, orc, experts, tokens):
+    """Below 5 routed rows per expert on average a fast-order call runs the exact-order GEMV (the
+    GEMM would pad most of its tiles): the layer output is bit-identical to the exact order's and
+    to the oracle's."""
+    assert tokens * 4 < 5 * experts and tokens >= 16
+    fast = Layer(gpu, H.MX, 2880, 2880, experts, 4, seed=91, router=False, order=gpu.ORDER_FAST)
+    x = gpu.synth_normal(91, 6, 0, tokens * 2880).reshape(tokens, 2880)
+    logits = gpu.synth_normal(91, 7, 0, tokens * experts).reshape(tokens, experts)
+    out, ids, _ = fast.forward_gpu(x, logits)
+    fast.order = gpu.ORDER_EXACT
+    exact, ids_e, _ = fast.forward_gpu(x, logits)
+    ref = fast.forward_cpu(orc, x, logits)
+    assert np.array_equal(ids, ids_e) and np.array_equal(ids, ref["ids"])
+    assert np.array_equal(out.view(np.uint32), exact.view(np.uint32))
+    assert np.array_equal(out.view(np.uint32), ref["out"].view(np.uint32)), H.diff_report(out, ref["out"])
+    fast.destroy()

@@ -197,7 +197,13 @@ struct LayerWorkspace {
     size_t total;
 };
 constexpr int64_t kGemmMinTokens = 16;
+// Below 5 routed rows per expert on average the exact-order batched GEMV outruns the MFMA
+// grouped GEMM (measured crossover between 4 and 6 rows at 32 and 128 experts, top-4).
+constexpr int64_t kGemmMinRowsPerExpert = 5;
 bool use_gemm(const vbm_moe_layer_desc & d, int64_t n_tokens);
+inline bool gemm_pays(int64_t n_tokens, int64_t top_k, int64_t n_expert) {
+    return n_tokens >= kGemmMinTokens && n_tokens * top_k >= kGemmMinRowsPerExpert * n_expert;
+}
 LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint8_t * base);
 // Prefill through the grouped GEMM in steps: the input rows and the token->expert grouping once,
 // then one or more passes over disjoint expert subsets (experts whose expert_to_slot entry is

@@ -56,8 +56,10 @@ void validate_ids_on_host(const int32_t * ids, int64_t n_ids, int64_t n_tokens, 
 
 namespace vbm {
 
-// Layers of at least kGemmMinTokens tokens use the MFMA grouped GEMM when the caller asks for the
-// fast accumulation order; below it the exact GEMV path is used (its results satisfy either order).
+// Layers of at least kGemmMinTokens tokens in the fast accumulation order may run the MFMA
+// grouped GEMM: their workspace holds either path's layout. The forward takes the GEMM when it
+// pays (gemm_pays: enough routed rows per expert), else the exact GEMV path, whose results
+// satisfy either order.
 bool use_gemm(const vbm_moe_layer_desc & d, int64_t n_tokens) {
     return d.order == VBM_ORDER_FAST && n_tokens >= kGemmMinTokens;
 }
@@ -76,9 +78,9 @@ LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint
     const GemmRowLayout gx{d.hidden / 32, type};
     const GemmRowLayout ga{d.intermediate / 32, type};
     const bool gemm = use_gemm(d, max_tokens);
-    w.xrows_x = take(static_cast<size_t>(max_tokens * (gemm ? gx.stride() : lx.stride())));
+    w.xrows_x = take(static_cast<size_t>(max_tokens * (gemm ? std::max(gx.stride(), lx.stride()) : lx.stride())));
     w.group = take(group_workspace_bytes(d.n_expert, entries));
-    w.xrows_act = take(static_cast<size_t>(entries * (gemm ? ga.stride() : la.stride())));
+    w.xrows_act = take(static_cast<size_t>(entries * (gemm ? std::max(ga.stride(), la.stride()) : la.stride())));
     w.tiles = gemm ? take(gemm_tiles_bytes(d.n_expert, entries)) : nullptr;
     w.y = reinterpret_cast<float *>(take(sizeof(float) * entries * d.hidden));
     w.total = off;
@@ -179,7 +181,7 @@ void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits
     float * logits_d = logits ? logits : w.logits;
     launch_router(d->router_w, d->router_b, x, H, logits_d, d->n_expert, n_tokens, K, ids_d, w_d, s);
     const GroupBuffers g = carve_group(w.group, d->n_expert, entries);
-    if (use_gemm(*d, n_tokens)) {
+    if (use_gemm(*d, n_tokens) && gemm_pays(n_tokens, K, d->n_expert)) {
         // Prefill-sized groups: MFMA grouped GEMM (exact block dots, fp32 accumulation order).
         prefill_prepare(*d, x, ids_d, n_tokens, w, s);
         prefill_pass(*d, d->expert_to_slot, n_tokens, w, events, s);
@@ -272,7 +274,7 @@ vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot,
         if (expert_to_slot_host) validate_ids_on_host(ids, n_ids, n_tokens, ids_stride, n_as, expert_to_slot_host, s);
         const int64_t entries = n_ids * n_tokens;
         const int64_t n_b = b_ne1 * n_tokens;
-        if (order == VBM_ORDER_FAST && n_tokens >= kGemmMinTokens) {
+        if (order == VBM_ORDER_FAST && gemm_pays(n_tokens, n_ids, n_as)) {
             const GemmRowLayout gl{bank->nb, bank->type};
             const size_t q_bytes = align_up(static_cast<size_t>(n_b * gl.stride()));
             const size_t g_bytes = align_up(group_workspace_bytes(n_as, entries));
