@@ -248,8 +248,10 @@ int orc_gemv_mxfp4x8_q8_0(int n, float * out, const void * vpacked, const void *
 /* ------------------------------------------------------------------ Q8_0 x Q8_0 */
 /* Integer part of ggml_vec_dot_q8_0_q8_0 on x86 (mul_sum_i8_pairs: |x| times VPSIGNB(y, x),
  * pairwise maddubs then madd, i.e. lane l = elements 4l..4l+3; no saturation is reachable since
- * |x| <= 128). The reference does not restate this function (a9, parity unpinned for the fp32
- * order); its call sites are tools/engine/native_cpu.cpp:100-102 (vec_dot through type_traits). */
+ * |x| <= 128). The reference does not restate this function; its call sites are
+ * tools/engine/native_cpu.cpp:100-102 (vec_dot through type_traits). Its fp32 order is pinned
+ * against the reference's compiled MXFP4 restatement on inputs where both are the same
+ * arithmetic (tests/test_oracle.py). */
 int32_t orc_q8_block_lanes(const void * vx, const void * vy, int32_t lanes[8]) {
     const int8_t * x = (const int8_t *)((const uint8_t *)vx + 2);
     const int8_t * y = (const int8_t *)((const uint8_t *)vy + 2);
@@ -268,8 +270,8 @@ int32_t orc_q8_block_lanes(const void * vx, const void * vy, int32_t lanes[8]) {
     return total;
 }
 
-/* AVX2 ggml_vec_dot_q8_0_q8_0: acc = fma(fp16(dx)*fp16(dy), float(lanes), acc) per block, then
- * the same hsum8 tree. Parity unpinned (order taken from upstream ggml x86, not vendored). */
+/* AVX2 ggml_vec_dot_q8_0_q8_0 (upstream ggml x86, not vendored): acc = fma(fp16(dx)*fp16(dy),
+ * float(lanes), acc) per block, then the same hsum8 tree as the MXFP4 dot. */
 float orc_vec_dot_q8_0_q8_0(int n, const void * vx, const void * vy) {
     const uint8_t * x = (const uint8_t *)vx;
     const uint8_t * y = (const uint8_t *)vy;
@@ -288,8 +290,9 @@ float orc_vec_dot_q8_0_q8_0(int n, const void * vx, const void * vy) {
 /* ------------------------------------------------------------------ f32 dot */
 /* ggml_vec_dot_f32 with GGML_SIMD on AVX2: four 8-wide accumulators over 32-element steps
  * (sum[j] = fma(x, y, sum[j])), reduce sum0+=sum2, sum1+=sum3, sum0+=sum1, then
- * (lo128 + hi128) and two horizontal adds; scalar tail. Parity unpinned (upstream, not vendored;
- * the router logits of the reference are computed by upstream build_lora_mm, HP:1357-1385). */
+ * (lo128 + hi128) and two horizontal adds; scalar tail (upstream ggml, not vendored; the router
+ * logits of the reference are computed by upstream build_lora_mm, HP:1357-1385). Pinned by
+ * hand-derived reduction-order probes for n % 32 == 0; the tail's accumulation width is not. */
 float orc_vec_dot_f32(int n, const float * x, const float * y) {
     float sum[4][8];
     memset(sum, 0, sizeof(sum));

@@ -222,6 +222,70 @@ def test_q8_block_lanes_brute_force(orc):
         assert total == prod.sum()
 
 
+@pytest.mark.skipif(not cpu_has_avx512vnni(), reason="oracle/_ref VNNI restatement needs AVX512VL+VNNI")
+def test_q8_0_dot_order_equals_reference_mxfp4_restatement(orc):
+    """The Q8_0 x Q8_0 dot's fp32 order (per-lane FMA chain over blocks, then hsum8) against the
+    reference's compiled MXFP4 restatement (cpu_mxfp4_vnni.cpp:49-68): Q8_0 weights that hold the
+    doubled e2m1 integers of an MXFP4 block with scale 2^(e-128) (an exact fp16), and zero weights
+    in the odd blocks (so the MXFP4 odd chain adds exact zeros), make both dots the same
+    arithmetic, so the results must agree bit for bit."""
+    if not orc.REF_VNNI.exists():
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    ref = C.CDLL(str(orc.REF_VNNI))
+    fn = ref.ggml_vec_dot_mxfp4_q8_0
+    fn.argtypes = [C.c_int, C.POINTER(C.c_float), C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t, C.c_int]
+    fn.restype = None
+    lib = orc.load()
+    rng = np.random.default_rng(2880)
+    for n in (64, 640, 2880):
+        for _ in range(40):
+            mx, q8, act = b"", b"", b""
+            for b in range(n // 32):
+                e = int(rng.integers(114, 144)) if b % 2 == 0 else int(rng.integers(0, 256))
+                qs = rng.integers(0, 256, 16).astype(np.uint8) if b % 2 == 0 else np.zeros(16, np.uint8)
+                blk = bytes([e]) + qs.tobytes()
+                mx += blk
+                d = np.float16(math.ldexp(1.0, e - 128)) if b % 2 == 0 else np.float16(1.0)
+                q8 += d.tobytes() + mx_values(blk).astype(np.int8).tobytes()
+                da = np.float16(rng.uniform(1e-3, 1e-1))
+                act += da.tobytes() + rng.integers(-127, 128, 32).astype(np.int8).tobytes()
+            out = C.c_float()
+            fn(n, C.byref(out), 0, C.create_string_buffer(mx), 0, C.create_string_buffer(act), 0, 1)
+            mine = lib.orc_vec_dot_q8_0_q8_0(n, q8, act)
+            assert struct.pack("<f", mine) == struct.pack("<f", out.value), n
+
+
+@pytest.mark.parametrize("y_entries,expected,ruled_out", [
+    # accumulators reduce as (s0 + s2) + (s1 + s3): big + (-big) first, then + 1
+    ({0: 2.0 ** 25, 8: 1.0, 16: -(2.0 ** 25)}, 1.0, "sequential"),
+    # the 4-wide horizontal adds: (t0 + t1) + (t2 + t3), each pair rounding 2^25 + 1 to 2^25
+    ({0: 2.0 ** 25, 1: 1.0, 2: -(2.0 ** 25), 3: 1.0}, 0.0, "sequential"),
+    # the 256-bit fold lo + hi comes first: (2^25 + 1) rounds before -2^25 joins
+    ({0: 2.0 ** 25, 4: 1.0, 1: -(2.0 ** 25)}, 0.0, "sequential"),
+    # one fp32 FMA chain per lane across 32-element steps (no wider accumulator)
+    ({0: 2.0 ** 25, 32: 1.0, 64: -(2.0 ** 25)}, 0.0, "exact"),
+])
+def test_f32_dot_reduction_order_probes(orc, y_entries, expected, ruled_out):
+    """ggml_vec_dot_f32 with GGML_SIMD on AVX2 (upstream ggml, not vendored: four 8-wide FMA
+    accumulators, GGML_F32x8_REDUCE, then (lo128 + hi128) and two hadds): each probe's answer,
+    derived by hand from that order, differs from a sequential fp32 sum or from the exact sum
+    (2^25 has an fp32 spacing of 4)."""
+    n = 96
+    x = np.ones(n, np.float32)
+    y = np.zeros(n, np.float32)
+    for i, v in y_entries.items():
+        y[i] = v
+    got = orc.load().orc_vec_dot_f32(n, x.ctypes.data, y.ctypes.data)
+    assert got == expected
+    if ruled_out == "sequential":
+        seq = np.float32(0.0)
+        for v in y:
+            seq = np.float32(seq + v)
+        assert seq != expected
+    else:
+        assert float(np.sum(y.astype(np.float64))) != expected
+
+
 def test_quantize_q8_0_closed_forms(orc):
     # q8-ties pattern of tools/trace/hybrid_layer.cpp:599-601: amax = 127 so codes are RNE(x).
     n = 32 * 6
