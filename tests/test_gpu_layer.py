@@ -102,3 +102,16 @@ def test_layer_q8_0_silu_given_logits(gpu, orc):
     logits = gpu.synth_normal(303, 7, 0, T * 128).reshape(T, 128)
     check(layer.forward_gpu(x, logits), layer.forward_cpu(orc, x, logits), "config3-shape T=16")
     layer.destroy()
+
+
+def test_layer_glu_epilogue_many_tokens_per_expert(gpu, orc):
+    """The fused gate_up GEMV's GLU + requantize epilogue over multi-chunk experts: 8 experts,
+    top-4, 40 tokens (20 jobs per expert on average: chunks of 8 and partial chunks), exact order."""
+    layer = Layer(gpu, H.MX, 1024, 512, 8, 4, seed=404)
+    T = 40
+    x = gpu.synth_normal(404, 6, 0, T * 1024).reshape(T, 1024)
+    out, ids, w = layer.forward_gpu(x)
+    ref = layer.forward_cpu(orc, x)
+    assert np.array_equal(ids, ref["ids"])
+    assert np.array_equal(out.view(np.uint32), ref["out"].view(np.uint32)), H.diff_report(out, ref["out"])
+    layer.destroy()

@@ -269,3 +269,25 @@ def test_combine_bitwise_and_order(gpu, orc):
     dy, dw, do = gpu.DeviceBuffer.from_array(probe), gpu.DeviceBuffer.from_array(np.ones((1, 3), np.float32)), gpu.DeviceBuffer(4)
     gpu.call("vbm_weighted_combine", dy.ptr, dw.ptr, 1, 3, 1, do.ptr, None)
     assert do.download(np.float32, 1)[0] == 1.0
+
+
+@pytest.mark.parametrize("type_id", [H.MX, H.Q8])
+def test_mul_mat_id_every_chunk_width_bitwise(gpu, orc, type_id):
+    """The batched GEMV runs each expert's jobs in chunks of up to 8 tokens at the narrowest width
+    in {1, 2, 4, 8} that holds the chunk: per-expert counts 1, 2, 3, 4, 5, 8, 9 and 17 reach every
+    width, partial chunks of widths 4 and 8 and several chunks per expert (top-1 ids, so each
+    count is exact), with biases, a half-live last tile pair (rows 96) and per-token activations."""
+    counts = [1, 2, 3, 4, 5, 8, 9, 17, 0]
+    experts, k, rows = len(counts), 512, 96
+    rng = np.random.default_rng(91)
+    ids = rng.permutation(np.repeat(np.arange(experts), counts)).astype(np.int32).reshape(-1, 1)
+    tokens = ids.shape[0]
+    w = H.synth_weights(type_id, 91, 1, experts, rows, k)
+    bank = H.make_bank(type_id, w, experts, rows, k)
+    bias = gpu.synth_normal(91, 2, 0, experts * rows, 0.0, 0.02)
+    x = gpu.synth_normal(91, 3, 0, tokens * k).reshape(tokens, 1, k)
+    print(f"[chunk widths type={type_id}] tokens={tokens} counts={counts}", flush=True)
+    got = H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, ids, 1, bias=bias)
+    ref = orc.mul_mat_id(type_id, w, k, rows, experts, 0, x, 1, ids, 1, tokens, 1, bias=bias)
+    assert H.bits_equal(got, ref), H.diff_report(got, ref)
+    bank.destroy()
