@@ -624,3 +624,35 @@ def test_seeded_replay_rejections(rt, vb):
     assert got["hit_fraction"] == hits / sum(len(e.experts) for e in events)
     assert got["decode_admission_bytes"] == 0 and got["evictions"] == 0 and got["seed_change_upload_bytes"] == 0
     assert rt.read_prefill(GOLDEN / "routing_trace_prefill_summary.json", data).keys() == prefill.keys()
+
+
+def test_belady_hits_is_optimal_by_exhaustive_search(rt):
+    """belady_hits against an exhaustive oracle (as tests/test_routing_analysis.py:271-294 of the
+    reference does): over every sequence of end-of-layer cache states (each a subset of at most
+    `slots` keys of the previous state and the event's experts), the most hits any schedule gets
+    on a tiny trace must equal the replay's."""
+    from itertools import combinations
+    rng = np.random.default_rng(5)
+    size = 10
+    for trial in range(40):
+        experts, active, slots, n_events = 5, 2, 2 + trial % 2, 7
+        layers = {0: rt.Layer(experts, active, size, size)}
+        requests = {"t": rt.Request("t", "test", "c", n_events, 1, n_events, True)}
+        events = [rt.Event("t", i, 0, tuple(int(e) for e in rng.choice(experts, active, replace=False)))
+                  for i in range(n_events)]
+        data = rt.Dataset({"static_device_expert_bytes": 0}, layers, requests, events)
+        got = rt.replay_residency(data, "belady_hits", slots * size, 64.0, 50.0)
+        best = {frozenset(): 0}
+        for ev in events:
+            keys = set(ev.experts)
+            nxt = {}
+            for state, hits in best.items():
+                h = hits + len(keys & state)
+                pool = sorted(state | keys)
+                for m in range(0, min(slots, len(pool)) + 1):
+                    for sub in combinations(pool, m):
+                        s = frozenset(sub)
+                        if nxt.get(s, -1) < h:
+                            nxt[s] = h
+            best = nxt
+        assert got["full_expert_hits"] == max(best.values()), (trial, [e.experts for e in events])
