@@ -9,6 +9,11 @@
 //       bytes (experts of them), the jobs (int64 row, rank, expert each) and the packed Q8_0
 //       rows; <out> receives the jobs x hidden floats. Then checks that a job on a non-resident
 //       expert and a short input are rejected with std::invalid_argument.
+//   experts <gguf> <layer> <in> <out> <ids...>
+//       NativeHipExperts over the loaded experts; <in> holds int64 n_rows, int64 n_jobs, the fp32
+//       input rows and the jobs; <out> receives execute() (jobs x hidden), activations() (jobs x
+//       intermediate), pack_down(activations) bytes and execute_down(activations) (jobs x
+//       hidden). Prints the number of observed stages and checks two rejections.
 #include "native_hip_down.hpp"
 
 #include <cstdio>
@@ -53,6 +58,44 @@ int main(int argc, char ** argv) {
         std::vector<std::uint32_t> ids;
         for (int i = first_id; i < argc; ++i) ids.push_back(static_cast<std::uint32_t>(std::atoi(argv[i])));
         const LoadedExperts loaded = load_gguf_experts(argv[2], layer, ids, F32Activation::openai_swiglu);
+        if (mode == "experts") {
+            std::ifstream in(argv[4], std::ios::binary);
+            const int64_t n_rows = get(in), n_jobs = get(in);
+            std::vector<float> input(static_cast<std::size_t>(n_rows) * loaded.weights.hidden);
+            in.read(reinterpret_cast<char *>(input.data()), static_cast<std::streamsize>(input.size() * sizeof(float)));
+            std::vector<ExpertJob> jobs(static_cast<std::size_t>(n_jobs));
+            for (auto & j : jobs) {
+                j.row = static_cast<std::size_t>(get(in));
+                j.rank = static_cast<std::size_t>(get(in));
+                j.expert = static_cast<std::uint32_t>(get(in));
+            }
+            NativeHipExperts gpu(loaded);
+            std::size_t observed = 0;
+            F32Transforms obs;
+            obs.observe = [&](const ExpertJob &, F32Stage, const std::vector<float> &) { ++observed; };
+            const auto out = gpu.execute(input, jobs, obs);
+            const auto act = gpu.activations(input, jobs);
+            const auto packed = gpu.pack_down(act);
+            const auto down = gpu.execute_down(act, jobs);
+            std::ofstream f(argv[5], std::ios::binary);
+            f.write(reinterpret_cast<const char *>(out.data()), static_cast<std::streamsize>(out.size() * sizeof(float)));
+            f.write(reinterpret_cast<const char *>(act.data()), static_cast<std::streamsize>(act.size() * sizeof(float)));
+            f.write(reinterpret_cast<const char *>(packed.data()), static_cast<std::streamsize>(packed.size()));
+            f.write(reinterpret_cast<const char *>(down.data()), static_cast<std::streamsize>(down.size() * sizeof(float)));
+            int rejected = 0;
+            try {
+                (void)gpu.execute(input, {ExpertJob{static_cast<std::size_t>(n_rows), 0, 0}});
+            } catch (const std::invalid_argument &) {
+                ++rejected;
+            }
+            try {
+                (void)gpu.execute_down_packed(std::vector<std::uint8_t>(packed.size() - 1), jobs);
+            } catch (const std::invalid_argument &) {
+                ++rejected;
+            }
+            std::cout << "observed " << observed << " stages; rejected " << rejected << "\n";
+            return 0;
+        }
         if (mode == "load") {
             std::ofstream f(argv[4], std::ios::binary);
             put(f, static_cast<int64_t>(loaded.weights.hidden));

@@ -114,3 +114,52 @@ def test_mxfp4_native_hip_down_matches_oracle(gpu, orc, tmp_path):
     ref = orc.mul_mat_id(39, bank, I, H, len(IDS), vb.TYPE_Q8_0, q8, 1, local.astype(np.int32).reshape(n_jobs, 1), 1,
                          n_jobs, 1, bias=bias)
     assert np.array_equal(got.view(np.uint32), ref.reshape(n_jobs, H).view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_native_hip_experts_matches_oracle(gpu, orc, tmp_path):
+    """NativeHipExperts (native_cpu.hpp:11-30 on the GPU): execute, activations, pack_down and
+    execute_down for one input row per job, bit-identical to the oracle's composition of the same
+    steps (Q8_0 input, gate / up with biases, SwiGLU-OAI, Q8_0 requantization, down with bias)."""
+    assert DRIVER.exists(), "build the driver first (unified-memory-scheduler_amd/build_lib.py)"
+    path, a = model(tmp_path)
+    rng = np.random.default_rng(8)
+    n_rows, n_jobs = 3, 7
+    x = gpu.synth_normal(8, 1, 0, n_rows * H).reshape(n_rows, H)
+    local = rng.integers(0, len(IDS), n_jobs)
+    jobs = np.stack([rng.integers(0, n_rows, n_jobs), rng.integers(0, 4, n_jobs), local], axis=1).astype(np.int64)
+    inp = tmp_path / "xin.bin"
+    inp.write_bytes(struct.pack("<qq", n_rows, n_jobs) + x.astype(np.float32).tobytes() + jobs.tobytes())
+    out = tmp_path / "xout.bin"
+    print(f"[native experts] {n_jobs} jobs over rows {jobs[:, 0].tolist()} experts {local.tolist()}", flush=True)
+    r = subprocess.run([str(DRIVER), "experts", str(path), "3", str(inp), str(out), *map(str, IDS)], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert f"observed {4 * n_jobs} stages; rejected 2" in r.stdout
+    raw = out.read_bytes()
+    q_bytes = n_jobs * (I // 32) * 34
+    got_out = np.frombuffer(raw, np.float32, n_jobs * H, 0).reshape(n_jobs, H)
+    got_act = np.frombuffer(raw, np.float32, n_jobs * I, 4 * n_jobs * H).reshape(n_jobs, I)
+    got_q = np.frombuffer(raw, np.uint8, q_bytes, 4 * n_jobs * (H + I))
+    got_down = np.frombuffer(raw, np.float32, n_jobs * H, 4 * n_jobs * (H + I) + q_bytes).reshape(n_jobs, H)
+
+    def bank(part):
+        return np.concatenate([a[part][e] for e in IDS])
+
+    def bias(part):
+        return np.concatenate([a[part + "_bias"][e] for e in IDS])
+
+    rows = x[jobs[:, 0]].reshape(n_jobs, 1, H)
+    ids = local.astype(np.int32).reshape(n_jobs, 1)
+    g = orc.mul_mat_id(39, bank("gate"), H, I, len(IDS), 0, rows, 1, ids, 1, n_jobs, 1, bias=bias("gate")).reshape(n_jobs, I)
+    u = orc.mul_mat_id(39, bank("up"), H, I, len(IDS), 0, rows, 1, ids, 1, n_jobs, 1, bias=bias("up")).reshape(n_jobs, I)
+    act = np.empty_like(g)
+    orc.load().orc_glu(1, np.ascontiguousarray(g).ctypes.data, np.ascontiguousarray(u).ctypes.data, act.ctypes.data,
+                       g.size, 1.702, 7.0)
+    q = orc.quantize_q8_0(act)
+    down = orc.mul_mat_id(39, bank("down"), I, H, len(IDS), 8, q.reshape(n_jobs, 1, -1), 1, ids, 1, n_jobs, 1,
+                          bias=bias("down")).reshape(n_jobs, H)
+    assert np.array_equal(got_act.view(np.uint32), act.view(np.uint32))
+    assert np.array_equal(got_q, q.reshape(-1))
+    assert np.array_equal(got_out.view(np.uint32), down.view(np.uint32))
+    assert np.array_equal(got_down.view(np.uint32), down.view(np.uint32))

@@ -264,4 +264,255 @@ std::vector<float> Mxfp4NativeHipDown::execute(const std::vector<std::uint8_t> &
     return output;
 }
 
+// ---------------------------------------------------------------------------------------------
+// NativeHipExperts
+
+namespace {
+
+// One device allocation per call, released on every path.
+struct DeviceBuffers {
+    std::vector<void *> ptrs;
+    void * get(std::size_t bytes, const char * what) {
+        void * p = nullptr;
+        check(vbm_malloc(&p, bytes ? bytes : 4), what);
+        ptrs.push_back(p);
+        return p;
+    }
+    ~DeviceBuffers() {
+        for (void * p : ptrs) (void)vbm_free(p);
+    }
+};
+
+}  // namespace
+
+struct NativeHipExperts::Impl {
+    int device = 0;
+    std::size_t hidden = 0, intermediate = 0, experts = 0;
+    F32Activation activation = F32Activation::openai_swiglu;
+    vbm_bank * banks[3] = {nullptr, nullptr, nullptr};   // gate, up, down (slot = local expert)
+    void * bias[3] = {nullptr, nullptr, nullptr};        // device [experts][rows] or null
+    void * stream = nullptr;
+    mutable std::mutex mutex;
+
+    ~Impl() {
+        (void)vbm_set_device(device);
+        if (stream) {
+            (void)vbm_stream_synchronize(stream);
+            (void)vbm_stream_destroy(stream);
+        }
+        for (int i = 0; i < 3; ++i) {
+            if (bias[i]) (void)vbm_free(bias[i]);
+            if (banks[i]) (void)vbm_bank_destroy(banks[i]);
+        }
+    }
+
+    void validate_jobs(const std::vector<float> & input, const std::vector<ExpertJob> & jobs) const {
+        if (input.empty() || input.size() % hidden || jobs.size() > kMaxFloats / hidden ||
+            jobs.size() > kMaxFloats / intermediate || !all_finite(input))
+            throw std::invalid_argument("invalid native expert input");
+        for (const auto & job : jobs)
+            if (job.row >= input.size() / hidden || job.expert >= experts)
+                throw std::invalid_argument("invalid native expert route");
+    }
+
+    std::vector<int32_t> route_ids(const std::vector<ExpertJob> & jobs) const {
+        std::vector<int32_t> ids;
+        ids.reserve(jobs.size());
+        for (const auto & job : jobs) {
+            if (job.expert >= experts) throw std::invalid_argument("invalid native expert route");
+            ids.push_back(static_cast<int32_t>(job.expert));
+        }
+        return ids;
+    }
+
+    // gate / up (part 0 / 1) or down (2) of one activation row per job: b [n][k] of b_type
+    void project(int part, int b_type, const void * d_b, const void * d_ids, int64_t n, float * d_out) const {
+        check(vbm_mul_mat_id(banks[part], nullptr, nullptr, static_cast<int64_t>(experts), b_type, d_b, 1,
+                             static_cast<const int32_t *>(d_ids), 1, n, 1, static_cast<const float *>(bias[part]), d_out,
+                             VBM_ORDER_EXACT, stream),
+              part == 2 ? "native down" : "native gate / up");
+    }
+
+    // activation rows [n][intermediate] on the device from the jobs' input rows
+    void activate(const std::vector<float> & input, const std::vector<ExpertJob> & jobs, const F32Transforms & obs,
+                  DeviceBuffers & mem, const void * d_ids, float * d_act) const {
+        const int64_t n = static_cast<int64_t>(jobs.size());
+        std::vector<float> rows(jobs.size() * hidden);
+        for (std::size_t j = 0; j < jobs.size(); ++j)
+            std::copy_n(input.data() + jobs[j].row * hidden, hidden, rows.data() + j * hidden);
+        float * d_x = static_cast<float *>(mem.get(sizeof(float) * rows.size(), "native input"));
+        float * d_g = static_cast<float *>(mem.get(sizeof(float) * jobs.size() * intermediate, "native gate"));
+        float * d_u = static_cast<float *>(mem.get(sizeof(float) * jobs.size() * intermediate, "native up"));
+        check(vbm_memcpy_h2d(d_x, rows.data(), sizeof(float) * rows.size(), stream), "native input upload");
+        project(0, VBM_TYPE_F32, d_x, d_ids, n, d_g);
+        project(1, VBM_TYPE_F32, d_x, d_ids, n, d_u);
+        const int64_t I = static_cast<int64_t>(intermediate);
+        check(vbm_glu(activation == F32Activation::silu ? VBM_ACT_SILU : VBM_ACT_SWIGLU_OAI, d_g, d_u, d_act, n, I, I, I, I,
+                      1.702f, 7.0f, stream),
+              "native activation");
+        if (obs.observe) {                       // the observed stages come back to the host
+            std::vector<float> g(jobs.size() * intermediate), u(g.size()), a(g.size());
+            check(vbm_memcpy_d2h(g.data(), d_g, sizeof(float) * g.size(), stream), "gate download");
+            check(vbm_memcpy_d2h(u.data(), d_u, sizeof(float) * u.size(), stream), "up download");
+            check(vbm_memcpy_d2h(a.data(), d_act, sizeof(float) * a.size(), stream), "activation download");
+            check(vbm_stream_synchronize(stream), "native activation");
+            for (std::size_t j = 0; j < jobs.size(); ++j) {
+                std::vector<float> gj(g.begin() + j * intermediate, g.begin() + (j + 1) * intermediate);
+                std::vector<float> uj(u.begin() + j * intermediate, u.begin() + (j + 1) * intermediate);
+                std::vector<float> aj(a.begin() + j * intermediate, a.begin() + (j + 1) * intermediate);
+                obs.observe(jobs[j], F32Stage::gate, gj);
+                obs.observe(jobs[j], F32Stage::up, uj);
+                obs.observe(jobs[j], F32Stage::activation, aj);
+            }
+        }
+    }
+
+    std::vector<float> download(const float * d, std::size_t count, const char * what) const {
+        std::vector<float> out(count);
+        check(vbm_memcpy_d2h(out.data(), d, sizeof(float) * count, stream), what);
+        check(vbm_stream_synchronize(stream), what);
+        if (!all_finite(out)) throw std::runtime_error(std::string(what) + ": non-finite output");
+        return out;
+    }
+};
+
+NativeHipExperts::NativeHipExperts(const LoadedExperts & loaded, int device) : impl_(std::make_unique<Impl>()) {
+    loaded.weights.validate();
+    Impl & m = *impl_;
+    m.device = device;
+    m.hidden = loaded.weights.hidden;
+    m.intermediate = loaded.weights.intermediate;
+    m.experts = loaded.weights.experts;
+    m.activation = loaded.weights.activation;
+    if (device < 0 || m.hidden % 32 || m.intermediate % 32) throw std::invalid_argument("unsupported native GPU expert shape");
+    check(vbm_set_device(device), "GPU device selection");
+    check(vbm_stream_create(&m.stream), "GPU stream creation");
+    const std::vector<float> * biases[3] = {&loaded.weights.gate_bias, &loaded.weights.up_bias, &loaded.weights.down_bias};
+    for (int part = 0; part < 3; ++part) {
+        const int type = loaded.quant_types[part];
+        if (type != VBM_TYPE_MXFP4 && type != VBM_TYPE_Q8_0) throw std::invalid_argument("unsupported native dot format");
+        const std::size_t rows = part == 2 ? m.hidden : m.intermediate, k = part == 2 ? m.intermediate : m.hidden;
+        const std::size_t row_bytes = k / 32 * (type == VBM_TYPE_MXFP4 ? 17 : 34), stride = rows * row_bytes;
+        if (loaded.packed_weights[part].size() != stride * m.experts)
+            throw std::runtime_error("invalid native packed expert shape");
+        check(vbm_bank_create(type, static_cast<int64_t>(rows), static_cast<int64_t>(k), static_cast<int64_t>(m.experts), 0,
+                              &m.banks[part]), "native bank");
+        for (std::size_t e = 0; e < m.experts; ++e)
+            check(vbm_bank_upload(m.banks[part], static_cast<int64_t>(e), loaded.packed_weights[part].data() + e * stride, 0,
+                                  m.stream), "native expert upload");
+        if (!biases[part]->empty()) {
+            check(vbm_malloc(&m.bias[part], sizeof(float) * biases[part]->size()), "native bias");
+            check(vbm_memcpy_h2d(m.bias[part], biases[part]->data(), sizeof(float) * biases[part]->size(), m.stream),
+                  "native bias upload");
+        }
+    }
+    check(vbm_stream_synchronize(m.stream), "native expert upload");
+}
+
+NativeHipExperts::~NativeHipExperts() = default;
+
+std::vector<float> NativeHipExperts::activations(const std::vector<float> & input, const std::vector<ExpertJob> & jobs,
+                                                 const F32Transforms & observations) const {
+    const Impl & m = *impl_;
+    std::lock_guard<std::mutex> lock(m.mutex);
+    m.validate_jobs(input, jobs);
+    if (jobs.empty()) return {};
+    check(vbm_set_device(m.device), "GPU device selection");
+    DeviceBuffers mem;
+    const auto ids = m.route_ids(jobs);
+    void * d_ids = mem.get(sizeof(int32_t) * ids.size(), "route buffer");
+    float * d_act = static_cast<float *>(mem.get(sizeof(float) * jobs.size() * m.intermediate, "activations"));
+    try {
+        check(vbm_memcpy_h2d(d_ids, ids.data(), sizeof(int32_t) * ids.size(), m.stream), "route upload");
+        m.activate(input, jobs, observations, mem, d_ids, d_act);
+        return m.download(d_act, jobs.size() * m.intermediate, "native activations");
+    } catch (...) {
+        (void)vbm_stream_synchronize(m.stream);
+        throw;
+    }
+}
+
+std::vector<float> NativeHipExperts::execute(const std::vector<float> & input, const std::vector<ExpertJob> & jobs,
+                                             const F32Transforms & observations) const {
+    const Impl & m = *impl_;
+    std::lock_guard<std::mutex> lock(m.mutex);
+    m.validate_jobs(input, jobs);
+    if (jobs.empty()) return {};
+    check(vbm_set_device(m.device), "GPU device selection");
+    DeviceBuffers mem;
+    const auto ids = m.route_ids(jobs);
+    const int64_t n = static_cast<int64_t>(jobs.size());
+    void * d_ids = mem.get(sizeof(int32_t) * ids.size(), "route buffer");
+    float * d_act = static_cast<float *>(mem.get(sizeof(float) * jobs.size() * m.intermediate, "activations"));
+    void * d_q = mem.get(jobs.size() * (m.intermediate / 32) * 34, "packed activations");
+    float * d_out = static_cast<float *>(mem.get(sizeof(float) * jobs.size() * m.hidden, "output"));
+    try {
+        check(vbm_memcpy_h2d(d_ids, ids.data(), sizeof(int32_t) * ids.size(), m.stream), "route upload");
+        m.activate(input, jobs, observations, mem, d_ids, d_act);
+        const int64_t I = static_cast<int64_t>(m.intermediate);
+        check(vbm_quantize_q8_0(d_act, n, I, I, d_q, m.stream), "down input quantization");
+        m.project(2, VBM_TYPE_Q8_0, d_q, d_ids, n, d_out);
+        auto out = m.download(d_out, jobs.size() * m.hidden, "native experts");
+        if (observations.observe)
+            for (std::size_t j = 0; j < jobs.size(); ++j) {
+                std::vector<float> dj(out.begin() + j * m.hidden, out.begin() + (j + 1) * m.hidden);
+                observations.observe(jobs[j], F32Stage::down, dj);
+            }
+        return out;
+    } catch (...) {
+        (void)vbm_stream_synchronize(m.stream);
+        throw;
+    }
+}
+
+std::vector<std::uint8_t> NativeHipExperts::pack_down(const std::vector<float> & activations) const {
+    const Impl & m = *impl_;
+    std::lock_guard<std::mutex> lock(m.mutex);
+    if (activations.empty() || activations.size() % m.intermediate || activations.size() > kMaxFloats ||
+        !all_finite(activations))
+        throw std::invalid_argument("invalid native down activations");
+    const int64_t n = static_cast<int64_t>(activations.size() / m.intermediate), I = static_cast<int64_t>(m.intermediate);
+    check(vbm_set_device(m.device), "GPU device selection");
+    DeviceBuffers mem;
+    std::vector<std::uint8_t> packed(static_cast<std::size_t>(n) * (m.intermediate / 32) * 34);
+    void * d_a = mem.get(sizeof(float) * activations.size(), "activations");
+    void * d_q = mem.get(packed.size(), "packed activations");
+    check(vbm_memcpy_h2d(d_a, activations.data(), sizeof(float) * activations.size(), m.stream), "activation upload");
+    check(vbm_quantize_q8_0(static_cast<const float *>(d_a), n, I, I, d_q, m.stream), "down input quantization");
+    check(vbm_memcpy_d2h(packed.data(), d_q, packed.size(), m.stream), "packed download");
+    check(vbm_stream_synchronize(m.stream), "pack_down");
+    return packed;
+}
+
+std::vector<float> NativeHipExperts::execute_down_packed(const std::vector<std::uint8_t> & packed,
+                                                         const std::vector<ExpertJob> & jobs) const {
+    const Impl & m = *impl_;
+    std::lock_guard<std::mutex> lock(m.mutex);
+    const std::size_t row_bytes = m.intermediate / 32 * 34;
+    if (jobs.size() > kMaxFloats / m.hidden || packed.size() != jobs.size() * row_bytes)
+        throw std::invalid_argument("invalid packed native down input");
+    if (jobs.empty()) return {};
+    const auto ids = m.route_ids(jobs);
+    check(vbm_set_device(m.device), "GPU device selection");
+    DeviceBuffers mem;
+    void * d_ids = mem.get(sizeof(int32_t) * ids.size(), "route buffer");
+    void * d_q = mem.get(packed.size(), "packed activations");
+    float * d_out = static_cast<float *>(mem.get(sizeof(float) * jobs.size() * m.hidden, "output"));
+    try {
+        check(vbm_memcpy_h2d(d_ids, ids.data(), sizeof(int32_t) * ids.size(), m.stream), "route upload");
+        check(vbm_memcpy_h2d(d_q, packed.data(), packed.size(), m.stream), "packed upload");
+        m.project(2, VBM_TYPE_Q8_0, d_q, d_ids, static_cast<int64_t>(jobs.size()), d_out);
+        return m.download(d_out, jobs.size() * m.hidden, "native down");
+    } catch (...) {
+        (void)vbm_stream_synchronize(m.stream);
+        throw;
+    }
+}
+
+std::vector<float> NativeHipExperts::execute_down(const std::vector<float> & activations,
+                                                  const std::vector<ExpertJob> & jobs) const {
+    if (activations.size() != jobs.size() * impl_->intermediate) throw std::invalid_argument("invalid native down activations");
+    return execute_down_packed(pack_down(activations), jobs);
+}
+
 }  // namespace vrambridge::experimental

@@ -16,6 +16,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <filesystem>
+#include <functional>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -24,6 +25,7 @@
 namespace vrambridge::experimental {
 
 enum class F32Activation { silu, openai_swiglu };
+enum class F32Stage { gate, up, activation, down };
 
 // Dequantized expert weights of one layer (f32_experts.hpp:17-29): gate / up [experts][intermediate
 // rows][hidden], down [experts][hidden rows][intermediate]; biases empty or per expert.
@@ -40,6 +42,13 @@ struct F32ExpertWeights {
     std::vector<float> down_bias;
 
     void validate() const;
+};
+
+// f32_experts.hpp:29-33: observation hooks (only `observe` is honoured by the GPU executor).
+struct F32Transforms {
+    std::function<void(std::vector<float> &)> gate_up_input;
+    std::function<void(std::vector<float> &)> down_input;
+    std::function<void(const ExpertJob &, F32Stage, const std::vector<float> &)> observe;
 };
 
 // gguf_experts.hpp:14-20: packed_weights[i] holds the selected experts' ggml bytes of gate (0),
@@ -69,6 +78,33 @@ public:
     Mxfp4NativeHipDown & operator=(const Mxfp4NativeHipDown &) = delete;
 
     std::vector<float> execute(const std::vector<std::uint8_t> & packed_q8, const std::vector<ExpertJob> & jobs);
+
+private:
+    struct Impl;
+    std::unique_ptr<Impl> impl_;
+};
+
+// native_cpu.hpp:11-30 on the GPU: every loaded expert resident in three banks (gate, up,
+// down; MXFP4 or Q8_0), the reference engine's CPU executor contract for one input row per job:
+// Q8_0 quantization of the input, gate and up projections with biases, the activation, Q8_0
+// requantization and the down projection with bias, all in the CPU vec_dot order (bit-identical
+// dots). `activations` stops after the activation, `pack_down` quantizes activation rows to the
+// ggml Q8_0 bytes `execute_down_packed` consumes. The constructor takes a device index where the
+// reference's takes the CPU plugin path.
+class NativeHipExperts {
+public:
+    explicit NativeHipExperts(const LoadedExperts & weights, int device = 0);
+    ~NativeHipExperts();
+    NativeHipExperts(const NativeHipExperts &) = delete;
+    NativeHipExperts & operator=(const NativeHipExperts &) = delete;
+
+    std::vector<float> execute(const std::vector<float> & input, const std::vector<ExpertJob> & jobs,
+                               const F32Transforms & observations = {}) const;
+    std::vector<float> activations(const std::vector<float> & input, const std::vector<ExpertJob> & jobs,
+                                   const F32Transforms & observations = {}) const;
+    std::vector<float> execute_down(const std::vector<float> & activations, const std::vector<ExpertJob> & jobs) const;
+    std::vector<std::uint8_t> pack_down(const std::vector<float> & activations) const;
+    std::vector<float> execute_down_packed(const std::vector<std::uint8_t> & packed, const std::vector<ExpertJob> & jobs) const;
 
 private:
     struct Impl;
