@@ -561,7 +561,7 @@ __device__ __forceinline__ void glu_requant_block(const float * vals, int lane, 
 // One chunk of mcount <= M tokens of the workgroup's tile pair: stage the activation rows in LDS,
 // stream every lane's row slice once applying each token, reduce the eight slices per token and
 // write the outputs (or the GLU block). M is the narrowest token width holding the chunk.
-template <int TYPE, int M>
+template <int TYPE, int M, bool NEG>
 __device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane & B, const __attribute__((address_space(4))) int32_t * jobs,
                                            int expert, int c0, int mcount, int k, int lane, int r, int tile, bool live,
                                            uint8_t * lds_tok, float * red, float * vals, int * s_flag) {
@@ -571,7 +571,8 @@ __device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane &
     const int tok_bytes = (copy_bytes + 15) & ~15;
     const uint8_t * la = lds_tok + static_cast<int64_t>(k) * nb * A.lay.code_entry();
     const float * lda = reinterpret_cast<const float *>(lds_tok + A.lay.da_offset());
-    constexpr int D = M == 1 ? 6 : kBatchDepth;
+    // rings without the -128 slow path can be deeper within the same registers
+    constexpr int D = NEG ? (M == 1 ? 6 : kBatchDepth) : (M == 1 ? 8 : 6);
     Group ring[D];
     preload_ring_buf<TYPE, D>(ring, B, nb);
     // Stage the chunk's activation rows (and their -128 flags) in LDS.
@@ -597,7 +598,7 @@ __device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane &
     // widths 1 and 2 only ever carry full chunks: a constant count drops the per-token checks
     const int mc = M <= 2 ? M : mcount;
     Tail tl;
-    if (*s_flag) {
+    if (NEG && *s_flag) {
         stream_groups_buf<TYPE, M, true, D>(ring, B, nb, la, lda, tok_bytes, mc, acc);
         preload_tail_buf<TYPE>(tl, B, nb);
         apply_tail<TYPE, M, true, false>(tl, nullptr, r, nb, la, lda, tok_bytes, mc, acc);
@@ -632,7 +633,7 @@ __device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane &
 // chunks of up to MT tokens, each chunk with the narrowest token width in {1, 2, 4, 8} that
 // holds it (a uniform branch: most experts of a small decode batch see one or two tokens, and a
 // narrow width keeps the per-block token loop short).
-template <int TYPE, int MT>
+template <int TYPE, int MT, bool NEG>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void expert_gemv_kernel(KernelArgs A) {
     __shared__ float red[MT * 8 * 64];
     __shared__ float vals[MT * 64];
@@ -658,13 +659,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     for (int c0 = 0; c0 < count; c0 += MT) {
         const int mcount = count - c0 < MT ? count - c0 : MT;
         if (MT >= 8 && mcount > 4)
-            gemv_chunk<TYPE, (MT >= 8 ? 8 : 1)>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
+            gemv_chunk<TYPE, (MT >= 8 ? 8 : 1), NEG>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
         else if (MT >= 4 && mcount > 2)
-            gemv_chunk<TYPE, (MT >= 4 ? 4 : 1)>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
+            gemv_chunk<TYPE, (MT >= 4 ? 4 : 1), NEG>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
         else if (MT >= 2 && mcount > 1)
-            gemv_chunk<TYPE, (MT >= 2 ? 2 : 1)>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
+            gemv_chunk<TYPE, (MT >= 2 ? 2 : 1), NEG>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
         else
-            gemv_chunk<TYPE, 1>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
+            gemv_chunk<TYPE, 1, NEG>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
     }
 }
 
@@ -1150,20 +1151,20 @@ __global__ __launch_bounds__(256) void expand_q8_kernel(const uint8_t * __restri
     if (threadIdx.x == 0) *reinterpret_cast<int *>(out + L.flag_offset()) = s_flag;
 }
 
-template <int TYPE, int MT>
+template <int TYPE, int MT, bool NEG>
 void launch_typed(const GemvArgs & g, const KernelArgs & ka, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>((ka.shape.rows + 63) / 64), static_cast<unsigned>(g.max_active));
     const size_t tok_bytes = (static_cast<size_t>(ka.lay.flag_offset()) + 15) & ~static_cast<size_t>(15);
-    hipLaunchKernelGGL((expert_gemv_kernel<TYPE, MT>), grid, dim3(kThreads), MT * tok_bytes, stream, ka);
+    hipLaunchKernelGGL((expert_gemv_kernel<TYPE, MT, NEG>), grid, dim3(kThreads), MT * tok_bytes, stream, ka);
     check_hip(hipGetLastError(), "expert GEMV launch");
 }
 
-template <int TYPE>
+template <int TYPE, bool NEG>
 void launch_mt(const GemvArgs & g, const KernelArgs & ka, hipStream_t stream) {
-    if (g.max_per_expert <= 1) launch_typed<TYPE, 1>(g, ka, stream);
-    else if (g.max_per_expert <= 2) launch_typed<TYPE, 2>(g, ka, stream);
-    else if (g.max_per_expert <= 4) launch_typed<TYPE, 4>(g, ka, stream);
-    else launch_typed<TYPE, 8>(g, ka, stream);
+    if (g.max_per_expert <= 1) launch_typed<TYPE, 1, NEG>(g, ka, stream);
+    else if (g.max_per_expert <= 2) launch_typed<TYPE, 2, NEG>(g, ka, stream);
+    else if (g.max_per_expert <= 4) launch_typed<TYPE, 4, NEG>(g, ka, stream);
+    else launch_typed<TYPE, 8, NEG>(g, ka, stream);
 }
 
 }  // namespace
@@ -1215,8 +1216,13 @@ void launch_gemv(const GemvArgs & g, hipStream_t stream) {
     ka.activation = g.activation;
     ka.alpha = g.alpha;
     ka.limit = g.limit;
-    if (bank.type == VBM_TYPE_MXFP4) launch_mt<39>(g, ka, stream);
-    else launch_mt<8>(g, ka, stream);
+    if (bank.type == VBM_TYPE_MXFP4) {
+        if (g.may_have_neg128) launch_mt<39, true>(g, ka, stream);
+        else launch_mt<39, false>(g, ka, stream);
+    } else {
+        if (g.may_have_neg128) launch_mt<8, true>(g, ka, stream);
+        else launch_mt<8, false>(g, ka, stream);
+    }
 }
 
 void launch_decode_gate_up(const DecodeGateUpArgs & d, hipStream_t stream) {

@@ -142,6 +142,10 @@ struct GemvArgs {
     int epilogue;                     // 0 plain, 1 GLU + requantize
     int activation;
     float alpha, limit;
+    // false when every activation row comes from this library's Q8_0 quantizer (fp32 inputs,
+    // the GLU requantization), whose codes are never -128: the kernel then carries no VPSIGNB
+    // slow path, which frees the registers for a deeper weight ring
+    bool may_have_neg128 = true;
 };
 void launch_gemv(const GemvArgs & a, hipStream_t stream);
 

@@ -209,6 +209,7 @@ void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits
     a.dst_xrows = w.xrows_act;
     a.dst_layout = la;
     a.epilogue = 1;
+    a.may_have_neg128 = false;               // fp32 input, and the GLU requantization feeds down
     record(events, 0, s);
     launch_gemv(a, s);
     record(events, 1, s);
@@ -332,6 +333,7 @@ vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot,
         a.bias = bias;
         a.dst = dst;
         a.epilogue = 0;
+        a.may_have_neg128 = b_type != VBM_TYPE_F32;   // ggml Q8_0 rows may hold -128 codes
         launch_gemv(a, s);
         check_hip(hipFreeAsync(scratch, s), "mul_mat_id scratch free");
     });
