@@ -3,6 +3,7 @@ its host-side generators are deterministic and range-consistent, and the bank la
 device kernels use are a bijection onto each slot (compiled and run on the host)."""
 import ctypes as C
 import subprocess
+import sys
 from pathlib import Path
 
 import numpy as np
@@ -61,3 +62,13 @@ def test_bank_layout_bijection_host(tmp_path):
     proc = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert proc.returncode == 0, proc.stdout + proc.stderr
     assert "bijective" in proc.stdout
+
+
+@pytest.mark.parametrize("args,needle", [(["--gpus", "2"], "exactly one GPU"), (["--tokens", "4"], "single-token")])
+def test_bench_refuses_unsupported_runs(args, needle):
+    """bench.py measures one GPU at batch 1: other requests exit with status 2 and a message,
+    before touching any device."""
+    repo = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(repo / "bench.py"), *args], capture_output=True, text=True, timeout=300,
+                       cwd=repo)
+    assert r.returncode == 2 and needle in r.stderr, (r.returncode, r.stderr[-400:])
