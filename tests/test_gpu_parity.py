@@ -291,3 +291,41 @@ def test_mul_mat_id_every_chunk_width_bitwise(gpu, orc, type_id):
     ref = orc.mul_mat_id(type_id, w, k, rows, experts, 0, x, 1, ids, 1, tokens, 1, bias=bias)
     assert H.bits_equal(got, ref), H.diff_report(got, ref)
     bank.destroy()
+
+
+def test_mul_mat_id_randomized_shapes_bitwise(gpu, orc):
+    """24 seeded random MUL_MAT_ID cases in the exact order against the oracle, bit for bit:
+    MXFP4 or Q8_0 weights, 1..40 experts, top-k 1..8 (distinct per token, some -1 masks), 1..48
+    tokens, rows 32..320 (half-live last tile pairs included), k 64..1024, fp32 or ggml Q8_0
+    activations (the latter with injected -128 codes), broadcast or per-rank activation rows,
+    with and without biases."""
+    rng = np.random.default_rng(20261202)
+    for case in range(24):
+        type_id = H.MX if case % 2 == 0 else H.Q8
+        experts = int(rng.integers(1, 41))
+        active = int(rng.integers(1, min(8, experts) + 1))
+        tokens = int(rng.integers(1, 49))
+        rows = 32 * int(rng.integers(1, 11))
+        k = 64 * int(rng.integers(1, 17))
+        b_ne1 = 1 if rng.random() < 0.5 else active
+        q8_input = rng.random() < 0.4
+        ids = np.stack([rng.choice(experts, active, replace=False) for _ in range(tokens)]).astype(np.int32)
+        if rng.random() < 0.3:
+            ids.reshape(-1)[rng.random(ids.size) < 0.2] = -1
+        w = H.synth_weights(type_id, 500 + case, 1, experts, rows, k)
+        bank = H.make_bank(type_id, w, experts, rows, k)
+        bias = gpu.synth_normal(500 + case, 2, 0, experts * rows, 0.0, 0.02) if rng.random() < 0.5 else None
+        x = gpu.synth_normal(500 + case, 3, 0, tokens * b_ne1 * k).reshape(tokens, b_ne1, k)
+        label = (f"case {case}: type={type_id} experts={experts} top{active} tokens={tokens} rows={rows} k={k} "
+                 f"b_ne1={b_ne1} q8={q8_input} bias={bias is not None}")
+        print(f"[random mul_mat_id] {label}", flush=True)
+        if q8_input:
+            q = orc.quantize_q8_0(x.reshape(tokens * b_ne1, k)).reshape(-1, 34)
+            q[rng.random(q.shape[0]) < 0.25, 2 + int(rng.integers(0, 32))] = 128      # -128 codes
+            b, b_type, orc_type = q.reshape(tokens, b_ne1, -1), gpu.TYPE_Q8_0, 8
+        else:
+            b, b_type, orc_type = x, gpu.TYPE_F32, 0
+        got = H.mul_mat_id(bank, experts, b, b_type, b_ne1, ids, active, bias=bias)
+        ref = orc.mul_mat_id(type_id, w, k, rows, experts, orc_type, b, b_ne1, ids, active, tokens, active, bias=bias)
+        assert H.bits_equal(got, ref), f"{label}: {H.diff_report(got, ref)}"
+        bank.destroy()
