@@ -115,3 +115,31 @@ def test_layer_glu_epilogue_many_tokens_per_expert(gpu, orc):
     assert np.array_equal(ids, ref["ids"])
     assert np.array_equal(out.view(np.uint32), ref["out"].view(np.uint32)), H.diff_report(out, ref["out"])
     layer.destroy()
+
+
+def test_layer_randomized_shapes_bitwise(gpu, orc):
+    """10 seeded random fused layers in the exact order against the oracle's layer: both weight
+    types and activations, hidden 64..1024, intermediate 64..768, 2..48 experts, top-1..6, 1..24
+    tokens, given logits or the fp32 router, with or without biases. Expert ids and outputs must be
+    bit-identical."""
+    rng = np.random.default_rng(4040)
+    for case in range(10):
+        type_id = H.MX if case % 2 == 0 else H.Q8
+        hidden, inter = 64 * int(rng.integers(1, 17)), 64 * int(rng.integers(1, 13))
+        experts = int(rng.integers(2, 49))
+        top_k = int(rng.integers(1, min(6, experts) + 1))
+        tokens = int(rng.integers(1, 25))
+        router, biases = bool(rng.random() < 0.5), bool(rng.random() < 0.6)
+        act = gpu.ACT_SWIGLU_OAI if rng.random() < 0.5 else gpu.ACT_SILU
+        label = (f"case {case}: type={type_id} H={hidden} I={inter} E={experts} top{top_k} T={tokens} "
+                 f"router={router} biases={biases} act={act}")
+        print(f"[random layer] {label}", flush=True)
+        layer = Layer(gpu, type_id, hidden, inter, experts, top_k, seed=700 + case, router=router, biases=biases,
+                      activation=act)
+        x = gpu.synth_normal(700 + case, 6, 0, tokens * hidden).reshape(tokens, hidden)
+        logits = None if router else gpu.synth_normal(700 + case, 7, 0, tokens * experts).reshape(tokens, experts)
+        out, ids, w = layer.forward_gpu(x, logits)
+        ref = layer.forward_cpu(orc, x, logits)
+        assert np.array_equal(ids, ref["ids"]), label
+        assert np.array_equal(out.view(np.uint32), ref["out"].view(np.uint32)), f"{label}: {H.diff_report(out, ref['out'])}"
+        layer.destroy()
