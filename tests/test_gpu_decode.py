@@ -94,3 +94,31 @@ def test_decode_step_q8_0_silu(gpu, orc):
     assert max_rel <= 1e-3 and cos >= 0.99999, (max_rel, cos)
     for layer in layers:
         layer.destroy()
+
+
+def test_decode_randomized_shapes_bitwise(gpu, orc):
+    """8 seeded random single-token decode plans (1..3 layers; both weight types and activations;
+    hidden 64..1024, intermediate 64..768, 2..200 experts, top-1..8, with or without biases)
+    against the oracle's layer chain: routing and output bit-identical."""
+    rng = np.random.default_rng(5150)
+    for case in range(8):
+        type_id = H.MX if case % 2 == 0 else H.Q8
+        hidden, inter = 64 * int(rng.integers(1, 17)), 64 * int(rng.integers(1, 13))
+        experts = int(rng.integers(2, 201))
+        top_k = int(rng.integers(1, min(8, experts) + 1))
+        n_layers = int(rng.integers(1, 4))
+        biases = bool(rng.random() < 0.6)
+        act = gpu.ACT_SWIGLU_OAI if rng.random() < 0.5 else gpu.ACT_SILU
+        label = (f"case {case}: type={type_id} H={hidden} I={inter} E={experts} top{top_k} L={n_layers} "
+                 f"biases={biases} act={act}")
+        print(f"[random decode] {label}", flush=True)
+        layers = [Layer(gpu, type_id, hidden, inter, experts, top_k, seed=800 + case, layer=l, router=False,
+                        biases=biases, activation=act) for l in range(n_layers)]
+        x = gpu.synth_normal(800 + case, 6, 0, hidden)
+        logits = gpu.synth_normal(800 + case, 7, 0, n_layers * experts).reshape(n_layers, experts)
+        out, ids, _ = run_decode(gpu, layers, x, logits)
+        ref, ref_ids, _ = oracle_chain(orc, layers, x, logits)
+        assert np.array_equal(ids, ref_ids), label
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), f"{label}: {H.diff_report(out, ref)}"
+        for layer in layers:
+            layer.destroy()
