@@ -148,3 +148,38 @@ def test_fast_order_small_groups_take_the_exact_gemv(gpu, orc, experts, tokens):
     assert np.array_equal(out.view(np.uint32), exact.view(np.uint32))
     assert np.array_equal(out.view(np.uint32), ref["out"].view(np.uint32)), H.diff_report(out, ref["out"])
     fast.destroy()
+
+
+def test_gemm_randomized_shapes_within_tolerance(gpu, orc):
+    """8 seeded random fast-order MUL_MAT_ID calls large enough for the MFMA grouped GEMM
+    (>= 16 tokens, >= 5 routed rows per expert): both weight types, 2..16 experts, top-1..4,
+    rows 64..320, k 64..1024, fp32 or ggml Q8_0 (with -128 codes) inputs, with or without biases,
+    against the oracle within the fast order's tolerance (max error / max |ref| <= 1e-3, cosine >=
+    0.99999)."""
+    rng = np.random.default_rng(6060)
+    for case in range(8):
+        type_id = H.MX if case % 2 == 0 else H.Q8
+        experts = int(rng.integers(2, 17))
+        active = int(rng.integers(1, min(4, experts) + 1))
+        tokens = max(16, -(-5 * experts // active) + int(rng.integers(0, 40)))
+        rows, k = 64 * int(rng.integers(1, 6)), 64 * int(rng.integers(1, 17))
+        q8_input = rng.random() < 0.4
+        ids = np.stack([rng.choice(experts, active, replace=False) for _ in range(tokens)]).astype(np.int32)
+        w = H.synth_weights(type_id, 900 + case, 1, experts, rows, k)
+        bank = H.make_bank(type_id, w, experts, rows, k)
+        bias = gpu.synth_normal(900 + case, 2, 0, experts * rows, 0.0, 0.02) if rng.random() < 0.5 else None
+        x = gpu.synth_normal(900 + case, 3, 0, tokens * k).reshape(tokens, 1, k)
+        label = (f"case {case}: type={type_id} experts={experts} top{active} tokens={tokens} rows={rows} k={k} "
+                 f"q8={q8_input} bias={bias is not None}")
+        print(f"[random gemm] {label}", flush=True)
+        if q8_input:
+            q = orc.quantize_q8_0(x.reshape(tokens, k)).reshape(-1, 34)
+            q[rng.random(q.shape[0]) < 0.25, 2 + int(rng.integers(0, 32))] = 128
+            b, b_type, orc_type = q.reshape(tokens, 1, -1), gpu.TYPE_Q8_0, 8
+        else:
+            b, b_type, orc_type = x, gpu.TYPE_F32, 0
+        got = H.mul_mat_id(bank, experts, b, b_type, 1, ids, active, bias=bias, order=gpu.ORDER_FAST)
+        ref = orc.mul_mat_id(type_id, w, k, rows, experts, orc_type, b, 1, ids, active, tokens, active, bias=bias)
+        max_rel, cos = H.rel_err_and_cos(got, ref)
+        assert max_rel <= 1e-3 and cos >= 0.99999, f"{label}: max_rel={max_rel:.3e} cos={cos:.9f}"
+        bank.destroy()
