@@ -134,6 +134,14 @@ def router(logits=None, router_w=None, router_b=None, x=None, n_expert=None, n_t
     return logits, ids, w
 
 
+def glu(activation: int, gate: np.ndarray, up: np.ndarray, alpha: float = 1.702, limit: float = 7.0) -> np.ndarray:
+    gate = np.ascontiguousarray(gate, dtype=np.float32)
+    up = np.ascontiguousarray(up, dtype=np.float32)
+    out = np.empty_like(gate)
+    load().orc_glu(activation, _p(gate), _p(up), _p(out), gate.size, alpha, limit)
+    return out
+
+
 def moe_layer(type_id, gate_up, down, gate_up_bias, down_bias, x, hidden, intermediate, n_expert, top_k,
               activation=1, logits=None, router_w=None, router_b=None, threads=0, want_intermediates=False):
     x = np.ascontiguousarray(x, dtype=np.float32)

@@ -387,11 +387,17 @@ static size_t row_bytes(int type, int64_t k) {
     return (size_t)(k / 32) * (type == ORC_TYPE_MXFP4 ? 17 : 34);
 }
 
-/* Rows [0, rows) of one expert matrix times one Q8_0 activation row. */
+/* Rows [0, rows) of one expert matrix times one Q8_0 activation row. threads > 0: SIMD dots on
+ * that many OpenMP threads; threads < 0: SIMD dots on the calling thread; 0: scalar dots. */
 static void gemv_rows(int type, const uint8_t * matrix, int64_t k, int64_t rows, const uint8_t * act,
                       const float * bias, float * out, int threads) {
     const size_t stride = row_bytes(type, k);
-    if (threads > 0) {
+    if (threads < 0) {
+        for (int64_t r = 0; r < rows; ++r) {
+            const float v = row_dot(type, (int)k, matrix + r * stride, act, 1);
+            out[r] = bias ? v + bias[r] : v;
+        }
+    } else if (threads > 0) {
 #ifdef _OPENMP
 #pragma omp parallel for num_threads(threads) schedule(static)
 #endif
@@ -567,25 +573,33 @@ int orc_moe_layer(const orc_layer * L, const float * x, float * logits, int64_t 
     const size_t qh = (size_t)(H / 32) * 34, qi = (size_t)(I / 32) * 34;
     const size_t gu_bytes = row_bytes(L->type, H) * (size_t)(2 * I);
     const size_t dn_bytes = row_bytes(L->type, I) * (size_t)H;
-    uint8_t * xq = (uint8_t *)malloc(qh), * aq = (uint8_t *)malloc(qi);
-    float * gu = (float *)malloc(sizeof(float) * (size_t)(2 * I));
-    float * act = (float *)malloc(sizeof(float) * (size_t)I);
-    float * y = (float *)malloc(sizeof(float) * (size_t)(K * H));
+    /* Tokens are independent: with many tokens each thread takes whole tokens (SIMD dots on the
+     * thread), otherwise the rows of each projection are split over the threads. Either way every
+     * output is the same function of its token's inputs, so the bits do not depend on it. */
+    const int per_token = threads > 0 && n_tokens >= 2 * threads;
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(per_token ? threads : 1) schedule(dynamic, 1)
+#endif
     for (int64_t t = 0; t < n_tokens; ++t) {
+        const int inner = per_token ? -1 : threads;
+        uint8_t * xq = (uint8_t *)malloc(qh), * aq = (uint8_t *)malloc(qi);
+        float * gu = (float *)malloc(sizeof(float) * (size_t)(2 * I));
+        float * act = (float *)malloc(sizeof(float) * (size_t)I);
+        float * y = (float *)malloc(sizeof(float) * (size_t)(K * H));
         orc_quantize_row_q8_0(x + t * H, xq, H);
         for (int64_t r = 0; r < K; ++r) {
             const int32_t e = ids[t * K + r];
             gemv_rows(L->type, (const uint8_t *)L->gate_up + (size_t)e * gu_bytes, H, 2 * I, xq,
-                      L->gate_up_bias ? L->gate_up_bias + (size_t)e * 2 * I : NULL, gu, threads);
+                      L->gate_up_bias ? L->gate_up_bias + (size_t)e * 2 * I : NULL, gu, inner);
             orc_glu(L->activation, gu, gu + I, act, I, 1.702f, 7.0f);
             if (act_out) memcpy(act_out + (t * K + r) * I, act, sizeof(float) * (size_t)I);
             orc_quantize_row_q8_0(act, aq, I);
             gemv_rows(L->type, (const uint8_t *)L->down + (size_t)e * dn_bytes, I, H, aq,
-                      L->down_bias ? L->down_bias + (size_t)e * H : NULL, y + r * H, threads);
+                      L->down_bias ? L->down_bias + (size_t)e * H : NULL, y + r * H, inner);
         }
         if (y_out) memcpy(y_out + t * K * H, y, sizeof(float) * (size_t)(K * H));
         orc_weighted_combine(y, weights + t * K, H, K, 1, out + t * H);
+        free(xq); free(aq); free(gu); free(act); free(y);
     }
-    free(xq); free(aq); free(gu); free(act); free(y);
     return 0;
 }

@@ -4,6 +4,8 @@ Bar: bit-exact for bank bytes, quantizer output, grouping, expert ids, integer b
 x86-contract GEMV (whose fp32 order is reproduced); fp32 layer outputs within 1e-3 max relative
 error (max|gpu - cpu| / max|cpu|) and cosine >= 0.99999.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -329,3 +331,118 @@ def test_mul_mat_id_randomized_shapes_bitwise(gpu, orc):
         ref = orc.mul_mat_id(type_id, w, k, rows, experts, orc_type, b, b_ne1, ids, active, tokens, active, bias=bias)
         assert H.bits_equal(got, ref), f"{label}: {H.diff_report(got, ref)}"
         bank.destroy()
+
+
+@pytest.mark.parametrize("order,tokens", [(0, 6), (1, 64)])
+def test_mul_mat_id_unmapped_expert_and_invalid_ids_are_nan(gpu, orc, order, tokens):
+    """Without a host copy of the map to check against, a routed expert whose expert->slot entry is
+    -1 gives NaN output rows (exact order: the batched GEMV; fast order at 64 tokens: the grouped
+    GEMM), and so do ids outside [-1, n_as), which the grouping skips; -1 ids stay zero rows and
+    every other row equals the oracle (bitwise in the exact order, within tolerance in the fast)."""
+    k, rows, experts, n_ids = 256, 128, 4, 2
+    rng = np.random.default_rng(31 + order)
+    w = H.synth_weights(H.MX, 31, 1, experts, rows, k)
+    bank = H.make_bank(H.MX, w, experts, rows, k)
+    slot_map = np.arange(experts, dtype=np.int32)
+    slot_map[2] = -1
+    ids = np.stack([rng.choice(experts, n_ids, replace=False) for _ in range(tokens)]).astype(np.int32)
+    ids[0] = [2, 0]
+    ids[1] = [-1, 1]
+    ids[2] = [experts, 3]      # invalid: one past the last expert
+    ids[3] = [1, -7]           # invalid: below -1
+    x = gpu.synth_normal(31, 2, 0, tokens * k).reshape(tokens, 1, k)
+    got = H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, ids, n_ids, order=order, slot_map=slot_map)
+    safe = np.where((ids >= 0) & (ids < experts) & (ids != 2), ids, -1).astype(np.int32)
+    ref = orc.mul_mat_id(39, w, k, rows, experts, 0, x, 1, safe, n_ids, tokens, n_ids, threads=8)
+    poisoned = ((ids == 2) | (ids >= experts) | (ids < -1))
+    assert poisoned.sum() >= 3
+    assert np.all(np.isnan(got[poisoned])), "unmapped / invalid rows must be NaN"
+    assert np.all(got[ids == -1] == 0.0)
+    keep = ~poisoned
+    if order == 0:
+        assert H.bits_equal(got[keep], ref[keep]), H.diff_report(got[keep], ref[keep])
+    else:
+        max_rel, cos = H.rel_err_and_cos(got[keep], ref[keep])
+        assert max_rel <= 1e-3 and cos >= 0.99999
+    bank.destroy()
+
+
+@pytest.mark.parametrize("order,tokens", [(0, 4), (1, 96)])
+def test_layer_unmapped_expert_gives_nan_rows(gpu, orc, order, tokens):
+    """The fused layer over banks whose expert->slot map holds -1 for a routed expert: the tokens
+    routed to it come out NaN (never stale workspace data from an earlier call), the others equal
+    the oracle (bitwise in the exact order, within tolerance in the fast)."""
+    from test_gpu_layer import Layer
+    E, K, Hd = 8, 2, 256
+    layer = Layer(gpu, H.MX, Hd, Hd, E, K, seed=57, router=False, order=order)
+    x = gpu.synth_normal(57, 6, 0, tokens * Hd).reshape(tokens, Hd)
+    logits = gpu.synth_normal(57, 7, 0, tokens * E).reshape(tokens, E)
+    ref = layer.forward_cpu(orc, x, logits)
+    # fill the workspace with a correct earlier result first, then unmap one routed expert
+    layer.forward_gpu(x, logits)
+    bad = int(ref["ids"][0, 0])
+    slot_map = np.arange(E, dtype=np.int32)
+    slot_map[bad] = -1
+    dmap = gpu.DeviceBuffer.from_array(slot_map)
+    d = layer.desc()
+    d.expert_to_slot = dmap.ptr
+    ws = C.c_size_t()
+    gpu.call("vbm_moe_layer_workspace", C.byref(d), tokens, C.byref(ws))
+    work = gpu.DeviceBuffer(ws.value)
+    dx, dl = gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer.from_array(logits)
+    out = gpu.DeviceBuffer(4 * tokens * Hd)
+    gpu.call("vbm_moe_layer_forward", C.byref(d), dx.ptr, dl.ptr, tokens, out.ptr, None, None, work.ptr, ws.value, None)
+    gpu.call("vbm_stream_synchronize", None)
+    got = out.download(np.float32, (tokens, Hd))
+    hit = np.any(ref["ids"] == bad, axis=1)
+    assert hit[0] and not hit.all()
+    assert np.all(np.isnan(got[hit]))
+    if order == 0:
+        assert H.bits_equal(got[~hit], ref["out"][~hit])
+    else:
+        max_rel, cos = H.rel_err_and_cos(got[~hit], ref["out"][~hit])
+        assert max_rel <= 1e-3 and cos >= 0.99999
+    layer.destroy()
+
+
+def test_add_id_matches_oracle(gpu, orc):
+    """GGML_OP_ADD_ID (hybrid-experts.patch:1464-1480): y[:, r, t] += bias[:, ids[r, t]], -1 ids
+    untouched, with a token stride on the ids (a top-k view of a wider argsort)."""
+    rng = np.random.default_rng(44)
+    rows, n_ids, tokens, n_as, stride = 96, 3, 17, 9, 5
+    y = rng.standard_normal((tokens, n_ids, rows)).astype(np.float32)
+    bias = rng.standard_normal((n_as, rows)).astype(np.float32)
+    ids_full = rng.integers(-1, n_as, (tokens, stride)).astype(np.int32)
+    ids = ids_full[:, :n_ids]
+    ref = y.copy()
+    for t in range(tokens):
+        for r in range(n_ids):
+            if ids[t, r] >= 0:
+                ref[t, r] = ref[t, r] + bias[ids[t, r]]
+    dy, db, di = (gpu.DeviceBuffer.from_array(a) for a in (y, bias, ids_full))
+    gpu.call("vbm_add_id", dy.ptr, db.ptr, di.ptr, rows, n_ids, tokens, stride, None)
+    got = dy.download(np.float32, y.shape)
+    assert H.bits_equal(got, ref)
+
+
+@pytest.mark.parametrize("activation", [0, 1])
+def test_glu_matches_oracle(gpu, orc, activation):
+    """GGML_OP_GLU swiglu / swiglu_oai (alpha 1.702, limit 7) on strided gate / up views of one
+    fused [2I] row per (rank, token), as ggml splits the fused gate_up output, against the oracle's
+    activation: within 2 ulp (expf bits are unpinned upstream), values past the clamp included."""
+    rng = np.random.default_rng(45 + activation)
+    n_rows, width = 37, 200
+    gu = (rng.standard_normal((n_rows, 2 * width)) * 6).astype(np.float32)
+    gu[0, :8] = [-30, -7.5, -7, 0, 7, 7.5, 30, np.float32(1e-30)]
+    out = gpu.DeviceBuffer(4 * n_rows * width)
+    dgu = gpu.DeviceBuffer.from_array(gu)
+    gpu.call("vbm_glu", activation, dgu.ptr, dgu.ptr + 4 * width, out.ptr, n_rows, width, 2 * width, 2 * width,
+             width, C.c_float(1.702), C.c_float(7.0), None)
+    got = out.download(np.float32, (n_rows, width))
+    ref = np.empty_like(got)
+    for i in range(n_rows):
+        ref[i] = orc.glu(activation, gu[i, :width], gu[i, width:])
+    ulp = np.abs(got.astype(np.float64) - ref.astype(np.float64)) / np.spacing(np.abs(ref)).astype(np.float64)
+    print(f"[glu act={activation}] max ulp {float(ulp.max()):.1f}, exact fraction {float(np.mean(got == ref)):.4f}",
+          flush=True)
+    assert ulp.max() <= 2

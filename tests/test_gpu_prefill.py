@@ -59,6 +59,57 @@ def test_gemm_integer_block_dots_exact(gpu, orc, type_id):
     bank.destroy()
 
 
+@pytest.mark.parametrize("type_id", [H.MX, H.Q8])
+@pytest.mark.parametrize("experts,n_ids,tokens", [(2, 2, 190), (3, 2, 257), (4, 2, 300)])
+def test_gemm_multi_tile_experts_exact(gpu, orc, type_id, experts, n_ids, tokens):
+    """Experts with 130..300 routed jobs run the grouped GEMM over several 64-job tiles (full ones
+    and a partial last one). With unit scales every fp32 sum is an exact integer, so the GEMM must
+    match the oracle bit for bit, for fp32 inputs and for ggml Q8_0 inputs carrying -128 codes
+    (the flagged kernel)."""
+    rng = np.random.default_rng(7000 + experts)
+    rows, k = 128, 256
+    w = (unit_scale_mxfp4 if type_id == H.MX else unit_scale_q8)(experts, rows, k, rng)
+    bank = H.make_bank(type_id, w, experts, rows, k)
+    ids = np.stack([rng.choice(experts, n_ids, replace=False) for _ in range(tokens)]).astype(np.int32)
+    per_expert = np.bincount(ids.ravel(), minlength=experts)
+    print(f"[multi-tile gemm type={type_id}] jobs per expert {per_expert.tolist()}", flush=True)
+    assert per_expert.max() > 128 and np.any(per_expert % 64 != 0)
+    x = unit_scale_activations(tokens, k, rng).reshape(tokens, 1, k)
+    got = H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, ids, n_ids, order=gpu.ORDER_FAST)
+    ref = orc.mul_mat_id(type_id, w, k, rows, experts, 0, x, 1, ids, n_ids, tokens, n_ids, threads=8)
+    assert H.bits_equal(got, ref), H.diff_report(got, ref)
+    q = orc.quantize_q8_0(x.reshape(tokens, k)).reshape(tokens, 1, -1)
+    qb = q.reshape(-1, 34)
+    qb[::5, 2 + 9] = 128
+    qb[::11, 2:8] = 128
+    got = H.mul_mat_id(bank, experts, q, gpu.TYPE_Q8_0, 1, ids, n_ids, order=gpu.ORDER_FAST)
+    ref = orc.mul_mat_id(type_id, w, k, rows, experts, 8, q, 1, ids, n_ids, tokens, n_ids, threads=8)
+    assert H.bits_equal(got, ref), H.diff_report(got, ref)
+    bank.destroy()
+
+
+@pytest.mark.parametrize("type_id", [H.MX, H.Q8])
+def test_prefill_layer_multi_tile_experts(gpu, orc, type_id):
+    """The fused layer (gate_up GEMM with the GLU + requantization epilogue, then the down GEMM)
+    with 4 experts top-2 at T = 300, so every expert holds 110..190 jobs over 2..3 job tiles:
+    ids exact, output within the fast order's tolerance of the oracle."""
+    layer = Layer(gpu, type_id, 256, 256, 4, 2, seed=4400 + type_id, router=False,
+                  activation=1 if type_id == H.MX else 0, order=gpu.ORDER_FAST)
+    T = 300
+    x = gpu.synth_normal(4400 + type_id, 6, 0, T * 256).reshape(T, 256)
+    logits = gpu.synth_normal(4400 + type_id, 7, 0, T * 4).reshape(T, 4)
+    out, ids, _ = layer.forward_gpu(x, logits)
+    ref = layer.forward_cpu(orc, x, logits)
+    assert np.array_equal(ids, ref["ids"])
+    per_expert = np.bincount(ids.ravel(), minlength=4)
+    assert per_expert.min() > 64, per_expert
+    max_rel, cos = H.rel_err_and_cos(out, ref["out"])
+    print(f"[prefill multi-tile type={type_id}] jobs {per_expert.tolist()} max_rel={max_rel:.3e} cos={cos:.9f}",
+          flush=True)
+    assert max_rel <= 1e-3 and cos >= 0.99999
+    layer.destroy()
+
+
 def test_gemm_mxfp4_exponent_ranges_exact(gpu, orc):
     """Row tiles whose block exponents sit inside the range folded into the f16 weight operand
     (e in [-14, 12]: bytes 114, 127, 140) and outside it (bytes 141 and 113, the ldexp path),
@@ -117,6 +168,28 @@ def test_prefill_layer_q8_0_config3_shape(gpu, orc):
     layer.destroy()
 
 
+def test_prefill_layer_q8_0_config3_full_2048_tokens(gpu, orc):
+    """Config 3 at its own size: 2048 tokens, hidden 2048, 128 experts top-8, intermediate 768,
+    Q8_0, SiLU, no biases, fast order (about 128 jobs per expert, so most experts span two or three
+    64-job tiles of the grouped GEMM). Ids exact; max |out - ref| / max |ref| <= 1e-3 and cosine
+    >= 0.99999 against the oracle's layer."""
+    layer = Layer(gpu, H.Q8, 2048, 768, 128, 8, seed=3030, router=False, biases=False, activation=0,
+                  order=gpu.ORDER_FAST)
+    T = 2048
+    x = gpu.synth_normal(3030, 6, 0, T * 2048).reshape(T, 2048)
+    logits = gpu.synth_normal(3030, 7, 0, T * 128).reshape(T, 128)
+    out, ids, _ = layer.forward_gpu(x, logits)
+    ref = layer.forward_cpu(orc, x, logits, threads=16)
+    assert np.array_equal(ids, ref["ids"])
+    per_expert = np.bincount(ids.ravel(), minlength=128)
+    max_rel, cos = H.rel_err_and_cos(out, ref["out"])
+    print(f"[prefill config3 T={T}] jobs per expert {per_expert.min()}..{per_expert.max()} "
+          f"max_rel={max_rel:.3e} cos={cos:.9f}", flush=True)
+    assert per_expert.max() > 128
+    assert max_rel <= 1e-3 and cos >= 0.99999
+    layer.destroy()
+
+
 def test_prefill_layer_mxfp4_config1_shape(gpu, orc):
     """Config 1 layer (MXFP4, 32 experts, top-4, 2880, SwiGLU-OAI, biases) at T = 64, fast order."""
     layer = Layer(gpu, H.MX, 2880, 2880, 32, 4, seed=78, order=gpu.ORDER_FAST)
@@ -152,7 +225,7 @@ def test_fast_order_small_groups_take_the_exact_gemv(gpu, orc, experts, tokens):
 
 def test_gemm_randomized_shapes_within_tolerance(gpu, orc):
     """8 seeded random fast-order MUL_MAT_ID calls large enough for the MFMA grouped GEMM
-    (>= 16 tokens, >= 5 routed rows per expert): both weight types, 2..16 experts, top-1..4,
+    (>= 16 tokens, 5..200 routed rows per expert on average): both weight types, 2..16 experts, top-1..4,
     rows 64..320, k 64..1024, fp32 or ggml Q8_0 (with -128 codes) inputs, with or without biases,
     against the oracle within the fast order's tolerance (max error / max |ref| <= 1e-3, cosine >=
     0.99999)."""
@@ -161,7 +234,8 @@ def test_gemm_randomized_shapes_within_tolerance(gpu, orc):
         type_id = H.MX if case % 2 == 0 else H.Q8
         experts = int(rng.integers(2, 17))
         active = int(rng.integers(1, min(4, experts) + 1))
-        tokens = max(16, -(-5 * experts // active) + int(rng.integers(0, 40)))
+        # 5..200 routed jobs per expert on average: one to four 64-job tiles per expert
+        tokens = max(16, -(-int(rng.integers(5, 201)) * experts // active))
         rows, k = 64 * int(rng.integers(1, 6)), 64 * int(rng.integers(1, 17))
         q8_input = rng.random() < 0.4
         ids = np.stack([rng.choice(experts, active, replace=False) for _ in range(tokens)]).astype(np.int32)

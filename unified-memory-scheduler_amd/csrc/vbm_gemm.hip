@@ -166,7 +166,26 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
     const int joff = cst<int32_t>(A.offsets)[expert];
     const int slot = A.expert_to_slot ? cst<int32_t>(A.expert_to_slot)[expert] : expert;
     const GemmShape S = A.shape;
-    if (slot < 0 || slot >= S.n_slots) return;
+    if (slot < 0 || slot >= S.n_slots) {
+        // Expert not resident in this bank (a tile filter removes the experts a pass skips on
+        // purpose, so this is a bad map): this workgroup's outputs become NaN, as in the decode
+        // kernels, rather than leaving stale workspace data. Epilogue 1 poisons the block scale
+        // of the GLU block of this tile pair.
+        const float nan = __builtin_nanf("");
+        const int live_jobs = count - j0 < kJobTile ? count - j0 : kJobTile;
+        if (EPI == 0) {
+            for (int i = threadIdx.x; i < live_jobs * 64; i += kGemmThreads) {
+                const int64_t brow = static_cast<int64_t>(pair) * 64 + (i & 63);
+                if (brow < S.rows)
+                    A.dst[static_cast<size_t>(A.jobs[joff + j0 + (i >> 6)]) * S.rows + ggml_row(brow, S.rows, S.interleave)] = nan;
+            }
+        } else {
+            for (int j = threadIdx.x; j < live_jobs; j += kGemmThreads)
+                reinterpret_cast<float *>(A.rows_out + static_cast<int64_t>(A.jobs[joff + j0 + j]) * A.out_lay.stride() +
+                                          A.out_lay.da_offset())[pair] = nan;
+        }
+        return;
+    }
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int lr = lane & 15, q = lane >> 4;
@@ -197,7 +216,11 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
         job[jh] = jlive[jh] ? A.jobs[joff + j0 + jl] : 0;
         if (FLAGGED && jlive[jh]) flagged |= *reinterpret_cast<const int *>(row_of(jl) + A.lay.flag_offset());
     }
-    const bool slow = FLAGGED && __any(flagged != 0);   // wave-uniform
+    // Workgroup-uniform: every wave then runs the same K-loop instantiation, so each of its
+    // barriers is reached from one control path (every thread gets here: the exits above are
+    // uniform per workgroup).
+    bool slow = false;
+    if constexpr (FLAGGED) slow = __syncthreads_or(flagged != 0) != 0;
 
     // Cooperative stage loaders. Activation piece i of this thread: job (t + 256i) / P, 16-byte
     // part (t + 256i) % P, P = pieces per job row; block scale: job t / 4, block t % 4. Weight

@@ -646,7 +646,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const int count = as_const<int32_t>(A.counts)[expert];
     const __attribute__((address_space(4))) int32_t * jobs = as_const<int32_t>(A.rows_list) + as_const<int32_t>(A.offsets)[expert];
     const int slot = A.expert_to_slot ? as_const<int32_t>(A.expert_to_slot)[expert] : expert;
-    if (slot < 0 || slot >= A.shape.n_slots || count <= 0) return;
+    if (count <= 0) return;
+    if (slot < 0 || slot >= A.shape.n_slots) {
+        // Expert not resident in this bank: its jobs' outputs of this tile pair become NaN, as in
+        // the decode kernels, so a bad expert->slot map can never leave stale workspace data in a
+        // result. Epilogue 1 poisons the block scale of the GLU block this workgroup owns.
+        const float nan = __builtin_nanf("");
+        if (A.epilogue == 0) {
+            for (int i = threadIdx.x; i < count * 64; i += kThreads) {
+                const int64_t brow = static_cast<int64_t>(blockIdx.x) * 64 + (i & 63);
+                if (brow < A.shape.rows)
+                    A.dst[static_cast<size_t>(jobs[i >> 6]) * A.shape.rows + ggml_row(brow, A.shape.rows, A.shape.interleave)] = nan;
+            }
+        } else {
+            for (int j = threadIdx.x; j < count; j += kThreads)
+                reinterpret_cast<float *>(A.dst_xrows + static_cast<size_t>(jobs[j]) * A.dst_lay.stride() +
+                                          A.dst_lay.da_offset())[blockIdx.x] = nan;
+        }
+        return;
+    }
 
     const Shape S = A.shape;
     const int k = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // lane slice, wave-uniform

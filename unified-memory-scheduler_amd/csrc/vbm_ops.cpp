@@ -25,15 +25,26 @@ namespace {
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-__global__ void zero_kernel(float * p, int64_t n) {
+// MUL_MAT_ID output rows before the expert kernels run: 0 for every row (the rows of -1 ids stay
+// zero, hybrid-experts.patch:617-621; routed rows are overwritten), NaN for ids outside
+// [-1, n_as), which the grouping pass skips (the reference asserts on them, :622), so an invalid id
+// is loud in the output even when no host copy of the ids was given for checking.
+__global__ void init_dst_kernel(float * dst, const int32_t * ids, int64_t n_ids, int64_t ids_stride, int64_t n_as,
+                                int64_t rows, int64_t n) {
     const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-    if (i < n) p[i] = 0.0f;
+    if (i >= n) return;
+    const int64_t entry = i / rows, t = entry / n_ids, r = entry - t * n_ids;
+    const int32_t id = ids[t * ids_stride + r];
+    dst[i] = id >= -1 && id < n_as ? 0.0f : __builtin_nanf("");
 }
 
-void zero_floats(float * p, int64_t n, hipStream_t stream) {
+void init_dst(float * dst, const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride, int64_t n_as,
+              int64_t rows, hipStream_t stream) {
+    const int64_t n = n_ids * n_tokens * rows;
     if (n <= 0) return;
-    hipLaunchKernelGGL(zero_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, p, n);
-    check_hip(hipGetLastError(), "zero fill launch");
+    hipLaunchKernelGGL(init_dst_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, dst, ids,
+                       n_ids, ids_stride, n_as, rows, n);
+    check_hip(hipGetLastError(), "output init launch");
 }
 
 // Synchronous host-side validation of device ids against an expert->slot map (the reference's
@@ -288,7 +299,7 @@ vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot,
             else
                 launch_gemm_rows_from_q8(static_cast<const uint8_t *>(b), n_b, bank->nb * 34, gl, q, s);
             launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
-            zero_floats(dst, entries * bank->rows, s);
+            init_dst(dst, ids, n_ids, n_tokens, ids_stride, n_as, bank->rows, s);
             GemmParams p{};
             p.bank = bank;
             p.expert_to_slot = expert_to_slot;
@@ -320,7 +331,7 @@ vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot,
         else
             launch_expand_q8(static_cast<const uint8_t *>(b), n_b, bank->nb * 34, lay, q, s);
         launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
-        zero_floats(dst, entries * bank->rows, s);
+        init_dst(dst, ids, n_ids, n_tokens, ids_stride, n_as, bank->rows, s);
         GemvArgs a{};
         a.bank = bank;
         a.expert_to_slot = expert_to_slot;
