@@ -1,6 +1,8 @@
 """Host-RAM expert tier (vbm_tier_*) on the GPU: every token's output must be bit-identical to the
-fully resident decode plan holding the same experts, routing identical, and the tier's admission
-counters equal to the Python restatement fed with the same routes."""
+fully resident decode plan holding the same experts and to the oracle's layer chain, routing
+identical, and the tier's admission counters equal to the Python restatement fed with the same
+routes; tier prefill must be bit-identical to the resident fused layer and within the fast order's
+tolerance of the oracle."""
 import ctypes as C
 import json
 import sys
@@ -40,8 +42,28 @@ def routed_logits(rng, L, E, K, tokens):
     return out, chosen
 
 
+def host_layer(vb, type_id, l, E, H, I, p0, p1):
+    """ggml bytes and biases of layer l, regenerated on the host: the bytes vbm_bank_generate and
+    vbm_tier_generate (layer stride 16, gate_up stream 1, down stream 2) put on the device."""
+    n_gu, n_dn = E * 2 * I * (H // 32), E * H * (I // 32)
+    if type_id == 39:
+        gu, dn = vb.synth_mxfp4(SEED, 16 * l + 1, 0, n_gu, p0, p1), vb.synth_mxfp4(SEED, 16 * l + 2, 0, n_dn, p0, p1)
+    else:
+        gu, dn = vb.synth_q8_0(SEED, 16 * l + 1, 0, n_gu, p0, p1), vb.synth_q8_0(SEED, 16 * l + 2, 0, n_dn, p0, p1)
+    return (gu, dn, vb.synth_normal(SEED, 16 * l + 3, 0, E * 2 * I, 0.0, 0.02),
+            vb.synth_normal(SEED, 16 * l + 4, 0, E * H, 0.0, 0.02))
+
+
+def oracle_chain(orc, host, type_id, act, x, logits_t, H, I, E, K):
+    """The oracle's single-token chain through every layer (ggml x86 CPU path, exact order)."""
+    for l, (gu, dn, gb, db) in enumerate(host):
+        x = orc.moe_layer(type_id, gu, dn, gb, db, x.reshape(1, H), H, I, E, K, activation=act,
+                          logits=logits_t[l].reshape(1, E))["out"][0]
+    return x
+
+
 @pytest.mark.parametrize("type_id,policy,margin", [(39, 0, 4), (39, 1, 1), (8, 2, 2)])
-def test_tier_matches_resident_plan(gpu, type_id, policy, margin):
+def test_tier_matches_resident_plan(gpu, orc, type_id, policy, margin):
     vb = gpu
     L, E, K, H, I, slots = 3, 16, 4, 256, 256, 4 + 9
     act = vb.ACT_SWIGLU_OAI if type_id == 39 else vb.ACT_SILU
@@ -75,10 +97,12 @@ def test_tier_matches_resident_plan(gpu, type_id, policy, margin):
     for l, e in ((0, 3), (2, 5)):
         vb.call("vbm_tier_seed", tier.value, l, e)
         py.seed(l, e)
+    host = [host_layer(vb, type_id, l, E, H, I, p0, p1) for l in range(L)]
     rng = np.random.default_rng(type_id + policy)
     tokens = 30
     logits, chosen = routed_logits(rng, L, E, K, tokens)
-    x = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 6, 0, H))
+    x_host = vb.synth_normal(SEED, 6, 0, H)
+    x = vb.DeviceBuffer.from_array(x_host)
     dl = vb.DeviceBuffer(logits[0].nbytes)
     o1, o2 = vb.DeviceBuffer(4 * H), vb.DeviceBuffer(4 * H)
     i1, i2 = vb.DeviceBuffer(4 * L * K), vb.DeviceBuffer(4 * L * K)
@@ -92,6 +116,8 @@ def test_tier_matches_resident_plan(gpu, type_id, policy, margin):
         ia, ib = i1.download(np.int32, (L, K)), i2.download(np.int32, (L, K))
         assert np.array_equal(ia, ib) and ia.tolist() == chosen[t], t
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), t
+        want = oracle_chain(orc, host, type_id, act, x_host, logits[t], H, I, E, K)
+        assert np.array_equal(want.view(np.uint32), b.view(np.uint32)), f"token {t} differs from the oracle"
         for l in range(L):
             hits, made = py.admit(l, chosen[t][l])
             admitted = {e for _, e, _ in made}
@@ -176,7 +202,7 @@ def test_tier_routing_trace_replays_to_the_same_decisions(gpu, tmp_path):
 
 
 @pytest.mark.parametrize("type_id", [39, 8])
-def test_tier_prefill_matches_resident_layer(gpu, type_id):
+def test_tier_prefill_matches_resident_layer(gpu, orc, type_id):
     """Multi-token prefill through the tier (resident experts in one pass, the others streamed
     through the reserved slots in chunks) is bit-identical to the fused layer forward over banks
     holding every expert (both in the fast accumulation order), before and after decode steps
@@ -204,6 +230,7 @@ def test_tier_prefill_matches_resident_layer(gpu, type_id):
     vb.call("vbm_tier_generate", tier.value, SEED, 16, 1, 2, p0, p1, None)
     for l, e in ((0, 3), (0, 5), (0, 7), (1, 2)):
         vb.call("vbm_tier_seed", tier.value, l, e)
+    host = [host_layer(vb, type_id, l, E, H, I, p0, p1) for l in range(L)]
     rng = np.random.default_rng(type_id)
     out1, out2 = vb.DeviceBuffer(4 * T * H), vb.DeviceBuffer(4 * T * H)
     i1, i2 = vb.DeviceBuffer(4 * T * K), vb.DeviceBuffer(4 * T * K)
@@ -211,8 +238,10 @@ def test_tier_prefill_matches_resident_layer(gpu, type_id):
 
     def compare(tag):
         for l in range(L):
-            x = vb.DeviceBuffer.from_array(rng.standard_normal((T, H)).astype(np.float32))
-            lg = vb.DeviceBuffer.from_array(rng.standard_normal((T, E)).astype(np.float32))
+            x_host = rng.standard_normal((T, H)).astype(np.float32)
+            lg_host = rng.standard_normal((T, E)).astype(np.float32)
+            x = vb.DeviceBuffer.from_array(x_host)
+            lg = vb.DeviceBuffer.from_array(lg_host)
             ws = C.c_size_t()
             vb.call("vbm_moe_layer_workspace", C.byref(descs[l]), T, C.byref(ws))
             work = vb.DeviceBuffer(ws.value)
@@ -224,6 +253,15 @@ def test_tier_prefill_matches_resident_layer(gpu, type_id):
             assert np.array_equal(w1.download(np.uint32, (T, K)), w2.download(np.uint32, (T, K))), (tag, l)
             a, b = out1.download(np.uint32, (T, H)), out2.download(np.uint32, (T, H))
             assert np.array_equal(a, b), (tag, l, int(np.count_nonzero(a != b)))
+            gu, dn, gb, db = host[l]
+            want = orc.moe_layer(type_id, gu, dn, gb, db, x_host, H, I, E, K, activation=act, logits=lg_host,
+                                 threads=8)
+            assert np.array_equal(want["ids"], i2.download(np.int32, (T, K))), (tag, l)
+            got = b.view(np.float32)
+            g, r = got.astype(np.float64).ravel(), want["out"].astype(np.float64).ravel()
+            max_rel = float(np.abs(g - r).max() / np.abs(r).max())
+            cos = float(g @ r / (np.linalg.norm(g) * np.linalg.norm(r)))
+            assert max_rel <= 1e-3 and cos >= 0.99999, (tag, l, max_rel, cos)
 
     compare("seeded")
     # decode steps admit experts into the pool and stage misses in the reserved slots
