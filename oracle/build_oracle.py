@@ -5,6 +5,8 @@
               (read in place under REF_ROOT, never copied):
                 - libref_mxfp4_vnni.so  <- tools/trace/cpu_mxfp4_vnni.cpp (exports
                   ggml_vec_dot_mxfp4_q8_0; needs an AVX512VL+VNNI host to run)
+                - libref_f32_experts.so <- tools/engine/f32_experts.cpp with oracle/ref_f32_experts_shim.cpp
+                  (exports ref_glu: the reference executor's own activation stage)
                 - test_expert_dispatch  <- tests/test_expert_dispatch.cpp linked against this
                   repository's ExpertPlan (unified-memory-scheduler_amd/host/expert_dispatch.cpp)
               The reference build is skipped (with a message) when REF_ROOT is absent.
@@ -51,6 +53,10 @@ def build_reference() -> list[Path]:
          "-mavx512vnni", "-mavxvnni", "-ffp-contract=off", str(REF_ROOT / "tools/trace/cpu_mxfp4_vnni.cpp"),
          "-o", str(vnni)])
     built.append(vnni)
+    f32 = REF_OUT / "libref_f32_experts.so"
+    run(["g++", "-O2", "-std=c++20", "-fPIC", "-shared", "-ffp-contract=off", f"-I{REF_ROOT / 'tools/engine'}",
+         str(HERE / "ref_f32_experts_shim.cpp"), str(REF_ROOT / "tools/engine/f32_experts.cpp"), "-o", str(f32)])
+    built.append(f32)
     dispatch = REF_OUT / "test_expert_dispatch"
     run(["g++", "-O2", "-std=c++20", "-ffp-contract=off", "-pthread", f"-I{HOST_DIR}",
          str(REF_ROOT / "tests/test_expert_dispatch.cpp"), str(HOST_DIR / "expert_dispatch.cpp"), "-o", str(dispatch)])

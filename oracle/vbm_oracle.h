@@ -10,13 +10,20 @@
  * points (AVX2/FMA/F16C or AVX-512 VNNI, multithreaded) must return identical bits and are
  * checked against the scalar form by the tests.
  *
- * Functions marked "parity unpinned" below have no golden vector, known answer or buildable
- * reference in the reference repository for their fp32 rounding order (their integer parts and
- * closed forms are still tested):
- *   orc_vec_dot_q8_0_q8_0  (fp32 order unpinned; integer block dot pinned by brute force)
- *   orc_vec_dot_f32        (fp32 order unpinned)
- *   orc_softmax_selected   (ggml soft_max expf bits unpinned)
- *   orc_glu                (ggml swiglu_oai / swiglu expf bits unpinned)
+ * Parts marked "parity unpinned" below have no golden vector, known answer or buildable reference
+ * in the reference repository (they live in upstream ggml, which it does not vendor); what the
+ * mathematics fixes is still tested for them:
+ *   orc_vec_dot_q8_0_q8_0  chain structure across blocks unpinned (one FMA chain per lane, as the
+ *                          upstream AVX2 dot); integer block dot pinned by brute force, lane
+ *                          arithmetic + tree bit-equal to the reference's compiled MXFP4 dot on
+ *                          equivalent inputs, result within its float64 error bound
+ *   orc_vec_dot_f32        summation order unpinned (router logits come from upstream
+ *                          ggml_mul_mat); within its float64 error bound, hand-derived order
+ *                          probes; router ids equal the float64 top-k wherever the gaps exceed
+ *                          the worst-case error of any fp32 order
+ *   orc_softmax_selected   ggml soft_max expf bits unpinned (closed forms tested)
+ * orc_glu is pinned bit for bit against the reference executor's activation
+ * (tools/engine/f32_experts.cpp:68-73) compiled into oracle/_ref with the same libm.
  */
 #ifndef VBM_ORACLE_H
 #define VBM_ORACLE_H

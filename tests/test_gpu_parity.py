@@ -259,6 +259,30 @@ def test_router_ids_exact(gpu, orc):
     assert di.download(np.int32, 4).tolist() == [1, 2, 4, 7]
 
 
+@pytest.mark.parametrize("n_expert,hidden,top_k", [(32, 2880, 4), (128, 2048, 8)])
+def test_router_ids_equal_float64_topk_where_determined(gpu, orc, n_expert, hidden, top_k):
+    """The reference's router fp32 order (upstream ggml_mul_mat) is parity-unpinned; wherever the
+    float64 logits separate the top k + 1 by more than twice the worst-case error of any fp32
+    summation order, the device's ids must equal the float64 top-k (so they equal the reference's
+    whatever its order), and they equal the oracle's everywhere."""
+    from test_oracle import router_near_ties
+    rng = np.random.default_rng(190 + n_expert)
+    tokens = 256
+    w = (rng.standard_normal((n_expert, hidden)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((tokens, hidden)).astype(np.float32)
+    dw, dx = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x)
+    dl = gpu.DeviceBuffer(4 * tokens * n_expert)
+    di, dwt = gpu.DeviceBuffer(4 * tokens * top_k), gpu.DeviceBuffer(4 * tokens * top_k)
+    gpu.call("vbm_router_topk_softmax", dw.ptr, None, dx.ptr, hidden, dl.ptr, n_expert, tokens, top_k, di.ptr,
+             dwt.ptr, None)
+    ids = di.download(np.int32, (tokens, top_k))
+    want, determined = router_near_ties(w, x, top_k)
+    _, oids, _ = orc.router(router_w=w, x=x, n_expert=n_expert, n_tokens=tokens, top_k=top_k, hidden=hidden)
+    print(f"[router {n_expert}x{hidden}] near-tie fraction {1 - determined.mean():.4f}", flush=True)
+    assert np.array_equal(ids[determined], want[determined])
+    assert np.array_equal(ids, oids)
+
+
 def test_combine_bitwise_and_order(gpu, orc):
     y = gpu.synth_normal(4, 1, 0, 3 * 4 * 2880).reshape(3, 4, 2880) * np.float32(1e3)
     w = gpu.synth_normal(4, 2, 0, 12).reshape(3, 4)

@@ -223,12 +223,16 @@ def test_q8_block_lanes_brute_force(orc):
 
 
 @pytest.mark.skipif(not cpu_has_avx512vnni(), reason="oracle/_ref VNNI restatement needs AVX512VL+VNNI")
-def test_q8_0_dot_order_equals_reference_mxfp4_restatement(orc):
-    """The Q8_0 x Q8_0 dot's fp32 order (per-lane FMA chain over blocks, then hsum8) against the
-    reference's compiled MXFP4 restatement (cpu_mxfp4_vnni.cpp:49-68): Q8_0 weights that hold the
-    doubled e2m1 integers of an MXFP4 block with scale 2^(e-128) (an exact fp16), and zero weights
-    in the odd blocks (so the MXFP4 odd chain adds exact zeros), make both dots the same
-    arithmetic, so the results must agree bit for bit."""
+def test_q8_0_dot_lane_arithmetic_equals_reference_mxfp4_restatement(orc):
+    """The Q8_0 x Q8_0 dot's per-lane arithmetic (block scale product, int -> fp32, FMA into the
+    lane) and final hsum8 tree against the reference's compiled MXFP4 restatement
+    (cpu_mxfp4_vnni.cpp:49-68): Q8_0 weights that hold the doubled e2m1 integers of an MXFP4 block
+    with scale 2^(e-128) (an exact fp16), and zero weights in the odd blocks (so the MXFP4 odd chain
+    adds exact zeros), make both dots the same arithmetic, so the results must agree bit for bit.
+    This does NOT pin the chain structure across blocks: with every odd block zero, one FMA chain
+    per lane and the MXFP4 dot's even/odd chains give the same bits. The structure the oracle uses
+    (one chain per lane, upstream AVX2 ggml_vec_dot_q8_0_q8_0) is parity-unpinned: upstream ggml is
+    not in the reference; the float64 bound test below checks its arithmetic."""
     if not orc.REF_VNNI.exists():
         pytest.skip("oracle/_ref not built (reference sources absent)")
     ref = C.CDLL(str(orc.REF_VNNI))
@@ -431,3 +435,124 @@ def test_reference_dispatch_test_passes_against_expert_plan(orc):
     proc = subprocess.run([str(orc.REF_DISPATCH_TEST)], capture_output=True, text=True, timeout=60)
     assert proc.returncode == 0, proc.stderr
     assert "passed" in proc.stdout
+
+
+U32 = 2.0 ** -24
+
+
+def gamma(n: int) -> float:
+    """Higham's gamma_n = n u / (1 - n u) for fp32 (u = 2^-24): |computed - exact| <= gamma_n *
+    sum |terms| for any sum of the terms evaluated with at most n roundings along each term's path."""
+    return n * U32 / (1.0 - n * U32)
+
+
+def test_q8_0_dot_within_float64_bound(orc):
+    """orc_vec_dot_q8_0_q8_0 against the exact value sum_b fp16(dx_b) fp16(dy_b) sum_i x_i y_i'
+    (float64; y_i' = the VPSIGNB-contract activation), within the rigorous bound of the oracle's
+    structure: per block one rounding of the scale product, one FMA per block along each of the 8
+    lane chains, then 3 tree levels, so every term meets at most nb + 4 roundings. A dropped block,
+    a wrong sign or a transposed scale moves the result far outside it."""
+    lib = orc.load()
+    rng = np.random.default_rng(88)
+    worst = 0.0
+    for n in (64, 768, 2048, 2880):
+        nb = n // 32
+        for _ in range(30):
+            w = np.empty((nb, 34), np.uint8)
+            a = np.empty((nb, 34), np.uint8)
+            w[:, :2] = np.float16(rng.uniform(1e-3, 1e-2, nb)).view(np.uint8).reshape(nb, 2)
+            a[:, :2] = np.float16(rng.uniform(1e-3, 1e-1, nb)).view(np.uint8).reshape(nb, 2)
+            wq = rng.integers(-128, 128, (nb, 32)).astype(np.int8)
+            aq = rng.integers(-128, 128, (nb, 32)).astype(np.int8)
+            w[:, 2:], a[:, 2:] = wq.view(np.uint8), aq.view(np.uint8)
+            dw = w[:, :2].copy().view(np.float16).astype(np.float64).ravel()
+            da = a[:, :2].copy().view(np.float16).astype(np.float64).ravel()
+            # VPSIGNB contract: |w| (w = -128 reads as 128) times a negated where w < 0 (-128 stays)
+            mag = np.where(wq == -128, 128, np.abs(wq.astype(np.int64)))
+            neg = np.where(aq == -128, -128, -aq.astype(np.int64))
+            signed = np.where(wq < 0, neg, np.where(wq == 0, 0, aq.astype(np.int64)))
+            lanes = (mag * signed).reshape(nb, 8, 4).sum(axis=2)
+            terms = (dw * da)[:, None] * lanes
+            exact = float(terms.sum())
+            got = lib.orc_vec_dot_q8_0_q8_0(n, w.ctypes.data, a.ctypes.data)
+            bound = gamma(nb + 4) * float(np.abs(terms).sum())
+            assert abs(got - exact) <= bound, (n, got, exact, bound)
+            worst = max(worst, abs(got - exact) / bound)
+    print(f"[q8 dot] worst error / bound = {worst:.3f}")
+
+
+def test_f32_dot_within_float64_bound(orc):
+    """orc_vec_dot_f32 (router logits) against the exact float64 dot, within the rigorous bound of
+    its structure (an FMA chain of n/32 steps per accumulator, 5 reduction levels)."""
+    lib = orc.load()
+    rng = np.random.default_rng(89)
+    for n in (32, 2048, 2880):
+        for _ in range(50):
+            x = rng.standard_normal(n).astype(np.float32)
+            y = (rng.standard_normal(n) * 0.02).astype(np.float32)
+            terms = x.astype(np.float64) * y.astype(np.float64)
+            got = lib.orc_vec_dot_f32(n, x.ctypes.data, y.ctypes.data)
+            bound = gamma(n // 32 + 5) * float(np.abs(terms).sum())
+            assert abs(got - float(terms.sum())) <= bound, (n, got)
+
+
+def router_near_ties(w, x, top_k):
+    """Float64 router logits and, per token, whether its top-k (ids and order) is determined for
+    every fp32 evaluation order: all gaps between consecutive logits among the top k + 1 exceed
+    twice gamma_H * sum |w_ij x_j| (the largest error any fp32 summation order can make)."""
+    prod = np.abs(w.astype(np.float64))[None, :, :] * np.abs(x.astype(np.float64))[:, None, :]
+    bound = gamma(w.shape[1]) * prod.sum(axis=2)
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    order = np.argsort(-exact, axis=1, kind="stable")
+    top = np.take_along_axis(exact, order[:, : top_k + 1], axis=1)
+    margin = 2 * bound.max(axis=1)
+    determined = np.all(top[:, :-1] - top[:, 1:] > margin[:, None], axis=1)
+    return order[:, :top_k].astype(np.int32), determined
+
+
+@pytest.mark.parametrize("n_expert,hidden,top_k", [(32, 2880, 4), (128, 2880, 4), (128, 2048, 8)])
+def test_router_ids_equal_float64_topk_where_determined(orc, n_expert, hidden, top_k):
+    """The reference computes router logits with upstream ggml_mul_mat (build_lora_mm,
+    llama-b11669-hybrid-experts.patch:1357-1385), whose fp32 order is parity-unpinned (upstream
+    ggml is not in the reference). What the mathematics fixes: wherever the top-k + 1 float64
+    logits are separated by more than twice the worst-case fp32 error of ANY summation order, every
+    order, the reference's included, picks the float64 top-k; the oracle's ids must equal it there.
+    Router weights N(0, 0.02) and hidden states N(0, 1) as in configs 0 and 1; the near-tie
+    fraction (tokens whose ids the bound cannot fix) is reported."""
+    rng = np.random.default_rng(90 + n_expert + top_k)
+    tokens = 512
+    w = (rng.standard_normal((n_expert, hidden)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((tokens, hidden)).astype(np.float32)
+    _, ids, _ = orc.router(router_w=w, x=x, n_expert=n_expert, n_tokens=tokens, top_k=top_k, hidden=hidden)
+    want, determined = router_near_ties(w, x, top_k)
+    print(f"[router {n_expert}x{hidden} top{top_k}] near-tie fraction {1 - determined.mean():.4f}")
+    assert determined.mean() > 0.5
+    assert np.array_equal(ids[determined], want[determined])
+
+
+def test_glu_bitwise_equals_reference_f32_experts(orc):
+    """orc_glu against the reference executor's own activation stage (tools/engine/f32_experts.cpp:
+    68-73, compiled in oracle/_ref with the host libm), bit for bit, for SwiGLU-OAI (alpha 1.702,
+    limit 7: values on both sides of the clamps) and SiLU."""
+    path = orc.HERE / "_ref" / "libref_f32_experts.so"
+    if not path.exists():
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    ref = C.CDLL(str(path))
+    ref.ref_glu.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64]
+    ref.ref_glu.restype = C.c_int
+    rng = np.random.default_rng(91)
+    n = 20000
+    g = (rng.standard_normal(n) * 6).astype(np.float32)
+    u = (rng.standard_normal(n) * 6).astype(np.float32)
+    edges = np.array([7.0, -7.0, 6.9999995, 7.0000005, -7.0000005, 30.0, -30.0, 88.0, -88.0, 1e-30, -1e-30, 1.0,
+                      -1.0], np.float32)
+    g[: edges.size], u[: edges.size] = edges, edges[::-1]
+    g[g == 0] = 1.0
+    u[u == 0] = 1.0
+    for activation in (0, 1):
+        want = np.empty(n, np.float32)
+        assert ref.ref_glu(activation, g.ctypes.data, u.ctypes.data, want.ctypes.data, n) == 0
+        got = orc.glu(activation, g, u)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), activation
+        if activation == 1:   # the clamps are active on this data (a dropped clamp fails above)
+            assert np.any(g > 7) and np.any(np.abs(u) > 7)
