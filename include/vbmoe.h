@@ -170,12 +170,30 @@ vbm_status vbm_quantize_q8_0(const float * x, int64_t n_rows, int64_t k, int64_t
  * - dst: fp32 [rows, n_ids, n_tokens] contiguous.
  * - order: VBM_ORDER_EXACT or VBM_ORDER_FAST.
  * Uses the device grouping pass (vbm_group_by_expert) so every expert's weights stream once per
- * call, whatever the number of tokens routed to it. */
+ * call, whatever the number of tokens routed to it. Rows of an id outside [-1, n_as), and rows of
+ * a routed expert whose expert_to_slot entry is -1 (when no host copy was given to check), come
+ * out NaN: the reference asserts on both (hybrid-experts.patch:622; quantized_cuda.cu:224-227).
+ * Device scratch: the library keeps one per (device, stream), grown stream-ordered only when a
+ * call needs more than any earlier call on that stream, so steady-state calls allocate nothing
+ * (a call under graph capture must not be the one that grows it); vbm_stream_destroy releases it. */
 vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot,
                           const int32_t * expert_to_slot_host, int64_t n_as,
                           int b_type, const void * b, int64_t b_ne1,
                           const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride,
                           const float * bias, float * dst, int order, void * stream);
+
+/* The same operator over caller-owned device scratch (the ownership of the reference's executor,
+ * whose buffers live as long as it does, tools/engine/quantized_cuda.cu:387-400): bytes needed
+ * for a call of this shape, then the call itself with `workspace` of at least that size. The
+ * workspace holds nothing between calls; calls that share one must not overlap. */
+vbm_status vbm_mul_mat_id_workspace(const vbm_bank * bank, int64_t n_as, int64_t b_ne1, int64_t n_ids,
+                                    int64_t n_tokens, int order, size_t * bytes);
+vbm_status vbm_mul_mat_id_ws(const vbm_bank * bank, const int32_t * expert_to_slot,
+                             const int32_t * expert_to_slot_host, int64_t n_as,
+                             int b_type, const void * b, int64_t b_ne1,
+                             const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride,
+                             const float * bias, float * dst, int order, void * workspace,
+                             size_t workspace_bytes, void * stream);
 
 /* GGML_OP_ADD_ID: y[:, r, t] += bias[:, ids[r,t]] for ids != -1 (rows x n_ids x n_tokens). */
 vbm_status vbm_add_id(float * y, const float * bias, const int32_t * ids, int64_t rows,
@@ -202,7 +220,8 @@ vbm_status vbm_router_topk_softmax(const float * router_w, const float * router_
  * counting sort of the (token, rank) pairs by expert.
  *   counts[n_as], offsets[n_as + 1] (exclusive prefix), rows[n_ids*n_tokens] = token*n_ids+rank
  *   listed expert by expert, token-major and rank-minor within an expert. -1 ids are skipped.
- * Invalid ids (outside [-1, n_as)) set *error_flag (device int, optional) to 1. */
+ * Invalid ids (outside [-1, n_as)) set *error_flag (device int, optional) to 1; otherwise it is
+ * set to 0. Device scratch is the per-stream scratch of vbm_mul_mat_id. */
 vbm_status vbm_group_by_expert(const int32_t * ids, int64_t n_ids, int64_t n_tokens,
                                int64_t ids_stride, int64_t n_as, int32_t * counts,
                                int32_t * offsets, int32_t * rows, int32_t * error_flag,

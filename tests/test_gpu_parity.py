@@ -470,3 +470,35 @@ def test_glu_matches_oracle(gpu, orc, activation):
     print(f"[glu act={activation}] max ulp {float(ulp.max()):.1f}, exact fraction {float(np.mean(got == ref)):.4f}",
           flush=True)
     assert ulp.max() <= 2
+
+
+@pytest.mark.parametrize("order,tokens", [(0, 12), (1, 96)])
+def test_mul_mat_id_caller_workspace_matches(gpu, orc, order, tokens):
+    """vbm_mul_mat_id_ws over a caller workspace of the size vbm_mul_mat_id_workspace reports is
+    bit-identical to vbm_mul_mat_id (library scratch) and to the oracle in the exact order; a
+    workspace one byte short is rejected before any work is enqueued."""
+    k, rows, experts, n_ids = 512, 128, 6, 2
+    rng = np.random.default_rng(61 + order)
+    w = H.synth_weights(H.Q8, 61, 1, experts, rows, k)
+    bank = H.make_bank(H.Q8, w, experts, rows, k)
+    ids = np.stack([rng.choice(experts, n_ids, replace=False) for _ in range(tokens)]).astype(np.int32)
+    x = gpu.synth_normal(61, 2, 0, tokens * k).reshape(tokens, 1, k)
+    ref = H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, ids, n_ids, order=order)
+    need = C.c_size_t()
+    gpu.call("vbm_mul_mat_id_workspace", bank.handle, experts, 1, n_ids, tokens, order, C.byref(need))
+    assert need.value > 0
+    ws = gpu.DeviceBuffer(need.value)
+    dx, di = gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer.from_array(ids)
+    dst = gpu.DeviceBuffer(tokens * n_ids * rows * 4)
+    gpu.call("vbm_mul_mat_id_ws", bank.handle, None, None, experts, gpu.TYPE_F32, dx.ptr, 1, di.ptr, n_ids, tokens,
+             n_ids, None, dst.ptr, order, ws.ptr, need.value, None)
+    gpu.call("vbm_stream_synchronize", None)
+    got = dst.download(np.float32, (tokens, n_ids, rows))
+    assert H.bits_equal(got, ref)
+    if order == 0:
+        want = orc.mul_mat_id(8, w, k, rows, experts, 0, x, 1, ids, n_ids, tokens, n_ids, threads=8)
+        assert H.bits_equal(got, want)
+    with pytest.raises(gpu.VbmError, match="workspace too small"):
+        gpu.call("vbm_mul_mat_id_ws", bank.handle, None, None, experts, gpu.TYPE_F32, dx.ptr, 1, di.ptr, n_ids, tokens,
+                 n_ids, None, dst.ptr, order, ws.ptr, need.value - 1, None)
+    bank.destroy()

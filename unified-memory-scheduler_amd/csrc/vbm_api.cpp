@@ -95,7 +95,13 @@ vbm_status vbm_stream_create(void ** stream) {
     });
 }
 vbm_status vbm_stream_destroy(void * stream) {
-    return guarded([&] { if (stream) check_hip(hipStreamDestroy(as_stream(stream)), "hipStreamDestroy"); });
+    return guarded([&] {
+        if (!stream) return;
+        check_hip(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+        release_stream_scratch(as_stream(stream));
+        check_hip(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+        check_hip(hipStreamDestroy(as_stream(stream)), "hipStreamDestroy");
+    });
 }
 vbm_status vbm_stream_synchronize(void * stream) {
     return guarded([&] { check_hip(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize"); });

@@ -255,4 +255,18 @@ struct DecodeDownParams {
 };
 void launch_decode_down(const DecodeDownParams & d, hipStream_t stream);
 
+// Ops-API device scratch reused per (device, stream); see vbm_ops.cpp.
+void * stream_scratch(hipStream_t s, size_t bytes);
+void release_stream_scratch(hipStream_t s);   // before the stream is destroyed
+
+// GGML_OP_MUL_MAT_ID over a caller-provided scratch of mul_mat_id_scratch_bytes().
+void check_mul_mat_id_shape(const vbm_bank & bank, int64_t n_as, int64_t b_ne1, int64_t n_ids, int64_t n_tokens,
+                            int64_t ids_stride, int order);
+size_t mul_mat_id_scratch_bytes(const vbm_bank & bank, int64_t n_as, int64_t b_ne1, int64_t n_ids, int64_t n_tokens,
+                                int order);
+void mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot, const int32_t * expert_to_slot_host, int64_t n_as,
+                int b_type, const void * b, int64_t b_ne1, const int32_t * ids, int64_t n_ids, int64_t n_tokens,
+                int64_t ids_stride, const float * bias, float * dst, int order, uint8_t * scratch, size_t scratch_bytes,
+                hipStream_t s);
+
 }  // namespace vbm

@@ -2,7 +2,10 @@
 #include "vbm_internal.hpp"
 
 #include <algorithm>
+#include <map>
 #include <memory>
+#include <mutex>
+#include <utility>
 #include <vector>
 
 using namespace vbm;
@@ -148,6 +151,137 @@ void prefill_pass(const vbm_moe_layer_desc & d, const int32_t * expert_to_slot, 
     if (events) check_hip(hipEventRecord(static_cast<hipEvent_t>(events[3]), s), "hipEventRecord");
 }
 
+// Per-(device, stream) scratch reused by the ops API entry points that need device scratch
+// (vbm_mul_mat_id, vbm_group_by_expert): it grows, stream-ordered, only when a call needs more
+// than any earlier call on that stream, so steady-state calls allocate nothing. Calls on one
+// stream are ordered, so they may share it; other streams get their own.
+namespace {
+struct ScratchCache {
+    std::mutex mu;
+    std::map<std::pair<int, hipStream_t>, std::pair<void *, size_t>> entries;   // (device, stream) -> (ptr, bytes)
+};
+ScratchCache & scratch_cache() {
+    static ScratchCache cache;
+    return cache;
+}
+}  // namespace
+
+void * stream_scratch(hipStream_t s, size_t bytes) {
+    int device = 0;
+    check_hip(hipGetDevice(&device), "hipGetDevice");
+    ScratchCache & c = scratch_cache();
+    std::lock_guard<std::mutex> lock(c.mu);
+    auto & e = c.entries[{device, s}];
+    if (e.second < bytes) {
+        if (e.first) check_hip(hipFreeAsync(e.first, s), "scratch release");
+        e = {nullptr, 0};
+        const size_t cap = std::max<size_t>(bytes + (bytes >> 2), size_t(1) << 20);
+        check_hip(hipMallocAsync(&e.first, cap, s), "scratch");
+        e.second = cap;
+    }
+    return e.first;
+}
+
+void release_stream_scratch(hipStream_t s) {
+    int device = 0;
+    check_hip(hipGetDevice(&device), "hipGetDevice");
+    ScratchCache & c = scratch_cache();
+    std::lock_guard<std::mutex> lock(c.mu);
+    auto it = c.entries.find({device, s});
+    if (it == c.entries.end()) return;
+    if (it->second.first) check_hip(hipFreeAsync(it->second.first, s), "scratch release");
+    c.entries.erase(it);
+}
+
+void check_mul_mat_id_shape(const vbm_bank & bank, int64_t n_as, int64_t b_ne1, int64_t n_ids, int64_t n_tokens,
+                            int64_t ids_stride, int order) {
+    require(order == VBM_ORDER_EXACT || order == VBM_ORDER_FAST, "unknown order");
+    require(n_ids > 0 && n_tokens > 0 && (b_ne1 == 1 || b_ne1 == n_ids), "b_ne1 must be 1 or n_ids");
+    require(ids_stride >= n_ids, "ids stride must be >= n_ids");
+    require(n_as > 0 && n_as <= 1024, "n_as must be in 1..1024");
+    (void)bank;
+}
+
+size_t mul_mat_id_scratch_bytes(const vbm_bank & bank, int64_t n_as, int64_t b_ne1, int64_t n_ids, int64_t n_tokens,
+                                int order) {
+    const int64_t entries = n_ids * n_tokens, n_b = b_ne1 * n_tokens;
+    if (order == VBM_ORDER_FAST && gemm_pays(n_tokens, n_ids, n_as)) {
+        const GemmRowLayout gl{bank.nb, bank.type};
+        return align_up(static_cast<size_t>(n_b * gl.stride())) + align_up(group_workspace_bytes(n_as, entries)) +
+               gemm_tiles_bytes(n_as, entries);
+    }
+    const XrowLayout lay{bank.nb, bank.type};
+    return align_up(static_cast<size_t>(n_b * lay.stride())) + group_workspace_bytes(n_as, entries);
+}
+
+void mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot, const int32_t * expert_to_slot_host, int64_t n_as,
+                int b_type, const void * b, int64_t b_ne1, const int32_t * ids, int64_t n_ids, int64_t n_tokens,
+                int64_t ids_stride, const float * bias, float * dst, int order, uint8_t * scratch, size_t scratch_bytes,
+                hipStream_t s) {
+    require(bank && b && ids && dst && scratch, "null buffer");
+    require(b_type == VBM_TYPE_F32 || b_type == VBM_TYPE_Q8_0, "b must be F32 or Q8_0");
+    check_mul_mat_id_shape(*bank, n_as, b_ne1, n_ids, n_tokens, ids_stride, order);
+    require(expert_to_slot != nullptr || n_as <= bank->n_slots, "identity map needs n_as <= bank slots");
+    require(scratch_bytes >= mul_mat_id_scratch_bytes(*bank, n_as, b_ne1, n_ids, n_tokens, order), "workspace too small");
+    if (expert_to_slot_host) validate_ids_on_host(ids, n_ids, n_tokens, ids_stride, n_as, expert_to_slot_host, s);
+    const int64_t entries = n_ids * n_tokens;
+    const int64_t n_b = b_ne1 * n_tokens;
+    if (order == VBM_ORDER_FAST && gemm_pays(n_tokens, n_ids, n_as)) {
+        const GemmRowLayout gl{bank->nb, bank->type};
+        const size_t q_bytes = align_up(static_cast<size_t>(n_b * gl.stride()));
+        const size_t g_bytes = align_up(group_workspace_bytes(n_as, entries));
+        uint8_t * q = scratch;
+        const GroupBuffers g = carve_group(q + q_bytes, n_as, entries);
+        if (b_type == VBM_TYPE_F32)
+            launch_gemm_rows_from_f32(static_cast<const float *>(b), n_b, bank->k, bank->k, gl, q, s);
+        else
+            launch_gemm_rows_from_q8(static_cast<const uint8_t *>(b), n_b, bank->nb * 34, gl, q, s);
+        launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
+        init_dst(dst, ids, n_ids, n_tokens, ids_stride, n_as, bank->rows, s);
+        GemmParams p{};
+        p.bank = bank;
+        p.expert_to_slot = expert_to_slot;
+        p.rows_in = q;
+        p.lay = gl;
+        p.n_ids = n_ids;
+        p.b_ne1 = b_ne1;
+        p.n_as = n_as;
+        p.n_entries = entries;
+        p.group = g;
+        p.tiles = q + q_bytes + g_bytes;
+        p.bias = bias;
+        p.dst = dst;
+        p.epilogue = 0;
+        p.flagged_rows = b_type != VBM_TYPE_F32;
+        launch_grouped_gemm(p, s);
+        return;
+    }
+    const XrowLayout lay{bank->nb, bank->type};
+    const size_t q_bytes = align_up(static_cast<size_t>(n_b * lay.stride()));
+    uint8_t * q = scratch;
+    const GroupBuffers g = carve_group(q + q_bytes, n_as, entries);
+    if (b_type == VBM_TYPE_F32)
+        launch_quantize_expand(static_cast<const float *>(b), n_b, bank->k, bank->k, lay, q, nullptr, s);
+    else
+        launch_expand_q8(static_cast<const uint8_t *>(b), n_b, bank->nb * 34, lay, q, s);
+    launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
+    init_dst(dst, ids, n_ids, n_tokens, ids_stride, n_as, bank->rows, s);
+    GemvArgs a{};
+    a.bank = bank;
+    a.expert_to_slot = expert_to_slot;
+    a.xrows = q;
+    a.n_ids = n_ids;
+    a.b_ne1 = b_ne1;
+    a.group = g;
+    a.max_active = std::min<int64_t>(n_as, entries);
+    a.max_per_expert = entries;
+    a.bias = bias;
+    a.dst = dst;
+    a.epilogue = 0;
+    a.may_have_neg128 = b_type != VBM_TYPE_F32;   // ggml Q8_0 rows may hold -128 codes
+    launch_gemv(a, s);
+}
+
 }  // namespace vbm
 
 namespace {
@@ -252,21 +386,39 @@ vbm_status vbm_group_by_expert(const int32_t * ids, int64_t n_ids, int64_t n_tok
                                int32_t * counts, int32_t * offsets, int32_t * rows, int32_t * error_flag, void * stream) {
     return guarded([&] {
         require(ids && counts && offsets && rows, "null buffer");
-        const hipStream_t s = as_stream(stream);
-        void * scratch = nullptr;
         require(n_as > 0 && n_ids > 0 && n_tokens > 0, "grouping sizes must be positive");
+        const hipStream_t s = as_stream(stream);
         const int64_t chunk_ints = group_chunk_ints(n_as, n_ids * n_tokens);
-        check_hip(hipMallocAsync(&scratch, sizeof(int32_t) * (n_as + 2 + chunk_ints + 8), s), "group scratch");
+        auto * scratch = static_cast<int32_t *>(stream_scratch(s, sizeof(int32_t) * (n_as + 2 + chunk_ints + 8)));
         GroupBuffers g{};
         g.counts = counts;
         g.offsets = offsets;
         g.rows = rows;
-        g.active = static_cast<int32_t *>(scratch);
+        g.active = scratch;
         g.n_active = g.active + n_as;
         g.chunk_counts = g.n_active + 2;
         g.error = error_flag ? error_flag : g.n_active + 1;
         launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
-        check_hip(hipFreeAsync(scratch, s), "group scratch free");
+    });
+}
+
+vbm_status vbm_mul_mat_id_workspace(const vbm_bank * bank, int64_t n_as, int64_t b_ne1, int64_t n_ids, int64_t n_tokens,
+                                    int order, size_t * bytes) {
+    return guarded([&] {
+        require(bank != nullptr && bytes != nullptr, "null argument");
+        check_mul_mat_id_shape(*bank, n_as, b_ne1, n_ids, n_tokens, n_ids, order);
+        *bytes = mul_mat_id_scratch_bytes(*bank, n_as, b_ne1, n_ids, n_tokens, order);
+    });
+}
+
+vbm_status vbm_mul_mat_id_ws(const vbm_bank * bank, const int32_t * expert_to_slot, const int32_t * expert_to_slot_host,
+                             int64_t n_as, int b_type, const void * b, int64_t b_ne1, const int32_t * ids, int64_t n_ids,
+                             int64_t n_tokens, int64_t ids_stride, const float * bias, float * dst, int order,
+                             void * workspace, size_t workspace_bytes, void * stream) {
+    return guarded([&] {
+        require(workspace != nullptr, "null workspace");
+        mul_mat_id(bank, expert_to_slot, expert_to_slot_host, n_as, b_type, b, b_ne1, ids, n_ids, n_tokens, ids_stride,
+                   bias, dst, order, static_cast<uint8_t *>(workspace), workspace_bytes, as_stream(stream));
     });
 }
 
@@ -275,78 +427,12 @@ vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot,
                           int64_t n_tokens, int64_t ids_stride, const float * bias, float * dst, int order,
                           void * stream) {
     return guarded([&] {
-        require(bank && b && ids && dst, "null buffer");
-        require(order == VBM_ORDER_EXACT || order == VBM_ORDER_FAST, "unknown order");
-        require(b_type == VBM_TYPE_F32 || b_type == VBM_TYPE_Q8_0, "b must be F32 or Q8_0");
-        require(n_ids > 0 && n_tokens > 0 && (b_ne1 == 1 || b_ne1 == n_ids), "b_ne1 must be 1 or n_ids");
-        require(ids_stride >= n_ids, "ids stride must be >= n_ids");
-        require(n_as > 0 && n_as <= 1024, "n_as must be in 1..1024");
-        require(expert_to_slot != nullptr || n_as <= bank->n_slots, "identity map needs n_as <= bank slots");
+        require(bank != nullptr, "null bank");
+        check_mul_mat_id_shape(*bank, n_as, b_ne1, n_ids, n_tokens, ids_stride, order);
         const hipStream_t s = as_stream(stream);
-        if (expert_to_slot_host) validate_ids_on_host(ids, n_ids, n_tokens, ids_stride, n_as, expert_to_slot_host, s);
-        const int64_t entries = n_ids * n_tokens;
-        const int64_t n_b = b_ne1 * n_tokens;
-        if (order == VBM_ORDER_FAST && gemm_pays(n_tokens, n_ids, n_as)) {
-            const GemmRowLayout gl{bank->nb, bank->type};
-            const size_t q_bytes = align_up(static_cast<size_t>(n_b * gl.stride()));
-            const size_t g_bytes = align_up(group_workspace_bytes(n_as, entries));
-            void * scratch = nullptr;
-            check_hip(hipMallocAsync(&scratch, q_bytes + g_bytes + gemm_tiles_bytes(n_as, entries), s), "mul_mat_id scratch");
-            uint8_t * q = static_cast<uint8_t *>(scratch);
-            const GroupBuffers g = carve_group(q + q_bytes, n_as, entries);
-            if (b_type == VBM_TYPE_F32)
-                launch_gemm_rows_from_f32(static_cast<const float *>(b), n_b, bank->k, bank->k, gl, q, s);
-            else
-                launch_gemm_rows_from_q8(static_cast<const uint8_t *>(b), n_b, bank->nb * 34, gl, q, s);
-            launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
-            init_dst(dst, ids, n_ids, n_tokens, ids_stride, n_as, bank->rows, s);
-            GemmParams p{};
-            p.bank = bank;
-            p.expert_to_slot = expert_to_slot;
-            p.rows_in = q;
-            p.lay = gl;
-            p.n_ids = n_ids;
-            p.b_ne1 = b_ne1;
-            p.n_as = n_as;
-            p.n_entries = entries;
-            p.group = g;
-            p.tiles = q + q_bytes + g_bytes;
-            p.bias = bias;
-            p.dst = dst;
-            p.epilogue = 0;
-            p.flagged_rows = b_type != VBM_TYPE_F32;
-            launch_grouped_gemm(p, s);
-            check_hip(hipFreeAsync(scratch, s), "mul_mat_id scratch free");
-            return;
-        }
-        const XrowLayout lay{bank->nb, bank->type};
-        const size_t q_bytes = static_cast<size_t>(n_b * lay.stride());
-        const size_t g_bytes = group_workspace_bytes(n_as, entries);
-        void * scratch = nullptr;
-        check_hip(hipMallocAsync(&scratch, align_up(q_bytes) + g_bytes, s), "mul_mat_id scratch");
-        uint8_t * q = static_cast<uint8_t *>(scratch);
-        const GroupBuffers g = carve_group(q + align_up(q_bytes), n_as, entries);
-        if (b_type == VBM_TYPE_F32)
-            launch_quantize_expand(static_cast<const float *>(b), n_b, bank->k, bank->k, lay, q, nullptr, s);
-        else
-            launch_expand_q8(static_cast<const uint8_t *>(b), n_b, bank->nb * 34, lay, q, s);
-        launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
-        init_dst(dst, ids, n_ids, n_tokens, ids_stride, n_as, bank->rows, s);
-        GemvArgs a{};
-        a.bank = bank;
-        a.expert_to_slot = expert_to_slot;
-        a.xrows = q;
-        a.n_ids = n_ids;
-        a.b_ne1 = b_ne1;
-        a.group = g;
-        a.max_active = std::min<int64_t>(n_as, entries);
-        a.max_per_expert = entries;
-        a.bias = bias;
-        a.dst = dst;
-        a.epilogue = 0;
-        a.may_have_neg128 = b_type != VBM_TYPE_F32;   // ggml Q8_0 rows may hold -128 codes
-        launch_gemv(a, s);
-        check_hip(hipFreeAsync(scratch, s), "mul_mat_id scratch free");
+        const size_t bytes = mul_mat_id_scratch_bytes(*bank, n_as, b_ne1, n_ids, n_tokens, order);
+        mul_mat_id(bank, expert_to_slot, expert_to_slot_host, n_as, b_type, b, b_ne1, ids, n_ids, n_tokens, ids_stride,
+                   bias, dst, order, static_cast<uint8_t *>(stream_scratch(s, bytes)), bytes, s);
     });
 }
 
