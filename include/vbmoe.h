@@ -195,6 +195,20 @@ vbm_status vbm_mul_mat_id_ws(const vbm_bank * bank, const int32_t * expert_to_sl
                              const float * bias, float * dst, int order, void * workspace,
                              size_t workspace_bytes, void * stream);
 
+/* MUL_MAT_ID without any allocation. No counterpart in the reference: it exists for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same kernels and results as vbm_mul_mat_id, minus the host-copy check of the
+ * map (a -1 entry for a routed expert gives NaN rows). Its device scratch is one fixed array of
+ * VBM_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends: a call whose shape needs more
+ * (vbm_mul_mat_id_workspace reports the need) fails with VBM_ERR_INVALID_ARGUMENT before anything
+ * is enqueued. Every call on one GPU shares that array, so calls that overlap on one GPU (on other
+ * streams or host threads) race; calls on one stream are ordered and do not. */
+#define VBM_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+vbm_status vbm_mul_mat_id_noalloc(const vbm_bank * bank, const int32_t * expert_to_slot, int64_t n_as,
+                                  int b_type, const void * b, int64_t b_ne1,
+                                  const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride,
+                                  const float * bias, float * dst, int order, void * stream);
+
 /* GGML_OP_ADD_ID: y[:, r, t] += bias[:, ids[r,t]] for ids != -1 (rows x n_ids x n_tokens). */
 vbm_status vbm_add_id(float * y, const float * bias, const int32_t * ids, int64_t rows,
                       int64_t n_ids, int64_t n_tokens, int64_t ids_stride, void * stream);

@@ -137,6 +137,7 @@ SIGNATURES = {
     "vbm_mul_mat_id": [vp, vp, vp, i64, C.c_int, vp, i64, vp, i64, i64, i64, vp, vp, C.c_int, vp],
     "vbm_mul_mat_id_workspace": [vp, i64, i64, i64, i64, C.c_int, C.POINTER(C.c_size_t)],
     "vbm_mul_mat_id_ws": [vp, vp, vp, i64, C.c_int, vp, i64, vp, i64, i64, i64, vp, vp, C.c_int, vp, C.c_size_t, vp],
+    "vbm_mul_mat_id_noalloc": [vp, vp, i64, C.c_int, vp, i64, vp, i64, i64, i64, vp, vp, C.c_int, vp],
     "vbm_add_id": [vp, vp, vp, i64, i64, i64, i64, vp],
     "vbm_glu": [C.c_int, vp, vp, vp, i64, i64, i64, i64, i64, C.c_float, C.c_float, vp],
     "vbm_router_topk_softmax": [vp, vp, vp, i64, vp, i64, i64, i64, vp, vp, vp],
