@@ -493,7 +493,7 @@ def policy_study(args, routes, n_slots, plan, group_bytes, live) -> dict:
                     w.token(routes[t])
                 w.request_end("limit")
         data = rt.read_trace(path)
-    out = {"trace_events": len(data.events)}
+    out = {"trace_events": len(data.route_layer)}
     names = ("classic", "lru", "ranked", "probation", "anchored", "lfu")
     for policy, name in enumerate(names):
         r = rt.replay_admission(data, n_slots, policy, 64, 1 if name == "lru" else 4, plan=plan)["all"]

@@ -403,14 +403,6 @@ typedef struct {
     double ram_gbps, pcie_gbps, gpu_expert_us, layer_sync_us;
     int staging_ram_passes;                  /* 0 or 2                                          */
     uint64_t static_device_expert_bytes;     /* the trace metadata's (measured_static)          */
-    /* Seeded replay (vrambridge-prefill-seed.py:133-154; lru, lfu, cost_aware): at the first
-     * held-out event the cache holds exactly these n_seed (layer index, expert) keys, whose bytes
-     * must fit the capacity; `frozen` then keeps it fixed (no admission). NULL / 0: no seed. */
-    const int32_t * seed_layer;
-    const int32_t * seed_expert;
-    int64_t n_seed;
-    int seeded;
-    int frozen;
 } vbm_residency_params;
 
 typedef struct {

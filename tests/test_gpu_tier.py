@@ -187,8 +187,8 @@ def test_tier_routing_trace_replays_to_the_same_decisions(gpu, tmp_path):
     vb.call("vbm_tier_set_trace", tiers[0], None)
     writer.close()
     data = rt.read_trace(path)
-    assert [list(e.experts) for e in data.events] == [sel for row in routed for sel in row]
-    assert [e.layer for e in data.events] == ids * len(routed)
+    assert [list(e) for e in data.route_experts] == [sel for row in routed for sel in row]
+    assert data.route_layer.tolist() == ids * len(routed)
     stats = rt.replay_admission(data, slots, policy, recent_window=8, margin=margin, plan=[(0, 3), (2, 5)])
     for tier in tiers:
         st = vb.TierStats()
@@ -197,7 +197,7 @@ def test_tier_routing_trace_replays_to_the_same_decisions(gpu, tmp_path):
         assert (st.dispatches, st.hits, st.admissions, st.evictions, st.staged) == \
             (a.dispatches, a.hits, a.admissions, a.evictions, a.staged)
         vb.call("vbm_tier_destroy", tier)
-    print(f"[tier trace] {len(data.events)} routes, hit rate {stats['all'].hit_rate:.3f} "
+    print(f"[tier trace] {len(data.route_layer)} routes, hit rate {stats['all'].hit_rate:.3f} "
           f"(train {stats['train'].hit_rate:.3f}, test {stats['test'].hit_rate:.3f})", flush=True)
 
 

@@ -5,8 +5,7 @@ reference, restated below), the reference analyzer's reading of a trace written 
 (tests/golden/routing_trace_small_report.json, made by tests/golden/make_routing_trace_golden.py),
 Python's JSON serializer as an independent rendering of the same compact sorted-key records, the
 admission restatement (oracle/admission.py) for replays, and the reference seed study's report of
-a trace and prefill summary written here (tests/golden/routing_trace_prefill_report.json, made by
-tests/golden/make_prefill_seed_golden.py).
+a trace written here.
 """
 import copy
 import hashlib
@@ -205,11 +204,11 @@ def test_writer_sorts_layers_and_token_strides(rt, tmp_path):
     assert meta["layers"][0]["tensor_types"] == ["f32", "q8_0"]
     assert meta["static_device_expert_bytes"] == 24
     data = rt.read_trace(path)
-    assert [e.experts for e in data.events] == [(0, 1), (0,), (1, 2), (1,), (1, 3), (2,)]
+    assert data.route_experts == [(0, 1), (0,), (1, 2), (1,), (1, 3), (2,)]
     # the reference analyzer test of the same shape: 3 calls, 32 cold bytes, gpu fraction 12/44
-    test_calls = sum(len(e.experts) for e in data.events_for("test"))
-    cold = sum(len(e.experts) * data.layers[e.layer].host_size for e in data.events_for("test"))
-    total = sum(len(e.experts) * data.layers[e.layer].size for e in data.events_for("test"))
+    test_calls = sum(len(e) for _, e in data.routes("test"))
+    cold = sum(len(e) * data.layers[l].host_bytes for l, e in data.routes("test"))
+    total = sum(len(e) * data.layers[l].bytes for l, e in data.routes("test"))
     assert (test_calls, cold) == (3, 32) and abs(1 - cold / total - 12 / 44) < 1e-12
 
 
@@ -219,9 +218,10 @@ def test_writer_sorts_layers_and_token_strides(rt, tmp_path):
 
 def test_reader_counts(rt, tmp_path):
     data = rt.read_trace(dump(tmp_path, records()))
-    assert data.tokens_for("train") == 3 and data.tokens_for("test") == 3
-    assert len(data.events) == 12 and len(data.sha256) == 64
-    assert all(r.verified for r in data.requests.values())
+    assert data.decoded("train") == 3 and data.decoded("test") == 3
+    assert len(data.route_layer) == 12 and len(data.sha256) == 64
+    assert all(r.equivalence_checked for r in data.requests)
+    assert [(r.first_route, r.end_route) for r in data.requests] == [(0, 6), (6, 12)]
 
 
 def test_reader_rejects_incomplete_or_reordered(rt, tmp_path):
@@ -269,16 +269,16 @@ def test_reader_legacy_trace_is_not_verified(rt, tmp_path):
     for v in values:
         v.pop("token_sequence_equivalent", None)
     data = rt.read_trace(dump(tmp_path, values))
-    assert not any(r.verified for r in data.requests.values())
+    assert not any(r.equivalence_checked for r in data.requests)
 
 
 def test_hotset_uses_training_counts_only(rt):
-    layers = {0: rt.Layer(3, 1, 10, 10)}
-    assert rt.hotset(rt.Counter({(0, 0): 10, (0, 1): 2}), layers, 10) == [(0, 0)]
-    layers = {0: rt.Layer(3, 1, 10, 10), 1: rt.Layer(3, 1, 25, 25)}
+    layers = {0: rt.LayerSpec(3, 1, 10, 10)}
+    assert rt.hot_experts(rt.Counter({(0, 0): 10, (0, 1): 2}), layers, 10) == [(0, 0)]
+    layers = {0: rt.LayerSpec(3, 1, 10, 10), 1: rt.LayerSpec(3, 1, 25, 25)}
     counts = rt.Counter({(1, 0): 5, (0, 2): 5, (0, 1): 4, (1, 1): 9})
     # budget 40: (1,1) 25 B; then count 5 ties by size: (0,2) 10 B; (1,0) no longer fits; (0,1) does not
-    assert rt.hotset(counts, layers, 40) == [(1, 1), (0, 2)]
+    assert rt.hot_experts(counts, layers, 40) == [(1, 1), (0, 2)]
 
 
 # ------------------------------------------------------------------------------------------------
@@ -293,10 +293,10 @@ def test_golden_trace_bytes_and_reference_reading(rt, tmp_path):
     assert hashlib.sha256(path.read_bytes()).hexdigest() == report["trace_sha256"]
     data = rt.read_trace(path)
     assert data.sha256 == report["trace_sha256"]
-    assert len(data.events) == report["events"]
-    assert {"train": data.tokens_for("train"), "test": data.tokens_for("test")} == report["tokens"]
+    assert len(data.route_layer) == report["events"]
+    assert {"train": data.decoded("train"), "test": data.decoded("test")} == report["tokens"]
     assert report["counts"] == {"layers": len(data.layers), "requests": len(data.requests),
-                                "train_tokens": data.tokens_for("train"), "test_tokens": data.tokens_for("test")}
+                                "train_tokens": data.decoded("train"), "test_tokens": data.decoded("test")}
     assert report["observation_equivalence"]["all_requests_verified"] is True
     plan = rt.plan_from_trace(data, mk.CAPACITY_EXPERTS)
     assert len(plan) == mk.CAPACITY_EXPERTS
@@ -352,16 +352,16 @@ def test_replay_admission_matches_restatement(rt, tmp_path, policy):
     for layer, expert in plan:
         py.seed(layer, expert)
     hits = admissions = evictions = staged = 0
-    for event in data.events:
-        h, adm = py.admit(event.layer, list(event.experts))
+    for layer, experts in data.routes():
+        h, adm = py.admit(layer, list(experts))
         hits += sum(h)
         admissions += len(adm)
         evictions += sum(1 for _, _, ev in adm if ev >= 0)
-        staged += sum(1 for e in event.experts if py.slot_map[event.layer * 16 + e] < 0)
+        staged += sum(1 for e in experts if py.slot_map[layer * 16 + e] < 0)
     a = stats["all"]
     assert (a.dispatches, a.hits, a.admissions, a.evictions, a.staged) == \
-        (len(data.events), hits, admissions, evictions, staged)
-    assert a.lookups == 2 * len(data.events) and a.admissions > 0
+        (len(data.route_layer), hits, admissions, evictions, staged)
+    assert a.lookups == 2 * len(data.route_layer) and a.admissions > 0
     assert stats["train"].dispatches + stats["test"].dispatches == a.dispatches
     assert stats["train"].hits + stats["test"].hits == a.hits
 
@@ -472,7 +472,7 @@ def test_prefill_summary_format_and_histograms(rt, tmp_path):
     assert not Path(str(summary) + ".part").exists()
     # the decode trace itself is unchanged by the prefill capture
     data = rt.read_trace(trace)
-    assert data.tokens_for("train") == 2 and data.tokens_for("test") == 1
+    assert data.decoded("train") == 2 and data.decoded("test") == 1
 
 
 def test_prefill_histogram_of_random_batches(rt, tmp_path):
@@ -540,92 +540,6 @@ def test_prefill_duplicate_expert_in_row(rt, vb, tmp_path):
             w.prefill_route(0, [[1, 2], [3, 3]])
 
 
-# ------------------------------------------------------------------------------------------------
-# the prompt-conditioned seed study against the reference study's own report (committed fixture)
-
-
-def test_prefill_seed_study_matches_reference_report(rt, tmp_path):
-    import make_prefill_seed_golden as mk
-    report = json.loads((GOLDEN / "routing_trace_prefill_report.json").read_text())
-    trace, summary = mk.write_trace(tmp_path / "p.jsonl", tmp_path / "p.json")
-    assert trace.read_bytes() == (GOLDEN / "routing_trace_prefill.jsonl").read_bytes()
-    assert summary.read_bytes() == (GOLDEN / "routing_trace_prefill_summary.json").read_bytes()
-    data = rt.read_trace(GOLDEN / "routing_trace_prefill.jsonl")
-    prefill = rt.read_prefill(GOLDEN / "routing_trace_prefill_summary.json", data)
-    for ident, want in report["prefill_read"].items():
-        got = prefill[ident]
-        assert sorted([l, e, c] for (l, e), c in got["counts"].items() if c) == want["counts"]
-        assert sorted([l, r] for l, r in got["rows"].items()) == want["rows"]
-        assert sorted([l, c] for l, c in got["coverage"].items()) == want["coverage"]
-    baseline = rt.read_baseline_plan(GOLDEN / "routing_trace_prefill_plan.txt", data)
-    ours = rt.prefill_seed_study(data, prefill, baseline, mk.COSTS["ram_gbps"], mk.COSTS["pcie_gbps"],
-                                 mk.COSTS["gpu_expert_us"])
-    for key in ("schema_version", "study", "capacity_bytes", "train_tokens", "test_tokens", "trace_sha256", "model",
-                "blend_weight", "costs"):
-        assert ours[key] == report[key], key
-    assert [r["id"] for r in ours["requests"]] == [r["id"] for r in report["requests"]]
-    checked = 0
-    for mine, ref in zip(ours["requests"], report["requests"]):
-        assert mine["partial_prefill_layers_using_training_prior"] == ref["partial_prefill_layers_using_training_prior"]
-        assert mine["decode_tokens"] == ref["decode_tokens"]
-        for policy, seeds in ref["policies"].items():
-            for seed, want in seeds.items():
-                got = mine["policies"][policy][seed]
-                assert set(got) == set(want)
-                for key, w in want.items():
-                    if isinstance(w, float):
-                        assert got[key] == pytest.approx(w, rel=1e-12, abs=0), (mine["id"], policy, seed, key)
-                    else:
-                        assert got[key] == w, (mine["id"], policy, seed, key)
-                checked += 1
-    assert checked == 2 * 2 * 5
-    # the fixture exercises what it is for: a partial layer falls back to the prior, and the
-    # prompt-conditioned seed differs from the training hot set
-    assert report["requests"][1]["partial_prefill_layers_using_training_prior"] == [3]
-    seeds = rt.prefill_seeds(data, prefill, baseline)
-    assert seeds["test-a"]["prompt_only"] != seeds["test-a"]["train_only"]
-
-
-@pytest.mark.parametrize("edit,match", [
-    (lambda d: d.update(collector_source_sha256="0" * 64), "provenance"),
-    (lambda d: d["requests"][0]["batches"][0]["expert_row_counts"].__setitem__(0, 99), "exceeds observed rows"),
-    (lambda d: d["requests"][0]["coverage"].pop(), "Missing prefill layer coverage"),
-    (lambda d: d["requests"].pop(), "request count"),
-    (lambda d: d["requests"][3]["coverage"][3].__setitem__("covers_all_prompt_rows", True), "coverage inconsistent"),
-])
-def test_read_prefill_rejections(rt, tmp_path, edit, match):
-    data = rt.read_trace(GOLDEN / "routing_trace_prefill.jsonl")
-    doc = json.loads((GOLDEN / "routing_trace_prefill_summary.json").read_text())
-    edit(doc)                                   # request 3 (test-b) observes part of its prompt at layer 3
-    path = tmp_path / "s.json"
-    path.write_text(json.dumps(doc))
-    with pytest.raises(ValueError, match=match):
-        rt.read_prefill(path, data)
-
-
-def test_seeded_replay_rejections(rt, vb):
-    data = rt.read_trace(GOLDEN / "routing_trace_prefill.jsonl")
-    prefill = rt.read_prefill(GOLDEN / "routing_trace_prefill_summary.json", data)
-    baseline = rt.read_baseline_plan(GOLDEN / "routing_trace_prefill_plan.txt", data)
-    big = {(l, e) for l in range(4) for e in range(16)}
-    events = [e for e in data.events if e.request == "test-a"]
-    params = vb.ResidencyParams(rt.RESIDENCY_POLICIES.index("cost_aware"), 0, 3, 64, 0, 64.0, 50.0, 0.0, 0.0, 0,
-                                data.metadata["static_device_expert_bytes"])
-    capacity = 12 * 13_253_760
-    with pytest.raises(vb.VbmError, match="exceeds the cache capacity"):
-        rt._seed_replay(data, events, big, baseline, capacity, params, True)
-    params.policy = rt.RESIDENCY_POLICIES.index("belady_hits")
-    with pytest.raises(vb.VbmError, match="lru, lfu or cost_aware"):
-        rt._seed_replay(data, events, baseline, baseline, capacity, params, True)
-    # frozen from the baseline: hits are exactly the routed experts inside the plan
-    params.policy = rt.RESIDENCY_POLICIES.index("cost_aware")
-    got = rt._seed_replay(data, events, baseline, baseline, capacity, params, False)
-    hits = sum(k in baseline for e in events for k in e.keys())
-    assert got["hit_fraction"] == hits / sum(len(e.experts) for e in events)
-    assert got["decode_admission_bytes"] == 0 and got["evictions"] == 0 and got["seed_change_upload_bytes"] == 0
-    assert rt.read_prefill(GOLDEN / "routing_trace_prefill_summary.json", data).keys() == prefill.keys()
-
-
 def test_belady_hits_is_optimal_by_exhaustive_search(rt):
     """belady_hits against an exhaustive oracle (as tests/test_routing_analysis.py:271-294 of the
     reference does): over every sequence of end-of-layer cache states (each a subset of at most
@@ -636,15 +550,15 @@ def test_belady_hits_is_optimal_by_exhaustive_search(rt):
     size = 10
     for trial in range(40):
         experts, active, slots, n_events = 5, 2, 2 + trial % 2, 7
-        layers = {0: rt.Layer(experts, active, size, size)}
-        requests = {"t": rt.Request("t", "test", "c", n_events, 1, n_events, True)}
-        events = [rt.Event("t", i, 0, tuple(int(e) for e in rng.choice(experts, active, replace=False)))
-                  for i in range(n_events)]
-        data = rt.Dataset({"static_device_expert_bytes": 0}, layers, requests, events)
+        layers = {0: rt.LayerSpec(experts, active, size, size)}
+        requests = [rt.RequestSpan("t", "test", "c", 1, n_events, n_events, True, 0, n_events)]
+        picks = [tuple(int(e) for e in rng.choice(experts, active, replace=False)) for _ in range(n_events)]
+        data = rt.RoutingTrace({"static_device_expert_bytes": 0}, layers, requests, np.zeros(n_events, np.int32),
+                               np.arange(n_events, dtype=np.int32), np.zeros(n_events, np.int32), picks)
         got = rt.replay_residency(data, "belady_hits", slots * size, 64.0, 50.0)
         best = {frozenset(): 0}
-        for ev in events:
-            keys = set(ev.experts)
+        for ev in picks:
+            keys = set(ev)
             nxt = {}
             for state, hits in best.items():
                 h = hits + len(keys & state)
@@ -655,4 +569,4 @@ def test_belady_hits_is_optimal_by_exhaustive_search(rt):
                         if nxt.get(s, -1) < h:
                             nxt[s] = h
             best = nxt
-        assert got["full_expert_hits"] == max(best.values()), (trial, [e.experts for e in events])
+        assert got["full_expert_hits"] == max(best.values()), (trial, picks)

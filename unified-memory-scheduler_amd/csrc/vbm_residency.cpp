@@ -238,10 +238,6 @@ vbm_status vbm_residency_replay(const vbm_residency_layer * layers, int64_t n_la
         require(std::isfinite(p->gpu_expert_us) && p->gpu_expert_us >= 0 && std::isfinite(p->layer_sync_us) &&
                     p->layer_sync_us >= 0, "GPU expert and layer-sync costs must be finite and nonnegative");
         require(p->staging_ram_passes == 0 || p->staging_ram_passes == 2, "staging RAM passes must be 0 or 2");
-        require(!p->seeded || p->policy == VBM_RESIDENCY_LRU || p->policy == VBM_RESIDENCY_LFU ||
-                    p->policy == VBM_RESIDENCY_COST_AWARE,
-                "a seeded replay needs the lru, lfu or cost_aware policy");
-        require(!p->seeded || p->n_seed == 0 || (p->n_seed > 0 && p->seed_layer && p->seed_expert), "invalid seed");
         for (int64_t l = 0; l < n_layers; ++l)
             require(layers[l].experts >= 1 && layers[l].bytes_per_expert >= 1 &&
                         layers[l].static_host_bytes_per_expert <= layers[l].bytes_per_expert,
@@ -297,17 +293,6 @@ vbm_status vbm_residency_replay(const vbm_residency_layer * layers, int64_t n_la
             for (int64_t i = 0; i < n_events; ++i)
                 for (const Key & k : ev[static_cast<size_t>(i)]) R.future[k].push_back(i);
         }
-        std::map<Key, uint64_t> seed;
-        if (p->seeded) {
-            uint64_t bytes = 0;
-            for (int64_t i = 0; i < p->n_seed; ++i) {
-                const int32_t l = p->seed_layer[i], e = p->seed_expert[i];
-                require(l >= 0 && l < n_layers && e >= 0 && e < layers[l].experts, "seed key out of range");
-                require(seed.emplace(Key{l, e}, 0).second, "duplicate seed key");
-                bytes += layers[l].bytes_per_expert;
-            }
-            require(bytes <= p->capacity_bytes, "the seed exceeds the cache capacity");
-        }
         out->supported = 1;
         bool testing = false;
         uint64_t warmup_rejected = 0;
@@ -319,11 +304,6 @@ vbm_status vbm_residency_replay(const vbm_residency_layer * layers, int64_t n_la
                 if (p->cold_cache) {
                     R.resident.clear();
                     R.used = 0;
-                }
-                if (p->seeded) {                        // keys at time 0, as a fresh cache's
-                    R.resident = seed;
-                    R.used = 0;
-                    for (const auto & kv : seed) R.used += R.size_of(kv.first);
                 }
                 uint64_t initial = R.used;
                 if (p->policy == VBM_RESIDENCY_MEASURED_STATIC) {
@@ -347,7 +327,7 @@ vbm_status vbm_residency_replay(const vbm_residency_layer * layers, int64_t n_la
             } else {
                 for (const Key & k : keys) hits += R.resident.count(k);
                 cold = (n - hits) * L.bytes_per_expert;
-                if (!(p->frozen && testing)) R.update(keys, i, uploads, evictions);
+                R.update(keys, i, uploads, evictions);
             }
             if (!test) {
                 out->warmup_upload_bytes += uploads;

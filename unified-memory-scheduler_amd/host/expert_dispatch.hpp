@@ -1,6 +1,6 @@
 // Expert dispatch boundary (C++ host side). Same public interface and semantics as the
 // reference's tools/engine/expert_dispatch.hpp:10-48 so callers and the reference's own tests
-// compile unchanged: routes (row, rank, expert, weight) are split into CPU and GPU job lists by
+// (tests/test_expert_dispatch.cpp) compile unchanged: routes (row, rank, expert, weight) are split into CPU and GPU job lists by
 // a 0/1 residency vector; the GPU runner runs asynchronously while the CPU runner runs on the
 // caller; outputs are checked for shape and finiteness and summed weight*value in route order.
 #pragma once
@@ -45,17 +45,15 @@ public:
     std::vector<float> execute(const ExpertRunner & cpu, const ExpertRunner & gpu) const;
 
 private:
-    struct Contribution {
-        std::size_t row;
-        std::size_t job_index;
-        float weight;
-        bool on_gpu;
-    };
     std::size_t width_;
     std::size_t rows_;
     std::vector<ExpertJob> cpu_jobs_;
     std::vector<ExpertJob> gpu_jobs_;
-    std::vector<Contribution> order_;
+    // Routes in row-major, rank-minor order: row r owns [row_begin_[r], row_begin_[r + 1]).
+    // source_[i] = 2 * (index of the route's job in its list) + (1 if that list is the GPU's).
+    std::vector<std::size_t> row_begin_;
+    std::vector<std::size_t> source_;
+    std::vector<float> weight_;
 };
 
 }  // namespace vrambridge::experimental

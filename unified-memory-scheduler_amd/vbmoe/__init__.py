@@ -78,7 +78,6 @@ class ResidencyParams(C.Structure):
         ("policy", C.c_int), ("capacity_bytes", u64), ("admit_after", C.c_int), ("payback_tokens", i64),
         ("cold_cache", C.c_int), ("ram_gbps", C.c_double), ("pcie_gbps", C.c_double), ("gpu_expert_us", C.c_double),
         ("layer_sync_us", C.c_double), ("staging_ram_passes", C.c_int), ("static_device_expert_bytes", u64),
-        ("seed_layer", vp), ("seed_expert", vp), ("n_seed", i64), ("seeded", C.c_int), ("frozen", C.c_int),
     ]
 
 
