@@ -209,8 +209,10 @@ vbm_status vbm_mul_mat_id_noalloc(const vbm_bank * bank, const int32_t * expert_
                                   const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride,
                                   const float * bias, float * dst, int order, void * stream);
 
-/* GGML_OP_ADD_ID: y[:, r, t] += bias[:, ids[r,t]] for ids != -1 (rows x n_ids x n_tokens). */
-vbm_status vbm_add_id(float * y, const float * bias, const int32_t * ids, int64_t rows,
+/* GGML_OP_ADD_ID in place: y[:, r, t] += bias[:, ids[r,t]] (rows x n_ids x n_tokens; bias fp32
+ * [n_as][rows]). An id of -1 adds nothing; ids outside [-1, n_as) set the row to NaN (the reference
+ * asserts on them). */
+vbm_status vbm_add_id(float * y, const float * bias, int64_t n_as, const int32_t * ids, int64_t rows,
                       int64_t n_ids, int64_t n_tokens, int64_t ids_stride, void * stream);
 
 /* GGML_OP_GLU swiglu_oai (alpha, limit) and swiglu (SiLU-gated) over n values:
@@ -646,16 +648,70 @@ vbm_status vbm_host_mailbox_stats(int device, uint64_t * posted, uint64_t * done
 /* Polls (~1 us each) a waited post makes before it expires; default 2^21. */
 vbm_status vbm_host_mailbox_set_spin_limit(uint32_t polls);
 
-/* supports_op for a ggml HIP backend: 1 when the node can run here. ne0 / ne1: ggml ne[4] of the
- * node's first and second operand (MUL_MAT_ID: as, b; ADD_ID: y, bias; GLU: gate, up; host join:
- * a, b); type0 / type1: their ggml types. Host-call nodes are supported whenever their inputs and
- * output are contiguous and have host buffers (checked by vbm_host_call_enqueue). */
-#define VBM_OP_MUL_MAT_ID 0
-#define VBM_OP_ADD_ID 1
-#define VBM_OP_GLU_SWIGLU 2
-#define VBM_OP_GLU_SWIGLU_OAI 3
-#define VBM_OP_HOST_JOIN 4
-int vbm_op_supported(int op, int type0, int type1, const int64_t * ne0, const int64_t * ne1);
+/* ----------------------------------------------------------------------------------------------
+ * ggml backend boundary: supports_op and compute_forward over ggml-layout graph nodes.
+ * The reference builds the routed-expert branch as ggml nodes
+ * (third_party/patches/llama-b11669-hybrid-experts.patch:1394-1683: MUL_MAT_ID, ADD_ID, gate/up
+ * views, GLU, MUL_MAT_ID, ADD_ID, MUL by the routing weights; :1905-1916: ADD of the resident and
+ * host halves, sequential ADDs of strided rank views, CONT; :966-1054: CUSTOM host calls) and
+ * hands each node to a backend through compute_forward (:1079-1083) and supports_op (:1101-1102; the
+ * pattern of fp32-experts-experimental.patch:74-82). vbm_node carries ggml_tensor's fields: a
+ * backend adapter copies type, ne, nb, data, op_params and src from its tensor, sets `op` to the
+ * VBM_NODE_* value of the tensor's ggml op, and sets `extra`:
+ *   - on a MUL_MAT_ID's src[0] (the expert tensor): a vbm_expert_tensor binding its bank;
+ *   - on a CUSTOM node: its host-call or join descriptor (a vbm_host_call), the node's userdata.
+ * Strides are byte strides (ggml nb); data pointers are device pointers.
+ * -------------------------------------------------------------------------------------------- */
+#define VBM_NODE_MAX_SRC 10
+#define VBM_NODE_NONE 0          /* leaf: no compute                                              */
+#define VBM_NODE_VIEW 1          /* VIEW / RESHAPE / PERMUTE / TRANSPOSE: no compute              */
+#define VBM_NODE_ADD 2           /* dst = src0 + src1 (src1 repeated over src0), F32, any strides */
+#define VBM_NODE_MUL 3           /* dst = src0 * src1 (src1 repeated over src0), F32, any strides */
+#define VBM_NODE_CONT 4          /* dst (contiguous) = src0 in its element order, F32             */
+#define VBM_NODE_MUL_MAT_ID 5    /* src0 expert tensor, src1 b, src2 ids (see vbm_mul_mat_id)     */
+#define VBM_NODE_ADD_ID 6        /* src0 y, src1 bias [rows, n_as], src2 ids (see vbm_add_id)     */
+#define VBM_NODE_GLU 7           /* src0 gate (src1 up, or the second half of src0's rows)        */
+#define VBM_NODE_CUSTOM 8        /* host call or host join (extra = vbm_host_call)                */
+/* ggml_glu_op values (GLU op_params[0]); op_params[1] = swapped; SWIGLU_OAI: op_params[2] alpha
+ * and op_params[3] limit, as float bits (ggml_swiglu_oai). */
+#define VBM_GLU_OP_SWIGLU 2
+#define VBM_GLU_OP_SWIGLU_OAI 3
+
+typedef struct vbm_node {
+    int32_t op;                              /* VBM_NODE_*                                       */
+    int32_t type;                            /* VBM_TYPE_* (ggml type id)                         */
+    int64_t ne[4];                           /* ggml ne, ne[0] fastest                            */
+    size_t nb[4];                            /* ggml nb, bytes                                    */
+    void * data;                             /* device pointer                                    */
+    void * extra;                            /* see above                                         */
+    int32_t op_params[16];                   /* ggml op_params (GGML_MAX_OP_PARAMS / 4)           */
+    const struct vbm_node * src[VBM_NODE_MAX_SRC];
+} vbm_node;
+
+/* The bank that holds an expert tensor, with its optional expert->slot maps (as in vbm_mul_mat_id). */
+typedef struct vbm_expert_tensor {
+    const vbm_bank * bank;
+    const int32_t * expert_to_slot;          /* device int32 [ne[2]] or NULL (identity)            */
+    const int32_t * expert_to_slot_host;     /* host copy for checking, or NULL                    */
+} vbm_expert_tensor;
+
+typedef struct vbm_compute_params {
+    int32_t order;                           /* VBM_ORDER_* for MUL_MAT_ID                        */
+    int32_t host_call_mode;                  /* VBM_HOST_CALL_FUNC or VBM_HOST_CALL_MAILBOX       */
+} vbm_compute_params;
+
+/* supports_op: 1 when this library can run the node with its types, shapes and strides
+ * (MUL_MAT_ID: MXFP4/Q8_0 experts [k % 64, rows % 32, n_as <= 1024]; F32 b with evenly spaced
+ * rows, any row stride, or contiguous Q8_0 b; I32 ids with contiguous rows and any token stride;
+ * contiguous F32 dst. GLU: gate/up rows evenly spaced, so the split views of a fused gate_up
+ * qualify. ADD / MUL / CONT / ADD_ID: F32 with any 4-byte strides). */
+int vbm_node_supported(const vbm_node * node);
+/* compute_forward: runs one node on `stream` (params NULL: exact order, hipLaunchHostFunc host
+ * calls). A node vbm_node_supported refuses fails with VBM_ERR_UNSUPPORTED and the reason. */
+vbm_status vbm_compute_forward(const vbm_node * node, const vbm_compute_params * params, void * stream);
+/* The nodes of a graph in order (views and leaves are skipped); the first failure names its node. */
+vbm_status vbm_graph_compute(const vbm_node * const * nodes, int64_t n_nodes, const vbm_compute_params * params,
+                             void * stream);
 
 /* ----------------------------------------------------------------------------------------------
  * HIP graph capture of stream-ordered work (per-token layer chains replay without host launch

@@ -444,7 +444,7 @@ def test_add_id_matches_oracle(gpu, orc):
             if ids[t, r] >= 0:
                 ref[t, r] = ref[t, r] + bias[ids[t, r]]
     dy, db, di = (gpu.DeviceBuffer.from_array(a) for a in (y, bias, ids_full))
-    gpu.call("vbm_add_id", dy.ptr, db.ptr, di.ptr, rows, n_ids, tokens, stride, None)
+    gpu.call("vbm_add_id", dy.ptr, db.ptr, n_as, di.ptr, rows, n_ids, tokens, stride, None)
     got = dy.download(np.float32, y.shape)
     assert H.bits_equal(got, ref)
 

@@ -198,30 +198,3 @@ def test_mailbox_wait_is_bounded(gpu):
     vb.call("vbm_host_mailbox_drain", 0, 10.0)
     assert call.runs == 1
     call.release()
-
-
-def test_op_supported_predicate(vb):
-    lib = vb.load()
-
-    def ok(op, t0, t1, ne0, ne1=None):
-        a = (C.c_int64 * 4)(*ne0)
-        b = (C.c_int64 * 4)(*ne1) if ne1 is not None else None
-        return lib.vbm_op_supported(op, t0, t1, a, b)
-
-    MX, Q8, F32, F16 = vb.TYPE_MXFP4, vb.TYPE_Q8_0, vb.TYPE_F32, vb.TYPE_F16
-    assert ok(vb.OP_MUL_MAT_ID, MX, F32, (2880, 5760, 128, 1), (2880, 1, 7, 1))
-    assert ok(vb.OP_MUL_MAT_ID, Q8, Q8, (2048, 1536, 128, 1), (2048, 8, 512, 1))
-    assert not ok(vb.OP_MUL_MAT_ID, F16, F32, (2880, 5760, 128, 1), (2880, 1, 7, 1))     # weight type
-    assert not ok(vb.OP_MUL_MAT_ID, MX, F16, (2880, 5760, 128, 1), (2880, 1, 7, 1))     # activation type
-    assert not ok(vb.OP_MUL_MAT_ID, MX, F32, (2880, 5760, 128, 1), (2816, 1, 7, 1))     # k mismatch
-    assert not ok(vb.OP_MUL_MAT_ID, MX, F32, (2848, 5760, 128, 1), (2848, 1, 7, 1))     # k % 64
-    assert not ok(vb.OP_MUL_MAT_ID, MX, F32, (2880, 5750, 128, 1), (2880, 1, 7, 1))     # rows % 32
-    assert not ok(vb.OP_MUL_MAT_ID, MX, F32, (2880, 5760, 2048, 1), (2880, 1, 7, 1))    # > 1024 experts
-    assert not ok(vb.OP_MUL_MAT_ID, MX, F32, (2880, 5760, 128, 1))                      # no b shape
-    assert ok(vb.OP_ADD_ID, F32, F32, (2880, 4, 7, 1), (2880, 128, 1, 1))
-    assert not ok(vb.OP_ADD_ID, F32, F32, (2880, 4, 7, 1), (2816, 128, 1, 1))
-    assert ok(vb.OP_GLU_SWIGLU_OAI, F32, F32, (2880, 4, 7, 1), (2880, 4, 7, 1))
-    assert not ok(vb.OP_GLU_SWIGLU, F32, F32, (2880, 4, 7, 1), (2880, 4, 6, 1))
-    assert ok(vb.OP_HOST_JOIN, F32, F32, (2880, 4, 7, 1), (2880, 4, 7, 1))
-    assert not ok(vb.OP_HOST_JOIN, F32, F16, (2880, 4, 7, 1), (2880, 4, 7, 1))
-    assert not ok(99, F32, F32, (1, 1, 1, 1), (1, 1, 1, 1))

@@ -95,8 +95,6 @@ void launch_router(const float * router_w, const float * router_b, const float *
                    float * weights, hipStream_t stream);
 void launch_combine(const float * y, const float * weights, int64_t rows, int64_t n_ids, int64_t n_tokens,
                     float * out, hipStream_t stream);
-void launch_add_id(float * y, const float * bias, const int32_t * ids, int64_t rows, int64_t n_ids,
-                   int64_t n_tokens, int64_t ids_stride, hipStream_t stream);
 void launch_glu(int activation, const float * gate, const float * up, float * out, int64_t n_rows,
                 int64_t width, int64_t gate_stride, int64_t up_stride, int64_t out_stride, float alpha,
                 float limit, hipStream_t stream);
@@ -259,7 +257,8 @@ void launch_decode_down(const DecodeDownParams & d, hipStream_t stream);
 void * stream_scratch(hipStream_t s, size_t bytes);
 void release_stream_scratch(hipStream_t s);   // before the stream is destroyed
 
-// GGML_OP_MUL_MAT_ID over a caller-provided scratch of mul_mat_id_scratch_bytes().
+// GGML_OP_MUL_MAT_ID over a caller-provided scratch of mul_mat_id_scratch_bytes(). b_row_stride:
+// floats between consecutive F32 rows of b (0 = contiguous rows of k floats); Q8_0 b is contiguous.
 void check_mul_mat_id_shape(const vbm_bank & bank, int64_t n_as, int64_t b_ne1, int64_t n_ids, int64_t n_tokens,
                             int64_t ids_stride, int order);
 size_t mul_mat_id_scratch_bytes(const vbm_bank & bank, int64_t n_as, int64_t b_ne1, int64_t n_ids, int64_t n_tokens,
@@ -267,6 +266,6 @@ size_t mul_mat_id_scratch_bytes(const vbm_bank & bank, int64_t n_as, int64_t b_n
 void mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot, const int32_t * expert_to_slot_host, int64_t n_as,
                 int b_type, const void * b, int64_t b_ne1, const int32_t * ids, int64_t n_ids, int64_t n_tokens,
                 int64_t ids_stride, const float * bias, float * dst, int order, uint8_t * scratch, size_t scratch_bytes,
-                hipStream_t s);
+                hipStream_t s, int64_t b_row_stride = 0);
 
 }  // namespace vbm

@@ -217,9 +217,12 @@ size_t mul_mat_id_scratch_bytes(const vbm_bank & bank, int64_t n_as, int64_t b_n
 void mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot, const int32_t * expert_to_slot_host, int64_t n_as,
                 int b_type, const void * b, int64_t b_ne1, const int32_t * ids, int64_t n_ids, int64_t n_tokens,
                 int64_t ids_stride, const float * bias, float * dst, int order, uint8_t * scratch, size_t scratch_bytes,
-                hipStream_t s) {
+                hipStream_t s, int64_t b_row_stride) {
     require(bank && b && ids && dst && scratch, "null buffer");
     require(b_type == VBM_TYPE_F32 || b_type == VBM_TYPE_Q8_0, "b must be F32 or Q8_0");
+    if (b_row_stride == 0) b_row_stride = bank->k;
+    require(b_row_stride >= bank->k && (b_type == VBM_TYPE_F32 || b_row_stride == bank->k),
+            "b rows must be at least k floats apart (Q8_0 b must be contiguous)");
     check_mul_mat_id_shape(*bank, n_as, b_ne1, n_ids, n_tokens, ids_stride, order);
     require(expert_to_slot != nullptr || n_as <= bank->n_slots, "identity map needs n_as <= bank slots");
     require(scratch_bytes >= mul_mat_id_scratch_bytes(*bank, n_as, b_ne1, n_ids, n_tokens, order), "workspace too small");
@@ -233,7 +236,7 @@ void mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot, const int
         uint8_t * q = scratch;
         const GroupBuffers g = carve_group(q + q_bytes, n_as, entries);
         if (b_type == VBM_TYPE_F32)
-            launch_gemm_rows_from_f32(static_cast<const float *>(b), n_b, bank->k, bank->k, gl, q, s);
+            launch_gemm_rows_from_f32(static_cast<const float *>(b), n_b, bank->k, b_row_stride, gl, q, s);
         else
             launch_gemm_rows_from_q8(static_cast<const uint8_t *>(b), n_b, bank->nb * 34, gl, q, s);
         launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
@@ -261,7 +264,7 @@ void mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot, const int
     uint8_t * q = scratch;
     const GroupBuffers g = carve_group(q + q_bytes, n_as, entries);
     if (b_type == VBM_TYPE_F32)
-        launch_quantize_expand(static_cast<const float *>(b), n_b, bank->k, bank->k, lay, q, nullptr, s);
+        launch_quantize_expand(static_cast<const float *>(b), n_b, bank->k, b_row_stride, lay, q, nullptr, s);
     else
         launch_expand_q8(static_cast<const uint8_t *>(b), n_b, bank->nb * 34, lay, q, s);
     launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
@@ -433,14 +436,6 @@ vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot,
         const size_t bytes = mul_mat_id_scratch_bytes(*bank, n_as, b_ne1, n_ids, n_tokens, order);
         mul_mat_id(bank, expert_to_slot, expert_to_slot_host, n_as, b_type, b, b_ne1, ids, n_ids, n_tokens, ids_stride,
                    bias, dst, order, static_cast<uint8_t *>(stream_scratch(s, bytes)), bytes, s);
-    });
-}
-
-vbm_status vbm_add_id(float * y, const float * bias, const int32_t * ids, int64_t rows, int64_t n_ids, int64_t n_tokens,
-                      int64_t ids_stride, void * stream) {
-    return guarded([&] {
-        require(y && bias && ids && rows > 0 && n_ids > 0 && n_tokens > 0 && ids_stride >= n_ids, "invalid add_id");
-        launch_add_id(y, bias, ids, rows, n_ids, n_tokens, ids_stride, as_stream(stream));
     });
 }
 

@@ -207,17 +207,6 @@ __global__ void combine_kernel(const float * __restrict__ y, const float * __res
     out[idx] = acc;
 }
 
-__global__ void add_id_kernel(float * __restrict__ y, const float * __restrict__ bias, const int32_t * __restrict__ ids,
-                              int64_t rows, int n_ids, int64_t n_tokens, int64_t ids_stride) {
-    const int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-    if (idx >= rows * n_ids * n_tokens) return;
-    const int64_t i = idx % rows, j = idx / rows;
-    const int64_t t = j / n_ids, r = j % n_ids;
-    const int id = ids[t * ids_stride + r];
-    if (id < 0) return;
-    y[idx] = y[idx] + bias[static_cast<int64_t>(id) * rows + i];
-}
-
 __global__ void glu_kernel(int activation, const float * __restrict__ gate, const float * __restrict__ up,
                            float * __restrict__ out, int64_t n_rows, int64_t width, int64_t gs, int64_t us,
                            int64_t os, float alpha, float limit) {
@@ -314,13 +303,6 @@ void launch_combine(const float * y, const float * weights, int64_t rows, int64_
     hipLaunchKernelGGL(combine_kernel, dim3(blocks_for(rows * n_tokens, 256)), dim3(256), 0, stream, y, weights, rows,
                        static_cast<int>(n_ids), n_tokens, out);
     check_hip(hipGetLastError(), "combine launch");
-}
-
-void launch_add_id(float * y, const float * bias, const int32_t * ids, int64_t rows, int64_t n_ids, int64_t n_tokens,
-                   int64_t ids_stride, hipStream_t stream) {
-    hipLaunchKernelGGL(add_id_kernel, dim3(blocks_for(rows * n_ids * n_tokens, 256)), dim3(256), 0, stream, y, bias, ids,
-                       rows, static_cast<int>(n_ids), n_tokens, ids_stride);
-    check_hip(hipGetLastError(), "add_id launch");
 }
 
 void launch_glu(int activation, const float * gate, const float * up, float * out, int64_t n_rows, int64_t width,

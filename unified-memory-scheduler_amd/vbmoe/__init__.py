@@ -55,7 +55,9 @@ class GgufExpertInfo(C.Structure):
 
 HOST_CALL_MAGIC, HOST_JOIN_MAGIC, HOST_MAX_SRC = 0x56424843414C4C31, 0x5642484A4F494E31, 10
 HOST_CALL_FUNC, HOST_CALL_MAILBOX = 0, 1
-OP_MUL_MAT_ID, OP_ADD_ID, OP_GLU_SWIGLU, OP_GLU_SWIGLU_OAI, OP_HOST_JOIN = 0, 1, 2, 3, 4
+NODE_NONE, NODE_VIEW, NODE_ADD, NODE_MUL, NODE_CONT, NODE_MUL_MAT_ID, NODE_ADD_ID, NODE_GLU, NODE_CUSTOM = range(9)
+NODE_MAX_SRC = 10
+GLU_OP_SWIGLU, GLU_OP_SWIGLU_OAI = 2, 3
 HOST_FN = C.CFUNCTYPE(None, C.c_void_p)
 
 
@@ -67,6 +69,24 @@ HostCall._fields_ = [
     ("magic", u64), ("fn", HOST_FN), ("ctx", vp), ("src_host", vp * HOST_MAX_SRC), ("dst_host", vp),
     ("backend_state", vp), ("call", C.POINTER(HostCall)), ("miss_src", C.c_int32),
 ]
+
+
+class Node(C.Structure):
+    """vbm_node: a ggml-layout graph node (type, ne, nb in bytes, data, op_params, src)."""
+
+
+Node._fields_ = [
+    ("op", C.c_int32), ("type", C.c_int32), ("ne", C.c_int64 * 4), ("nb", C.c_size_t * 4), ("data", vp), ("extra", vp),
+    ("op_params", C.c_int32 * 16), ("src", C.POINTER(Node) * NODE_MAX_SRC),
+]
+
+
+class ExpertTensor(C.Structure):
+    _fields_ = [("bank", vp), ("expert_to_slot", vp), ("expert_to_slot_host", vp)]
+
+
+class ComputeParams(C.Structure):
+    _fields_ = [("order", C.c_int32), ("host_call_mode", C.c_int32)]
 
 
 class ResidencyLayer(C.Structure):
@@ -137,7 +157,9 @@ SIGNATURES = {
     "vbm_mul_mat_id_workspace": [vp, i64, i64, i64, i64, C.c_int, C.POINTER(C.c_size_t)],
     "vbm_mul_mat_id_ws": [vp, vp, vp, i64, C.c_int, vp, i64, vp, i64, i64, i64, vp, vp, C.c_int, vp, C.c_size_t, vp],
     "vbm_mul_mat_id_noalloc": [vp, vp, i64, C.c_int, vp, i64, vp, i64, i64, i64, vp, vp, C.c_int, vp],
-    "vbm_add_id": [vp, vp, vp, i64, i64, i64, i64, vp],
+    "vbm_add_id": [vp, vp, i64, vp, i64, i64, i64, i64, vp],
+    "vbm_compute_forward": [C.POINTER(Node), vp, vp],
+    "vbm_graph_compute": [vp, i64, vp, vp],
     "vbm_glu": [C.c_int, vp, vp, vp, i64, i64, i64, i64, i64, C.c_float, C.c_float, vp],
     "vbm_router_topk_softmax": [vp, vp, vp, i64, vp, i64, i64, i64, vp, vp, vp],
     "vbm_group_by_expert": [vp, i64, i64, i64, i64, vp, vp, vp, vp, vp],
@@ -219,7 +241,7 @@ OTHER = {
     "vbm_moe_anchor_slots": ([C.c_int, C.c_int, C.c_int], C.c_int),
     "vbm_moe_cold_gpu_budget": ([C.c_int], C.c_int),
     "vbm_moe_gpu_slot_limit": ([C.c_int32, C.c_int], C.c_int32),
-    "vbm_op_supported": ([C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_int64)], C.c_int),
+    "vbm_node_supported": ([C.POINTER(Node)], C.c_int),
 }
 ADMIT_CLASSIC, ADMIT_LRU, ADMIT_RANKED, ADMIT_PROBATION, ADMIT_ANCHORED, ADMIT_LFU = 0, 1, 2, 3, 4, 5
 
