@@ -15,6 +15,7 @@ import argparse
 import ctypes as C
 import json
 import os
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -95,16 +96,43 @@ def distinct_experts(ids: np.ndarray) -> int:
     return int(sum(len(np.unique(ids[l].reshape(-1))) for l in range(ids.shape[0])))
 
 
+def host_cpu() -> dict:
+    """The host's CPU model (lscpu, else /proc/cpuinfo), its logical CPU count and this process's
+    CPU affinity."""
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if model is None:
+        try:
+            for line in Path("/proc/cpuinfo").read_text().splitlines():
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+    return {"model": model, "nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+
+
+def baseline_threads() -> int:
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    return max(1, min(threads, len(os.sched_getaffinity(0))))
+
+
 def cpu_baseline(args, logits_host: np.ndarray) -> dict:
     """The CPU oracle (a port of the reference's ggml x86 MXFP4 x Q8_0 path) timed on this host on
     a bounded sample: the first `--cpu-layers` layers of the same seeded stack, each with all 128
-    experts on the host, for as many tokens as fit in --cpu-seconds; per-token time scaled to 36
-    layers."""
+    experts on the host, for as many tokens as fit in --cpu-seconds (all threads) and
+    --cpu-seconds-1core (one thread); per-token time scaled to 36 layers."""
     sys.path.insert(0, str(REPO / "oracle"))
     import oracle_py
     oracle_py.load()
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
-    threads = max(1, min(threads, len(os.sched_getaffinity(0))))
+    threads = baseline_threads()
     E, H, I, K = args.experts, 2880, 2880, 4
     layers = []
     t0 = time.time()
@@ -114,27 +142,73 @@ def cpu_baseline(args, logits_host: np.ndarray) -> dict:
         dn = vb.synth_mxfp4(SEED, 16 * l + 2, 0, blocks_dn)
         layers.append((gu, dn, vb.synth_normal(SEED, 16 * l + 3, 0, E * 2 * I, 0.0, 0.02),
                        vb.synth_normal(SEED, 16 * l + 4, 0, E * H, 0.0, 0.02)))
-    log(f"cpu baseline: {args.cpu_layers} host layers ready in {time.time() - t0:.1f} s; timing with {threads} threads")
+    log(f"cpu baseline: {args.cpu_layers} host layers ready in {time.time() - t0:.1f} s; timing with {threads} threads "
+        f"and with 1")
     x0 = vb.synth_normal(SEED, 6, 0, H).reshape(1, H)
-    done = 0
-    elapsed = 0.0
-    while True:
-        tok = done % logits_host.shape[0]
-        x = x0
+
+    def time_decode(n_threads: int, seconds: float):
+        done, elapsed = 0, 0.0
+        while True:
+            tok = done % logits_host.shape[0]
+            x = x0
+            t = time.perf_counter()
+            for l, (gu, dn, gub, dnb) in enumerate(layers):
+                r = oracle_py.moe_layer(39, gu, dn, gub, dnb, x, H, I, E, K, activation=1,
+                                        logits=logits_host[tok, l].reshape(1, E), threads=n_threads)
+                x = r["out"]
+            elapsed += time.perf_counter() - t
+            done += 1
+            if (elapsed >= seconds and done >= 2) or done >= 1_000_000:
+                return done, elapsed
+
+    def line(n_threads: int, done: int, elapsed: float) -> dict:
+        per_layer_token = elapsed / (done * args.cpu_layers)
+        return {"value": round(1.0 / (per_layer_token * args.layers), 3), "unit": "tok/s", "cores": n_threads,
+                "kind": "port",
+                "sample": f"{done} decode tokens x first {args.cpu_layers} of {args.layers} layers (all {E} experts "
+                          f"on host, bs1) in {elapsed:.1f} s; per-layer time scaled x{args.layers}; oracle fast path "
+                          f"(ISA level {oracle_py.load().orc_fast_isa()})"}
+
+    result = line(threads, *time_decode(threads, args.cpu_seconds))
+    result["single_core"] = line(1, *time_decode(1, args.cpu_seconds_1core))
+    result["host"] = host_cpu()
+    return result
+
+
+def cpu_prefill_baseline(args) -> dict:
+    """The CPU oracle's Q8_0 x Q8_0 layer (the reference's vec_dot path, tools/engine/native_cpu.cpp:91-104,
+    as restated in the oracle) on the prefill workload's own seeded layer: the full 2048-token
+    batch with all threads, and a bounded prefix of it with one thread."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle_py
+    oracle_py.load()
+    Hp, Ip, Ep, Kp, Tp = 2048, 768, 128, 8, 2048
+    gu = vb.synth_q8_0(SEED, 901, 0, Ep * 2 * Ip * (Hp // 32), 1e-3, 1e-2)
+    dn = vb.synth_q8_0(SEED, 902, 0, Ep * Hp * (Ip // 32), 1e-3, 1e-2)
+    x = vb.synth_normal(SEED, 903, 0, Tp * Hp).reshape(Tp, Hp)
+    logits = vb.synth_normal(SEED, 904, 0, Tp * Ep).reshape(Tp, Ep)
+    threads = baseline_threads()
+
+    def run(n_threads: int, tokens: int) -> float:
         t = time.perf_counter()
-        for l, (gu, dn, gub, dnb) in enumerate(layers):
-            r = oracle_py.moe_layer(39, gu, dn, gub, dnb, x, H, I, E, K, activation=1,
-                                    logits=logits_host[tok, l].reshape(1, E), threads=threads)
-            x = r["out"]
-        elapsed += time.perf_counter() - t
-        done += 1
-        if (elapsed >= args.cpu_seconds and done >= 2) or done >= 1_000_000:
-            break
-    per_layer_token = elapsed / (done * args.cpu_layers)
-    return {"value": round(1.0 / (per_layer_token * args.layers), 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{done} decode tokens x first {args.cpu_layers} of {args.layers} layers (all {E} experts on host, "
-                      f"bs1) in {elapsed:.1f} s; per-layer time scaled x{args.layers}; oracle fast path "
-                      f"(ISA level {oracle_py.load().orc_fast_isa()})"}
+        oracle_py.moe_layer(8, gu, dn, None, None, x[:tokens], Hp, Ip, Ep, Kp, activation=0, logits=logits[:tokens],
+                            threads=n_threads)
+        return time.perf_counter() - t
+
+    elapsed, reps = 0.0, 0
+    while reps < 1 or (elapsed < args.cpu_seconds and reps < 8):
+        elapsed += run(threads, Tp)
+        reps += 1
+    one_tokens = max(8, min(Tp, int(args.prefill_cpu_tokens_1core)))
+    one = run(1, one_tokens)
+    return {
+        "value": round(reps * Tp / elapsed, 1), "unit": "tok/s", "cores": threads, "kind": "port",
+        "sample": f"{reps} x the full {Tp}-token Q8_0 layer (hidden {Hp}, {Ep} experts top-{Kp}, intermediate {Ip}, "
+                  f"SiLU) in {elapsed:.1f} s; oracle fast path (ISA level {oracle_py.load().orc_fast_isa()}), "
+                  "exact x86 order",
+        "single_core": {"value": round(one_tokens / one, 2), "unit": "tok/s", "cores": 1, "kind": "port",
+                        "sample": f"the first {one_tokens} tokens of the same layer on one thread in {one:.1f} s"},
+    }
 
 
 INT8_MFMA_PEAK_TOPS = 5000.0
@@ -531,6 +605,9 @@ def main() -> int:
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph")
     ap.add_argument("--kernel-reps", type=int, default=20, help="launches per layer in the kernel timing pass")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds-1core", type=float, default=8.0)
+    ap.add_argument("--prefill-cpu-tokens-1core", type=int, default=512,
+                    help="tokens of the Q8_0 prefill layer timed on one CPU thread")
     ap.add_argument("--cpu-layers", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the Q8_0 prefill GEMM measurement")
@@ -674,7 +751,12 @@ def main() -> int:
     cpu = None
     if not args.no_cpu and T == 1:
         cpu = cpu_baseline(args, logits_host[:, :, 0, :])
-        log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads")
+        log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads, {cpu['single_core']['value']} tok/s on 1; "
+            f"host {cpu['host']}")
+        if prefill is not None:
+            prefill["cpu_baseline"] = cpu_prefill_baseline(args)
+            log(f"cpu prefill baseline: {prefill['cpu_baseline']['value']} tok/s on {prefill['cpu_baseline']['cores']} "
+                f"threads, {prefill['cpu_baseline']['single_core']['value']} tok/s on 1")
 
     result = {
         "metric": METRIC,

@@ -9,6 +9,7 @@
                   (exports ref_glu: the reference executor's own activation stage)
                 - test_expert_dispatch  <- tests/test_expert_dispatch.cpp linked against this
                   repository's ExpertPlan (unified-memory-scheduler_amd/host/expert_dispatch.cpp)
+                - test_expert_dispatch_asan  <- the same, built with -fsanitize=address,undefined
               The reference build is skipped (with a message) when REF_ROOT is absent.
 
 Usage: python oracle/build_oracle.py [--no-ref]
@@ -61,6 +62,13 @@ def build_reference() -> list[Path]:
     run(["g++", "-O2", "-std=c++20", "-ffp-contract=off", "-pthread", f"-I{HOST_DIR}",
          str(REF_ROOT / "tests/test_expert_dispatch.cpp"), str(HOST_DIR / "expert_dispatch.cpp"), "-o", str(dispatch)])
     built.append(dispatch)
+    # the same test under host AddressSanitizer + UndefinedBehaviorSanitizer (the ExpertPlan indexes
+    # by caller data)
+    dispatch_asan = REF_OUT / "test_expert_dispatch_asan"
+    run(["g++", "-O1", "-g", "-std=c++20", "-ffp-contract=off", "-pthread", "-fsanitize=address,undefined",
+         "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer", f"-I{HOST_DIR}",
+         str(REF_ROOT / "tests/test_expert_dispatch.cpp"), str(HOST_DIR / "expert_dispatch.cpp"), "-o", str(dispatch_asan)])
+    built.append(dispatch_asan)
     return built
 
 

@@ -435,6 +435,12 @@ def test_reference_dispatch_test_passes_against_expert_plan(orc):
     proc = subprocess.run([str(orc.REF_DISPATCH_TEST)], capture_output=True, text=True, timeout=60)
     assert proc.returncode == 0, proc.stderr
     assert "passed" in proc.stdout
+    asan = orc.REF_DISPATCH_TEST.with_name("test_expert_dispatch_asan")
+    if asan.exists():   # the same test with AddressSanitizer + UBSan over ExpertPlan
+        proc = subprocess.run([str(asan)], capture_output=True, text=True, timeout=120,
+                              env={"ASAN_OPTIONS": "detect_leaks=1", "UBSAN_OPTIONS": "halt_on_error=1"})
+        assert proc.returncode == 0, proc.stderr
+        assert "passed" in proc.stdout and "runtime error" not in proc.stderr
 
 
 U32 = 2.0 ** -24

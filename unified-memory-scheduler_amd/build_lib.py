@@ -45,9 +45,22 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp")) + sorted(HOST.glob("*.cpp"))
 
 
-def compile_one(src: Path) -> Path:
-    obj = BUILD / (src.parent.name + "_" + src.name + ".o")
-    cmd = [hipcc(), *HIP_FLAGS, f"-I{HOST}", "-x", "hip", "-c", str(src), "-o", str(obj)]
+# Host-side AddressSanitizer + UndefinedBehaviorSanitizer (the device code is built as usual): a
+# CPU-only variant of the library for running the CPU test suite over the host parsers and control
+# code (GGUF container parsing, traces, admission, residency replays, the engine-level mirror).
+SANITIZE_FLAGS = [
+    "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer",
+]
+SANITIZE_DIR = BUILD / "sanitize"
+SANITIZE_LIB = SANITIZE_DIR / "libvbmoe.so"
+
+
+def compile_one(src: Path, sanitize: bool = False) -> Path:
+    out_dir = SANITIZE_DIR if sanitize else BUILD
+    obj = out_dir / (src.parent.name + "_" + src.name + ".o")
+    extra = SANITIZE_FLAGS if sanitize else []
+    cmd = [hipcc(), *HIP_FLAGS, *extra, f"-I{HOST}", "-x", "hip", "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"compile failed: {src.name}\n{' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
@@ -89,8 +102,47 @@ def build_host_tests() -> Path:
     return TEST_BIN
 
 
+def build_sanitized(jobs: int = 8) -> Path:
+    SANITIZE_DIR.mkdir(parents=True, exist_ok=True)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
+        objs = list(pool.map(lambda src: compile_one(src, True), sources()))
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-shared-libsan", "-fsanitize=address,undefined",
+           "-o", str(SANITIZE_LIB), *map(str, objs), "-lpthread"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"sanitized link failed\n{' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
+    return SANITIZE_LIB
+
+
+def asan_runtime() -> str:
+    out = subprocess.run([hipcc(), "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+    path = out.stdout.strip()
+    if not path or not Path(path).exists():
+        raise RuntimeError("clang's ASan runtime (libclang_rt.asan-x86_64.so) not found")
+    return path
+
+
+def run_sanitized_suite(pytest_args: list[str]) -> int:
+    """The CPU test suite (-m "not gpu") in a child process that loads the sanitized library, with the
+    ASan runtime preloaded (the Python interpreter itself is not instrumented, so leak checking is
+    off); any ASan report or UBSan finding aborts the run."""
+    env = dict(os.environ)
+    env["VBM_LIBRARY"] = str(SANITIZE_LIB)
+    env["LD_PRELOAD"] = asan_runtime()
+    env["ASAN_OPTIONS"] = "detect_leaks=0:abort_on_error=1:halt_on_error=1"
+    env["UBSAN_OPTIONS"] = "print_stacktrace=1:halt_on_error=1"
+    cmd = [sys.executable, "-m", "pytest", str(HERE.parent / "tests"), "-q", "-m", "not gpu", "-p", "no:cacheprovider",
+           *pytest_args]
+    return subprocess.run(cmd, env=env, cwd=str(HERE.parent)).returncode
+
+
 if __name__ == "__main__":
     parser = argparse.ArgumentParser()
     parser.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
-    args = parser.parse_args()
+    parser.add_argument("--sanitize", action="store_true",
+                        help="build the host-ASan/UBSan variant under _build/sanitize and run the CPU tests on it")
+    args, rest = parser.parse_known_args()
+    if args.sanitize:
+        print(build_sanitized(args.jobs))
+        sys.exit(run_sanitized_suite(rest))
     print(build(args.jobs))

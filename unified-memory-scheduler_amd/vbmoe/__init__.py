@@ -259,7 +259,7 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
     global _lib
     if _lib is not None:
         return _lib
-    p = Path(path) if path else LIB_PATH
+    p = Path(path) if path else Path(os.environ.get("VBM_LIBRARY") or LIB_PATH)
     if not p.exists():
         raise FileNotFoundError(f"{p} not built; run unified-memory-scheduler_amd/build_lib.py")
     lib = C.CDLL(str(p))
