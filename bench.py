@@ -500,19 +500,14 @@ def tier_measure(args, stack) -> dict:
         log(f"tier prefill: {T} tokens x {L} layers in {pms.value:.1f} ms ({prefill['value']} tok/s); "
             f"{prefill['streamed_experts']} experts streamed, {prefill['resident_experts']} resident; "
             f"{prefill['h2d_gbs_overall']} GB/s of expert copies overall")
-    vb.call("vbm_tier_destroy", tier.value)
     policies = policy_study(args, routes, n_slots, plan, group_bytes, st) if args.tier_policies else None
     live_policy = None
     if args.tier_live_policy != "none":
         # the same trace through a second pool under another admission policy, live
         names = ("classic", "lru", "ranked", "probation", "anchored", "lfu")
         pol = names.index(args.tier_live_policy)
-        desc2 = vb.TierDesc(vb.TYPE_MXFP4, H, I, L, E, K, vb.ACT_SWIGLU_OAI, n_slots, 64,
-                            1 if args.tier_live_policy == "lru" else 4, pol,
-                            C.cast(gub, C.POINTER(C.c_void_p)), C.cast(dnb, C.POINTER(C.c_void_p)))
-        tier2 = C.c_void_p()
-        vb.call("vbm_tier_create", C.byref(desc2), C.byref(tier2))
-        vb.call("vbm_tier_generate", tier2.value, SEED, 16, 1, 2, -8.0, -3.0, None)
+        tier2 = tier     # the same host copies, a fresh pool and admission
+        vb.call("vbm_tier_reset", tier2.value, pol, 64, 1 if args.tier_live_policy == "lru" else 4)
         for layer, expert in plan:
             vb.call("vbm_tier_seed", tier2.value, layer, expert)
         vb.call("vbm_event_record", ev0.value, stream)
@@ -524,11 +519,51 @@ def tier_measure(args, stack) -> dict:
         vb.call("vbm_event_elapsed_ms", ev0.value, ev1.value, C.byref(ms2))
         st2 = vb.TierStats()
         vb.call("vbm_tier_get_stats", tier2.value, C.byref(st2))
-        vb.call("vbm_tier_destroy", tier2.value)
         live_policy = {"policy": args.tier_live_policy, "value": round(tokens / (ms2.value * 1e-3), 2), "unit": "tok/s",
-                       "hit_rate": round(st2.hits / (tokens * L * K), 4), "uploaded_gb": round(st2.uploaded_bytes / 1e9, 2)}
+                       "hit_rate": round(st2.hits / (tokens * L * K), 4), "uploaded_gb": round(st2.uploaded_bytes / 1e9, 2),
+                       "hits": int(st2.hits), "admissions": int(st2.admissions), "evictions": int(st2.evictions)}
         log(f"tier ({args.tier_live_policy} admission, live): {live_policy['value']} tok/s, hit rate "
             f"{live_policy['hit_rate']}, {live_policy['uploaded_gb']} GB uploaded")
+    deferred = None
+    if args.tier_deferred:
+        # deferred mode: no host wait inside a step (misses streamed from the pinned host copy by the
+        # decode kernels, admission at the step boundary); the same trace under classic and LRU
+        deferred = {}
+        sync_counters = {"classic": (int(st.hits), int(st.admissions), int(st.evictions))}
+        if live_policy is not None and args.tier_live_policy == "lru":
+            sync_counters["lru"] = (live_policy["hits"], live_policy["admissions"], live_policy["evictions"])
+        for name, pol, margin in (("classic", vb.ADMIT_CLASSIC, 4), ("lru", vb.ADMIT_LRU, 1)):
+            tier3 = tier
+            vb.call("vbm_tier_reset", tier3.value, pol, 64, margin)
+            for layer, expert in plan:
+                vb.call("vbm_tier_seed", tier3.value, layer, expert)
+            vb.call("vbm_tier_set_deferred", tier3.value, 1)
+            wall3 = time.perf_counter()
+            vb.call("vbm_event_record", ev0.value, stream)
+            for t in range(tokens):
+                vb.call("vbm_tier_step", tier3.value, stack.x0.ptr, dl.ptr + t * step, out.ptr, None, stream)
+            vb.call("vbm_event_record", ev1.value, stream)
+            vb.call("vbm_stream_synchronize", stream)
+            wall3 = time.perf_counter() - wall3
+            ms3 = C.c_float()
+            vb.call("vbm_event_elapsed_ms", ev0.value, ev1.value, C.byref(ms3))
+            vb.call("vbm_tier_flush", tier3.value)
+            st3 = vb.TierStats()
+            vb.call("vbm_tier_get_stats", tier3.value, C.byref(st3))
+            vb.call("vbm_tier_set_deferred", tier3.value, 0)
+            entry = {"value": round(tokens / (ms3.value * 1e-3), 2),
+                     "unit": "tok/s", "host_wall_s": round(wall3, 2), "hit_rate": round(st3.hits / (tokens * L * K), 4),
+                     "admissions": int(st3.admissions), "experts_read_from_host": int(st3.host_reads),
+                     "uploaded_gb": round(st3.uploaded_bytes / 1e9, 2),
+                     "host_read_gb": round(st3.host_reads * group_bytes / 1e9, 2)}
+            ref_counters = sync_counters.get(name)
+            if ref_counters is not None:
+                mine = (int(st3.hits), int(st3.admissions), int(st3.evictions))
+                entry["counters_match_sync"] = ref_counters == mine
+            deferred[name] = entry
+            log(f"tier deferred ({name}): {entry['value']} tok/s, hit rate {entry['hit_rate']}, "
+                f"{entry['host_read_gb']} GB read from host by the kernels, {entry['uploaded_gb']} GB uploaded")
+    vb.call("vbm_tier_destroy", tier.value)
     lookups = tokens * L * K
     h2d = st.uploaded_bytes / (st.copy_ms * 1e-3) / 1e9 if st.copy_ms > 0 else None
     res = {
@@ -540,7 +575,7 @@ def tier_measure(args, stack) -> dict:
         "evictions": int(st.evictions), "staged_misses": int(st.staged),
         "uploaded_gb": round(st.uploaded_bytes / 1e9, 2), "h2d_gbs": round(h2d, 1) if h2d else None,
         "copy_busy_ms": round(st.copy_ms, 1), "seeded": len(plan), "prefill": prefill, "policies": policies,
-        "live_policy": live_policy,
+        "live_policy": live_policy, "deferred": deferred,
     }
     log(f"tier: {res['value']} tok/s, hit rate {res['hit_rate']}, {res['uploaded_gb']} GB uploaded at "
         f"{res['h2d_gbs']} GB/s copy-busy")
@@ -618,6 +653,8 @@ def main() -> int:
     ap.add_argument("--no-tier", action="store_true",
                     help="skip the host-RAM tier workload (it pins 61 GB of host memory)")
     ap.add_argument("--tier-tokens", type=int, default=512)
+    ap.add_argument("--no-tier-deferred", dest="tier_deferred", action="store_false",
+                    help="skip the deferred-mode tier runs (classic and LRU)")
     ap.add_argument("--tier-live-policy", default="lru",
                     choices=("none", "classic", "lru", "ranked", "probation", "anchored", "lfu"),
                     help="run the tier trace a second time live under this admission policy")

@@ -550,6 +550,8 @@ typedef struct {
     uint64_t prefill_tokens;             /* tokens through vbm_tier_prefill                       */
     uint64_t prefill_resident;           /* routed experts computed from resident slots (per call) */
     uint64_t prefill_streamed;           /* routed experts streamed through the reserved slots    */
+    uint64_t host_reads;                 /* deferred mode: routed experts the decode kernels read  */
+                                         /* from the pinned host copy (not visible in the map)    */
 } vbm_tier_stats;
 
 typedef struct vbm_tier vbm_tier;
@@ -588,6 +590,31 @@ vbm_status vbm_tier_step(vbm_tier * tier, const float * x, const float * logits,
 vbm_status vbm_tier_prefill(vbm_tier * tier, int64_t layer, const float * x, const float * logits,
                             int64_t n_tokens, float * out, int32_t * ids, float * weights, void * stream);
 vbm_status vbm_tier_get_stats(const vbm_tier * tier, vbm_tier_stats * stats);
+/* Empties the pool (every slot free) and restarts admission with the given policy, window and
+ * margin and zeroed stats, keeping the host copies: a new run over the same experts without
+ * re-storing them. Seeds, if any, follow with vbm_tier_seed. */
+vbm_status vbm_tier_reset(vbm_tier * tier, int policy, int64_t recent_window, int64_t margin);
+/* Deferred mode (enable = 1; 0 returns to the synchronous per-layer mode), the device-side
+ * counterpart of the reference's hosted flush (llama-b11669-hybrid-experts.patch:2953-3005) and
+ * event-protected ID hand-off (:3421-3453): a step's layers run back to back with no host wait,
+ * reading each layer's expert->slot map from the device and streaming the weights of routed
+ * experts that are not visible there straight from the pinned host copy; the step's routed ids
+ * come back behind an event, and the next step (or vbm_tier_flush) runs admission on them, uploads
+ * the admitted experts on the copy stream and publishes them one flush later. Admission sees the
+ * same routes in the same order as the synchronous mode, so the counters and outputs are the same;
+ * `staged` counts the misses read from host memory. Stats lag one step until vbm_tier_flush. No
+ * routing trace is recorded in this mode. */
+vbm_status vbm_tier_set_deferred(vbm_tier * tier, int enable);
+/* Deferred mode: waits for the step in flight, runs its admission and publishes every upload. */
+vbm_status vbm_tier_flush(vbm_tier * tier);
+/* Deferred mode, vbm_tier_step split in two: the host part (the flush above) and the device part,
+ * which makes no host call and may be captured in a HIP graph once and replayed after each
+ * vbm_tier_step_begin (its map upload and id hand-off read and write the tier's pinned buffers at
+ * replay time). Every begin is followed by exactly one enqueue or replay before the next begin or
+ * flush: the next begin admits that step's routed ids. */
+vbm_status vbm_tier_step_begin(vbm_tier * tier);
+vbm_status vbm_tier_step_enqueue(vbm_tier * tier, const float * x, const float * logits, float * out, int32_t * ids,
+                                 void * stream);
 
 /* Attach a routing trace (or NULL to detach): every vbm_tier_step then records each layer's
  * routed experts, as they reach the host for admission, as one route record (tier layer l is the

@@ -62,8 +62,16 @@ def oracle_chain(orc, host, type_id, act, x, logits_t, H, I, E, K):
     return x
 
 
-@pytest.mark.parametrize("type_id,policy,margin", [(39, 0, 4), (39, 1, 1), (8, 2, 2)])
-def test_tier_matches_resident_plan(gpu, orc, type_id, policy, margin):
+@pytest.mark.parametrize("type_id,policy,margin,mode", [
+    (39, 0, 4, "sync"), (39, 1, 1, "sync"), (8, 2, 2, "sync"),
+    (39, 0, 4, "deferred"), (39, 1, 1, "deferred"), (8, 2, 2, "graph"), (39, 1, 1, "graph"),
+])
+def test_tier_matches_resident_plan(gpu, orc, type_id, policy, margin, mode):
+    """Synchronous mode (per-layer admission and staging), deferred mode (no host wait inside a
+    step: misses read from the pinned host copy, admission at the step boundary) and deferred mode
+    with the step's device part captured once as a HIP graph and replayed per token: every token
+    bit-identical to the resident plan and to the oracle chain, counters equal to the Python
+    admission fed the same routes."""
     vb = gpu
     L, E, K, H, I, slots = 3, 16, 4, 256, 256, 4 + 9
     act = vb.ACT_SWIGLU_OAI if type_id == 39 else vb.ACT_SILU
@@ -107,10 +115,27 @@ def test_tier_matches_resident_plan(gpu, orc, type_id, policy, margin):
     o1, o2 = vb.DeviceBuffer(4 * H), vb.DeviceBuffer(4 * H)
     i1, i2 = vb.DeviceBuffer(4 * L * K), vb.DeviceBuffer(4 * L * K)
     staged = 0
+    stream, graph = None, None
+    if mode != "sync":
+        vb.call("vbm_tier_set_deferred", tier.value, 1)
+    if mode == "graph":
+        st_ = C.c_void_p()
+        vb.call("vbm_stream_create", C.byref(st_))
+        stream = st_.value
+        g = C.c_void_p()
+        vb.call("vbm_graph_begin_capture", stream)
+        vb.call("vbm_tier_step_enqueue", tier.value, x.ptr, dl.ptr, o2.ptr, i2.ptr, stream)
+        vb.call("vbm_graph_end_capture", stream, C.byref(g))
+        graph = g.value
     for t in range(tokens):
         dl.upload(logits[t])
         vb.call("vbm_decode_step", plan.value, x.ptr, dl.ptr, o1.ptr, i1.ptr, None, None, None)
-        vb.call("vbm_tier_step", tier.value, x.ptr, dl.ptr, o2.ptr, i2.ptr, None)
+        if mode == "graph":
+            vb.call("vbm_tier_step_begin", tier.value)
+            vb.call("vbm_graph_launch", graph, stream)
+            vb.call("vbm_stream_synchronize", stream)
+        else:
+            vb.call("vbm_tier_step", tier.value, x.ptr, dl.ptr, o2.ptr, i2.ptr, None)
         vb.call("vbm_stream_synchronize", None)
         a, b = o1.download(np.float32, H), o2.download(np.float32, H)
         ia, ib = i1.download(np.int32, (L, K)), i2.download(np.int32, (L, K))
@@ -122,13 +147,22 @@ def test_tier_matches_resident_plan(gpu, orc, type_id, policy, margin):
             hits, made = py.admit(l, chosen[t][l])
             admitted = {e for _, e, _ in made}
             staged += sum(1 for r, e in enumerate(chosen[t][l]) if not hits[r] and e not in admitted)
+    if mode != "sync":
+        vb.call("vbm_tier_flush", tier.value)            # the last step's admissions
     st = vb.TierStats()
     vb.call("vbm_tier_get_stats", tier.value, C.byref(st))
-    print(f"[tier type={type_id} policy={policy}] hits={st.hits}/{tokens * L * K} admissions={st.admissions} "
+    print(f"[tier type={type_id} policy={policy} mode={mode}] hits={st.hits}/{tokens * L * K} admissions={st.admissions} "
           f"evictions={st.evictions} staged={st.staged} uploaded={st.uploaded_bytes}", flush=True)
     assert (st.dispatches, st.hits, st.admissions, st.evictions) == (tokens * L, py.hits, py.admissions, py.evictions)
     assert st.staged == staged and st.admissions > 0
     assert st.staged > 0 or policy == ref.LRU          # lru with margin 1 admits every miss
+    if mode == "sync":
+        assert st.host_reads == 0
+    else:   # every miss, and every admission not yet published, streamed from the host copy
+        assert st.host_reads >= tokens * L * K - st.hits > 0
+    if graph is not None:
+        vb.call("vbm_graph_destroy", graph)
+        vb.call("vbm_stream_destroy", stream)
     vb.call("vbm_tier_destroy", tier.value)
     vb.call("vbm_decode_plan_destroy", plan.value)
     for gu, dn in banks:

@@ -718,6 +718,8 @@ struct DecodeArgs {
     int32_t * route_slots;     // [top_k] bank slot of each pick (expert_to_slot applied), or null
     int activation;
     float alpha, limit;
+    const uint8_t * host_base; // pinned host copy of the layer's experts (slot layout), or null
+    int64_t host_stride;
 };
 
 constexpr int kDownThreads = 256;
@@ -896,9 +898,12 @@ __global__ __launch_bounds__(kDownThreads) __attribute__((amdgpu_waves_per_eu(3)
         if ((expert >> 6) == i) sv = sl[i];
     const int slot = __builtin_amdgcn_readlane(sv, expert & 63);
 
-    // 3. the weight stream: tile meta, the ring, the tail, the bias
-    const bool slot_ok = slot >= 0 && slot < S.n_slots;
-    const uint8_t * slot_base = A.bank + static_cast<size_t>(slot_ok ? slot : 0) * S.slot_bytes;
+    // 3. the weight stream: tile meta, the ring, the tail, the bias. A pick outside the bank
+    // streams the pinned host copy when there is one (and is otherwise poisoned below).
+    const bool in_bank = slot >= 0 && slot < S.n_slots;
+    const bool slot_ok = in_bank || A.host_base != nullptr;
+    const uint8_t * slot_base = in_bank ? A.bank + static_cast<size_t>(slot) * S.slot_bytes
+                                        : (slot_ok ? A.host_base + static_cast<size_t>(expert) * A.host_stride : A.bank);
     const uint8_t * codes_tile = slot_base + static_cast<size_t>(tile) * 32 * nb * (TYPE == 39 ? 16 : 32);
     const int mbytes = meta_tile_bytes<TYPE>(nb);
     u32x4 mst[2];
@@ -999,6 +1004,8 @@ struct DecodeDownArgs {
     const int32_t * route_slots;  // [top_k] slots written by kernel A (same map), or null
     const float * bias;        // down bias [n_expert][rows] or null
     float * y;                 // [top_k][rows]
+    const uint8_t * host_base; // pinned host copy of the layer's experts (slot layout), or null
+    int64_t host_stride;
 };
 
 // Kernel B: one 32-row tile of one rank; wave w holds lane slices 2w (lanes 0..31) and 2w + 1
@@ -1034,8 +1041,10 @@ __global__ __launch_bounds__(kDownThreads) void decode_down_kernel(DecodeDownArg
     const int expert = as_const<int32_t>(A.route_ids)[rank];
     const int slot = A.route_slots ? as_const<int32_t>(A.route_slots)[rank]
                                    : (A.expert_to_slot ? as_const<int32_t>(A.expert_to_slot)[expert] : expert);
-    const bool slot_ok = slot >= 0 && slot < S.n_slots;
-    const uint8_t * slot_base = A.bank + static_cast<size_t>(slot_ok ? slot : 0) * S.slot_bytes;
+    const bool in_bank = slot >= 0 && slot < S.n_slots;
+    const bool slot_ok = in_bank || A.host_base != nullptr;
+    const uint8_t * slot_base = in_bank ? A.bank + static_cast<size_t>(slot) * S.slot_bytes
+                                        : (slot_ok ? A.host_base + static_cast<size_t>(expert) * A.host_stride : A.bank);
     const uint8_t * codes_tile = slot_base + static_cast<size_t>(tile) * 32 * nb * (TYPE == 39 ? 16 : 32);
     const int mbytes = meta_tile_bytes<TYPE>(nb);
     u32x4 mst[2];
@@ -1270,6 +1279,9 @@ void launch_decode_gate_up(const DecodeGateUpArgs & d, hipStream_t stream) {
     a.activation = d.activation;
     a.alpha = d.alpha;
     a.limit = d.limit;
+    require(d.host_base == nullptr || d.host_stride >= static_cast<int64_t>(bank.slot_bytes), "host copy stride too small");
+    a.host_base = d.host_base;
+    a.host_stride = d.host_stride;
     if (bank.type == VBM_TYPE_MXFP4) launch_decode_typed<39>(a, stream);
     else launch_decode_typed<8>(a, stream);
 }
@@ -1290,6 +1302,9 @@ void launch_decode_down(const DecodeDownParams & d, hipStream_t stream) {
     a.route_slots = d.route_slots;
     a.bias = d.bias;
     a.y = d.y;
+    require(d.host_base == nullptr || d.host_stride >= static_cast<int64_t>(bank.slot_bytes), "host copy stride too small");
+    a.host_base = d.host_base;
+    a.host_stride = d.host_stride;
     if (bank.type == VBM_TYPE_MXFP4) launch_decode_down_typed<39>(a, static_cast<int>(d.top_k), stream);
     else launch_decode_down_typed<8>(a, static_cast<int>(d.top_k), stream);
 }

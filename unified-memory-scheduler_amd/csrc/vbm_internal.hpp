@@ -236,6 +236,11 @@ struct DecodeGateUpArgs {
     int32_t * route_slots;            // [top_k] slots of the picks for kernel B, or null
     int activation;
     float alpha, limit;
+    // Optional: device-visible base of this layer's experts in pinned host memory, in the bank's
+    // slot layout (expert e at host_base + e * host_stride). A pick whose map entry is -1 streams
+    // its weights from there instead of being poisoned.
+    const uint8_t * host_base = nullptr;
+    int64_t host_stride = 0;
 };
 void launch_decode_gate_up(const DecodeGateUpArgs & d, hipStream_t stream);
 
@@ -250,6 +255,8 @@ struct DecodeDownParams {
     int64_t top_k;
     const float * bias;               // [n_expert][hidden] or null
     float * y;                        // [top_k][hidden]
+    const uint8_t * host_base = nullptr;   // as in DecodeGateUpArgs (the down bank's slot layout)
+    int64_t host_stride = 0;
 };
 void launch_decode_down(const DecodeDownParams & d, hipStream_t stream);
 

@@ -15,6 +15,17 @@
 //      stream's event (publish after event, llama-b11669-hybrid-experts.patch:2953-3005).
 // Because step 1 waits for the layer's routing, every kernel that could read an overwritten slot
 // has already finished, so eviction never races a reader.
+//
+// Deferred mode (vbm_tier_set_deferred) takes the host off the per-layer path, in the manner of the
+// reference's hosted flush (llama-b11669-hybrid-experts.patch:2953-3005) and its event-protected ID
+// hand-off (:3421-3453): the layers of a step run back to back on the device against per-layer
+// expert->slot maps published at the step boundary; a routed expert that is not visible in the map
+// streams its weights from the pinned host copy inside the decode kernels (the device-side
+// counterpart of the reference's CPU miss path, :1728-1847). The step's routed ids come back
+// asynchronously behind an event; the next step's flush runs admission on them, issues the
+// admitted experts' uploads into their victim slots on the copy stream, and publishes those
+// experts one flush later, after the copy event. Victims leave the map in the same flush that
+// starts overwriting them, and the previous step has finished by then, so no reader races a copy.
 #include "vbm_internal.hpp"
 
 #include <algorithm>
@@ -57,6 +68,17 @@ struct vbm_tier {
     vbm_trace * trace = nullptr;      // optional routing trace (caller-owned)
     std::vector<int64_t> trace_layer_ids;
     bool started = false;             // seeded or stepped: the pool's slots are live
+    // deferred mode
+    bool deferred = false;
+    const uint8_t * host_dev = nullptr;   // device-visible address of host_store
+    int32_t * dev_maps = nullptr;     // [L][E] published expert->slot maps (-1: the pinned host copy)
+    int32_t * host_maps = nullptr;    // pinned mirror, rebuilt at each flush
+    int32_t * step_ids_host = nullptr;   // pinned [L][K]: the last step's routed ids
+    hipEvent_t step_done = nullptr;   // after that step's id hand-off
+    bool step_pending = false;        // its ids still await admission
+    bool awaiting = false;            // a step was begun; its device part (eager or a graph replay) follows
+    std::vector<std::pair<int64_t, int64_t>> unpublished;   // (layer, expert) uploads in flight
+    bool uploads_timed = false;       // copy_begin / copy_end bracket the uploads in flight
 
     ~vbm_tier() {
         (void)hipSetDevice(device);
@@ -81,6 +103,10 @@ struct vbm_tier {
         if (pf_maps) (void)hipFree(pf_maps);
         if (pf_maps_host) (void)hipHostFree(pf_maps_host);
         if (pf_ids_host) (void)hipHostFree(pf_ids_host);
+        if (dev_maps) (void)hipFree(dev_maps);
+        if (host_maps) (void)hipHostFree(host_maps);
+        if (step_ids_host) (void)hipHostFree(step_ids_host);
+        if (step_done) (void)hipEventDestroy(step_done);
     }
 
     uint8_t * host_expert(int64_t layer, int64_t expert) const {
@@ -105,6 +131,140 @@ void stage(vbm_tier & t, int64_t layer, int64_t expert, int64_t slot) {
     check_hip(hipMemcpyAsync(t.down->base + static_cast<size_t>(slot) * t.dn_bytes, src + t.gu_bytes, t.dn_bytes,
                              hipMemcpyHostToDevice, t.copy_stream), "tier down stage");
     t.stats.uploaded_bytes += t.gu_bytes + t.dn_bytes;
+}
+
+// Deferred mode, at a step boundary: (1) wait for the last step and publish the uploads of the
+// previous flush (their copies were issued a step ago); (2) run admission on the last step's
+// routed ids, layer by layer, as the synchronous mode does per layer; (3) issue the admitted
+// experts' uploads on the copy stream; (4) rebuild the per-layer maps: the admission's slot map
+// minus the uploads still in flight. The maps reach the device at the start of the next step.
+void tier_flush(vbm_tier & t) {
+    const vbm_tier_desc & d = t.desc;
+    const int64_t L = d.n_layers, E = d.n_expert, K = d.top_k;
+    if (t.step_pending) check_hip(hipEventSynchronize(t.step_done), "tier step hand-off");
+    if (!t.unpublished.empty()) {
+        check_hip(hipEventSynchronize(t.copy_end), "tier upload");
+        if (t.uploads_timed) {
+            float ms = 0.0f;
+            check_hip(hipEventElapsedTime(&ms, t.copy_begin, t.copy_end), "tier copy timing");
+            t.stats.copy_ms += ms;
+        }
+        t.unpublished.clear();
+        t.uploads_timed = false;
+    }
+    std::vector<std::pair<int64_t, int64_t>> uploads;
+    if (t.step_pending) {
+        std::vector<int32_t> hits(static_cast<size_t>(K)), slots(static_cast<size_t>(K)),
+            experts(static_cast<size_t>(K)), evicted(static_cast<size_t>(K));
+        std::vector<int32_t> map(static_cast<size_t>(E));
+        for (int64_t l = 0; l < L; ++l) {
+            const int32_t * ids = t.step_ids_host + l * K;
+            for (int64_t r = 0; r < K; ++r) t.stats.host_reads += t.host_maps[l * E + ids[r]] < 0;   // the step's map
+            int64_t n_admitted = 0;
+            check_status(vbm_admission_admit(t.admission, l, ids, hits.data(), slots.data(), experts.data(),
+                                             evicted.data(), &n_admitted), "tier admission");
+            ++t.stats.dispatches;
+            check_status(vbm_admission_slot_map(t.admission, l, map.data()), "tier slot map");
+            for (int64_t r = 0; r < K; ++r) {
+                t.stats.hits += hits[r];
+                if (map[static_cast<size_t>(ids[r])] < 0) ++t.stats.staged;   // served from the host copy
+            }
+            t.stats.admissions += static_cast<uint64_t>(n_admitted);
+            for (int64_t i = 0; i < n_admitted; ++i) {
+                t.stats.evictions += evicted[i] >= 0;
+                uploads.emplace_back(l, experts[i]);
+            }
+            if (n_admitted > 0) {
+                if (!t.uploads_timed) {
+                    check_hip(hipEventRecord(t.copy_begin, t.copy_stream), "tier copy event");
+                    t.uploads_timed = true;
+                }
+                for (int64_t i = 0; i < n_admitted; ++i) stage(t, l, experts[i], slots[i]);
+            }
+        }
+        t.step_pending = false;
+    }
+    if (!uploads.empty()) check_hip(hipEventRecord(t.copy_end, t.copy_stream), "tier copy event");
+    t.unpublished = std::move(uploads);
+    for (int64_t l = 0; l < L; ++l)
+        check_status(vbm_admission_slot_map(t.admission, l, t.host_maps + l * E), "tier slot map");
+    for (const auto & u : t.unpublished) t.host_maps[u.first * E + u.second] = -1;
+}
+
+// Completes everything in flight and publishes it (before a prefill, a mode change or teardown).
+void tier_quiesce(vbm_tier & t) {
+    if (!t.deferred) return;
+    if (t.awaiting) t.step_pending = true;
+    t.awaiting = false;
+    tier_flush(t);
+    if (!t.unpublished.empty()) {
+        check_hip(hipEventSynchronize(t.copy_end), "tier upload");
+        t.unpublished.clear();
+        t.uploads_timed = false;
+        const int64_t L = t.desc.n_layers, E = t.desc.n_expert;
+        for (int64_t l = 0; l < L; ++l)
+            check_status(vbm_admission_slot_map(t.admission, l, t.host_maps + l * E), "tier slot map");
+    }
+}
+
+// The device part of a deferred step (no host waits): publish the maps, the layers back to back
+// with misses from the pinned host copy, the combine, the id hand-off.
+void tier_enqueue_step(vbm_tier & t, const float * x, const float * logits, float * out, int32_t * ids, hipStream_t s) {
+    const vbm_tier_desc & d = t.desc;
+    const int64_t L = d.n_layers, E = d.n_expert, K = d.top_k, H = d.hidden;
+    const int64_t stride = static_cast<int64_t>(t.gu_bytes + t.dn_bytes);
+    check_hip(hipMemcpyAsync(t.dev_maps, t.host_maps, sizeof(int32_t) * L * E, hipMemcpyHostToDevice, s), "tier maps");
+    for (int64_t l = 0; l < L; ++l) {
+        const uint8_t * layer_host = t.host_dev + static_cast<size_t>(l) * E * static_cast<size_t>(stride);
+        DecodeGateUpArgs a{};
+        a.bank = t.gate_up;
+        a.expert_to_slot = t.dev_maps + l * E;
+        a.logits = logits + l * E;
+        a.n_expert = E;
+        a.top_k = K;
+        a.hidden = H;
+        a.x_in = l == 0 ? x : nullptr;
+        a.prev_y = t.y;
+        a.prev_w = l == 0 ? nullptr : t.route_w + (l - 1) * K;
+        a.bias = t.gu_bias[l];
+        a.act_f = t.act_f;
+        a.route_ids = t.route_ids + l * K;
+        a.route_w = t.route_w + l * K;
+        a.activation = d.activation;
+        a.alpha = 1.702f;
+        a.limit = 7.0f;
+        a.host_base = layer_host;
+        a.host_stride = stride;
+        launch_decode_gate_up(a, s);
+        DecodeDownParams b{};
+        b.bank = t.down;
+        b.expert_to_slot = t.dev_maps + l * E;
+        b.act_f = t.act_f;
+        b.act_layout = t.act_layout;
+        b.route_ids = t.route_ids + l * K;
+        b.top_k = K;
+        b.bias = t.dn_bias[l];
+        b.y = t.y;
+        b.host_base = layer_host + t.gu_bytes;
+        b.host_stride = stride;
+        launch_decode_down(b, s);
+    }
+    launch_combine(t.y, t.route_w + (L - 1) * K, H, K, 1, out, s);
+    if (ids) check_hip(hipMemcpyAsync(ids, t.route_ids, sizeof(int32_t) * L * K, hipMemcpyDeviceToDevice, s), "ids copy");
+    check_hip(hipMemcpyAsync(t.step_ids_host, t.route_ids, sizeof(int32_t) * L * K, hipMemcpyDeviceToHost, s),
+              "tier id hand-off");
+    check_hip(hipEventRecord(t.step_done, s), "tier step event");
+    check_hip(hipEventRecord(t.last_use, s), "tier last use");
+    t.used = true;
+}
+
+// Host part of a deferred step: the step begun last time has run (eagerly or as a graph replay),
+// so its ids are the next to admit.
+void tier_begin_step(vbm_tier & t) {
+    if (t.awaiting) t.step_pending = true;
+    tier_flush(t);
+    t.awaiting = true;
+    t.started = true;
 }
 
 }  // namespace
@@ -254,11 +414,15 @@ vbm_status vbm_tier_load_gguf(vbm_tier * t, const vbm_gguf * g, const int64_t * 
 vbm_status vbm_tier_seed(vbm_tier * t, int64_t layer, int64_t expert) {
     return guarded([&] {
         require(t != nullptr, "null tier");
+        tier_quiesce(*t);
+        if (t->used) check_hip(hipEventSynchronize(t->last_use), "tier seed");
         int32_t slot = -1;
         check_status(vbm_admission_seed(t->admission, layer, expert, &slot), "tier seed");
         t->started = true;
         stage(*t, layer, expert, slot);
         check_hip(hipStreamSynchronize(t->copy_stream), "tier seed synchronize");
+        if (t->deferred)
+            check_status(vbm_admission_slot_map(t->admission, layer, t->host_maps + layer * t->desc.n_expert), "tier slot map");
     });
 }
 
@@ -267,6 +431,11 @@ vbm_status vbm_tier_step(vbm_tier * t, const float * x, const float * logits, fl
         require(t != nullptr && x && logits && out, "null buffer");
         require(reinterpret_cast<uintptr_t>(x) % 16 == 0, "decode input must be 16-byte aligned");
         const hipStream_t s = as_stream(stream);
+        if (t->deferred) {
+            tier_begin_step(*t);
+            tier_enqueue_step(*t, x, logits, out, ids, s);
+            return;
+        }
         const vbm_tier_desc & d = t->desc;
         const int64_t L = d.n_layers, E = d.n_expert, K = d.top_k, H = d.hidden;
         if (t->trace) {
@@ -365,6 +534,7 @@ vbm_status vbm_tier_prefill(vbm_tier * t, int64_t layer, const float * x, const 
         require(n_tokens >= kGemmMinTokens && n_tokens <= 65536,
                 "tier prefill takes 16..65536 tokens (single tokens: vbm_tier_step)");
         const hipStream_t s = as_stream(stream);
+        tier_quiesce(*t);                 // deferred mode: admissions applied, uploads published
         const int64_t E = d.n_expert, K = d.top_k, H = d.hidden, T = n_tokens;
         vbm_moe_layer_desc desc{};
         desc.gate_up = t->gate_up;
@@ -467,9 +637,91 @@ vbm_status vbm_tier_prefill(vbm_tier * t, int64_t layer, const float * x, const 
     });
 }
 
+vbm_status vbm_tier_set_deferred(vbm_tier * t, int enable) {
+    return guarded([&] {
+        require(t != nullptr, "null tier");
+        require(!enable || t->trace == nullptr, "deferred mode records no routing trace; detach it first");
+        if (static_cast<bool>(enable) == t->deferred) return;
+        const vbm_tier_desc & d = t->desc;
+        const int64_t L = d.n_layers, E = d.n_expert, K = d.top_k;
+        if (enable) {
+            if (!t->dev_maps) {
+                check_hip(hipHostGetDevicePointer(reinterpret_cast<void **>(const_cast<uint8_t **>(&t->host_dev)),
+                                                  t->host_store, 0), "tier host store device address");
+                check_hip(hipMalloc(reinterpret_cast<void **>(&t->dev_maps), sizeof(int32_t) * L * E), "tier maps");
+                check_hip(hipHostMalloc(reinterpret_cast<void **>(&t->host_maps), sizeof(int32_t) * L * E,
+                                        hipHostMallocDefault), "tier maps");
+                check_hip(hipHostMalloc(reinterpret_cast<void **>(&t->step_ids_host), sizeof(int32_t) * L * K,
+                                        hipHostMallocDefault), "tier ids");
+                check_hip(hipEventCreateWithFlags(&t->step_done, hipEventDisableTiming), "tier event");
+            }
+            if (t->used) check_hip(hipEventSynchronize(t->last_use), "tier mode change");
+            check_hip(hipStreamSynchronize(t->copy_stream), "tier mode change");
+            for (int64_t l = 0; l < L; ++l)
+                check_status(vbm_admission_slot_map(t->admission, l, t->host_maps + l * E), "tier slot map");
+            t->deferred = true;
+        } else {
+            tier_quiesce(*t);
+            t->deferred = false;
+        }
+    });
+}
+
+vbm_status vbm_tier_reset(vbm_tier * t, int policy, int64_t recent_window, int64_t margin) {
+    return guarded([&] {
+        require(t != nullptr, "null tier");
+        tier_quiesce(*t);
+        if (t->used) check_hip(hipEventSynchronize(t->last_use), "tier reset");
+        check_hip(hipStreamSynchronize(t->copy_stream), "tier reset");
+        const vbm_tier_desc & d = t->desc;
+        vbm_admission * fresh = nullptr;
+        check_status(vbm_admission_create(d.n_layers, d.n_expert, d.top_k, d.n_slots, recent_window, margin, policy,
+                                          &fresh), "tier admission");
+        vbm_admission_destroy(t->admission);
+        t->admission = fresh;
+        t->desc.policy = policy;
+        t->desc.recent_window = recent_window;
+        t->desc.margin = margin;
+        t->stats = vbm_tier_stats{};
+        t->step_pending = t->awaiting = false;
+        t->unpublished.clear();
+        t->uploads_timed = false;
+        t->started = false;
+        t->used = false;
+        if (t->deferred)
+            for (int64_t l = 0; l < d.n_layers; ++l)
+                check_status(vbm_admission_slot_map(t->admission, l, t->host_maps + l * d.n_expert), "tier slot map");
+    });
+}
+
+vbm_status vbm_tier_step_begin(vbm_tier * t) {
+    return guarded([&] {
+        require(t != nullptr && t->deferred, "vbm_tier_step_begin needs deferred mode");
+        tier_begin_step(*t);
+    });
+}
+
+vbm_status vbm_tier_step_enqueue(vbm_tier * t, const float * x, const float * logits, float * out, int32_t * ids,
+                                 void * stream) {
+    return guarded([&] {
+        require(t != nullptr && t->deferred, "vbm_tier_step_enqueue needs deferred mode");
+        require(x && logits && out, "null buffer");
+        require(reinterpret_cast<uintptr_t>(x) % 16 == 0, "decode input must be 16-byte aligned");
+        tier_enqueue_step(*t, x, logits, out, ids, as_stream(stream));
+    });
+}
+
+vbm_status vbm_tier_flush(vbm_tier * t) {
+    return guarded([&] {
+        require(t != nullptr, "null tier");
+        tier_quiesce(*t);
+    });
+}
+
 vbm_status vbm_tier_set_trace(vbm_tier * t, vbm_trace * trace) {
     return guarded([&] {
         require(t != nullptr, "null tier");
+        require(trace == nullptr || !t->deferred, "deferred mode records no routing trace");
         std::vector<int64_t> ids;
         if (trace) {
             int64_t n = 0;

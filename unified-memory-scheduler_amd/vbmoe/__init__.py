@@ -35,7 +35,7 @@ class TierStats(C.Structure):
     _fields_ = [
         ("dispatches", u64), ("hits", u64), ("admissions", u64), ("evictions", u64), ("staged", u64),
         ("uploaded_bytes", u64), ("copy_ms", C.c_double), ("prefill_tokens", u64), ("prefill_resident", u64),
-        ("prefill_streamed", u64),
+        ("prefill_streamed", u64), ("host_reads", u64),
     ]
 
 
@@ -194,6 +194,11 @@ SIGNATURES = {
     "vbm_tier_seed": [vp, i64, i64],
     "vbm_tier_step": [vp, vp, vp, vp, vp, vp],
     "vbm_tier_get_stats": [vp, C.POINTER(TierStats)],
+    "vbm_tier_set_deferred": [vp, C.c_int],
+    "vbm_tier_flush": [vp],
+    "vbm_tier_reset": [vp, C.c_int, i64, i64],
+    "vbm_tier_step_begin": [vp],
+    "vbm_tier_step_enqueue": [vp, vp, vp, vp, vp, vp],
     "vbm_tier_set_trace": [vp, vp],
     "vbm_tier_load_gguf": [vp, vp, vp, vp],
     "vbm_residency_replay": [C.POINTER(ResidencyLayer), i64, vp, vp, vp, vp, i64, C.POINTER(ResidencyParams),
