@@ -666,7 +666,10 @@ vbm_status vbm_host_join(vbm_host_call * call, const float * a, const float * b,
                          void * stream);
 /* Makes `stream` wait for the call's completion without a join. */
 vbm_status vbm_host_call_wait(vbm_host_call * call, void * stream);
-/* Waits for the call's last enqueue and frees what the library attached to it. */
+/* Waits for the call's last enqueue, and for the worker to have run fn for its last mailbox post
+ * (also one that was not waited for; bounded, VBM_ERR_RUNTIME on expiry), then frees what the
+ * library attached to it. Re-enqueuing a descriptor is safe too: in either mode the new input
+ * copies wait on the device (bounded) until the worker has handled the call's previous post. */
 vbm_status vbm_host_call_release(vbm_host_call * call);
 /* Returns once the device's worker has handled every posted request (call after the stream is idle). */
 vbm_status vbm_host_mailbox_drain(int device, double timeout_s);

@@ -198,3 +198,42 @@ def test_mailbox_wait_is_bounded(gpu):
     vb.call("vbm_host_mailbox_drain", 0, 10.0)
     assert call.runs == 1
     call.release()
+
+
+@pytest.mark.gpu
+def test_mailbox_reenqueue_and_release_wait_for_an_unwaited_post(gpu):
+    """A bookkeeping-only post (no miss, not waited for) whose fn is still sleeping when the same
+    descriptor is enqueued again with new inputs: fn must read the inputs of its own post (the new
+    input copies wait until the worker has handled the previous post), and release must not return
+    while fn is still queued or running."""
+    vb = gpu
+    n = 512
+    seen = []
+    call = AxpyCall(vb, n)
+    inner = call.fn
+
+    def observing(ctx):
+        import time as _t
+        _t.sleep(0.05)
+        seen.append(float(call.src[0].arr[0]))
+        inner(ctx)
+    call.fn = vb.HOST_FN(observing)
+    call.call.fn = call.fn
+    ones = vb.DeviceBuffer.from_array(np.ones(n, np.float32))
+    a1 = vb.DeviceBuffer.from_array(np.full(n, 1.0, np.float32))
+    a2 = vb.DeviceBuffer.from_array(np.full(n, 2.0, np.float32))
+    out = vb.DeviceBuffer(4 * n)
+    hits = vb.DeviceBuffer.from_array(np.array([1, 1], np.int32))          # no miss: not waited for
+    call.enqueue(a1, ones, out, vb.HOST_CALL_MAILBOX, miss=hits, n_miss=2, wait=True)
+    call.enqueue(a2, ones, out, vb.HOST_CALL_MAILBOX, wait=True)           # waited, new inputs
+    vb.call("vbm_stream_synchronize", None)
+    assert np.array_equal(out.download(np.float32, n), np.full(n, 5.0, np.float32))
+    vb.call("vbm_host_mailbox_drain", 0, 10.0)
+    assert seen == [1.0, 2.0], seen
+    # release right after an unwaited post: returns only once its fn has run
+    call.enqueue(a1, ones, out, vb.HOST_CALL_MAILBOX, miss=hits, n_miss=2, wait=True)
+    vb.call("vbm_stream_synchronize", None)
+    vb.call("vbm_host_call_release", C.byref(call.call))
+    assert seen == [1.0, 2.0, 1.0], seen
+    for p in call.src + [call.dst]:
+        p.free()

@@ -59,6 +59,8 @@ struct CallState {
     int device = 0;
     hipEvent_t ready = nullptr, done = nullptr;
     int32_t * skipped = nullptr;   // device flag: output is zero-filled
+    uint64_t * seq_host = nullptr; // mapped host word: the ring sequence of this call's last post (0: none)
+    uint64_t * seq_dev = nullptr;  // its device address
 };
 
 void worker_loop(Worker * w) {
@@ -125,6 +127,7 @@ struct PostArgs {
     Mailbox * box;          // device view of the ring
     int device;
     int32_t * skipped;
+    uint64_t * seq_out;     // the call's last-post word (mapped host memory)
     uint32_t spin_limit;
 };
 
@@ -141,6 +144,7 @@ __global__ void __launch_bounds__(256) host_call_post_kernel(PostArgs a) {
         __builtin_amdgcn_s_sleep(32);
     }
     __hip_atomic_store(&a.box->call[seq % kRing], a.call, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(a.seq_out, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __hip_atomic_store(&a.box->posted, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     int skipped = !need;
     if (need) {
@@ -155,6 +159,19 @@ __global__ void __launch_bounds__(256) host_call_post_kernel(PostArgs a) {
         }
     }
     *a.skipped = skipped;
+}
+
+// Before a call's inputs are overwritten: its previous post (possibly one that was not waited for)
+// must have been handled by the host worker, whose fn may still read them. Bounded like the post's
+// own wait; an expiry counts as a timeout.
+__global__ void wait_handled_kernel(const Mailbox * box, const uint64_t * seq_slot, int device, uint32_t spin_limit) {
+    if (threadIdx.x != 0) return;
+    const uint64_t seq = __hip_atomic_load(seq_slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    for (uint32_t i = 0; i < spin_limit; ++i) {
+        if (__hip_atomic_load(&box->done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) >= seq) return;
+        __builtin_amdgcn_s_sleep(32);
+    }
+    atomicAdd(&g_timeouts[device], 1u);
 }
 
 __global__ void zero_if_skipped_kernel(uint8_t * dst, int64_t n, const int32_t * skipped) {
@@ -182,6 +199,12 @@ CallState & state_of(vbm_host_call * call, int device) {
         check_hip(hipEventCreateWithFlags(&st->ready, hipEventDisableTiming), "host-call event");
         check_hip(hipEventCreateWithFlags(&st->done, hipEventDisableTiming), "host-call event");
         check_hip(hipMalloc(reinterpret_cast<void **>(&st->skipped), sizeof(int32_t)), "host-call flag");
+        check_hip(hipHostMalloc(reinterpret_cast<void **>(&st->seq_host), sizeof(uint64_t),
+                                hipHostMallocMapped | hipHostMallocCoherent | hipHostMallocPortable),
+                  "host-call sequence word");
+        *st->seq_host = 0;
+        check_hip(hipHostGetDevicePointer(reinterpret_cast<void **>(&st->seq_dev), st->seq_host, 0),
+                  "host-call sequence word");
         call->backend_state = st;
     }
     require(st->device == device, "a host call is bound to the device it first ran on");
@@ -225,6 +248,11 @@ vbm_status vbm_host_call_enqueue(vbm_host_call * call, const void * const * srcs
         const hipStream_t main = as_stream(stream), side = side_stream(device);
         check_hip(hipEventRecord(st.ready, main), "host-call fork");
         check_hip(hipStreamWaitEvent(side, st.ready, 0), "host-call fork");
+        if (g_workers[device]) {   // a mailbox post of this call may still be queued or running
+            hipLaunchKernelGGL(wait_handled_kernel, dim3(1), dim3(64), 0, side, g_workers[device]->box_dev, st.seq_dev,
+                               device, g_spin_limit.load());
+            check_hip(hipGetLastError(), "host-call handled-wait launch");
+        }
         for (int i = 0; i < n_src; ++i)
             check_hip(hipMemcpyAsync(call->src_host[i], srcs[i], src_bytes[i], hipMemcpyDeviceToHost, side),
                       "host-call input copy");
@@ -240,6 +268,7 @@ vbm_status vbm_host_call_enqueue(vbm_host_call * call, const void * const * srcs
             a.box = w->box_dev;
             a.device = device;
             a.skipped = st.skipped;
+            a.seq_out = st.seq_dev;
             a.spin_limit = g_spin_limit.load();
             hipLaunchKernelGGL(host_call_post_kernel, dim3(1), dim3(256), 0, side, a);
             check_hip(hipGetLastError(), "host-call post launch");
@@ -281,9 +310,23 @@ vbm_status vbm_host_call_release(vbm_host_call * call) {
         auto * st = static_cast<CallState *>(call->backend_state);
         if (!st) return;
         check_hip(hipEventSynchronize(st->done), "host-call release");
+        // a post that was not waited for (or whose wait expired) may still be queued at the worker,
+        // which holds the descriptor's address: wait for it, bounded, before anything is freed
+        const uint64_t seq = __atomic_load_n(st->seq_host, __ATOMIC_ACQUIRE);
+        Worker * w = g_workers[st->device];
+        if (w && seq) {
+            const auto start = std::chrono::steady_clock::now();
+            const double limit_s = 1e-6 * static_cast<double>(g_spin_limit.load()) + 1.0;
+            while (__atomic_load_n(&w->box->done, __ATOMIC_ACQUIRE) < seq) {
+                if (std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count() > limit_s)
+                    fail(VBM_ERR_RUNTIME, "host call release: its function is still queued or running at the worker");
+                std::this_thread::sleep_for(std::chrono::microseconds(20));
+            }
+        }
         (void)hipEventDestroy(st->ready);
         (void)hipEventDestroy(st->done);
         (void)hipFree(st->skipped);
+        (void)hipHostFree(st->seq_host);
         delete st;
         call->backend_state = nullptr;
     });
