@@ -601,8 +601,9 @@ vbm_status vbm_tier_reset(vbm_tier * tier, int policy, int64_t recent_window, in
  * experts that are not visible there straight from the pinned host copy; the step's routed ids
  * come back behind an event, and the next step (or vbm_tier_flush) runs admission on them, uploads
  * the admitted experts on the copy stream and publishes them one flush later. Admission sees the
- * same routes in the same order as the synchronous mode, so the counters and outputs are the same;
- * `staged` counts the misses read from host memory. Stats lag one step until vbm_tier_flush. No
+ * same routes in the same order as the synchronous mode, so the counters (staged included: the
+ * misses that mode would stage) and outputs are the same; `host_reads` counts the routed experts
+ * the kernels actually read from host memory. Stats lag one step until vbm_tier_flush. No
  * routing trace is recorded in this mode. */
 vbm_status vbm_tier_set_deferred(vbm_tier * tier, int enable);
 /* Deferred mode: waits for the step in flight, runs its admission and publishes every upload. */
