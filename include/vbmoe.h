@@ -684,7 +684,9 @@ vbm_status vbm_host_mailbox_set_spin_limit(uint32_t polls);
  * The reference builds the routed-expert branch as ggml nodes
  * (third_party/patches/llama-b11669-hybrid-experts.patch:1394-1683: MUL_MAT_ID, ADD_ID, gate/up
  * views, GLU, MUL_MAT_ID, ADD_ID, MUL by the routing weights; :1905-1916: ADD of the resident and
- * host halves, sequential ADDs of strided rank views, CONT; :966-1054: CUSTOM host calls) and
+ * host halves, sequential ADDs of strided rank views, CONT; :966-1054: CUSTOM host calls;
+ * :1860-1916: the frozen-hybrid dispatch, whose packed slot remap (vbm_admission_write_dispatch)
+ * reaches MUL_MAT_ID through strided views and I32 casts) and
  * hands each node to a backend through compute_forward (:1079-1083) and supports_op (:1101-1102; the
  * pattern of fp32-experts-experimental.patch:74-82). vbm_node carries ggml_tensor's fields: a
  * backend adapter copies type, ne, nb, data, op_params and src from its tensor, sets `op` to the
@@ -703,6 +705,7 @@ vbm_status vbm_host_mailbox_set_spin_limit(uint32_t polls);
 #define VBM_NODE_ADD_ID 6        /* src0 y, src1 bias [rows, n_as], src2 ids (see vbm_add_id)     */
 #define VBM_NODE_GLU 7           /* src0 gate (src1 up, or the second half of src0's rows)        */
 #define VBM_NODE_CUSTOM 8        /* host call or host join (extra = vbm_host_call)                */
+#define VBM_NODE_CPY 9           /* ggml_cast: contiguous dst = src0 converted, F32 <-> I32       */
 /* ggml_glu_op values (GLU op_params[0]); op_params[1] = swapped; SWIGLU_OAI: op_params[2] alpha
  * and op_params[3] limit, as float bits (ggml_swiglu_oai). */
 #define VBM_GLU_OP_SWIGLU 2

@@ -135,6 +135,21 @@ def test_custom_rules(vb, g):
     assert not ok(g.tensor(F32, (64,), FAKE, op=vb.NODE_CUSTOM, srcs=(a, b)))           # no descriptor
 
 
+def test_cpy_rules(vb, g):
+    ok = g.supported
+    packed = g.leaf(F32, (4, 4, 7), FAKE)                                   # a dispatch packet [K, 4, T]
+    row = g.view(packed, (4, 7), [4, packed.nb[2], packed.nb[2] * 7, packed.nb[2] * 7], packed.nb[1])
+    cast = g.tensor(I32, (4, 7), FAKE, op=vb.NODE_CPY, srcs=(row,))
+    cast.src[1] = C.pointer(cast)                                            # ggml_cast names itself
+    assert ok(cast)
+    assert ok(g.tensor(F32, (4, 7), FAKE, op=vb.NODE_CPY, srcs=(g.leaf(I32, (4, 7), FAKE),)))
+    assert ok(g.tensor(F32, (28,), FAKE, op=vb.NODE_CPY, srcs=(row,)))       # same element count
+    assert not ok(g.tensor(F16, (4, 7), FAKE, op=vb.NODE_CPY, srcs=(row,)))
+    assert not ok(g.tensor(I32, (4, 6), FAKE, op=vb.NODE_CPY, srcs=(row,)))
+    assert not ok(g.tensor(I32, (4, 7), FAKE, op=vb.NODE_CPY, srcs=(row,), nb=[4, 32, 32 * 7, 32 * 7]))  # strided dst
+    assert not ok(g.tensor(I32, (4, 7), FAKE, op=vb.NODE_CPY, srcs=(g.view(packed, (4, 7), [2, 64, 448, 448], 0),)))
+
+
 def test_compute_forward_refuses_unsupported_nodes_before_device_work(vb, g):
     node = mmid(vb, g, rows=5750)
     with pytest.raises(vb.VbmError, match="rows % 32"):

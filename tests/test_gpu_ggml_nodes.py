@@ -124,6 +124,117 @@ def test_expert_branch_nodes_match_oracle_layer(gpu, orc, case):
         layer.up_bank.destroy()
 
 
+def weighted_branch(vb, g, new, x, ids, bias_ids, weights, gu_as, gu_bias, dn_as, dn_bias, dims):
+    """MUL_MAT_ID -> ADD_ID -> split views -> GLU (swiglu_oai) -> MUL_MAT_ID -> ADD_ID -> MUL by the
+    weights, on a fused gate_up expert tensor (the reference's expert_branch, weights after the FFN)."""
+    Hd, I, K, T = dims
+    gate_up = g.tensor(F32, (2 * I, K, T), new((2 * I, K, T)), op=vb.NODE_MUL_MAT_ID, srcs=(gu_as, x, ids))
+    gate_up = g.tensor(F32, (2 * I, K, T), new((2 * I, K, T)), op=vb.NODE_ADD_ID, srcs=(gate_up, gu_bias, bias_ids))
+    nb = list(gate_up.nb)
+    gate, up = g.view(gate_up, (I, K, T), nb, 0), g.view(gate_up, (I, K, T), nb, I * 4)
+    act = g.tensor(F32, (I, K, T), new((I, K, T)), op=vb.NODE_GLU, srcs=(gate, up),
+                   params=(vb.GLU_OP_SWIGLU_OAI, 0, f32_bits(1.702), f32_bits(7.0)))
+    y = g.tensor(F32, (Hd, K, T), new((Hd, K, T)), op=vb.NODE_MUL_MAT_ID, srcs=(dn_as, act, ids))
+    y = g.tensor(F32, (Hd, K, T), new((Hd, K, T)), op=vb.NODE_ADD_ID, srcs=(y, dn_bias, bias_ids))
+    return g.tensor(F32, (Hd, K, T), new((Hd, K, T)), op=vb.NODE_MUL, srcs=(y, weights))
+
+
+@pytest.mark.parametrize("cold_rank", [-1, 2])
+def test_frozen_hybrid_dispatch_nodes_match_oracle_layer(gpu, orc, cold_rank):
+    """The reference's frozen-hybrid dispatch as nodes (hybrid-experts.patch:1860-1916): the packed
+    slot remap written by vbm_admission_write_dispatch (:3059-3084) is read through strided views of
+    its rows and I32 casts; the resident branch runs over the slot bank with the full routing
+    weights (a miss reads the all-zero slot of its rank, token 0's cold rank the scratch slot
+    n_slots), the cold branch over every expert with the cpu ids (-1 on resident ranks) and the
+    cold weights; their ADD, the rank ADDs and CONT give the oracle's plain layer bit for bit in the
+    exact order."""
+    from test_admission import LibAdmission
+    from test_gpu_layer import Layer
+    vb = gpu
+    E, K, T, Hd, I = 16, 4, 6, 256, 192
+    layer = Layer(vb, H.MX, Hd, I, E, K, seed=95, router=False, biases=True, activation=vb.ACT_SWIGLU_OAI)
+    x = vb.synth_normal(95, 6, 0, T * Hd).reshape(T, Hd)
+    logits = vb.synth_normal(95, 7, 0, T * E).reshape(T, E)
+    ref = layer.forward_cpu(orc, x, logits)
+    ids, w = ref["ids"].astype(np.int32), np.ascontiguousarray(ref["weights"], np.float32)
+    n_slots = K + 8
+    adm = LibAdmission(vb, 1, E, K, n_slots)
+    routed = sorted(set(ids.reshape(-1).tolist()))
+    seeds = routed[::2][:5] + [e for e in range(E) if e not in routed][:2]   # some routed experts resident
+    assert len(seeds) <= n_slots - K
+    for e in seeds:
+        adm.seed(0, e)
+    slot_map = adm.slot_map(0)
+    packet = adm.write_dispatch(0, ids, w, cold_rank)
+    adm.close()
+    cold = packet[:, 3, :] == 1.0
+    print(f"[hybrid cold_rank={cold_rank}] resident {int((~cold).sum())} cold {int(cold.sum())} of {T * K}", flush=True)
+    assert cold.any() and (~cold).any()
+    # slot bank: n_slots + 1 slots; [0, K) stay zero, held slots get their expert, n_slots the cold rank's
+    per_gu, per_dn = 2 * I * (Hd // 32) * 17, Hd * (I // 32) * 17
+    slot_expert = [-1] * (n_slots + 1)
+    for e, s_ in enumerate(slot_map):
+        if s_ >= 0:
+            slot_expert[s_] = e
+    if cold_rank >= 0:
+        slot_expert[n_slots] = int(ids[0, cold_rank])
+    gu_s = np.zeros((n_slots + 1, per_gu), np.uint8)
+    dn_s = np.zeros((n_slots + 1, per_dn), np.uint8)
+    gub_s = np.zeros((n_slots + 1, 2 * I), np.float32)
+    dnb_s = np.zeros((n_slots + 1, Hd), np.float32)
+    for s_, e in enumerate(slot_expert):
+        if e >= 0:
+            gu_s[s_] = layer.gu[e * per_gu:(e + 1) * per_gu]
+            dn_s[s_] = layer.dn[e * per_dn:(e + 1) * per_dn]
+            gub_s[s_] = layer.gu_b.reshape(E, 2 * I)[e]
+            dnb_s[s_] = layer.dn_b.reshape(E, Hd)[e]
+    gu_bank = H.make_bank(H.MX, gu_s.reshape(-1), n_slots + 1, 2 * I, Hd, interleave=True)
+    dn_bank = H.make_bank(H.MX, dn_s.reshape(-1), n_slots + 1, Hd, I)
+    keep = [vb.DeviceBuffer.from_array(v) for v in (x, packet, ids, w, gub_s, dnb_s)]
+    dx, dpacket, dids, dw, dgub, ddnb = keep
+
+    def new(ne):
+        buf = vb.DeviceBuffer(4 * int(np.prod(ne)))
+        keep.append(buf)
+        return buf.ptr
+
+    g = Graph(vb)
+    X = g.leaf(F32, (Hd, 1, T), dx.ptr)
+    packed = g.leaf(F32, (K, 4, T), dpacket.ptr)
+    selected = g.leaf(I32, (K, T), dids.ptr)
+    weights = g.leaf(F32, (1, K, T), dw.ptr)
+    rows_nb = [4, packed.nb[2], packed.nb[2] * T, packed.nb[2] * T]
+    cpu_ids = g.tensor(I32, (K, T), new((K, T)), op=vb.NODE_CPY, srcs=(g.view(packed, (K, T), rows_nb, 0),))
+    gpu_ids = g.tensor(I32, (K, T), new((K, T)), op=vb.NODE_CPY, srcs=(g.view(packed, (K, T), rows_nb, packed.nb[1]),))
+    cpu_ids.src[1] = C.pointer(cpu_ids)                  # ggml_cast: a CPY node's src[1] is itself
+    cold_weights = g.view(packed, (1, K, T), [4, 4, packed.nb[2], packed.nb[2] * T], 2 * packed.nb[1])
+    dims = (Hd, I, K, T)
+    resident = weighted_branch(vb, g, new, X, gpu_ids, gpu_ids, weights,
+                               g.expert_tensor(gu_bank, H.MX, Hd, 2 * I, n_slots + 1), g.leaf(F32, (2 * I, n_slots + 1), dgub.ptr),
+                               g.expert_tensor(dn_bank, H.MX, I, Hd, n_slots + 1), g.leaf(F32, (Hd, n_slots + 1), ddnb.ptr), dims)
+    host = weighted_branch(vb, g, new, X, cpu_ids, selected, cold_weights,
+                           g.expert_tensor(layer.gu_bank, H.MX, Hd, 2 * I, E), g.leaf(F32, (2 * I, E), layer.d_gu_b.ptr),
+                           g.expert_tensor(layer.dn_bank, H.MX, I, Hd, E), g.leaf(F32, (Hd, E), layer.d_dn_b.ptr), dims)
+    joined = g.tensor(F32, (Hd, K, T), new((Hd, K, T)), op=vb.NODE_ADD, srcs=(resident, host))
+    output = None
+    for rank in range(K):
+        row = g.view(joined, (Hd, T), [4, joined.nb[2], joined.nb[2] * T, joined.nb[2] * T], rank * joined.nb[1])
+        output = row if output is None else g.tensor(F32, (Hd, T), new((Hd, T)), op=vb.NODE_ADD, srcs=(output, row))
+    final = g.tensor(F32, (Hd, T), new((Hd, T)), op=vb.NODE_CONT, srcs=(output,))
+    for n in g.nodes:
+        assert g.supported(n), n.op
+    g.compute(order=vb.ORDER_EXACT)
+    vb.call("vbm_stream_synchronize", None)
+    got_gpu_ids = download(vb, gpu_ids.data, (T, K), np.int32)
+    assert np.array_equal(got_gpu_ids, packet[:, 1, :].astype(np.int32))
+    assert np.array_equal(download(vb, cpu_ids.data, (T, K), np.int32), packet[:, 0, :].astype(np.int32))
+    out = download(vb, final.data, (T, Hd))
+    assert H.bits_equal(out, ref["out"]), H.diff_report(out, ref["out"])
+    gu_bank.destroy()
+    dn_bank.destroy()
+    layer.destroy()
+
+
 @pytest.mark.parametrize("b_type", [F32, H.Q8])
 def test_node_mul_mat_id_strided_views_match_flat_call(gpu, orc, b_type):
     """MUL_MAT_ID nodes whose b and ids are views into wider buffers (b rows with a padded stride,

@@ -413,16 +413,21 @@ __device__ __forceinline__ void q8_block_s(unsigned w, float s, unsigned a, floa
 // Streams one lane's row slice (full groups through the D-deep ring, then the tail) against one
 // token: `la` is the wave's activation slice (8 B per block for MXFP4, 4 B for Q8_0), `ls` the
 // lane's row in the scale table.
-template <int TYPE, int D>
+//
+// With NB (blocks per row) a compile-time constant the group loop unrolls completely, every
+// reload is unconditional straight-line code, and the compiler's wait counts stay exact: the
+// consumer of group g waits for group g only, while the reloads issued after it stay in flight.
+// With a run-time NB (NB = 0) the conditional reloads of the rolled loop leave the waits
+// conservative (each group waits for every load issued before it, the latest reload included).
+template <int TYPE, int D, int NB = 0>
 __device__ __forceinline__ void decode_stream(Group (&ring)[D], const Tail & tl, const uint8_t * codes_tile, int k, int r,
-                                              int nb, bool live, const uint8_t * la, const float * ls,
+                                              int nb_rt, bool live, const uint8_t * la, const float * ls,
                                               float (&acc)[2]) {
     constexpr int kGroupBlocks = TYPE == 39 ? 8 : 4;
+    const int nb = NB > 0 ? NB : nb_rt;
     const int groups = nb / kGroupBlocks, tail = nb % kGroupBlocks;
     const uint8_t * cp = codes_tile + (k * 32 + r) * 16;
-    for (int g0 = 0; g0 < groups; g0 += D) {
-#pragma unroll
-        for (int i = 0; i < D; ++i) {
+    auto group_step = [&](int g0, int i) {
             const int g = g0 + i;
             if (g < groups) {
                 const u32x4 c = ring[i].c;
@@ -452,6 +457,17 @@ __device__ __forceinline__ void decode_stream(Group (&ring)[D], const Tail & tl,
                     q8_block_s(c.w, s0.w, a23.y, acc);
                 }
             }
+    };
+    if constexpr (NB > 0) {
+#pragma unroll
+        for (int g0 = 0; g0 < NB / kGroupBlocks; g0 += D) {
+#pragma unroll
+            for (int i = 0; i < D; ++i) group_step(g0, i);
+        }
+    } else {
+        for (int g0 = 0; g0 < groups; g0 += D) {
+#pragma unroll
+            for (int i = 0; i < D; ++i) group_step(g0, i);
         }
     }
     const int n = TYPE == 39 ? tail / 2 : tail;
@@ -724,6 +740,7 @@ struct DecodeArgs {
 
 constexpr int kDownThreads = 256;
 
+
 // x86 quantize_row_q8_0 of eight elements (part p of block b, thread t = 4b + p) of the layer input
 // into the activation row `act` (codes + block scales); block maximum over the thread quad (DPP),
 // so all four threads of a quad must call it together.
@@ -835,14 +852,14 @@ size_t decode_lds_bytes(int nb) {
 // the routing weight, then ADD in rank order) and quantized, thread t owning elements 8t..8t+7
 // and 8(t + 256).., straight from registers into the activation row. The tile's 16 GLU outputs
 // go out as fp32; kernel B quantizes each 32-element block of them (the pair of tiles).
-template <int TYPE, int NPL>
+template <int TYPE, int NPL, int NB>
 __global__ __launch_bounds__(kDownThreads) __attribute__((amdgpu_waves_per_eu(3))) void decode_gate_up_kernel(DecodeArgs A) {
     constexpr int D = gate_up_depth<TYPE>();
     constexpr int kChunks = 2;                     // 8-element input chunks per thread (hidden <= 4096)
     __shared__ float red[8][32];
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
     const Shape S = A.shape;
-    const int nb = S.nb;
+    const int nb = NB > 0 ? NB : S.nb;
     uint8_t * lmeta = lds_dyn;
     uint8_t * act = lmeta + meta_tile_bytes<TYPE>(nb);
     float * lscale = reinterpret_cast<float *>(act + ((A.lay.flag_offset() + 15) & ~15ll));
@@ -910,8 +927,10 @@ __global__ __launch_bounds__(kDownThreads) __attribute__((amdgpu_waves_per_eu(3)
     load_meta<kDownThreads>(mst, slot_base + S.codes_bytes + static_cast<size_t>(tile) * mbytes, slot_ok ? mbytes : 0);
     Group ring[D];
     Tail tl;
-    preload_ring<TYPE, D, true>(ring, codes_tile, nullptr, k, r, nb, slot_ok);
-    preload_tail<TYPE, true>(tl, codes_tile, nullptr, k, r, nb, slot_ok);
+    // unconditional loads (a pick with no valid slot reads the bank's first slot and is poisoned
+    // below), so the stream's wait counts stay exact
+    preload_ring<TYPE, D, true>(ring, codes_tile, nullptr, k, r, nb, true);
+    preload_tail<TYPE, true>(tl, codes_tile, nullptr, k, r, nb, true);
     const int grow = static_cast<int>(ggml_row(static_cast<int64_t>(tile) * 32 + r, S.rows, S.interleave));
     float bias_v = 0.0f;
     if (k == 0 && slot_ok && A.bias) bias_v = A.bias[static_cast<size_t>(expert) * S.rows + grow];
@@ -960,8 +979,8 @@ __global__ __launch_bounds__(kDownThreads) __attribute__((amdgpu_waves_per_eu(3)
     build_scales<TYPE, kDownThreads, 1>(lscale, lmeta, reinterpret_cast<const float *>(act + A.lay.da_offset()), nb, mbytes);
     __syncthreads();
     float acc[2] = {0.0f, 0.0f};
-    decode_stream<TYPE, D>(ring, tl, codes_tile, k, r, nb, slot_ok, act + static_cast<int64_t>(k) * nb * A.lay.code_entry(),
-                           lscale + r * 4, acc);
+    decode_stream<TYPE, D, NB>(ring, tl, codes_tile, k, r, nb, true, act + static_cast<int64_t>(k) * nb * A.lay.code_entry(),
+                               lscale + r * 4, acc);
     red[k][r] = acc[0] + acc[1];
     __syncthreads();
     if (threadIdx.x < 32) {
@@ -1012,13 +1031,13 @@ struct DecodeDownArgs {
 // (lanes 32..63) of the tile's rows. Its prologue requantizes the rank's GLU outputs (x86
 // quantize_row_q8_0 per 32-element block, the arithmetic of the reference's activation
 // quantization) into the LDS activation row while its weight stream is in flight.
-template <int TYPE>
+template <int TYPE, int NB>
 __global__ __launch_bounds__(kDownThreads) void decode_down_kernel(DecodeDownArgs A) {
     constexpr int D = down_depth<TYPE>();
     __shared__ float red[8][32];
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
     const Shape S = A.shape;
-    const int nb = S.nb;
+    const int nb = NB > 0 ? NB : S.nb;
     uint8_t * lmeta = lds_dyn;
     uint8_t * act = lmeta + meta_tile_bytes<TYPE>(nb);
     float * lscale = reinterpret_cast<float *>(act + ((A.lay.flag_offset() + 15) & ~15ll));
@@ -1051,8 +1070,8 @@ __global__ __launch_bounds__(kDownThreads) void decode_down_kernel(DecodeDownArg
     load_meta<kDownThreads>(mst, slot_base + S.codes_bytes + static_cast<size_t>(tile) * mbytes, slot_ok ? mbytes : 0);
     Group ring[D];
     Tail tl;
-    preload_ring<TYPE, D, true>(ring, codes_tile, nullptr, k, r, nb, slot_ok);
-    preload_tail<TYPE, true>(tl, codes_tile, nullptr, k, r, nb, slot_ok);
+    preload_ring<TYPE, D, true>(ring, codes_tile, nullptr, k, r, nb, true);   // unconditional, as in kernel A
+    preload_tail<TYPE, true>(tl, codes_tile, nullptr, k, r, nb, true);
     const int row = tile * 32 + r;
     float bias_v = 0.0f;
     if (k == 0 && slot_ok && A.bias) bias_v = A.bias[static_cast<size_t>(expert) * S.rows + row];
@@ -1067,8 +1086,8 @@ __global__ __launch_bounds__(kDownThreads) void decode_down_kernel(DecodeDownArg
                                         mbytes);
     __syncthreads();
     float acc[2] = {0.0f, 0.0f};
-    decode_stream<TYPE, D>(ring, tl, codes_tile, k, r, nb, slot_ok, act + static_cast<int64_t>(k) * nb * A.lay.code_entry(),
-                           lscale + r * 4, acc);
+    decode_stream<TYPE, D, NB>(ring, tl, codes_tile, k, r, nb, true, act + static_cast<int64_t>(k) * nb * A.lay.code_entry(),
+                               lscale + r * 4, acc);
     red[k][r] = acc[0] + acc[1];
     __syncthreads();
     if (threadIdx.x < 32) {
@@ -1082,22 +1101,35 @@ __global__ __launch_bounds__(kDownThreads) void decode_down_kernel(DecodeDownArg
     }
 }
 
-template <int TYPE, int NPL>
+template <int TYPE, int NPL, int NB>
 void launch_gate_up_npl(const DecodeArgs & a, dim3 grid, size_t lds, hipStream_t stream) {
     if (lds > 65536)
-        check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_gate_up_kernel<TYPE, NPL>),
+        check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_gate_up_kernel<TYPE, NPL, NB>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)),
                   "decode gate_up LDS attribute");
-    hipLaunchKernelGGL((decode_gate_up_kernel<TYPE, NPL>), grid, dim3(kDownThreads), lds, stream, a);
+    hipLaunchKernelGGL((decode_gate_up_kernel<TYPE, NPL, NB>), grid, dim3(kDownThreads), lds, stream, a);
+}
+
+// Row lengths (blocks) with a fully unrolled weight stream: hidden = intermediate = 2880 (MXFP4,
+// 90 blocks) and the Q8_0 layer with hidden 2048 (64 blocks) and intermediate 768 (24 blocks).
+template <int TYPE>
+constexpr int fixed_gate_up_nb() {
+    return TYPE == 39 ? 90 : 64;
+}
+template <int TYPE>
+constexpr int fixed_down_nb() {
+    return TYPE == 39 ? 90 : 24;
 }
 
 template <int TYPE>
 void launch_decode_typed(const DecodeArgs & a, hipStream_t stream) {
     const size_t lds = decode_lds_bytes<TYPE>(a.shape.nb);
     const dim3 grid(static_cast<unsigned>(a.shape.rows / 32), static_cast<unsigned>(a.top_k));
-    if (a.n_expert <= 128) launch_gate_up_npl<TYPE, 2>(a, grid, lds, stream);
-    else if (a.n_expert <= 256) launch_gate_up_npl<TYPE, 4>(a, grid, lds, stream);
-    else launch_gate_up_npl<TYPE, 16>(a, grid, lds, stream);
+    constexpr int kFixed = fixed_gate_up_nb<TYPE>();
+    if (a.n_expert <= 128 && a.shape.nb == kFixed) launch_gate_up_npl<TYPE, 2, kFixed>(a, grid, lds, stream);
+    else if (a.n_expert <= 128) launch_gate_up_npl<TYPE, 2, 0>(a, grid, lds, stream);
+    else if (a.n_expert <= 256) launch_gate_up_npl<TYPE, 4, 0>(a, grid, lds, stream);
+    else launch_gate_up_npl<TYPE, 16, 0>(a, grid, lds, stream);
     check_hip(hipGetLastError(), "decode gate_up launch");
 }
 
@@ -1105,7 +1137,9 @@ template <int TYPE>
 void launch_decode_down_typed(const DecodeDownArgs & a, int top_k, hipStream_t stream) {
     const size_t lds = decode_lds_bytes<TYPE>(a.shape.nb);
     const dim3 grid(static_cast<unsigned>(a.shape.rows / 32), static_cast<unsigned>(top_k));
-    hipLaunchKernelGGL((decode_down_kernel<TYPE>), grid, dim3(kDownThreads), lds, stream, a);
+    constexpr int kFixed = fixed_down_nb<TYPE>();
+    if (a.shape.nb == kFixed) hipLaunchKernelGGL((decode_down_kernel<TYPE, kFixed>), grid, dim3(kDownThreads), lds, stream, a);
+    else hipLaunchKernelGGL((decode_down_kernel<TYPE, 0>), grid, dim3(kDownThreads), lds, stream, a);
     check_hip(hipGetLastError(), "decode down launch");
 }
 

@@ -84,6 +84,34 @@ __global__ void add_id_kernel(char * dst, Strides sd, const char * a, Strides sa
     }
 }
 
+// GGML_OP_CPY (ggml_cast): element idx of src's row-major order goes to element idx of dst's,
+// converted between F32 and I32. F32 -> I32 truncates toward zero, the C conversion ggml's CPU
+// cast applies; where C leaves it undefined, out-of-range values saturate and NaN gives 0 here.
+// I32 -> F32 rounds to nearest.
+__global__ void convert_kernel(char * dst, Strides sd, Dims dshape, int dst_i32, const char * a, Strides sa,
+                               Dims ashape, int src_i32, int64_t n) {
+    for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < n;
+         idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        int64_t i[4], j[4];
+        unflatten(idx, ashape, i);
+        unflatten(idx, dshape, j);
+        const char * s = a + offset(i, sa);
+        char * d = dst + offset(j, sd);
+        if (src_i32) {
+            const int32_t v = *reinterpret_cast<const int32_t *>(s);
+            if (dst_i32) *reinterpret_cast<int32_t *>(d) = v;
+            else *reinterpret_cast<float *>(d) = static_cast<float>(v);
+        } else {
+            const float v = *reinterpret_cast<const float *>(s);
+            if (dst_i32)
+                *reinterpret_cast<int32_t *>(d) = v != v ? 0
+                                                 : v >= 2147483648.0f ? INT32_MAX
+                                                 : v <= -2147483648.0f ? INT32_MIN : static_cast<int32_t>(v);
+            else *reinterpret_cast<float *>(d) = v;
+        }
+    }
+}
+
 unsigned grid_for(int64_t n) {
     const int64_t blocks = (n + 255) / 256;
     return static_cast<unsigned>(blocks < 65536 ? blocks : 65536);
@@ -255,6 +283,19 @@ const char * check_cont(const vbm_node & t) {
     return nullptr;
 }
 
+// ggml_cast / ggml_cpy between F32 and I32 into a contiguous dst with src's element count
+// (src[1] of a ggml CPY node is its destination, itself for a cast: not read here).
+const char * check_cpy(const vbm_node & t) {
+    const vbm_node * a = t.src[0];
+    if (!a) return "CPY needs a source";
+    if (!shape_valid(*a) || !shape_valid(t)) return "bad tensor shape or type";
+    if ((a->type != VBM_TYPE_F32 && a->type != VBM_TYPE_I32) || (t.type != VBM_TYPE_F32 && t.type != VBM_TYPE_I32))
+        return "CPY converts between F32 and I32 here";
+    if (nelements(*a) != nelements(t) || !contiguous(t)) return "dst must be contiguous with src's element count";
+    if (!aligned_strides(*a) || !aligned_strides(t)) return "strides must be multiples of 4 bytes";
+    return nullptr;
+}
+
 const char * check_glu(const vbm_node & t) {
     const vbm_node * a = t.src[0], * b = t.src[1];
     const int op = t.op_params[0];
@@ -310,6 +351,7 @@ const char * why_unsupported(const vbm_node & t) {
         case VBM_NODE_ADD_ID: return check_add_id(t);
         case VBM_NODE_GLU: return check_glu(t);
         case VBM_NODE_CUSTOM: return check_custom(t);
+        case VBM_NODE_CPY: return check_cpy(t);
         default: return "op not handled by this library";
     }
 }
@@ -331,6 +373,14 @@ void launch_elementwise(const vbm_node & dst, const vbm_node & a, const vbm_node
                        static_cast<const char *>(a.data), strides_of(a.nb), static_cast<const char *>(bb.data),
                        strides_of(bb.nb), dims_of(a.ne), dims_of(bb.ne), n);
     check_hip(hipGetLastError(), "elementwise launch");
+}
+
+void launch_convert(const vbm_node & dst, const vbm_node & a, hipStream_t s) {
+    const int64_t n = nelements(a);
+    hipLaunchKernelGGL(convert_kernel, dim3(grid_for(n)), dim3(256), 0, s, static_cast<char *>(dst.data),
+                       strides_of(dst.nb), dims_of(dst.ne), dst.type == VBM_TYPE_I32 ? 1 : 0,
+                       static_cast<const char *>(a.data), strides_of(a.nb), dims_of(a.ne), a.type == VBM_TYPE_I32 ? 1 : 0, n);
+    check_hip(hipGetLastError(), "convert launch");
 }
 
 void forward_mul_mat_id(const vbm_node & t, int order, hipStream_t s) {
@@ -424,6 +474,7 @@ void compute_forward(const vbm_node * node, const vbm_compute_params * params, h
         case VBM_NODE_ADD_ID: forward_add_id(t, s); break;
         case VBM_NODE_GLU: forward_glu(t, s); break;
         case VBM_NODE_CUSTOM: forward_custom(t, mode, s); break;
+        case VBM_NODE_CPY: launch_convert(t, *t.src[0], s); break;
         default: fail(VBM_ERR_UNSUPPORTED, "op not handled by this library");
     }
 }

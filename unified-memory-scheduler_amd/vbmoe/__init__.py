@@ -55,7 +55,7 @@ class GgufExpertInfo(C.Structure):
 
 HOST_CALL_MAGIC, HOST_JOIN_MAGIC, HOST_MAX_SRC = 0x56424843414C4C31, 0x5642484A4F494E31, 10
 HOST_CALL_FUNC, HOST_CALL_MAILBOX = 0, 1
-NODE_NONE, NODE_VIEW, NODE_ADD, NODE_MUL, NODE_CONT, NODE_MUL_MAT_ID, NODE_ADD_ID, NODE_GLU, NODE_CUSTOM = range(9)
+NODE_NONE, NODE_VIEW, NODE_ADD, NODE_MUL, NODE_CONT, NODE_MUL_MAT_ID, NODE_ADD_ID, NODE_GLU, NODE_CUSTOM, NODE_CPY = range(10)
 NODE_MAX_SRC = 10
 GLU_OP_SWIGLU, GLU_OP_SWIGLU_OAI = 2, 3
 HOST_FN = C.CFUNCTYPE(None, C.c_void_p)
