@@ -705,7 +705,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 
 // ------------------------------------------------------------------------------ fused decode
 // Single-token decode runs two launches per layer.
-// Kernel A (gate_up, 512 threads = 8 lane slices x 64 rows): every workgroup routes (top-k +
+// Kernel A (gate_up, 256 threads = 8 lane slices x 32 rows): every workgroup routes (top-k +
 //   softmax over the layer's given logits; a few hundred bytes from L2) and, with the same
 //   loads in flight, combines the previous layer (ggml MUL by the routing weight, then ADD in
 //   rank order) or takes the input; it then issues its expert's weights, quantizes the input to
