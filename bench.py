@@ -279,6 +279,72 @@ def prefill_measure(args) -> dict:
     }
 
 
+def mxfp8_experiment(args) -> dict:
+    """MXFP4 x MXFP8 on the CDNA4 block-scaled matrix cores (vbm_mul_mat_id_mxfp8) beside the
+    f16 MFMA path of vbm_mul_mat_id (fast order) on the gate_up projection of the 120B-shape layer:
+    hidden 2880 -> 5760 rows, 128 experts, top-4, 2048 tokens of N(0,1) activations with uniformly
+    drawn distinct ids. Times each call (activation quantization + grouping + GEMM) with events and
+    reports the MXFP8 result's distance from the Q8_0 result. An experiment beside the product
+    path: its activations are not the reference's Q8_0."""
+    Hm, Rm, Em, Km, Tm = 2880, 5760, 128, 4, 2048
+    bank = vb.Bank(vb.TYPE_MXFP4, Rm, Hm, Em, True)
+    bank.generate(0, Em, SEED, 905, 0, -8, -3)
+    x = vb.DeviceBuffer.from_array(vb.synth_normal(SEED, 906, 0, Tm * Hm))
+    rng = np.random.default_rng(SEED)
+    ids = np.stack([rng.choice(Em, Km, replace=False) for _ in range(Tm)]).astype(np.int32)
+    dids = vb.DeviceBuffer.from_array(ids)
+    outs = {"f16": vb.DeviceBuffer(4 * Tm * Km * Rm), "mxfp8": vb.DeviceBuffer(4 * Tm * Km * Rm)}
+    stream = C.c_void_p()
+    vb.call("vbm_stream_create", C.byref(stream))
+    stream = stream.value
+    ev = []
+    for _ in range(2):
+        e = C.c_void_p()
+        vb.call("vbm_event_create", C.byref(e))
+        ev.append(e.value)
+
+    def run(name):
+        if name == "f16":
+            vb.call("vbm_mul_mat_id", bank.handle, None, None, Em, vb.TYPE_F32, x.ptr, 1, dids.ptr, Km, Tm, Km, None,
+                    outs[name].ptr, vb.ORDER_FAST, stream)
+        else:
+            vb.call("vbm_mul_mat_id_mxfp8", bank.handle, None, Em, x.ptr, 1, dids.ptr, Km, Tm, Km, outs[name].ptr, stream)
+
+    times = {}
+    for name in ("f16", "mxfp8"):
+        for _ in range(2):
+            run(name)
+        vb.call("vbm_event_record", ev[0], stream)
+        for _ in range(args.prefill_reps):
+            run(name)
+        vb.call("vbm_event_record", ev[1], stream)
+        vb.call("vbm_stream_synchronize", stream)
+        ms = C.c_float()
+        vb.call("vbm_event_elapsed_ms", ev[0], ev[1], C.byref(ms))
+        times[name] = ms.value / args.prefill_reps * 1e3
+    ref = outs["f16"].download(np.float32, (Tm * Km, Rm)).astype(np.float64)
+    got = outs["mxfp8"].download(np.float32, (Tm * Km, Rm)).astype(np.float64)
+    rel = float(np.abs(got - ref).max() / np.abs(ref).max())
+    cos = float(np.dot(got.ravel(), ref.ravel()) / (np.linalg.norm(got) * np.linalg.norm(ref)))
+    ops = 2.0 * Tm * Km * Rm * Hm
+    wbytes = Em * bank.slot_bytes
+    bank.destroy()
+    vb.call("vbm_stream_destroy", stream)
+    log(f"MXFP8 experiment (gate_up, 2048 tokens, 128 experts top-4): f16 MFMA path {times['f16']:.1f} us, "
+        f"block-scaled MXFP8 path {times['mxfp8']:.1f} us; max deviation {rel:.2e} of max |out|, cos {cos:.6f}")
+    return {
+        "workload": "MXFP4 gate_up projection of the 120B-shape layer: 2048 tokens, hidden 2880 -> 5760 rows, 128 experts, top-4",
+        "f16_mfma_us": round(times["f16"], 2),
+        "mxfp8_block_scaled_us": round(times["mxfp8"], 2),
+        "speedup": round(times["f16"] / times["mxfp8"], 3),
+        "f16_tops": round(ops / (times["f16"] * 1e-6) / 1e12, 1),
+        "mxfp8_tops": round(ops / (times["mxfp8"] * 1e-6) / 1e12, 1),
+        "expert_weight_bytes": wbytes,
+        "mxfp8_vs_q8_0_max_rel": rel, "mxfp8_vs_q8_0_cos": round(cos, 8),
+        "note": "experiment beside the product path: MXFP8 activations (e4m3 + e8m0 per 32) are not the reference's Q8_0",
+    }
+
+
 def graph_layers(descs, T: int, x0, logits, ids, reps: int) -> float:
     """One step = the layers chained through vbm_moe_layer_forward at T tokens, captured as a HIP
     graph; returns the average step time (ms) over `reps` replays (inputs resident, events on the
@@ -646,6 +712,8 @@ def main() -> int:
     ap.add_argument("--cpu-layers", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the Q8_0 prefill GEMM measurement")
+    ap.add_argument("--no-mxfp8-experiment", dest="mxfp8_experiment", action="store_false",
+                    help="skip the MXFP4 x MXFP8 block-scaled MFMA experiment beside the prefill GEMM")
     ap.add_argument("--no-batched", action="store_true",
                     help="skip the batched decode lines (config 2 at batch 32, config 1 at batches 1/8/64)")
     ap.add_argument("--batch-reps", type=int, default=5, help="graph replays per batched decode line")
@@ -783,6 +851,8 @@ def main() -> int:
     batched = None if args.no_batched else batched_measure(args, stack)
     config1 = None if args.no_batched else config1_measure(args)
     prefill = None if args.no_prefill else prefill_measure(args)
+    if prefill is not None and args.mxfp8_experiment:
+        prefill["mxfp8_experiment"] = mxfp8_experiment(args)
     tier = None if args.no_tier else tier_measure(args, stack)
 
     cpu = None

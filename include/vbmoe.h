@@ -209,6 +209,22 @@ vbm_status vbm_mul_mat_id_noalloc(const vbm_bank * bank, const int32_t * expert_
                                   const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride,
                                   const float * bias, float * dst, int order, void * stream);
 
+/* Experimental, outside the parity contract, no counterpart in the reference (its activations are
+ * Q8_0): MUL_MAT_ID on an MXFP4 bank with the fp32 activations quantized to MXFP8 (e4m3 codes
+ * rounded to nearest even, one e8m0 scale per 32 values: the smallest power of two X with
+ * amax / X <= 448, so nothing saturates) and the products on the CDNA4 block-scaled matrix cores
+ * (v_mfma_scale_f32_16x16x128_f8f6f4), which apply both block scales in hardware. Results follow the
+ * MXFP8 x MXFP4 arithmetic (about 1e-2 relative from the reference's Q8_0 path). b fp32
+ * [n_tokens][b_ne1][k] contiguous; ids, expert_to_slot (device map or NULL), -1 ids and dst
+ * [n_tokens][n_ids][rows] as in vbm_mul_mat_id (no bias). Device scratch as vbm_mul_mat_id. */
+vbm_status vbm_mul_mat_id_mxfp8(const vbm_bank * bank, const int32_t * expert_to_slot, int64_t n_as, const float * b,
+                                int64_t b_ne1, const int32_t * ids, int64_t n_ids, int64_t n_tokens,
+                                int64_t ids_stride, float * dst, void * stream);
+/* The MXFP8 quantizer of vbm_mul_mat_id_mxfp8 alone: n_rows rows of k fp32 (row stride x_stride
+ * floats) -> codes [n_rows][k] bytes and e8m0 scales [n_rows][k / 32] bytes. */
+vbm_status vbm_quantize_mxfp8(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, void * codes, void * scales,
+                              void * stream);
+
 /* GGML_OP_ADD_ID in place: y[:, r, t] += bias[:, ids[r,t]] (rows x n_ids x n_tokens; bias fp32
  * [n_as][rows]). An id of -1 adds nothing; ids outside [-1, n_as) set the row to NaN (the reference
  * asserts on them). */

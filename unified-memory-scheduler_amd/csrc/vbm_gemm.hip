@@ -746,6 +746,261 @@ void launch_gemm_typed(const GemmArgs & a, int row_pairs, int max_tiles, hipStre
     check_hip(hipGetLastError(), "grouped GEMM launch");
 }
 
+// ------------------------------------------------------------------ MXFP4 x MXFP8 experiment
+// The CDNA4 block-scaled matrix core (v_mfma_scale_f32_16x16x128_f8f6f4) takes MXFP4 weights as
+// they are stored (e2m1 codes, e8m0 exponents) and 8-bit activations with their own e8m0 block
+// scales, applies both scales and accumulates four 32-element blocks per instruction: no
+// per-block scale-accumulate work is left on the vector ALUs. Its activations must be an MX
+// format, so this path quantizes them to MXFP8 (OCP MX e4m3, one e8m0 scale per 32 values)
+// instead of the reference's Q8_0: a measured experiment beside the f16 MFMA path, outside the
+// parity contract.
+//
+// Operand layout of one 128-element K step (blocks blk = 0..3), checked on the device:
+//   A: lane row + 16 blk holds block blk of its row, element i at nibble i (low nibble first);
+//      scale_a of that lane is the block's e8m0 exponent;
+//   B: lane col + 16 g, byte j holds block g / 2 + 2 (j / 16), element 16 (g % 2) + j % 16;
+//      scale_b of lane col + 16 blk is the block's e8m0 scale;
+//   D: lane l holds column l % 16, rows 4 (l / 16) .. + 3.
+// Products and block sums inside the instruction are not rounded as an fp32 chain would be (a
+// random-data check puts the difference near 6e-5 of the sum of |products|).
+typedef int mx_v8i __attribute__((ext_vector_type(8)));
+
+// MXFP8 (e4m3) quantization of fp32 rows, one e8m0 scale X per 32 values: the smallest power of two
+// with amax / X <= 448 (the e4m3 maximum), i.e. the OCP MX choice 2^(floor(log2 amax) - 8) raised
+// by one when amax / 2^floor(log2 amax) > 1.75, so no value saturates; code = e4m3 of v / X
+// rounded to nearest even; scale byte = 127 + log2 X. One thread per 4 values; the 8 threads of a
+// block are adjacent lanes.
+__device__ __forceinline__ uint32_t e4m3_rne(float v) {
+    const uint32_t sign = __builtin_bit_cast(uint32_t, v) >> 31 << 7;
+    float a = fabsf(v);
+    a = a > 448.0f ? 448.0f : a;
+    if (!(a >= 0.015625f)) {                                   // below 2^-6: subnormal steps of 2^-9
+        const float m = rintf(a * 512.0f);                     // 0..8 (8 rounds up to the smallest normal)
+        return sign | static_cast<uint32_t>(m);
+    }
+    const int e = static_cast<int>((__builtin_bit_cast(uint32_t, a) >> 23) & 0xFF) - 127;   // -6..8
+    float m = rintf(__builtin_amdgcn_ldexpf(a, 3 - e));         // 8..16
+    int ee = e;
+    if (m >= 16.0f) { m = 8.0f; ++ee; }                        // carry into the next binade (<= 448 by the clamp)
+    return sign | static_cast<uint32_t>((ee + 7) << 3) | (static_cast<uint32_t>(m) - 8u);
+}
+
+__global__ __launch_bounds__(256) void quantize_mxfp8_kernel(const float * __restrict__ x, int64_t n_rows, int nb,
+                                                             int64_t x_stride, uint8_t * __restrict__ codes,
+                                                             uint8_t * __restrict__ scales) {
+    const int64_t t = blockIdx.x * 256ll + threadIdx.x;
+    const bool live = t < n_rows * nb * 8;
+    const int64_t blk = live ? t / 8 : 0;
+    const int part = static_cast<int>(t & 7);
+    const int64_t row = blk / nb, b = blk % nb;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = live ? x[row * x_stride + b * 32 + part * 4 + i] : 0.0f;
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    const uint32_t ab = __builtin_bit_cast(uint32_t, amax);
+    const int ea = ab >= 0x00800000u ? static_cast<int>(ab >> 23) - 127 : -127;   // subnormal or zero: X = 2^-127
+    int sx = ea - 8 + (ab >= 0x00800000u && (ab & 0x7FFFFFu) > 0x600000u ? 1 : 0);
+    sx = sx < -127 ? -127 : (sx > 127 ? 127 : sx);
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) packed |= e4m3_rne(__builtin_amdgcn_ldexpf(v[i], -sx)) << (8 * i);
+    if (live) {
+        reinterpret_cast<uint32_t *>(codes + row * nb * 32 + b * 32)[part] = packed;
+        if (part == 0) scales[row * nb + b] = static_cast<uint8_t>(sx + 127);
+    }
+}
+
+struct MxArgs {
+    const uint8_t * bank;
+    GemmShape shape;
+    const int32_t * expert_to_slot;
+    const uint8_t * codes;     // MXFP8 rows [n_rows][nb * 32]
+    const uint8_t * scales;    // [n_rows][nb]
+    int64_t n_ids, b_ne1;
+    const int32_t * counts;
+    const int32_t * offsets;
+    const int32_t * jobs;
+    const int32_t * tile_expert;
+    const int32_t * tile_start;
+    const int32_t * n_tiles;
+    int row_pairs;
+    float * dst;               // [job][rows]
+};
+
+// A workgroup (4 waves) computes 64 bank rows (a tile pair) x 64 jobs of one expert, like the f16
+// path; wave w owns rows 32 (w & 1) .. + 31 and jobs 32 (w >> 1) .. + 31 as 2 x 2 fragments. Per
+// bank group (8 blocks = two 128-element K steps) the tile pair's codes are restaged in LDS as
+// [block][row][16 B], the operand order of the matrix core, and its exponents as [block][row]; the
+// activation operands go from the MXFP8 rows straight into registers. The next group's loads
+// (codes, exponents, activation operands) are in flight while the current group computes.
+struct MxStage {
+    uint32_t w[2][4];          // two (tile, slice, row) code entries: 8 blocks x 2 bytes each
+    uint32_t m[2];             // threads 0..63: the row's 8 exponent bytes (stored as e - 128)
+    u32x4g b[2][2][2];         // [K step][job half][low / high 16 bytes] activation operand
+    int sb[2][2];              // [K step][job half] activation block scale
+};
+
+__global__ __launch_bounds__(256) void mx_gemm_kernel(MxArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t wl[8 * 64 * 16];
+    __shared__ uint8_t el[8 * 64];
+    const int n_items = *cst<int32_t>(A.n_tiles) * A.row_pairs;
+    const int per_xcd = (n_items + 7) >> 3;
+    const int slot8 = static_cast<int>(blockIdx.x >> 3);
+    const int item = static_cast<int>(blockIdx.x & 7) * per_xcd + slot8;
+    if (slot8 >= per_xcd || item >= n_items) return;
+    const int ti = item / A.row_pairs;
+    const int pair = item - ti * A.row_pairs;
+    const int expert = cst<int32_t>(A.tile_expert)[ti];
+    const int j0 = cst<int32_t>(A.tile_start)[ti];
+    const int count = cst<int32_t>(A.counts)[expert];
+    const int joff = cst<int32_t>(A.offsets)[expert];
+    const int slot = A.expert_to_slot ? cst<int32_t>(A.expert_to_slot)[expert] : expert;
+    const GemmShape S = A.shape;
+    const int nb = S.nb, groups = nb / 8, tail = nb % 8;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
+    const bool slot_ok = slot >= 0 && slot < S.n_slots;
+    const uint8_t * slot_base = A.bank + static_cast<size_t>(slot_ok ? slot : 0) * S.slot_bytes;
+
+    // this lane's two job columns
+    const uint8_t * bcode[2];
+    const uint8_t * bscale[2];
+    int job[2];
+    bool jlive[2];
+#pragma unroll
+    for (int jh = 0; jh < 2; ++jh) {
+        const int jl = 32 * (wave >> 1) + 16 * jh + lr;
+        jlive[jh] = j0 + jl < count;
+        job[jh] = jlive[jh] ? A.jobs[joff + j0 + jl] : 0;
+        const int64_t row_index = A.b_ne1 == 1 ? job[jh] / A.n_ids : job[jh];
+        bcode[jh] = A.codes + row_index * nb * 32;
+        bscale[jh] = A.scales + row_index * nb;
+    }
+    // this thread's two staging entries: e = t + 256 h -> tile tt, slice k, row r
+    auto load = [&](int g, MxStage & R) {
+        const bool is_tail = g == groups;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int e = threadIdx.x + 256 * h;
+            const int tile = pair * 2 + (e >> 8), k = (e >> 5) & 7, r = e & 31;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) R.w[h][d] = 0u;
+            if (tile * 32 < S.rows) {
+                const uint8_t * ct = slot_base + static_cast<size_t>(tile) * 32 * nb * 16;
+                if (!is_tail) {
+                    const u32x4g v = *reinterpret_cast<const u32x4g *>(ct + static_cast<size_t>(g) * 4096 + (k * 32 + r) * 16);
+                    R.w[h][0] = v[0], R.w[h][1] = v[1], R.w[h][2] = v[2], R.w[h][3] = v[3];
+                } else {
+                    const uint8_t * tp = ct + static_cast<size_t>(groups) * 4096 + (k * 32 + r) * (tail * 2);
+#pragma unroll
+                    for (int b = 0; b < 8; ++b)       // constant indices keep the stage in registers
+                        if (b < tail)
+                            R.w[h][b >> 1] |= static_cast<uint32_t>(*reinterpret_cast<const uint16_t *>(tp + 2 * b)) << (16 * (b & 1));
+                }
+            }
+        }
+        R.m[0] = R.m[1] = 0x80808080u;                         // blocks past the tail: 2^0
+        if (threadIdx.x < 64) {
+            const int row = threadIdx.x, tile = pair * 2 + (row >> 5), r = row & 31;
+            if (tile * 32 < S.rows) {
+                const uint8_t * mt = slot_base + S.codes_bytes + static_cast<size_t>(tile) * 32 * nb;
+                if (!is_tail) {
+                    const u32x2g v = *reinterpret_cast<const u32x2g *>(mt + static_cast<size_t>(g) * 256 + r * 8);
+                    R.m[0] = v[0], R.m[1] = v[1];
+                } else {
+#pragma unroll
+                    for (int b = 0; b < 8; ++b) {
+                        if (b < tail) {
+                            const uint32_t byte = mt[groups * 256 + r * tail + b];
+                            R.m[b >> 2] = (R.m[b >> 2] & ~(0xFFu << (8 * (b & 3)))) | (byte << (8 * (b & 3)));
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const int b0 = 8 * g + 4 * st, blo = b0 + (q >> 1), bhi = b0 + 2 + (q >> 1);
+#pragma unroll
+            for (int jh = 0; jh < 2; ++jh) {
+                R.b[st][jh][0] = R.b[st][jh][1] = u32x4g{0u, 0u, 0u, 0u};
+                if (jlive[jh] && blo < nb) R.b[st][jh][0] = *reinterpret_cast<const u32x4g *>(bcode[jh] + blo * 32 + 16 * (q & 1));
+                if (jlive[jh] && bhi < nb) R.b[st][jh][1] = *reinterpret_cast<const u32x4g *>(bcode[jh] + bhi * 32 + 16 * (q & 1));
+                R.sb[st][jh] = jlive[jh] && b0 + q < nb ? bscale[jh][b0 + q] : 127;
+            }
+        }
+    };
+    auto stage = [&](const MxStage & R) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int e = threadIdx.x + 256 * h;
+            const int row = 32 * (e >> 8) + (e & 31), k = (e >> 5) & 7;
+#pragma unroll
+            for (int b = 0; b < 8; ++b)
+                *reinterpret_cast<uint16_t *>(wl + (b * 64 + row) * 16 + 2 * k) = static_cast<uint16_t>(R.w[h][b >> 1] >> (16 * (b & 1)));
+        }
+        if (threadIdx.x < 64) {
+#pragma unroll
+            for (int b = 0; b < 8; ++b) el[b * 64 + threadIdx.x] = static_cast<uint8_t>((R.m[b >> 2] >> (8 * (b & 3))) ^ 0x80u);
+        }
+    };
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int jh = 0; jh < 2; ++jh) acc[i][jh] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int n_groups = groups + (tail > 0 ? 1 : 0);
+    MxStage cur, nxt;
+    load(0, cur);
+    stage(cur);
+    __syncthreads();
+    for (int g = 0; g < n_groups; ++g) {
+        if (g + 1 < n_groups) load(g + 1, nxt);
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            if (8 * g + 4 * st >= nb) break;
+            mx_v8i bop[2];
+#pragma unroll
+            for (int jh = 0; jh < 2; ++jh) {
+                const u32x4g lo = cur.b[st][jh][0], hi = cur.b[st][jh][1];
+                bop[jh] = mx_v8i{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
+                                 static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int row = 32 * (wave & 1) + 16 * i + lr;
+                const u32x4g a = *reinterpret_cast<const u32x4g *>(wl + ((4 * st + q) * 64 + row) * 16);
+                const mx_v8i aop = mx_v8i{static_cast<int>(a[0]), static_cast<int>(a[1]), static_cast<int>(a[2]), static_cast<int>(a[3]), 0, 0, 0, 0};
+                const int sa = el[(4 * st + q) * 64 + row];
+#pragma unroll
+                for (int jh = 0; jh < 2; ++jh)
+                    acc[i][jh] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aop, bop[jh], acc[i][jh], 4, 0, 0, sa, 0, cur.sb[st][jh]);
+            }
+        }
+        __syncthreads();
+        if (g + 1 < n_groups) {
+            stage(nxt);
+            cur = nxt;
+        }
+        __syncthreads();
+    }
+    const float nan = __builtin_nanf("");
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int jh = 0; jh < 2; ++jh) {
+            if (!jlive[jh]) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t brow = static_cast<int64_t>(pair) * 64 + 32 * (wave & 1) + 16 * i + 4 * q + j;
+                if (brow < S.rows)
+                    A.dst[static_cast<size_t>(job[jh]) * S.rows + ggml_row(brow, S.rows, S.interleave)] = slot_ok ? acc[i][jh][j] : nan;
+            }
+        }
+}
+
 }  // namespace
 
 int64_t gemm_max_tiles(int64_t n_as, int64_t n_entries) {
@@ -827,6 +1082,50 @@ void launch_grouped_gemm(const GemmParams & p, hipStream_t stream) {
         else if (p.epilogue == 0) launch_gemm_typed<8, 0, false>(a, row_pairs, mt, stream);
         else launch_gemm_typed<8, 1, false>(a, row_pairs, mt, stream);
     }
+}
+
+void launch_quantize_mxfp8(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, uint8_t * codes, uint8_t * scales,
+                           hipStream_t stream) {
+    require(k > 0 && k % 32 == 0 && n_rows > 0 && x_stride >= k, "MXFP8 quantize shape mismatch");
+    const int64_t threads = n_rows * (k / 32) * 8;
+    hipLaunchKernelGGL(quantize_mxfp8_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, stream, x,
+                       n_rows, static_cast<int>(k / 32), x_stride, codes, scales);
+    check_hip(hipGetLastError(), "MXFP8 quantize launch");
+}
+
+void launch_mx_gemm(const vbm_bank & bank, const int32_t * expert_to_slot, const uint8_t * codes, const uint8_t * scales,
+                    int64_t n_ids, int64_t b_ne1, int64_t n_as, int64_t n_entries, const GroupBuffers & group, void * tiles,
+                    float * dst, hipStream_t stream) {
+    require(bank.type == VBM_TYPE_MXFP4, "the MXFP8 experiment runs on MXFP4 banks");
+    require(n_as >= 1 && n_as <= 1024 && n_entries >= 1, "GEMM group shape out of range");
+    const int64_t max_tiles = gemm_max_tiles(n_as, n_entries);
+    require(max_tiles <= 65535, "too many GEMM tiles for one launch");
+    int32_t * tile_expert = static_cast<int32_t *>(tiles);
+    int32_t * tile_start = tile_expert + max_tiles;
+    int32_t * n_tiles = tile_start + max_tiles;
+    hipLaunchKernelGGL(gemm_tiles_kernel, dim3(1), dim3(1024), 0, stream, group.counts, group.active, group.n_active,
+                       nullptr, static_cast<int>(max_tiles), tile_expert, tile_start, n_tiles, group.error);
+    check_hip(hipGetLastError(), "GEMM tile list launch");
+    MxArgs a{};
+    a.bank = bank.base;
+    a.shape = GemmShape{static_cast<int>(bank.nb), static_cast<int>(bank.rows), bank.interleave, bank.slot_bytes,
+                        bank.geometry().codes_bytes(), bank.n_slots};
+    a.expert_to_slot = expert_to_slot;
+    a.codes = codes;
+    a.scales = scales;
+    a.n_ids = n_ids;
+    a.b_ne1 = b_ne1;
+    a.counts = group.counts;
+    a.offsets = group.offsets;
+    a.jobs = group.rows;
+    a.tile_expert = tile_expert;
+    a.tile_start = tile_start;
+    a.n_tiles = n_tiles;
+    a.row_pairs = static_cast<int>((bank.rows + 63) / 64);
+    a.dst = dst;
+    const int64_t items = static_cast<int64_t>(a.row_pairs) * max_tiles;
+    hipLaunchKernelGGL(mx_gemm_kernel, dim3(static_cast<unsigned>((items + 7) / 8 * 8)), dim3(256), 0, stream, a);
+    check_hip(hipGetLastError(), "MXFP8 GEMM launch");
 }
 
 }  // namespace vbm

@@ -184,6 +184,13 @@ struct GemmParams {
 int64_t gemm_max_tiles(int64_t n_as, int64_t n_entries);
 size_t gemm_tiles_bytes(int64_t n_as, int64_t n_entries);
 void launch_grouped_gemm(const GemmParams & p, hipStream_t stream);
+// MXFP4 x MXFP8 experiment on the block-scaled matrix cores: OCP MX quantization of fp32 rows
+// (codes [n_rows][k], e8m0 scales [n_rows][k / 32]) and the grouped GEMM over them ([job][rows]).
+void launch_quantize_mxfp8(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, uint8_t * codes, uint8_t * scales,
+                           hipStream_t stream);
+void launch_mx_gemm(const vbm_bank & bank, const int32_t * expert_to_slot, const uint8_t * codes, const uint8_t * scales,
+                    int64_t n_ids, int64_t b_ne1, int64_t n_as, int64_t n_entries, const GroupBuffers & group, void * tiles,
+                    float * dst, hipStream_t stream);
 
 // Device workspace of one fused layer forward (vbm_moe_layer_forward), carved from `base` (NULL:
 // sizes only).

@@ -439,6 +439,38 @@ vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot,
     });
 }
 
+vbm_status vbm_mul_mat_id_mxfp8(const vbm_bank * bank, const int32_t * expert_to_slot, int64_t n_as, const float * b,
+                                int64_t b_ne1, const int32_t * ids, int64_t n_ids, int64_t n_tokens,
+                                int64_t ids_stride, float * dst, void * stream) {
+    return guarded([&] {
+        require(bank != nullptr && b != nullptr && ids != nullptr && dst != nullptr, "null buffer");
+        require(bank->type == VBM_TYPE_MXFP4, "the MXFP8 path needs an MXFP4 bank");
+        check_mul_mat_id_shape(*bank, n_as, b_ne1, n_ids, n_tokens, ids_stride, VBM_ORDER_FAST);
+        require(expert_to_slot != nullptr || n_as <= bank->n_slots, "identity map needs n_as <= bank slots");
+        const hipStream_t s = as_stream(stream);
+        const int64_t entries = n_ids * n_tokens, n_b = b_ne1 * n_tokens;
+        const size_t c_bytes = align_up(static_cast<size_t>(n_b * bank->k));
+        const size_t s_bytes = align_up(static_cast<size_t>(n_b * bank->nb));
+        const size_t g_bytes = align_up(group_workspace_bytes(n_as, entries));
+        auto * base = static_cast<uint8_t *>(stream_scratch(s, c_bytes + s_bytes + g_bytes + gemm_tiles_bytes(n_as, entries)));
+        const GroupBuffers g = carve_group(base + c_bytes + s_bytes, n_as, entries);
+        launch_quantize_mxfp8(b, n_b, bank->k, bank->k, base, base + c_bytes, s);
+        launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
+        init_dst(dst, ids, n_ids, n_tokens, ids_stride, n_as, bank->rows, s);
+        launch_mx_gemm(*bank, expert_to_slot, base, base + c_bytes, n_ids, b_ne1, n_as, entries, g,
+                       base + c_bytes + s_bytes + g_bytes, dst, s);
+    });
+}
+
+vbm_status vbm_quantize_mxfp8(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, void * codes, void * scales,
+                              void * stream) {
+    return guarded([&] {
+        require(x && codes && scales, "null buffer");
+        launch_quantize_mxfp8(x, n_rows, k, x_stride, static_cast<uint8_t *>(codes), static_cast<uint8_t *>(scales),
+                              as_stream(stream));
+    });
+}
+
 vbm_status vbm_glu(int activation, const float * gate, const float * up, float * out, int64_t n_rows, int64_t width,
                    int64_t gate_stride, int64_t up_stride, int64_t out_stride, float alpha, float limit, void * stream) {
     return guarded([&] {

@@ -158,6 +158,8 @@ SIGNATURES = {
     "vbm_mul_mat_id_ws": [vp, vp, vp, i64, C.c_int, vp, i64, vp, i64, i64, i64, vp, vp, C.c_int, vp, C.c_size_t, vp],
     "vbm_mul_mat_id_noalloc": [vp, vp, i64, C.c_int, vp, i64, vp, i64, i64, i64, vp, vp, C.c_int, vp],
     "vbm_add_id": [vp, vp, i64, vp, i64, i64, i64, i64, vp],
+    "vbm_mul_mat_id_mxfp8": [vp, vp, i64, vp, i64, vp, i64, i64, i64, vp, vp],
+    "vbm_quantize_mxfp8": [vp, i64, i64, i64, vp, vp, vp],
     "vbm_compute_forward": [C.POINTER(Node), vp, vp],
     "vbm_graph_compute": [vp, i64, vp, vp],
     "vbm_glu": [C.c_int, vp, vp, vp, i64, i64, i64, i64, i64, C.c_float, C.c_float, vp],
