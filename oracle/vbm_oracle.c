@@ -564,42 +564,51 @@ void orc_weighted_combine(const float * y, const float * weights, int64_t rows, 
  * gate_up MUL_MAT_ID -> ADD_ID biases after the gate|up split (HP:1472-1480) -> GLU ->
  * MUL_MAT_ID down (activation requantized to Q8_0, tools/engine/native_cpu.cpp:190) -> ADD_ID ->
  * MUL weights -> sequential rank sum. */
+/* One token of orc_moe_layer: quantize, then per rank gate_up -> GLU -> requantize -> down, then
+ * the weighted rank combine. `inner` is gemv_rows' thread argument. */
+static void moe_token(const orc_layer * L, const float * x, int64_t t, const int32_t * ids, const float * weights,
+                      float * out, float * act_out, float * y_out, int inner) {
+    const int64_t H = L->hidden, I = L->intermediate, K = L->top_k;
+    const size_t qh = (size_t)(H / 32) * 34, qi = (size_t)(I / 32) * 34;
+    const size_t gu_bytes = row_bytes(L->type, H) * (size_t)(2 * I);
+    const size_t dn_bytes = row_bytes(L->type, I) * (size_t)H;
+    uint8_t * xq = (uint8_t *)malloc(qh), * aq = (uint8_t *)malloc(qi);
+    float * gu = (float *)malloc(sizeof(float) * (size_t)(2 * I));
+    float * act = (float *)malloc(sizeof(float) * (size_t)I);
+    float * y = (float *)malloc(sizeof(float) * (size_t)(K * H));
+    orc_quantize_row_q8_0(x + t * H, xq, H);
+    for (int64_t r = 0; r < K; ++r) {
+        const int32_t e = ids[t * K + r];
+        gemv_rows(L->type, (const uint8_t *)L->gate_up + (size_t)e * gu_bytes, H, 2 * I, xq,
+                  L->gate_up_bias ? L->gate_up_bias + (size_t)e * 2 * I : NULL, gu, inner);
+        orc_glu(L->activation, gu, gu + I, act, I, 1.702f, 7.0f);
+        if (act_out) memcpy(act_out + (t * K + r) * I, act, sizeof(float) * (size_t)I);
+        orc_quantize_row_q8_0(act, aq, I);
+        gemv_rows(L->type, (const uint8_t *)L->down + (size_t)e * dn_bytes, I, H, aq,
+                  L->down_bias ? L->down_bias + (size_t)e * H : NULL, y + r * H, inner);
+    }
+    if (y_out) memcpy(y_out + t * K * H, y, sizeof(float) * (size_t)(K * H));
+    orc_weighted_combine(y, weights + t * K, H, K, 1, out + t * H);
+    free(xq); free(aq); free(gu); free(act); free(y);
+}
+
 int orc_moe_layer(const orc_layer * L, const float * x, float * logits, int64_t n_tokens,
                   float * out, int32_t * ids, float * weights, float * act_out, float * y_out,
                   int threads) {
     const int64_t H = L->hidden, I = L->intermediate, K = L->top_k;
     if (H % 64 || I % 64 || K <= 0 || K > L->n_expert) return -1;
     orc_router(L->router_w, L->router_b, x, H, logits, L->n_expert, n_tokens, K, ids, weights);
-    const size_t qh = (size_t)(H / 32) * 34, qi = (size_t)(I / 32) * 34;
-    const size_t gu_bytes = row_bytes(L->type, H) * (size_t)(2 * I);
-    const size_t dn_bytes = row_bytes(L->type, I) * (size_t)H;
     /* Tokens are independent: with many tokens each thread takes whole tokens (SIMD dots on the
-     * thread), otherwise the rows of each projection are split over the threads. Either way every
-     * output is the same function of its token's inputs, so the bits do not depend on it. */
-    const int per_token = threads > 0 && n_tokens >= 2 * threads;
+     * thread), otherwise the rows of each projection are split over the threads (a top-level
+     * parallel region per projection, never nested in another). Either way every output is the
+     * same function of its token's inputs, so the bits do not depend on it. */
+    if (threads > 0 && n_tokens >= 2 * threads) {
 #ifdef _OPENMP
-#pragma omp parallel for num_threads(per_token ? threads : 1) schedule(dynamic, 1)
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1)
 #endif
-    for (int64_t t = 0; t < n_tokens; ++t) {
-        const int inner = per_token ? -1 : threads;
-        uint8_t * xq = (uint8_t *)malloc(qh), * aq = (uint8_t *)malloc(qi);
-        float * gu = (float *)malloc(sizeof(float) * (size_t)(2 * I));
-        float * act = (float *)malloc(sizeof(float) * (size_t)I);
-        float * y = (float *)malloc(sizeof(float) * (size_t)(K * H));
-        orc_quantize_row_q8_0(x + t * H, xq, H);
-        for (int64_t r = 0; r < K; ++r) {
-            const int32_t e = ids[t * K + r];
-            gemv_rows(L->type, (const uint8_t *)L->gate_up + (size_t)e * gu_bytes, H, 2 * I, xq,
-                      L->gate_up_bias ? L->gate_up_bias + (size_t)e * 2 * I : NULL, gu, inner);
-            orc_glu(L->activation, gu, gu + I, act, I, 1.702f, 7.0f);
-            if (act_out) memcpy(act_out + (t * K + r) * I, act, sizeof(float) * (size_t)I);
-            orc_quantize_row_q8_0(act, aq, I);
-            gemv_rows(L->type, (const uint8_t *)L->down + (size_t)e * dn_bytes, I, H, aq,
-                      L->down_bias ? L->down_bias + (size_t)e * H : NULL, y + r * H, inner);
-        }
-        if (y_out) memcpy(y_out + t * K * H, y, sizeof(float) * (size_t)(K * H));
-        orc_weighted_combine(y, weights + t * K, H, K, 1, out + t * H);
-        free(xq); free(aq); free(gu); free(act); free(y);
+        for (int64_t t = 0; t < n_tokens; ++t) moe_token(L, x, t, ids, weights, out, act_out, y_out, -1);
+    } else {
+        for (int64_t t = 0; t < n_tokens; ++t) moe_token(L, x, t, ids, weights, out, act_out, y_out, threads);
     }
     return 0;
 }

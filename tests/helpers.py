@@ -41,6 +41,7 @@ def mul_mat_id(bank: vb.Bank, n_as: int, b: np.ndarray, b_type: int, b_ne1: int,
     dmap = vb.DeviceBuffer.from_array(np.asarray(slot_map, np.int32)) if slot_map is not None else None
     hmap = np.ascontiguousarray(slot_map_host, dtype=np.int32) if slot_map_host is not None else None
     dst = vb.DeviceBuffer(n_tokens * n_ids * bank.rows * 4)
+    vb.call("vbm_memset", dst.ptr, 0x7F, dst.nbytes, None)      # a row the call leaves unwritten shows up
     vb.call("vbm_mul_mat_id", bank.handle, vb.ptr(dmap), vb.ptr(hmap), n_as, b_type, db.ptr, b_ne1, dids.ptr, n_ids,
             n_tokens, ids_stride, vb.ptr(dbias), dst.ptr, order, None)
     vb.call("vbm_stream_synchronize", None)

@@ -28,17 +28,19 @@ namespace {
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-// MUL_MAT_ID output rows before the expert kernels run: 0 for every row (the rows of -1 ids stay
-// zero, hybrid-experts.patch:617-621; routed rows are overwritten), NaN for ids outside
-// [-1, n_as), which the grouping pass skips (the reference asserts on them, :622), so an invalid id
-// is loud in the output even when no host copy of the ids was given for checking.
+// MUL_MAT_ID output rows the expert kernels do not write: 0 for the rows of -1 ids
+// (hybrid-experts.patch:617-621), NaN for ids outside [-1, n_as), which the grouping pass skips
+// (the reference asserts on them, :622), so an invalid id is loud in the output even when no host
+// copy of the ids was given for checking. Rows of routed ids are left to the expert kernels, which
+// write every one of them (NaN where the expert has no slot).
 __global__ void init_dst_kernel(float * dst, const int32_t * ids, int64_t n_ids, int64_t ids_stride, int64_t n_as,
                                 int64_t rows, int64_t n) {
     const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
     if (i >= n) return;
     const int64_t entry = i / rows, t = entry / n_ids, r = entry - t * n_ids;
     const int32_t id = ids[t * ids_stride + r];
-    dst[i] = id >= -1 && id < n_as ? 0.0f : __builtin_nanf("");
+    if (id >= 0 && id < n_as) return;
+    dst[i] = id == -1 ? 0.0f : __builtin_nanf("");
 }
 
 void init_dst(float * dst, const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride, int64_t n_as,
