@@ -326,6 +326,36 @@ def test_node_elementwise_and_add_id_on_views(gpu):
     assert H.bits_equal(download(vb, dy.ptr, y.shape), y)           # the source is not modified
 
 
+def test_node_cpy_casts_on_views(gpu):
+    """CPY nodes (ggml_cast) F32 -> I32 from a transposed view (truncation toward zero, saturation
+    and NaN -> 0 where C leaves the conversion undefined), I32 -> F32 (round to nearest), and the
+    same-type copies, into contiguous destinations, against numpy."""
+    vb = gpu
+    f = np.array([[0.0, -0.0, 1.5, -1.5, 2.999, -2.999, 7.0, -128.0],
+                  [3e9, -3e9, np.nan, 16777217.0, 0.49, -0.51, 12.0, 1e-40]], np.float32)   # ne [8, 2]
+    i = np.array([[0, -1, 16777217, -16777219, 2147483647, -2147483648, 5, 7]], np.int32)  # ne [8, 1]
+    df, di = vb.DeviceBuffer.from_array(f), vb.DeviceBuffer.from_array(i)
+    outs = [vb.DeviceBuffer(64) for _ in range(4)]
+    g = Graph(vb)
+    F = g.leaf(F32, (8, 2), df.ptr)
+    Ft = g.view(F, (2, 8), [F.nb[1], F.nb[0], F.nb[2], F.nb[3]], 0)       # ne [2, 8]: transposed
+    I = g.leaf(I32, (8, 1), di.ptr)
+    g.tensor(I32, (2, 8), outs[0].ptr, op=vb.NODE_CPY, srcs=(Ft,))
+    g.tensor(F32, (8, 1), outs[1].ptr, op=vb.NODE_CPY, srcs=(I,))
+    g.tensor(F32, (2, 8), outs[2].ptr, op=vb.NODE_CPY, srcs=(Ft,))
+    g.tensor(I32, (8, 1), outs[3].ptr, op=vb.NODE_CPY, srcs=(I,))
+    for n in g.nodes:
+        assert g.supported(n)
+    g.compute()
+    vb.call("vbm_stream_synchronize", None)
+    ft = np.ascontiguousarray(f.T).astype(np.float64)                   # numpy [8, 2] = ggml ne [2, 8]
+    want = np.where(np.isnan(ft), 0, np.clip(np.trunc(np.nan_to_num(ft)), -2**31, 2**31 - 1)).astype(np.int64)
+    assert np.array_equal(download(vb, outs[0].ptr, ft.shape, np.int32), want.astype(np.int32))
+    assert H.bits_equal(download(vb, outs[1].ptr, i.shape), i.astype(np.float32))
+    assert H.bits_equal(download(vb, outs[2].ptr, ft.shape), np.ascontiguousarray(f.T))
+    assert np.array_equal(download(vb, outs[3].ptr, i.shape, np.int32), i)
+
+
 @pytest.mark.parametrize("mode", [0, 1])
 def test_node_host_call_and_join(gpu, mode):
     """A CUSTOM host-call node (fn: 2a + b on the host) and its join node (call output + c) through
