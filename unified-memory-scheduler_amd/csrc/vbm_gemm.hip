@@ -119,33 +119,73 @@ __device__ __forceinline__ half8_t i8_to_f16(long v) {
     for (int i = 0; i < 8; ++i) r[i] = static_cast<_Float16>(static_cast<signed char>(v >> (8 * i)));
     return r;
 }
-// Pipeline stages. Activations: chunks of CB blocks of the 64 jobs' codes (rows padded
-// by 16 bytes against bank conflicts) and their block scales. Weights: one bank group of both
-// tiles of the pair (8 slices x 32 rows x 16 bytes each) and its exponent / scale bytes. Both are
-// double-buffered in LDS; the next stage's global loads are in flight while the current one
-// computes, and one barrier per chunk separates them.
+// Pipeline stages, filled by global-to-LDS DMA: a ring of S chunks of CB blocks, each stage
+// holding everything its chunk reads: the 64 jobs' activation codes and block scales, both tiles'
+// weight dwords of those blocks (Q8_0: the [slice pair][row] interleave of 16-byte units
+// (2q, b), (2q+1, b), (2q, b+1), (2q+1, b+1); MXFP4: [slice][row] dwords, rows of odd slice pairs
+// rotated by 16 against bank conflicts) and their exponent / scale dword per row. Chunk c issues
+// the loads of chunk c + S - 1; one wait and one barrier per chunk. With two stages (17.5 KiB
+// for Q8_0) and no staging registers the VGPRs, not the LDS, bound occupancy (Q8_0 six to seven
+// waves per SIMD), which measured faster than deeper rings at lower occupancy (Q8_0 layer of
+// 2048 tokens: gate_up 343 vs 350 / 364 us with three / four stages).
 template <int TYPE>
 struct GemmStage {
     static constexpr int EB = TYPE == 39 ? 2 : 1;                       // bytes per activation code
     static constexpr int GB = TYPE == 39 ? 8 : 4;                       // blocks per bank group
     static constexpr int CB = 2;                                        // blocks per chunk
     static constexpr int CPG = GB / CB;                                 // chunks per group
-    static constexpr int RB = CB * 32 * EB + 16;                        // LDS bytes per job row
-    static constexpr int ACT = kJobTile * RB;
+    static constexpr int S = 2;                                         // ring depth
+    static constexpr int ROW = CB * 32 * EB;                            // bytes per job row and chunk
+    static constexpr int ACT = kJobTile * ROW;
     static constexpr int DA = kJobTile * CB * 4;
-    static constexpr int WT = 8 * (512 + 16);                          // one tile's group, slices padded
-    static constexpr int W = 2 * WT;
-    static constexpr int M = TYPE == 39 ? 2 * 256 : 2 * 32 * 4 * 4;    // exponents, or fp32 Q8_0 scales
-    static constexpr int ACT_PIECES = kJobTile * CB * 32 * EB / 16 / kGemmThreads;   // per thread
-    static constexpr int W_PIECES = W / 16 / kGemmThreads;
-    static constexpr int OFF_DA = 2 * ACT, OFF_W = OFF_DA + 2 * DA, OFF_M = OFF_W + 2 * W;
-    static constexpr int BYTES = OFF_M + 2 * M;
+    static constexpr int W = TYPE == 39 ? 2 * 8 * 32 * 4 : 2 * 4 * 32 * 16;
+    static constexpr int M = 2 * 32 * 4;
+    static constexpr int OFF_DA = ACT, OFF_W = OFF_DA + DA, OFF_M = OFF_W + W;
+    static constexpr int STAGE = OFF_M + M;
+    static constexpr int BYTES = S * STAGE;
+    // DMA instructions per wave and chunk: activation rows (1 KiB each), block scales, weights, meta
+    static constexpr int ACT_DMA = ACT / 1024 / 4;
+    static constexpr int W_DMA = W / 256 / 4;
+    static constexpr int PER_CHUNK = ACT_DMA + 1 + W_DMA + 1;
+    static_assert((S - 2) * PER_CHUNK < 64, "vmcnt range");
 };
+
+// Global-to-LDS DMA (global_load_lds_*): lane l's bytes land at LDS address m0 + l * size. The
+// loads are issued through inline assembly so that the compiler's wait-count pass, which would
+// wait for every such load before any LDS read it cannot prove disjoint, leaves the multi-stage
+// ring alone; the kernel waits for them explicitly (lds_dma_wait) before each barrier. The
+// compiler's own waits stay correct: loads it does not know of only make its counts stricter.
+__device__ __forceinline__ void lds_dma_x4(const void * src, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma_x4_s(const void * base, uint32_t off, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma_x1(const void * src, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma_x1_s(const void * base, uint32_t off, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m0) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void lds_dma_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// fp16 x fp32 product on one instruction: v_fma_mix_f32 with the half in the low (HI = 0) or high
+// half of `h2` and -0 as the addend, i.e. exactly float(h) * x rounded once, signed zeros included.
+template <int HI>
+__device__ __forceinline__ float mul_half(unsigned h2, float x, float neg_zero) {
+    float r;
+    if constexpr (HI) asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(x), "s"(neg_zero));
+    else asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(x), "s"(neg_zero));
+    return r;
+}
 
 template <int TYPE, int EPI, bool FLAGGED>
 __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) {
     using G = GemmStage<TYPE>;
-    constexpr int EB = G::EB, RB = G::RB, CB = G::CB;
+    constexpr int CB = G::CB;
     static_assert(G::BYTES >= kJobTile * 65 * 4, "epilogue tile must fit the stage buffers");
     __shared__ __attribute__((aligned(16))) uint8_t lds[G::BYTES];
     float (*tile_vals)[65] = reinterpret_cast<float (*)[65]>(lds);    // epilogue 1, after the K loop
@@ -222,91 +262,66 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
     bool slow = false;
     if constexpr (FLAGGED) slow = __syncthreads_or(flagged != 0) != 0;
 
-    // Cooperative stage loaders. Activation piece i of this thread: job (t + 256i) / P, 16-byte
-    // part (t + 256i) % P, P = pieces per job row; block scale: job t / 4, block t % 4. Weight
-    // piece i: byte 16(t + 256i) of the pair's 8 KiB group; exponent / scale piece: threads
-    // 0..31, byte 16t of the pair's 512-byte group meta.
-    constexpr int P = CB * 32 * EB / 16;
-    const uint8_t * ld_row[G::ACT_PIECES];
+    // Stage loaders (global-to-LDS DMA). Every wave issues the same G::PER_CHUNK loads per chunk
+    // (lanes that have nothing to load are masked, clamped sources keep every address inside the
+    // operands), so the wait before each barrier is a constant count.
+    //   - activations: wave w's x4 loads j cover 16 (Q8_0) or 8 (MXFP4) job rows of the chunk;
+    //     the 16-byte parts of row r sit at part p ^ s(r) (s(r) = (r >> 1) & 3, resp. r & 7) so
+    //     the fragment reads of 16 consecutive rows spread over the banks; a row past the tile's
+    //     jobs reads the first job's row (its columns are never stored);
+    //   - block scales: lanes 0..31 of wave w load jobs 16w..16w+15 x 2 blocks;
+    //   - weights: dword loads; Q8_0 load I = 4w + i covers tile I >> 3, slice pair (I >> 1) & 3,
+    //     rows 16 (I & 1) .. +15 (lane: row l >> 2, unit dword l & 3); MXFP4 load I = 2w + i covers
+    //     tile I >> 2, slices 2 (I & 3) and 2 (I & 3) + 1 (lane: slice l >> 5, position l & 31);
+    //     a tile past the bank's rows reads the pair's first tile (its rows are never stored);
+    //   - meta: lanes 0..15 of wave w load the dword of rows 16 (w & 1) .. +15 of tile w >> 1.
+    const int wu = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+    const uint8_t * act_src[G::ACT_DMA];
 #pragma unroll
-    for (int i = 0; i < G::ACT_PIECES; ++i) {
-        const int jl = (threadIdx.x + i * kGemmThreads) / P;
-        ld_row[i] = j0 + jl < count ? row_of(jl) + ((threadIdx.x + i * kGemmThreads) % P) * 16 : nullptr;
+    for (int j = 0; j < G::ACT_DMA; ++j) {
+        const int jr = TYPE == 39 ? 8 * (wave * G::ACT_DMA + j) + (lane >> 3) : 16 * (wave * G::ACT_DMA + j) + (lane >> 2);
+        const int part = TYPE == 39 ? (lane & 7) ^ (jr & 7) : (lane & 3) ^ ((jr >> 1) & 3);
+        act_src[j] = row_of(j0 + jr < count ? jr : 0) + 16 * part;
     }
-    const int sd_job = threadIdx.x / CB;
-    const float * sd_row = sd_job < kJobTile && j0 + sd_job < count
-                               ? reinterpret_cast<const float *>(row_of(sd_job) + A.lay.da_offset()) + threadIdx.x % CB
-                               : nullptr;
-    const uint8_t * w_src[G::W_PIECES];
-#pragma unroll
-    for (int i = 0; i < G::W_PIECES; ++i) {
-        const int byte = 16 * (threadIdx.x + i * kGemmThreads);
-        const int t = pair * 2 + byte / 4096;
-        w_src[i] = t * 32 < S.rows ? slot_base + static_cast<size_t>(t) * 32 * nb * kCodeRow + byte % 4096 : nullptr;
+    const int jd = 16 * wave + ((lane & 31) >> 1);
+    const uint8_t * da_src = row_of(j0 + jd < count ? jd : 0) + A.lay.da_offset() + 4 * (lane & 1);
+    // weight dword of this lane within its load's group-relative source
+    uint32_t woff;
+    if constexpr (TYPE == 39) {
+        const int k = lane >> 5, pos = lane & 31;            // slice within the pair of slices
+        woff = static_cast<uint32_t>((k * 32 + pos) * 16);   // the rotation depends on the pair: added per load
+    } else {
+        woff = static_cast<uint32_t>(((lane & 1) * 32 + (lane >> 2)) * 16 + 4 * ((lane >> 1) & 1));
     }
-    const uint8_t * m_src = nullptr;
-    if (threadIdx.x < 32) {
-        const int t = pair * 2 + static_cast<int>(threadIdx.x) / 16;
-        if (t * 32 < S.rows)
-            m_src = slot_base + S.codes_bytes + static_cast<size_t>(t) * 32 * nb * kMetaRow + (threadIdx.x % 16) * 16;
-    }
-
-    u32x4g st_act[G::ACT_PIECES];
-    float st_da = 0.0f;
-    u32x4g st_w[G::W_PIECES];
-    u32x4g st_m = u32x4g{0u, 0u, 0u, 0u};
-    auto load_act = [&](int c) {
+    const uint32_t moff = static_cast<uint32_t>(lane) * 8;
+    const size_t tile_bytes = static_cast<size_t>(32) * nb * kCodeRow, meta_tile_bytes = static_cast<size_t>(32) * nb * kMetaRow;
+    auto tsel = [&](int t) -> size_t { return (pair * 2 + t) * 32 < S.rows ? pair * 2 + t : pair * 2; };
+    auto dma_stage = [&](int c, int st) {
+        const int grp = c / G::CPG, sub = c % G::CPG;
+        const uint32_t sb = lds0 + st * G::STAGE;
 #pragma unroll
-        for (int i = 0; i < G::ACT_PIECES; ++i) {
-            st_act[i] = u32x4g{0u, 0u, 0u, 0u};
-            if (ld_row[i]) st_act[i] = *reinterpret_cast<const u32x4g *>(ld_row[i] + static_cast<int64_t>(c) * CB * 32 * EB);
-        }
-        st_da = sd_row ? sd_row[c * CB] : 0.0f;
-    };
-    auto store_act = [&](int buf) {
+        for (int j = 0; j < G::ACT_DMA; ++j)
+            lds_dma_x4(act_src[j] + static_cast<int64_t>(c) * G::ROW, sb + (wu * G::ACT_DMA + j) * 1024);
+        if (lane < 32) lds_dma_x1(da_src + static_cast<int64_t>(c) * CB * 4, sb + G::OFF_DA + wu * 128);
 #pragma unroll
-        for (int i = 0; i < G::ACT_PIECES; ++i) {
-            const int piece = threadIdx.x + i * kGemmThreads;
-            *reinterpret_cast<u32x4g *>(lds + buf * G::ACT + (piece / P) * RB + (piece % P) * 16) = st_act[i];
-        }
-        if (threadIdx.x < kJobTile * CB) reinterpret_cast<float *>(lds + G::OFF_DA + buf * G::DA)[threadIdx.x] = st_da;
-    };
-    auto load_w = [&](int g) {
-#pragma unroll
-        for (int i = 0; i < G::W_PIECES; ++i) {
-            st_w[i] = u32x4g{0u, 0u, 0u, 0u};
-            if (w_src[i]) st_w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4g *>(w_src[i] + static_cast<size_t>(g) * 4096));
-        }
-        if (m_src) st_m = *reinterpret_cast<const u32x4g *>(m_src + static_cast<size_t>(g) * 256);
-    };
-    auto store_w = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < G::W_PIECES; ++i) {
-            const int off = 16 * (threadIdx.x + i * kGemmThreads);    // byte of the pair's 8 KiB group
-            const int t = off >> 12, o = off & 4095;
+        for (int i = 0; i < G::W_DMA; ++i) {
+            const int I = wu * G::W_DMA + i;
             if constexpr (TYPE == 39) {
-                *reinterpret_cast<u32x4g *>(lds + G::OFF_W + buf * G::W + t * G::WT + o + (o >> 9) * 16) = st_w[i];
+                // slices 2 (I & 3) + (l >> 5): odd slice pairs hold row r at position r ^ 16
+                const int t = I >> 2, kp = I & 3;
+                const uint8_t * base = slot_base + tsel(t) * tile_bytes + static_cast<size_t>(grp) * 4096 + kp * 2 * 512 + 4 * sub;
+                lds_dma_x1_s(base, (kp & 1) ? (woff ^ (16 * 16)) : woff, sb + G::OFF_W + (t * 8 + kp * 2) * 128);
             } else {
-                // Q8_0: [slice pair q][block pair][row][16 B = (2q, b), (2q+1, b), (2q, b+1), (2q+1, b+1)],
-                // so one 16-byte read brings both int8 operands of a two-block chunk
-                const int k = o >> 9, r = (o >> 4) & 31;
-                uint8_t * base = lds + G::OFF_W + buf * G::W + t * G::WT + ((k >> 1) * 2 * 32 + r) * 16 + (k & 1) * 4;
-#pragma unroll
-                for (int d = 0; d < 4; ++d) *reinterpret_cast<unsigned *>(base + (d >> 1) * 32 * 16 + (d & 1) * 8) = st_w[i][d];
+                const int t = I >> 3, qq = (I >> 1) & 3, rh = I & 1;
+                const uint8_t * base =
+                    slot_base + tsel(t) * tile_bytes + static_cast<size_t>(grp) * 4096 + (2 * qq * 32 + rh * 16) * 16 + 8 * sub;
+                lds_dma_x1_s(base, woff, sb + G::OFF_W + t * 2048 + (qq * 32 + rh * 16) * 16);
             }
         }
-        if (threadIdx.x < 32) {
-            if constexpr (TYPE == 39) {
-                *reinterpret_cast<u32x4g *>(lds + G::OFF_M + buf * G::M + 16 * threadIdx.x) = st_m;
-            } else {   // rows 2p, 2p + 1 of tile t: four fp16 scales each, widened once here
-                float f[8];
-#pragma unroll
-                for (int h = 0; h < 8; ++h) f[h] = half_bits_to_float(static_cast<uint16_t>(st_m[h >> 1] >> ((h & 1) * 16)));
-                float * dstm = reinterpret_cast<float *>(lds + G::OFF_M + buf * G::M) + threadIdx.x * 8;
-                *reinterpret_cast<f32x4 *>(dstm) = f32x4{f[0], f[1], f[2], f[3]};
-                *reinterpret_cast<f32x4 *>(dstm + 4) = f32x4{f[4], f[5], f[6], f[7]};
-            }
-        }
+        const uint8_t * mbase = slot_base + S.codes_bytes + tsel(wu >> 1) * meta_tile_bytes + static_cast<size_t>(grp) * 256 +
+                                16 * (wu & 1) * 8 + (TYPE == 39 ? 4 * (sub >> 1) : 4 * sub);
+        if (lane < 16) lds_dma_x1_s(mbase, moff, sb + G::OFF_M + wu * 64);
     };
 
     f32x4 acc[2][2];
@@ -316,16 +331,13 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
         for (int jh = 0; jh < 2; ++jh) acc[i][jh] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     // One block: weight operands a_op[i] (row halves i), activation operand and scale of job half
-    // jh from bsrc(jh) / dsrc(jh); mscale(i, j) is the weight exponent (MXFP4, signed) or fp16
-    // scale (Q8_0) of output row 16i + 4q + j. SLOW adds the exact -128 correction, accumulated
-    // into the same MFMA result (its operands scaled by 256 are exact in fp16).
-    auto block_step = [&](auto slow_c, const auto & a_op, auto && mscale, auto && bsrc, auto && dsrc) {
+    // jh from bsrc(jh) / dsrc(jh); factor(i, j, da) is the block's fp32 scale for output row
+    // 16i + 4q + j: ldexp(da, e) for MXFP4 exponent e, fp16(d_w) * da for Q8_0. SLOW adds the
+    // exact -128 correction, accumulated into the same MFMA result (its operands scaled by 256
+    // are exact in fp16).
+    const float neg_zero = -0.0f;
+    auto block_step = [&](auto slow_c, const auto & a_op, auto && factor, auto && bsrc, auto && dsrc) {
         constexpr bool SLOW = decltype(slow_c)::value;
-        decltype(mscale(0, 0)) ms[2][4];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) ms[i][j] = mscale(i, j);
 #pragma unroll
         for (int jh = 0; jh < 2; ++jh) {
             const float da = dsrc(jh);
@@ -346,12 +358,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                     d = __builtin_amdgcn_mfma_f32_16x16x32_f16(neg_part(a16), is_neg128_x256(b16), d, 0, 0, 0);
                 }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if constexpr (TYPE == 39)
-                        acc[i][jh][j] = __builtin_fmaf(__builtin_amdgcn_ldexpf(da, ms[i][j]), d[j], acc[i][jh][j]);
-                    else
-                        acc[i][jh][j] = __builtin_fmaf(ms[i][j] * da, d[j], acc[i][jh][j]);
-                }
+                for (int j = 0; j < 4; ++j) acc[i][jh][j] = __builtin_fmaf(factor(i, j, da), d[j], acc[i][jh][j]);
             }
         }
     };
@@ -359,122 +366,137 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
     // The K loop, instantiated with and without the -128 correction (wave-uniform choice).
     const int n_chunks = groups * G::CPG;
     auto k_loop = [&](auto slow_c) {
-        const uint8_t * w_lds = lds + G::OFF_W + (wave & 1) * G::WT + (TYPE == 39 ? 2 * q * 528 : q * 2 * 32 * 16) + lr * 16;
-        const uint8_t * m_lds = lds + G::OFF_M + (wave & 1) * (G::M / 2) + 4 * q * (TYPE == 39 ? 8 : 16);   // output rows 4q + j
-        const uint8_t * ma_lds = lds + G::OFF_M + (wave & 1) * 256 + lr * 8;      // A rows lr (+16i)
-        const uint8_t * b_lds = lds + (32 * (wave >> 1) + lr) * RB + 8 * q * EB;
+        // weight dwords of A rows lr + 16i, slices 2q / 2q + 1 (MXFP4: row r of an odd slice pair
+        // at position r ^ 16), or their 16-byte unit (Q8_0)
+        const uint8_t * w_lds[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            w_lds[i] = lds + G::OFF_W + (TYPE == 39 ? ((wave & 1) * 256 + 2 * q * 32 + 16 * (i ^ (q & 1)) + lr) * 4
+                                                     : (wave & 1) * 2048 + (q * 32 + 16 * i + lr) * 16);
+        const uint8_t * m_lds = lds + G::OFF_M + ((wave & 1) * 32 + 4 * q) * 4;   // output rows 4q + j (+16i)
+        const uint8_t * ma_lds = lds + G::OFF_M + ((wave & 1) * 32 + lr) * 4;     // A rows lr (+16i)
         const float * d_lds = reinterpret_cast<const float *>(lds + G::OFF_DA) + (32 * (wave >> 1) + lr) * CB;
-        for (int g = 0; g < groups; ++g) {
-            const int wb = g & 1;
+        // fragment columns' activation codes: row rr = 32(w >> 1) + 16jh + lr, block bb, codes 8q..8q+7
+        uint32_t aoff[2][2];
+#pragma unroll
+        for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb) {
+                const int rr = 32 * (wave >> 1) + 16 * jh + lr;
+                aoff[jh][bb] = TYPE == 39 ? rr * 128 + (((4 * bb + q) ^ (rr & 7)) << 4)
+                                          : rr * 64 + (((2 * bb + (q >> 1)) ^ ((rr >> 1) & 3)) << 4) + 8 * (q & 1);
+            }
 #pragma clang loop unroll(disable)
-            for (int sub = 0; sub < G::CPG; ++sub) {
-                const int c = g * G::CPG + sub;
-                const bool next_act = c + 1 < n_chunks, next_w = sub == 0 && g + 1 < groups;
-                if (next_act) load_act(c + 1);
-                if (next_w) load_w(g + 1);
-                const int ab = c & 1;
-                // This chunk's blocks 2sub, 2sub+1 in the group: weight dwords of slices 2q, 2q+1
-                // (MXFP4: one dword holds both blocks; Q8_0: one dword each).
-                unsigned w0[2][2], w1[2][2];
+        for (int c = 0; c < n_chunks; ++c) {
+            const int sub = c % G::CPG;
+            // this chunk's loads: the stage of chunk c + S - 1, clamped to the last chunk
+            // (the stage it fills is free either way)
+            dma_stage(c + G::S - 1 < n_chunks ? c + G::S - 1 : n_chunks - 1, (c + G::S - 1) % G::S);
+            const int ab = c % G::S;
+            const uint8_t * st = lds + ab * G::STAGE;     // this chunk's stage
+            // This chunk's blocks 2sub, 2sub+1 in the group: weight dwords of slices 2q, 2q+1
+            // (MXFP4: one dword holds both blocks; Q8_0: one dword each).
+            unsigned w0[2][2], w1[2][2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                if constexpr (TYPE == 39) {
+                    const uint8_t * w = w_lds[i] + ab * G::STAGE;
+                    w0[i][0] = w0[i][1] = *reinterpret_cast<const unsigned *>(w);
+                    w1[i][0] = w1[i][1] = *reinterpret_cast<const unsigned *>(w + 32 * 4);
+                } else {
+                    const u32x4g v = *reinterpret_cast<const u32x4g *>(w_lds[i] + ab * G::STAGE);
+                    w0[i][0] = v[0], w1[i][0] = v[1], w0[i][1] = v[2], w1[i][1] = v[3];
+                }
+            }
+            // MXFP4 fast path: when every exponent e of the wave's A rows (16i + lr) lies in
+            // [-14, 12], 2^(e+1) times the e2m1 values is an exact normal f16, so the exponent
+            // rides in the A operand and the block result needs one FMA with d_act:
+            // da * (2^e * dot) rounds the same product as ldexp(da, e) * dot.
+            bool folded = false;
+            float fsc[2][2];
+            if constexpr (TYPE == 39 && !decltype(slow_c)::value) {
+                bool ok = true;
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
-                    const uint8_t * w = w_lds + wb * G::W + i * 16 * 16;
-                    if constexpr (TYPE == 39) {
-                        w0[i][0] = w0[i][1] = *reinterpret_cast<const unsigned *>(w + sub * 4);
-                        w1[i][0] = w1[i][1] = *reinterpret_cast<const unsigned *>(w + 528 + sub * 4);
-                    } else {
-                        const u32x4g v = *reinterpret_cast<const u32x4g *>(w + sub * 32 * 16);
-                        w0[i][0] = v[0], w1[i][0] = v[1], w0[i][1] = v[2], w1[i][1] = v[3];
+                    const unsigned ea = *reinterpret_cast<const uint16_t *>(ma_lds + ab * G::STAGE + i * 16 * 4 + (sub & 1) * 2);
+#pragma unroll
+                    for (int bb = 0; bb < 2; ++bb) {
+                        const int e = static_cast<signed char>(ea >> (8 * bb));
+                        ok = ok && e >= -14 && e <= 12;
+                        fsc[i][bb] = __builtin_bit_cast(float, static_cast<unsigned>(e + 128) << 23);
                     }
                 }
-                // MXFP4 fast path: when every exponent e of the wave's A rows (16i + lr) lies in
-                // [-14, 12], 2^(e+1) times the e2m1 values is an exact normal f16, so the exponent
-                // rides in the A operand and the block result needs one FMA with d_act:
-                // da * (2^e * dot) rounds the same product as ldexp(da, e) * dot.
-                bool folded = false;
-                float fsc[2][2];
-                if constexpr (TYPE == 39 && !decltype(slow_c)::value) {
-                    bool ok = true;
+                folded = __all(ok);
+            }
+            if (folded) {
 #pragma unroll
-                    for (int i = 0; i < 2; ++i) {
-                        const unsigned ea = *reinterpret_cast<const uint16_t *>(ma_lds + wb * G::M + i * 16 * 8 + sub * 2);
+                for (int bb = 0; bb < CB; ++bb) {
+                    half8_t a_op[2];
 #pragma unroll
-                        for (int bb = 0; bb < 2; ++bb) {
-                            const int e = static_cast<signed char>(ea >> (8 * bb));
-                            ok = ok && e >= -14 && e <= 12;
-                            fsc[i][bb] = __builtin_bit_cast(float, static_cast<unsigned>(e + 128) << 23);
+                    for (int i = 0; i < 2; ++i) a_op[i] = mx_a_operand(w0[i][bb], w1[i][bb], bb, fsc[i][bb]);
+#pragma unroll
+                    for (int jh = 0; jh < 2; ++jh) {
+                        const float da = d_lds[ab * (G::STAGE / 4) + 16 * jh * CB + bb];
+                        const half8_t bv = *reinterpret_cast<const half8_t *>(st + aoff[jh][bb]);
+#pragma unroll
+                        for (int i = 0; i < 2; ++i) {
+                            const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_op[i], bv, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) acc[i][jh][j] = __builtin_fmaf(da, d[j], acc[i][jh][j]);
                         }
                     }
-                    folded = __all(ok);
                 }
-                if (folded) {
+            } else {
+                // exponent / scale bytes of output rows 16i + 4q + j (MXFP4 one byte, Q8_0 two per block)
+                // (Q8_0: both blocks' fp16 scales of a row in one dword)
+                unsigned mw[2][4];
 #pragma unroll
-                    for (int bb = 0; bb < CB; ++bb) {
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if constexpr (TYPE == 39)
+                            mw[i][j] = *reinterpret_cast<const uint16_t *>(m_lds + ab * G::STAGE + (16 * i + j) * 4 + (sub & 1) * 2);
+                        else
+                            mw[i][j] = *reinterpret_cast<const unsigned *>(m_lds + ab * G::STAGE + (16 * i + j) * 4);
+                    }
+                auto do_block = [&](int bb) {
+                    auto bsrc = [&](int jh) {
+                        const uint8_t * p = st + aoff[jh][bb];
+                        if constexpr (TYPE == 39) return *reinterpret_cast<const half8_t *>(p);
+                        else return *reinterpret_cast<const long *>(p);
+                    };
+                    auto dsrc = [&](int jh) { return d_lds[ab * (G::STAGE / 4) + 16 * jh * CB + bb]; };
+                    if constexpr (TYPE == 39) {
+                        auto factor = [&](int i, int j, float da) {
+                            return __builtin_amdgcn_ldexpf(da, static_cast<signed char>(mw[i][j] >> (8 * bb)));
+                        };
                         half8_t a_op[2];
 #pragma unroll
-                        for (int i = 0; i < 2; ++i) a_op[i] = mx_a_operand(w0[i][bb], w1[i][bb], bb, fsc[i][bb]);
-#pragma unroll
-                        for (int jh = 0; jh < 2; ++jh) {
-                            const float da = d_lds[ab * (G::DA / 4) + 16 * jh * CB + bb];
-                            const half8_t bv = *reinterpret_cast<const half8_t *>(b_lds + ab * G::ACT + 16 * jh * RB + bb * 32 * EB);
-#pragma unroll
-                            for (int i = 0; i < 2; ++i) {
-                                const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_op[i], bv, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-                                for (int j = 0; j < 4; ++j) acc[i][jh][j] = __builtin_fmaf(da, d[j], acc[i][jh][j]);
-                            }
-                        }
-                    }
-                } else {
-                    // exponent / scale bytes of output rows 16i + 4q + j (MXFP4 one byte, Q8_0 two per block)
-                    unsigned mw[2][4];
-                    float mf[2][4][2];
-#pragma unroll
-                    for (int i = 0; i < 2; ++i)
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            if constexpr (TYPE == 39) {
-                                mw[i][j] = *reinterpret_cast<const uint16_t *>(m_lds + wb * G::M + (16 * i + j) * 8 + sub * 2);
-                            } else {
-                                const float * m = reinterpret_cast<const float *>(m_lds + wb * G::M + (16 * i + j) * 16) + sub * 2;
-                                mf[i][j][0] = m[0];
-                                mf[i][j][1] = m[1];
-                            }
-                        }
-                    auto do_block = [&](int bb) {
-                        auto bsrc = [&](int jh) {
-                            const uint8_t * p = b_lds + ab * G::ACT + 16 * jh * RB + bb * 32 * EB;
-                            if constexpr (TYPE == 39) return *reinterpret_cast<const half8_t *>(p);
-                            else return *reinterpret_cast<const long *>(p);
-                        };
-                        auto dsrc = [&](int jh) { return d_lds[ab * (G::DA / 4) + 16 * jh * CB + bb]; };
-                        if constexpr (TYPE == 39) {
-                            auto mscale = [&](int i, int j) { return static_cast<int>(static_cast<signed char>(mw[i][j] >> (8 * bb))); };
-                            half8_t a_op[2];
-#pragma unroll
-                            for (int i = 0; i < 2; ++i) a_op[i] = mx_a_operand(w0[i][bb], w1[i][bb], bb);
-                            block_step(slow_c, a_op, mscale, bsrc, dsrc);
-                        } else {
-                            auto mscale = [&](int i, int j) { return mf[i][j][bb]; };
-                            long a_op[2];
-#pragma unroll
-                            for (int i = 0; i < 2; ++i)
-                                a_op[i] = static_cast<long>(static_cast<uint64_t>(w0[i][bb]) | (static_cast<uint64_t>(w1[i][bb]) << 32));
-                            block_step(slow_c, a_op, mscale, bsrc, dsrc);
-                        }
-                    };
-                    if constexpr (decltype(slow_c)::value) {
-#pragma clang loop unroll(disable)
-                        for (int bb = 0; bb < CB; ++bb) do_block(bb);
+                        for (int i = 0; i < 2; ++i) a_op[i] = mx_a_operand(w0[i][bb], w1[i][bb], bb);
+                        block_step(slow_c, a_op, factor, bsrc, dsrc);
                     } else {
+                        auto factor = [&](int i, int j, float da) {
+                            return bb ? mul_half<1>(mw[i][j], da, neg_zero) : mul_half<0>(mw[i][j], da, neg_zero);
+                        };
+                        long a_op[2];
 #pragma unroll
-                        for (int bb = 0; bb < CB; ++bb) do_block(bb);
+                        for (int i = 0; i < 2; ++i)
+                            a_op[i] = static_cast<long>(static_cast<uint64_t>(w0[i][bb]) | (static_cast<uint64_t>(w1[i][bb]) << 32));
+                        block_step(slow_c, a_op, factor, bsrc, dsrc);
                     }
+                };
+                if constexpr (decltype(slow_c)::value) {
+#pragma clang loop unroll(disable)
+                    for (int bb = 0; bb < CB; ++bb) do_block(bb);
+                } else {
+#pragma unroll
+                    for (int bb = 0; bb < CB; ++bb) do_block(bb);
                 }
-                if (next_act) store_act((c + 1) & 1);
-                if (next_w) store_w((g + 1) & 1);
-                __syncthreads();
             }
+            // the stage of chunk c + 1, issued S - 1 chunks before it is read: only the loads of
+            // the last S - 2 chunks may remain in flight
+            lds_dma_wait<(G::S - 2) * G::PER_CHUNK>();
+            __syncthreads();
         }
 
         // Tail blocks (nb even: MXFP4 tail in {0,2,4,6}, Q8_0 tail in {0,2}), per-row packed, read
@@ -493,9 +515,9 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                         else m[i][j] = *reinterpret_cast<const uint16_t *>(meta + groups * 256 + (orow * tail + bt) * 2);
                     }
                 }
-            auto mscale = [&](int i, int j) {
-                if constexpr (TYPE == 39) return static_cast<int>(static_cast<signed char>(m[i][j]));
-                else return half_bits_to_float(static_cast<uint16_t>(m[i][j]));
+            auto factor = [&](int i, int j, float da) {
+                if constexpr (TYPE == 39) return __builtin_amdgcn_ldexpf(da, static_cast<signed char>(m[i][j]));
+                else return half_bits_to_float(static_cast<uint16_t>(m[i][j])) * da;
             };
             const uint8_t * brow[2];
 #pragma unroll
@@ -525,7 +547,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                     const half2_g p0 = fp4x2(w0, 0), p1 = fp4x2(w0, 1), p2 = fp4x2(w1, 0), p3 = fp4x2(w1, 1);
                     a[i] = half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
                 }
-                block_step(slow_c, a, mscale, bsrc, dsrc);
+                block_step(slow_c, a, factor, bsrc, dsrc);
             } else {
                 long a[2];
 #pragma unroll
@@ -538,15 +560,14 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                     }
                     a[i] = static_cast<long>(w0 | (w1 << 32));
                 }
-                block_step(slow_c, a, mscale, bsrc, dsrc);
+                block_step(slow_c, a, factor, bsrc, dsrc);
             }
         }
     };
+    // Prologue: stages 0 .. S - 2 (clamped).
     if (groups > 0) {
-        load_act(0);
-        load_w(0);
-        store_act(0);
-        store_w(0);
+        for (int c = 0; c < G::S - 1; ++c) dma_stage(c < n_chunks ? c : n_chunks - 1, c);
+        lds_dma_wait<0>();
     }
     __syncthreads();
     if constexpr (FLAGGED) {
@@ -555,6 +576,9 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
     } else {
         k_loop(std::false_type{});
     }
+    // The clamped loads of the last chunks may still be landing in the stages the epilogue reuses.
+    lds_dma_wait<0>();
+    __syncthreads();
 
     // Epilogue: biases (ggml row order), then either fp32 rows or GLU + Q8_0 requantization.
 #pragma unroll
