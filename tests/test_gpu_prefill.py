@@ -93,6 +93,25 @@ def test_gemm_multi_tile_experts_exact(gpu, orc, type_id, experts, n_ids, tokens
 
 
 @pytest.mark.parametrize("type_id", [H.MX, H.Q8])
+def test_gemm_unaligned_destination_exact(gpu, orc, type_id):
+    """A destination 4 bytes past a 16-byte boundary takes the per-element stores of the fp32
+    epilogue (aligned ones leave through the LDS tile as 16-byte stores): bit-identical to the
+    oracle with unit scales, biases included, over a bank whose last tile pair is half live."""
+    rng = np.random.default_rng(7100 + type_id)
+    experts, n_ids, tokens, rows, k = 3, 2, 150, 96, 256
+    w = (unit_scale_mxfp4 if type_id == H.MX else unit_scale_q8)(experts, rows, k, rng)
+    bank = H.make_bank(type_id, w, experts, rows, k)
+    ids = np.stack([rng.choice(experts, n_ids, replace=False) for _ in range(tokens)]).astype(np.int32)
+    x = unit_scale_activations(tokens, k, rng).reshape(tokens, 1, k)
+    bias = rng.integers(-4, 5, experts * rows).astype(np.float32)
+    ref = orc.mul_mat_id(type_id, w, k, rows, experts, 0, x, 1, ids, n_ids, tokens, n_ids, bias=bias, threads=8)
+    for off in (0, 4):
+        got = H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, ids, n_ids, bias=bias, order=gpu.ORDER_FAST, dst_offset=off)
+        assert H.bits_equal(got, ref), (off, H.diff_report(got, ref))
+    bank.destroy()
+
+
+@pytest.mark.parametrize("type_id", [H.MX, H.Q8])
 def test_prefill_layer_multi_tile_experts(gpu, orc, type_id):
     """The fused layer (gate_up GEMM with the GLU + requantization epilogue, then the down GEMM)
     with 4 experts top-2 at T = 300, so every expert holds 110..190 jobs over 2..3 job tiles:

@@ -69,6 +69,7 @@ struct GemmArgs {
     GemmRowLayout out_lay;
     int activation;
     float alpha, limit;
+    int dst_vec4;              // epilogue 0: dst is 16-byte aligned (rows are multiples of 32)
 };
 
 __device__ __forceinline__ half2_g fp4x2(unsigned dw, int sel, float scale = 2.0f) {
@@ -186,9 +187,9 @@ template <int TYPE, int EPI, bool FLAGGED>
 __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) {
     using G = GemmStage<TYPE>;
     constexpr int CB = G::CB;
-    static_assert(G::BYTES >= kJobTile * 65 * 4, "epilogue tile must fit the stage buffers");
+    static_assert(G::BYTES >= kJobTile * 68 * 4, "epilogue tile must fit the stage buffers");
     __shared__ __attribute__((aligned(16))) uint8_t lds[G::BYTES];
-    float (*tile_vals)[65] = reinterpret_cast<float (*)[65]>(lds);    // epilogue 1, after the K loop
+    float (*tile_vals)[68] = reinterpret_cast<float (*)[68]>(lds);    // epilogue tile [job][pair row], after the K loop
 
     // XCD-aware order: workgroup i runs on XCD i % 8, so hand each XCD a contiguous range of
     // (tile, pair) items; the pairs of one job tile then share its activation rows in one L2 and
@@ -580,7 +581,10 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
     lds_dma_wait<0>();
     __syncthreads();
 
-    // Epilogue: biases (ggml row order), then either fp32 rows or GLU + Q8_0 requantization.
+    // Epilogue: biases (ggml row order), then either fp32 rows or GLU + Q8_0 requantization. The
+    // fp32 rows go through the LDS tile too when the output allows 16-byte stores, so that each
+    // job's 64 rows leave as four full 64-byte segments instead of 4-byte scatter.
+    const bool via_lds = EPI == 1 || A.dst_vec4;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -592,11 +596,28 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
             for (int jh = 0; jh < 2; ++jh) {
                 float v = acc[i][jh][j];
                 if (A.bias) v = v + bv;
-                if (EPI == 0) {
+                if (!via_lds) {
                     if (jlive[jh] && tile_live) A.dst[static_cast<size_t>(job[jh]) * S.rows + grow] = v;
                 } else {
                     tile_vals[32 * (wave >> 1) + 16 * jh + lr][32 * (wave & 1) + orow] = v;
                 }
+            }
+        }
+    }
+    if (EPI == 0 && via_lds) {
+        __syncthreads();
+        // four threads per job, 16 pair rows each; aligned runs of 4 device rows are 4
+        // consecutive ggml rows (also in interleaved gate|up banks)
+        const int jl = threadIdx.x >> 2, seg = threadIdx.x & 3;
+        if (j0 + jl < count) {
+            float * out = A.dst + static_cast<size_t>(A.jobs[joff + j0 + jl]) * S.rows;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int col = seg * 16 + 4 * k;
+                const int64_t brow = static_cast<int64_t>(pair) * 64 + col;
+                if (brow < S.rows)
+                    *reinterpret_cast<float4 *>(out + ggml_row(brow, S.rows, S.interleave)) =
+                        *reinterpret_cast<const float4 *>(&tile_vals[jl][col]);
             }
         }
     }
@@ -1086,6 +1107,7 @@ void launch_grouped_gemm(const GemmParams & p, hipStream_t stream) {
     a.n_tiles = n_tiles;
     a.bias = p.bias;
     a.dst = p.dst;
+    a.dst_vec4 = p.dst != nullptr && reinterpret_cast<uintptr_t>(p.dst) % 16 == 0 && bank.rows % 4 == 0;
     a.rows_out = p.rows_out;
     a.out_lay = p.out_layout;
     a.activation = p.activation;
