@@ -257,6 +257,10 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
         job[jh] = jlive[jh] ? A.jobs[joff + j0 + jl] : 0;
         if (FLAGGED && jlive[jh]) flagged |= *reinterpret_cast<const int *>(row_of(jl) + A.lay.flag_offset());
     }
+    // A fragment column of 16 jobs none of which is live (the tile's live jobs are a prefix) costs
+    // the wave no matrix or scale work: the last tile of an expert is often nearly empty.
+    const int wq = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 7));
+    const bool frag_live[2] = {j0 + 32 * wq < count, j0 + 32 * wq + 16 < count};
     // Workgroup-uniform: every wave then runs the same K-loop instantiation, so each of its
     // barriers is reached from one control path (every thread gets here: the exits above are
     // uniform per workgroup).
@@ -341,6 +345,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
         constexpr bool SLOW = decltype(slow_c)::value;
 #pragma unroll
         for (int jh = 0; jh < 2; ++jh) {
+            if (!frag_live[jh]) continue;
             const float da = dsrc(jh);
             const auto bv = bsrc(jh);
 #pragma unroll
@@ -437,6 +442,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                     for (int i = 0; i < 2; ++i) a_op[i] = mx_a_operand(w0[i][bb], w1[i][bb], bb, fsc[i][bb]);
 #pragma unroll
                     for (int jh = 0; jh < 2; ++jh) {
+                        if (!frag_live[jh]) continue;
                         const float da = d_lds[ab * (G::STAGE / 4) + 16 * jh * CB + bb];
                         const half8_t bv = *reinterpret_cast<const half8_t *>(st + aoff[jh][bb]);
 #pragma unroll
