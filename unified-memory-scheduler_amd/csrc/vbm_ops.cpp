@@ -33,22 +33,25 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // (the reference asserts on them, :622), so an invalid id is loud in the output even when no host
 // copy of the ids was given for checking. Rows of routed ids are left to the expert kernels, which
 // write every one of them (NaN where the expert has no slot).
+// One workgroup per (token, rank) entry: a routed entry returns at once (its row is written by
+// the expert kernels), a -1 entry gets a zero row and an invalid id a NaN row.
 __global__ void init_dst_kernel(float * dst, const int32_t * ids, int64_t n_ids, int64_t ids_stride, int64_t n_as,
-                                int64_t rows, int64_t n) {
-    const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-    if (i >= n) return;
-    const int64_t entry = i / rows, t = entry / n_ids, r = entry - t * n_ids;
+                                int64_t rows) {
+    const int64_t entry = blockIdx.x, t = entry / n_ids, r = entry - t * n_ids;
     const int32_t id = ids[t * ids_stride + r];
     if (id >= 0 && id < n_as) return;
-    dst[i] = id == -1 ? 0.0f : __builtin_nanf("");
+    const float v = id == -1 ? 0.0f : __builtin_nanf("");
+    float * row = dst + entry * rows;
+    for (int64_t i = threadIdx.x; i < rows; i += blockDim.x) row[i] = v;
 }
 
 void init_dst(float * dst, const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride, int64_t n_as,
               int64_t rows, hipStream_t stream) {
-    const int64_t n = n_ids * n_tokens * rows;
-    if (n <= 0) return;
-    hipLaunchKernelGGL(init_dst_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, dst, ids,
-                       n_ids, ids_stride, n_as, rows, n);
+    const int64_t entries = n_ids * n_tokens;
+    if (entries <= 0 || rows <= 0) return;
+    require(entries < (int64_t{1} << 25), "too many MUL_MAT_ID entries for one launch");   // 128 x entries work-items
+    hipLaunchKernelGGL(init_dst_kernel, dim3(static_cast<unsigned>(entries)), dim3(128), 0, stream, dst, ids, n_ids,
+                       ids_stride, n_as, rows);
     check_hip(hipGetLastError(), "output init launch");
 }
 
