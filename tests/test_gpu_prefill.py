@@ -38,11 +38,12 @@ def unit_scale_activations(n, k, rng):
 
 
 @pytest.mark.parametrize("type_id", [H.MX, H.Q8])
-@pytest.mark.parametrize("rows,k", [(256, 512), (96, 320), (160, 448), (64, 384)])
+@pytest.mark.parametrize("rows,k", [(256, 512), (96, 320), (160, 448), (64, 384), (128, 64)])
 def test_gemm_integer_block_dots_exact(gpu, orc, type_id, rows, k):
     """Unit-scale weights and activations: bit-identical to the oracle. The shapes cover bank
     groups with and without tail blocks (k = 320, 448: MXFP4 tails of 2 and 6 blocks, Q8_0 tails
-    of 2) and tile pairs whose second 32-row tile is past the last row (rows = 96, 160)."""
+    of 2), rows of tail blocks only (k = 64: no full group, so no staged chunk at all) and tile
+    pairs whose second 32-row tile is past the last row (rows = 96, 160)."""
     rng = np.random.default_rng(71 + k)
     experts, n_ids, tokens = 8, 4, 64
     w = (unit_scale_mxfp4 if type_id == H.MX else unit_scale_q8)(experts, rows, k, rng)

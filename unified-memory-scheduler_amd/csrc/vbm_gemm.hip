@@ -1092,10 +1092,12 @@ void launch_grouped_gemm(const GemmParams & p, hipStream_t stream) {
     int32_t * tile_expert = static_cast<int32_t *>(p.tiles);
     int32_t * tile_start = tile_expert + max_tiles;
     int32_t * n_tiles = tile_start + max_tiles;
-    hipLaunchKernelGGL(gemm_tiles_kernel, dim3(1), dim3(1024), 0, stream, p.group.counts, p.group.active,
-                       p.group.n_active, p.tile_filter, static_cast<int>(max_tiles), tile_expert, tile_start, n_tiles,
-                       p.group.error);
-    check_hip(hipGetLastError(), "GEMM tile list launch");
+    if (!p.tiles_ready) {
+        hipLaunchKernelGGL(gemm_tiles_kernel, dim3(1), dim3(1024), 0, stream, p.group.counts, p.group.active,
+                           p.group.n_active, p.tile_filter, static_cast<int>(max_tiles), tile_expert, tile_start, n_tiles,
+                           p.group.error);
+        check_hip(hipGetLastError(), "GEMM tile list launch");
+    }
     GemmArgs a{};
     a.bank = bank.base;
     a.shape = GemmShape{static_cast<int>(bank.nb), static_cast<int>(bank.rows), bank.interleave, bank.slot_bytes,

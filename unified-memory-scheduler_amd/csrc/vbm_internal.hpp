@@ -180,6 +180,7 @@ struct GemmParams {
     bool flagged_rows;                // rows_in may hold -128 codes (converted from caller Q8_0)
     const int32_t * tile_filter;      // device [n_as]: experts with a negative entry get no tiles, or null
     int64_t grid_tiles;               // > 0: bound on the tiles left by tile_filter (launch size), else 0
+    bool tiles_ready;                 // `tiles` already holds this group's list (same group and filter)
 };
 int64_t gemm_max_tiles(int64_t n_as, int64_t n_entries);
 size_t gemm_tiles_bytes(int64_t n_as, int64_t n_entries);

@@ -144,6 +144,7 @@ void prefill_pass(const vbm_moe_layer_desc & d, const int32_t * expert_to_slot, 
     launch_grouped_gemm(p, s);
     if (events) check_hip(hipEventRecord(static_cast<hipEvent_t>(events[1]), s), "hipEventRecord");
     p.bank = d.down;
+    p.tiles_ready = true;                 // same group and tile filter as the gate_up pass
     p.rows_in = w.xrows_act;
     p.lay = ga;
     p.b_ne1 = K;
