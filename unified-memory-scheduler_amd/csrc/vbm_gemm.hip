@@ -719,12 +719,12 @@ __global__ __launch_bounds__(1024) void gemm_tiles_kernel(const int32_t * counts
 // fp16-rounded fp32 block scales, and a 0 flag: this quantizer never produces -128).
 __global__ __launch_bounds__(256) void gemm_rows_from_f32_kernel(const float * __restrict__ x, int64_t n_rows, int nb,
                                                                  int64_t x_stride, GemmRowLayout L, uint8_t * __restrict__ out) {
-    const int64_t total = n_rows * nb * 4;
-    const int64_t t = blockIdx.x * 256ll + threadIdx.x;
-    const bool live = t < total;
-    const int64_t quad = live ? t / 4 : 0;
-    const int part = static_cast<int>(t & 3);
-    const int64_t row = quad / nb, b = quad % nb;
+    // workgroup (row, 64-block segment); four threads per block, eight elements each
+    const int64_t row = blockIdx.x;
+    const int bq = static_cast<int>(blockIdx.y) * 64 + static_cast<int>(threadIdx.x >> 2);
+    const bool live = bq < nb;
+    const int b = live ? bq : 0;
+    const int part = static_cast<int>(threadIdx.x & 3);
     float v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = live ? x[row * x_stride + b * 32 + part * 8 + i] : 0.0f;
@@ -1065,8 +1065,9 @@ size_t gemm_tiles_bytes(int64_t n_as, int64_t n_entries) {
 void launch_gemm_rows_from_f32(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, const GemmRowLayout & lay,
                                uint8_t * rows, hipStream_t stream) {
     require(k > 0 && k % 32 == 0 && n_rows > 0 && x_stride >= k && lay.nb == k / 32, "GEMM quantize shape mismatch");
-    const int64_t threads = n_rows * (k / 32) * 4;
-    hipLaunchKernelGGL(gemm_rows_from_f32_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, stream,
+    require(n_rows < (1ll << 31), "too many GEMM activation rows for one launch");
+    const unsigned segments = static_cast<unsigned>((k / 32 + 63) / 64);
+    hipLaunchKernelGGL(gemm_rows_from_f32_kernel, dim3(static_cast<unsigned>(n_rows), segments), dim3(256), 0, stream,
                        x, n_rows, static_cast<int>(k / 32), x_stride, lay, rows);
     check_hip(hipGetLastError(), "GEMM quantize launch");
 }

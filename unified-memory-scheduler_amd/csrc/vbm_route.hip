@@ -192,11 +192,13 @@ __global__ __launch_bounds__(64) void topk_softmax_kernel(const float * __restri
 }
 
 // out[t][i] = ((w0*y0 + w1*y1) + w2*y2) + ... : ggml MUL by the weight then sequential ADD.
+// Workgroup (token, 256-row segment).
 __global__ void combine_kernel(const float * __restrict__ y, const float * __restrict__ w, int64_t rows,
                                int n_ids, int64_t n_tokens, float * __restrict__ out) {
-    const int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-    if (idx >= rows * n_tokens) return;
-    const int64_t t = idx / rows, i = idx % rows;
+    const int64_t t = blockIdx.x;
+    const int64_t i = blockIdx.y * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (i >= rows) return;
+    const int64_t idx = t * rows + i;
     const float * yt = y + t * n_ids * rows + i;
     const float * wt = w + t * n_ids;
     float acc = yt[0] * wt[0];
@@ -300,8 +302,9 @@ void launch_router(const float * router_w, const float * router_b, const float *
 
 void launch_combine(const float * y, const float * weights, int64_t rows, int64_t n_ids, int64_t n_tokens, float * out,
                     hipStream_t stream) {
-    hipLaunchKernelGGL(combine_kernel, dim3(blocks_for(rows * n_tokens, 256)), dim3(256), 0, stream, y, weights, rows,
-                       static_cast<int>(n_ids), n_tokens, out);
+    require(n_tokens > 0 && n_tokens < (1ll << 31) && rows > 0 && (rows + 255) / 256 <= 65535, "combine shape out of range");
+    hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(n_tokens), static_cast<unsigned>((rows + 255) / 256)), dim3(256),
+                       0, stream, y, weights, rows, static_cast<int>(n_ids), n_tokens, out);
     check_hip(hipGetLastError(), "combine launch");
 }
 
