@@ -32,20 +32,21 @@ def make_bank(type_id: int, ggml: np.ndarray, experts: int, rows: int, k: int, i
 
 def mul_mat_id(bank: vb.Bank, n_as: int, b: np.ndarray, b_type: int, b_ne1: int, ids: np.ndarray, n_ids: int,
                bias: np.ndarray | None = None, order=vb.ORDER_EXACT, slot_map=None, slot_map_host=None,
-               dst_offset: int = 0) -> np.ndarray:
-    """dst_offset (bytes, a multiple of 4) places the output that far into its allocation, e.g. 4
-    for a destination that is not 16-byte aligned."""
+               dst_offset: int = 0, b_offset: int = 0) -> np.ndarray:
+    """dst_offset / b_offset (bytes, multiples of 4) place the output / the activations that far
+    into their allocations, e.g. 4 for buffers that are not 16-byte aligned."""
     ids = np.ascontiguousarray(ids, dtype=np.int32)
     n_tokens = ids.shape[0]
     ids_stride = ids.shape[1]
-    db = vb.DeviceBuffer.from_array(np.ascontiguousarray(b))
+    braw = np.ascontiguousarray(b).view(np.uint8).reshape(-1)
+    db = vb.DeviceBuffer.from_array(np.concatenate([np.zeros(b_offset, np.uint8), braw]))
     dids = vb.DeviceBuffer.from_array(ids)
     dbias = vb.DeviceBuffer.from_array(bias.astype(np.float32)) if bias is not None else None
     dmap = vb.DeviceBuffer.from_array(np.asarray(slot_map, np.int32)) if slot_map is not None else None
     hmap = np.ascontiguousarray(slot_map_host, dtype=np.int32) if slot_map_host is not None else None
     dst = vb.DeviceBuffer(n_tokens * n_ids * bank.rows * 4 + dst_offset)
     vb.call("vbm_memset", dst.ptr, 0x7F, dst.nbytes, None)      # a row the call leaves unwritten shows up
-    vb.call("vbm_mul_mat_id", bank.handle, vb.ptr(dmap), vb.ptr(hmap), n_as, b_type, db.ptr, b_ne1, dids.ptr, n_ids,
+    vb.call("vbm_mul_mat_id", bank.handle, vb.ptr(dmap), vb.ptr(hmap), n_as, b_type, db.ptr + b_offset, b_ne1, dids.ptr, n_ids,
             n_tokens, ids_stride, vb.ptr(dbias), dst.ptr + dst_offset, order, None)
     vb.call("vbm_stream_synchronize", None)
     raw = dst.download(np.uint8, (dst.nbytes,))

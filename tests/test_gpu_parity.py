@@ -259,6 +259,33 @@ def test_router_ids_exact(gpu, orc):
     assert di.download(np.int32, 4).tolist() == [1, 2, 4, 7]
 
 
+@pytest.mark.parametrize("n_expert", [300, 1024])
+def test_router_topk_given_logits_canonical_order(gpu, n_expert):
+    """Top-k of given logits (the router takes up to 1024 experts and refuses more): ids in the
+    canonical order (value descending, lower index first on ties), including rows full of ties and
+    a row whose winners sit in the last lanes; weights are the softmax of the picks within 1e-6."""
+    rng = np.random.default_rng(300 + n_expert)
+    tokens, top_k = 24, 8
+    logits = rng.standard_normal((tokens, n_expert)).astype(np.float32)
+    logits[1] = np.round(logits[1])                                  # many exact ties
+    logits[2] = 1.0                                                  # all tied: indices 0..k-1
+    logits[3, -top_k:] = 10.0                                        # winners at the end
+    dl = gpu.DeviceBuffer.from_array(logits)
+    di, dwt = gpu.DeviceBuffer(4 * tokens * top_k), gpu.DeviceBuffer(4 * tokens * top_k)
+    gpu.call("vbm_router_topk_softmax", None, None, None, 0, dl.ptr, n_expert, tokens, top_k, di.ptr, dwt.ptr, None)
+    ids = di.download(np.int32, (tokens, top_k))
+    wts = dwt.download(np.float32, (tokens, top_k))
+    idx = np.arange(n_expert)
+    for t in range(tokens):
+        want = np.lexsort((idx, -logits[t].astype(np.float64)))[:top_k]
+        assert ids[t].tolist() == want.tolist(), t
+        v = logits[t, want].astype(np.float64)
+        e = np.exp(v - v.max())
+        assert np.allclose(wts[t], e / e.sum(), rtol=1e-6, atol=0), t
+    with pytest.raises(gpu.VbmError):
+        gpu.call("vbm_router_topk_softmax", None, None, None, 0, dl.ptr, 1025, 1, top_k, di.ptr, dwt.ptr, None)
+
+
 @pytest.mark.parametrize("n_expert,hidden,top_k", [(32, 2880, 4), (128, 2048, 8)])
 def test_router_ids_equal_float64_topk_where_determined(gpu, orc, n_expert, hidden, top_k):
     """The reference's router fp32 order (upstream ggml_mul_mat) is parity-unpinned; wherever the

@@ -96,8 +96,9 @@ def test_gemm_multi_tile_experts_exact(gpu, orc, type_id, experts, n_ids, tokens
 @pytest.mark.parametrize("type_id", [H.MX, H.Q8])
 def test_gemm_unaligned_destination_exact(gpu, orc, type_id):
     """A destination 4 bytes past a 16-byte boundary takes the per-element stores of the fp32
-    epilogue (aligned ones leave through the LDS tile as 16-byte stores): bit-identical to the
-    oracle with unit scales, biases included, over a bank whose last tile pair is half live."""
+    epilogue (aligned ones leave through the LDS tile as 16-byte stores), and fp32 activations 4
+    bytes past one take the scalar loads of the row quantizer: bit-identical to the oracle with
+    unit scales, biases included, over a bank whose last tile pair is half live."""
     rng = np.random.default_rng(7100 + type_id)
     experts, n_ids, tokens, rows, k = 3, 2, 150, 96, 256
     w = (unit_scale_mxfp4 if type_id == H.MX else unit_scale_q8)(experts, rows, k, rng)
@@ -106,9 +107,10 @@ def test_gemm_unaligned_destination_exact(gpu, orc, type_id):
     x = unit_scale_activations(tokens, k, rng).reshape(tokens, 1, k)
     bias = rng.integers(-4, 5, experts * rows).astype(np.float32)
     ref = orc.mul_mat_id(type_id, w, k, rows, experts, 0, x, 1, ids, n_ids, tokens, n_ids, bias=bias, threads=8)
-    for off in (0, 4):
-        got = H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, ids, n_ids, bias=bias, order=gpu.ORDER_FAST, dst_offset=off)
-        assert H.bits_equal(got, ref), (off, H.diff_report(got, ref))
+    for off, boff in ((0, 0), (4, 0), (0, 4), (4, 4)):
+        got = H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, ids, n_ids, bias=bias, order=gpu.ORDER_FAST,
+                           dst_offset=off, b_offset=boff)
+        assert H.bits_equal(got, ref), (off, boff, H.diff_report(got, ref))
     bank.destroy()
 
 

@@ -33,13 +33,21 @@ __device__ __forceinline__ void wave_topk_softmax(const float * logits, int n, i
     int prev_i = -1;
     float sel_v = 0.0f;   // lane j keeps pick j
     int sel_i = -1;
+    // The lane's logits (n <= 1024, checked by the launcher) stay in registers across the k
+    // rounds: one load each instead of one per round.
+    constexpr int kRegs = 16;
+    float lv[kRegs];
+#pragma unroll
+    for (int c = 0; c < kRegs; ++c) lv[c] = lane + 64 * c < n ? logits[lane + 64 * c] : 0.0f;
     for (int j = 0; j < k; ++j) {
         float best = 0.0f;
         int best_i = -1;
-        for (int i = lane; i < n; i += 64) {
-            const float v = logits[i];
+#pragma unroll
+        for (int c = 0; c < kRegs; ++c) {
+            const int i = lane + 64 * c;
+            const float v = lv[c];
             const bool after_prev = v < prev_v || (v == prev_v && i > prev_i);
-            if (after_prev && (best_i < 0 || v > best)) { best = v; best_i = i; }
+            if (i < n && after_prev && (best_i < 0 || v > best)) { best = v; best_i = i; }
         }
         for (int off = 32; off > 0; off >>= 1) {
             const float ov = __shfl_xor(best, off);

@@ -717,7 +717,7 @@ __global__ __launch_bounds__(1024) void gemm_tiles_kernel(const int32_t * counts
 
 // x86 quantize_row_q8_0 of fp32 rows into GEMM activation rows (row-major codes as f16 or int8,
 // fp16-rounded fp32 block scales, and a 0 flag: this quantizer never produces -128).
-__global__ __launch_bounds__(256) void gemm_rows_from_f32_kernel(const float * __restrict__ x, int64_t n_rows, int nb,
+__global__ __launch_bounds__(256) void gemm_rows_from_f32_kernel(const float * __restrict__ x, int vec4, int nb,
                                                                  int64_t x_stride, GemmRowLayout L, uint8_t * __restrict__ out) {
     // workgroup (row, 64-block segment); four threads per block, eight elements each
     const int64_t row = blockIdx.x;
@@ -726,8 +726,15 @@ __global__ __launch_bounds__(256) void gemm_rows_from_f32_kernel(const float * _
     const int b = live ? bq : 0;
     const int part = static_cast<int>(threadIdx.x & 3);
     float v[8];
+    const float * src = x + row * x_stride + b * 32 + part * 8;
+    if (vec4) {   // 16-byte aligned rows: two 16-byte loads per thread
+        const float4 lo = live ? *reinterpret_cast<const float4 *>(src) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        const float4 hi = live ? *reinterpret_cast<const float4 *>(src + 4) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        v[0] = lo.x, v[1] = lo.y, v[2] = lo.z, v[3] = lo.w, v[4] = hi.x, v[5] = hi.y, v[6] = hi.z, v[7] = hi.w;
+    } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = live ? x[row * x_stride + b * 32 + part * 8 + i] : 0.0f;
+        for (int i = 0; i < 8; ++i) v[i] = live ? src[i] : 0.0f;
+    }
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -1067,8 +1074,9 @@ void launch_gemm_rows_from_f32(const float * x, int64_t n_rows, int64_t k, int64
     require(k > 0 && k % 32 == 0 && n_rows > 0 && x_stride >= k && lay.nb == k / 32, "GEMM quantize shape mismatch");
     require(n_rows < (1ll << 31), "too many GEMM activation rows for one launch");
     const unsigned segments = static_cast<unsigned>((k / 32 + 63) / 64);
+    const int vec4 = reinterpret_cast<uintptr_t>(x) % 16 == 0 && x_stride % 4 == 0;
     hipLaunchKernelGGL(gemm_rows_from_f32_kernel, dim3(static_cast<unsigned>(n_rows), segments), dim3(256), 0, stream,
-                       x, n_rows, static_cast<int>(k / 32), x_stride, lay, rows);
+                       x, vec4, static_cast<int>(k / 32), x_stride, lay, rows);
     check_hip(hipGetLastError(), "GEMM quantize launch");
 }
 
