@@ -156,11 +156,14 @@ struct GemmStage {
 // wait for every such load before any LDS read it cannot prove disjoint, leaves the multi-stage
 // ring alone; the kernel waits for them explicitly (lds_dma_wait) before each barrier. The
 // compiler's own waits stay correct: loads it does not know of only make its counts stricter.
+// M0 is a register the compiler reserves; the kernels of this file use it for nothing else (no
+// v_movrel, s_sendmsg or LDS-DMA builtin: their assembly holds no other M0 access), so the
+// clobber it is told of costs nothing and -Winline-asm's caution about reserved registers does
+// not apply.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_dma_x4(const void * src, uint32_t m0) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
-}
-__device__ __forceinline__ void lds_dma_x4_s(const void * base, uint32_t off, uint32_t m0) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0) : "memory", "m0");
 }
 __device__ __forceinline__ void lds_dma_x1(const void * src, uint32_t m0) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
@@ -168,6 +171,7 @@ __device__ __forceinline__ void lds_dma_x1(const void * src, uint32_t m0) {
 __device__ __forceinline__ void lds_dma_x1_s(const void * base, uint32_t off, uint32_t m0) {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m0) : "memory", "m0");
 }
+#pragma clang diagnostic pop
 template <int N>
 __device__ __forceinline__ void lds_dma_wait() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
