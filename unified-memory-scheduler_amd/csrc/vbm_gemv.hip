@@ -186,18 +186,17 @@ __device__ __forceinline__ void q8_group(const u32x4 & c, const u32x2 & m, int b
     q8_block<MT, SLOW>(c.w, static_cast<unsigned short>(m.y >> 16), b + 3, la, lda, tok_bytes, mcount, acc);
 }
 
-// Weight groups a lane keeps in flight. The gate_up decode kernel (two workgroups per CU on most
-// CUs) streams through a 6-deep ring so compute overlaps the arrivals; the down decode kernel
-// (about 1.4 workgroups per CU) issues its whole row slice (K <= 3072 MXFP4: 11-12 groups) at
-// once; the batched kernel keeps a 4-deep ring because its per-token accumulators need the
-// registers.
+// Weight groups a lane keeps in flight. Both MXFP4 decode kernels stream through a 5-deep ring
+// so compute overlaps the arrivals (120B-shape decode, A / B depth 6 / 12: 1511-1514 tok/s, 5 / 6:
+// 1600-1618, 5 / 5: 1627-1638, 6 / 4: 1540-1561, 7 / 6: 1522-1531); the batched kernel keeps a
+// 4-deep ring because its per-token accumulators need the registers.
 template <int TYPE>
 constexpr int gate_up_depth() {
-    return TYPE == 39 ? 6 : 4;
+    return TYPE == 39 ? 5 : 4;
 }
 template <int TYPE>
 constexpr int down_depth() {
-    return TYPE == 39 ? 12 : 8;
+    return TYPE == 39 ? 5 : 8;
 }
 constexpr int kBatchDepth = 4;
 
