@@ -586,8 +586,11 @@ __device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane &
     const int tok_bytes = (copy_bytes + 15) & ~15;
     const uint8_t * la = lds_tok + static_cast<int64_t>(k) * nb * A.lay.code_entry();
     const float * lda = reinterpret_cast<const float *>(lds_tok + A.lay.da_offset());
-    // rings without the -128 slow path can be deeper within the same registers
-    constexpr int D = NEG ? (M == 1 ? 6 : kBatchDepth) : (M == 1 ? 8 : 6);
+    // Launches whose rows cannot hold -128 codes keep two groups in flight: with many workgroups
+    // per CU the memory system stays busy and the VGPRs a deeper ring would hold go to occupancy
+    // (batch 32 of the 120B shape: depth 8 / 6 (single-token / wider) 2587-2620 tok/s, 5 / 4
+    // 2677-2721, 3 / 3 2755-2800, 2 / 2 2873-2911, 1 / 1 2763-2782).
+    constexpr int D = NEG ? (M == 1 ? 6 : kBatchDepth) : 2;
     Group ring[D];
     preload_ring_buf<TYPE, D>(ring, B, nb);
     // Stage the chunk's activation rows (and their -128 flags) in LDS.
