@@ -285,6 +285,8 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
     //     a tile past the bank's rows reads the pair's first tile (its rows are never stored);
     //   - meta: lanes 0..15 of wave w load the dword of rows 16 (w & 1) .. +15 of tile w >> 1.
     const int wu = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // LDS address of the stage buffers: a generic pointer to LDS is the aperture base plus the
+    // LDS address in its low 32 bits.
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
     const uint8_t * act_src[G::ACT_DMA];
 #pragma unroll
