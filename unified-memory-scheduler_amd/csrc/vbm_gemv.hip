@@ -188,8 +188,8 @@ __device__ __forceinline__ void q8_group(const u32x4 & c, const u32x2 & m, int b
 
 // Weight groups a lane keeps in flight. Both MXFP4 decode kernels stream through a 5-deep ring
 // so compute overlaps the arrivals (120B-shape decode, A / B depth 6 / 12: 1511-1514 tok/s, 5 / 6:
-// 1600-1618, 5 / 5: 1627-1638, 6 / 4: 1540-1561, 7 / 6: 1522-1531); the batched kernel keeps a
-// 4-deep ring because its per-token accumulators need the registers.
+// 1600-1618, 5 / 5: 1627-1638, 6 / 4: 1540-1561, 7 / 6: 1522-1531); the batched kernel's depth is
+// set where it streams (gemv_chunk).
 template <int TYPE>
 constexpr int gate_up_depth() {
     return TYPE == 39 ? 5 : 4;
@@ -198,7 +198,6 @@ template <int TYPE>
 constexpr int down_depth() {
     return TYPE == 39 ? 5 : 8;
 }
-constexpr int kBatchDepth = 4;
 
 // The blocks past the last full group of a lane's row slice (nb is even: MXFP4 tail in
 // {0,2,4,6}, Q8_0 tail in {0,2}): MXFP4 keeps two blocks per code dword and two exponents per
@@ -586,11 +585,11 @@ __device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane &
     const int tok_bytes = (copy_bytes + 15) & ~15;
     const uint8_t * la = lds_tok + static_cast<int64_t>(k) * nb * A.lay.code_entry();
     const float * lda = reinterpret_cast<const float *>(lds_tok + A.lay.da_offset());
-    // Launches whose rows cannot hold -128 codes keep two groups in flight: with many workgroups
-    // per CU the memory system stays busy and the VGPRs a deeper ring would hold go to occupancy
-    // (batch 32 of the 120B shape: depth 8 / 6 (single-token / wider) 2587-2620 tok/s, 5 / 4
-    // 2677-2721, 3 / 3 2755-2800, 2 / 2 2873-2911, 1 / 1 2763-2782).
-    constexpr int D = NEG ? (M == 1 ? 6 : kBatchDepth) : 2;
+    // Two groups in flight: with many workgroups per CU the memory system stays busy and the VGPRs
+    // a deeper ring would hold go to occupancy (batch 32 of the 120B shape: depth 8 / 6 (single-
+    // token / wider) 2587-2620 tok/s, 5 / 4 2677-2721, 3 / 3 2755-2800, 2 / 2 2873-2911, 1 / 1
+    // 2763-2782); the variant with the -128 slow path spilled with its former 6 / 4-deep rings.
+    constexpr int D = 2;
     Group ring[D];
     preload_ring_buf<TYPE, D>(ring, B, nb);
     // Stage the chunk's activation rows (and their -128 flags) in LDS.
