@@ -16,7 +16,8 @@
 // MFMA 16x16x32 lane layouts (checked on the device): A: lane l holds row l%16, k = 8(l/16)..+7;
 // B: k = 8(l/16)..+7 of column l%16; D: rows 4(l/16)..+3 of column l%16. The bank's slice layout
 // puts slices 2q and 2q+1 of a block (elements 8q..8q+7) in two 16-byte group entries, which is
-// exactly lane group q's k range, so weights go from HBM to the matrix core without reshuffling.
+// exactly lane group q's k range, so a lane's A operand is two dwords of the bank as stored (the
+// staging loads only place them in LDS).
 //
 // A workgroup (4 waves) computes 64 bank rows (a tile pair) x 64 jobs of one expert; wave w owns
 // bank tile 2p + (w & 1) and jobs 32(w >> 1)..+31 as a 2x2 grid of 16x16 fragments.
