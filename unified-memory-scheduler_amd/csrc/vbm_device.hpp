@@ -27,23 +27,24 @@ __device__ __forceinline__ float glu(int activation, float g0, float u0, float a
 // tools/trace/topk-tie-probe.cpp:111-113), pick j being the best element strictly after pick j-1,
 // then ggml soft_max over the k selected values (expf(v - max), sum in double, scale by
 // (float)(1/sum)). Lane 0 writes ids[0..k) and weights[0..k). k <= 64.
+// NPL: logits per lane (n <= 64 * NPL, chosen by the launcher).
+template <int NPL>
 __device__ __forceinline__ void wave_topk_softmax(const float * logits, int n, int k, int32_t * ids, float * weights) {
     const int lane = threadIdx.x & 63;
     float prev_v = INFINITY;
     int prev_i = -1;
     float sel_v = 0.0f;   // lane j keeps pick j
     int sel_i = -1;
-    // The lane's logits (n <= 1024, checked by the launcher) stay in registers across the k
-    // rounds: one load each instead of one per round.
-    constexpr int kRegs = 16;
-    float lv[kRegs];
+    // The lane's logits stay in registers across the k rounds: one load each instead of one per
+    // round.
+    float lv[NPL];
 #pragma unroll
-    for (int c = 0; c < kRegs; ++c) lv[c] = lane + 64 * c < n ? logits[lane + 64 * c] : 0.0f;
+    for (int c = 0; c < NPL; ++c) lv[c] = lane + 64 * c < n ? logits[lane + 64 * c] : 0.0f;
     for (int j = 0; j < k; ++j) {
         float best = 0.0f;
         int best_i = -1;
 #pragma unroll
-        for (int c = 0; c < kRegs; ++c) {
+        for (int c = 0; c < NPL; ++c) {
             const int i = lane + 64 * c;
             const float v = lv[c];
             const bool after_prev = v < prev_v || (v == prev_v && i > prev_i);

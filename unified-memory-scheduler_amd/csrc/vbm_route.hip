@@ -183,12 +183,13 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float * __rest
     }
 }
 
-// One wave per token: top-k + softmax over the selected (wave_topk_softmax).
+// One wave per token: top-k + softmax over the selected (wave_topk_softmax), NPL logits per lane.
+template <int NPL>
 __global__ __launch_bounds__(64) void topk_softmax_kernel(const float * __restrict__ logits, int n_expert,
                                                           int top_k, int32_t * __restrict__ ids,
                                                           float * __restrict__ weights) {
     const int64_t t = blockIdx.x;
-    wave_topk_softmax(logits + t * n_expert, n_expert, top_k, ids + t * top_k, weights + t * top_k);
+    wave_topk_softmax<NPL>(logits + t * n_expert, n_expert, top_k, ids + t * top_k, weights + t * top_k);
 }
 
 // out[t][i] = ((w0*y0 + w1*y1) + w2*y2) + ... : ggml MUL by the weight then sequential ADD.
@@ -295,8 +296,11 @@ void launch_router(const float * router_w, const float * router_b, const float *
                            static_cast<int>(n_tokens), logits);
         check_hip(hipGetLastError(), "router logits launch");
     }
-    hipLaunchKernelGGL(topk_softmax_kernel, dim3(static_cast<unsigned>(n_tokens)), dim3(64), 0, stream, logits,
-                       static_cast<int>(n_expert), static_cast<int>(top_k), ids, weights);
+    const dim3 grid(static_cast<unsigned>(n_tokens));
+    const int ne = static_cast<int>(n_expert), tk = static_cast<int>(top_k);
+    if (n_expert <= 128) hipLaunchKernelGGL(topk_softmax_kernel<2>, grid, dim3(64), 0, stream, logits, ne, tk, ids, weights);
+    else if (n_expert <= 256) hipLaunchKernelGGL(topk_softmax_kernel<4>, grid, dim3(64), 0, stream, logits, ne, tk, ids, weights);
+    else hipLaunchKernelGGL(topk_softmax_kernel<16>, grid, dim3(64), 0, stream, logits, ne, tk, ids, weights);
     check_hip(hipGetLastError(), "top-k launch");
 }
 
