@@ -65,6 +65,34 @@ def test_gemm_integer_block_dots_exact(gpu, orc, type_id, rows, k):
 
 
 @pytest.mark.parametrize("type_id", [H.MX, H.Q8])
+def test_gemm_power_of_two_scales_exact(gpu, orc, type_id):
+    """Per-block power-of-two scales: Q8_0 weight scales 2^-22 .. 2^-20 (fp16 subnormals), MXFP4
+    exponents 2^-2 .. 1, activation scales 2^-2 .. 1. Every product and every fp32 sum is exact,
+    so the fast order must equal the oracle bit for bit; a kernel that flushed subnormal fp16
+    scales, or paired one block's scale with another block's dot, fails it."""
+    rng = np.random.default_rng(7200 + type_id)
+    experts, n_ids, tokens, rows, k = 4, 2, 160, 128, 256
+    if type_id == H.Q8:
+        w = unit_scale_q8(experts, rows, k, rng).reshape(-1, 34)
+        bits = np.array([0x0004, 0x0008, 0x0010], np.uint16)[rng.integers(0, 3, w.shape[0])]
+        w[:, 0:2] = bits.astype("<u2").view(np.uint8).reshape(-1, 2)
+    else:
+        w = unit_scale_mxfp4(experts, rows, k, rng).reshape(-1, 17)
+        w[:, 0] = rng.integers(125, 128, w.shape[0])
+    w = w.reshape(-1)
+    bank = H.make_bank(type_id, w, experts, rows, k)
+    ids = np.stack([rng.choice(experts, n_ids, replace=False) for _ in range(tokens)]).astype(np.int32)
+    x = unit_scale_activations(tokens, k, rng)
+    x *= np.repeat(np.exp2(-rng.integers(0, 3, (tokens, k // 32))), 32, axis=1).astype(np.float32)
+    x = x.reshape(tokens, 1, k)
+    got = H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, ids, n_ids, order=gpu.ORDER_FAST)
+    ref = orc.mul_mat_id(type_id, w, k, rows, experts, 0, x, 1, ids, n_ids, tokens, n_ids, threads=8)
+    assert np.any(ref != 0)
+    assert H.bits_equal(got, ref), H.diff_report(got, ref)
+    bank.destroy()
+
+
+@pytest.mark.parametrize("type_id", [H.MX, H.Q8])
 @pytest.mark.parametrize("experts,n_ids,tokens", [(2, 2, 190), (3, 2, 257), (4, 2, 300)])
 def test_gemm_multi_tile_experts_exact(gpu, orc, type_id, experts, n_ids, tokens):
     """Experts with 130..300 routed jobs run the grouped GEMM over several 64-job tiles (full ones

@@ -7,7 +7,9 @@
 //     exact in fp32 whatever the order inside the matrix core.
 //   - Q8_0 weights: v_mfma_i32_16x16x32_i8 on the int8 codes (exact int32).
 // The block dot is then scaled (MXFP4: ldexp(d_act, e - 128); Q8_0: fp16(d_w) * d_act, the
-// CPU's own products) and accumulated in fp32 block after block. That accumulation order is not
+// CPU's own products; in the Q8_0 loop those products come from a v_mfma_f32_16x16x16_f16 per
+// fragment whose only nonzero terms are d_w and d_act, exact in fp32) and accumulated in fp32
+// block after block. That accumulation order is not
 // the CPU's 8-lane chains, so outputs agree with the reference within fp32 rounding (the
 // tolerance-checked order), while every integer block dot is bit-exact. The x86 VPSIGNB corner
 // (activation code -128 against a negative weight) is applied as an exact correction on rows
@@ -35,6 +37,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4g __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2g __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_g __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmThreads = 256;
 constexpr int kJobTile = 64;
@@ -457,6 +460,46 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                             const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_op[i], bv, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
                             for (int j = 0; j < 4; ++j) acc[i][jh][j] = __builtin_fmaf(da, d[j], acc[i][jh][j]);
+                        }
+                    }
+                }
+            } else if constexpr (TYPE == 8 && !decltype(slow_c)::value) {
+                // Q8_0: the scale products fp16(d_w) * d_act of a 16 x 16 output fragment come
+                // from one f16 MFMA per block: A holds d_w of the fragment's 16 rows at k = bb
+                // (lanes 0..15, zero elsewhere), B the 16 jobs' d_act at k = bb. Each output is
+                // the exact fp32 product of two fp16 values (11-bit significands) plus zeros:
+                // the value the per-output VALU product gives, off the vector ALU.
+                const unsigned sel[2] = {lane < 16 ? 0x0000FFFFu : 0u, lane < 16 ? 0xFFFF0000u : 0u};
+                unsigned dw_row[2], da_pk[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) dw_row[i] = *reinterpret_cast<const unsigned *>(ma_lds + ab * G::STAGE + i * 16 * 4);
+#pragma unroll
+                for (int jh = 0; jh < 2; ++jh) {
+                    // d_act holds fp16 values, so the packing conversion is exact
+                    const float * dp = d_lds + ab * (G::STAGE / 4) + 16 * jh * CB;
+                    da_pk[jh] = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(dp[0], dp[1]));
+                }
+#pragma unroll
+                for (int bb = 0; bb < CB; ++bb) {
+                    long a_op[2];
+                    half4_g as[2];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        a_op[i] = static_cast<long>(static_cast<uint64_t>(w0[i][bb]) | (static_cast<uint64_t>(w1[i][bb]) << 32));
+                        as[i] = __builtin_bit_cast(half4_g, u32x2g{dw_row[i] & sel[bb], 0u});
+                    }
+#pragma unroll
+                    for (int jh = 0; jh < 2; ++jh) {
+                        if (!frag_live[jh]) continue;
+                        const long bv = *reinterpret_cast<const long *>(st + aoff[jh][bb]);
+                        const half4_g bs = __builtin_bit_cast(half4_g, u32x2g{da_pk[jh] & sel[bb], 0u});
+#pragma unroll
+                        for (int i = 0; i < 2; ++i) {
+                            const i32x4 di = __builtin_amdgcn_mfma_i32_16x16x32_i8(a_op[i], bv, i32x4{0, 0, 0, 0}, 0, 0, 0);
+                            const f32x4 sc = __builtin_amdgcn_mfma_f32_16x16x16f16(as[i], bs, f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)
+                                acc[i][jh][j] = __builtin_fmaf(sc[j], static_cast<float>(di[j]), acc[i][jh][j]);
                         }
                     }
                 }
