@@ -5,6 +5,8 @@ different order than the CPU's 8-lane chains. With unit scales all fp32 sums are
 so there the GEMM must reproduce the oracle bit for bit (including the x86 VPSIGNB correction for
 activation code -128); with the benchmark's value distributions the outputs must be within 1e-3
 max relative error and cosine >= 0.99999 of the oracle, with expert ids identical."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -242,6 +244,49 @@ def test_prefill_layer_q8_0_config3_full_2048_tokens(gpu, orc):
     assert per_expert.max() > 128
     assert max_rel <= 1e-3 and cos >= 0.99999
     layer.destroy()
+
+
+def test_prefill_layer_graph_replays_match_eager(gpu):
+    """The fast-order layer (top-k, grouping, both grouped GEMMs, combine) captured as one HIP
+    graph: every replay gives the eager call's ids and output bits, with the output cleared before
+    it and an eager layer call on other inputs through the same workspace after it."""
+    layer = Layer(gpu, H.Q8, 2048, 768, 128, 8, seed=3131, router=False, biases=False, activation=0,
+                  order=gpu.ORDER_FAST)
+    T, Hd, K = 512, 2048, 8
+    x = gpu.synth_normal(3131, 6, 0, T * Hd).reshape(T, Hd)
+    logits = gpu.synth_normal(3131, 7, 0, T * 128).reshape(T, 128)
+    ref, ref_ids, _ = layer.forward_gpu(x, logits)
+    d = layer.desc()
+    ws = C.c_size_t()
+    gpu.call("vbm_moe_layer_workspace", C.byref(d), T, C.byref(ws))
+    work = gpu.DeviceBuffer(ws.value)
+    dx, dl = gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer.from_array(logits)
+    dx2 = gpu.DeviceBuffer.from_array(gpu.synth_normal(3131, 8, 0, T * Hd))
+    dl2 = gpu.DeviceBuffer.from_array(gpu.synth_normal(3131, 9, 0, T * 128))
+    out, ids, out2 = gpu.DeviceBuffer(4 * T * Hd), gpu.DeviceBuffer(4 * T * K), gpu.DeviceBuffer(4 * T * Hd)
+    stream = C.c_void_p()
+    gpu.call("vbm_stream_create", C.byref(stream))
+    s = stream.value
+    g = C.c_void_p()
+    gpu.call("vbm_graph_begin_capture", s)
+    gpu.call("vbm_moe_layer_forward", C.byref(d), dx.ptr, dl.ptr, T, out.ptr, ids.ptr, None, work.ptr, ws.value, s)
+    gpu.call("vbm_graph_end_capture", s, C.byref(g))
+    try:
+        for rep in range(3):
+            gpu.call("vbm_memset", out.ptr, 0, 4 * T * Hd, s)
+            gpu.call("vbm_graph_launch", g.value, s)
+            gpu.call("vbm_stream_synchronize", s)
+            print(f"[prefill graph replay {rep}]", flush=True)
+            assert np.array_equal(ids.download(np.int32, (T, K)), ref_ids)
+            got = out.download(np.float32, (T, Hd))
+            assert H.bits_equal(got, ref), H.diff_report(got, ref)
+            gpu.call("vbm_moe_layer_forward", C.byref(d), dx2.ptr, dl2.ptr, T, out2.ptr, None, None, work.ptr,
+                     ws.value, s)
+            gpu.call("vbm_stream_synchronize", s)
+    finally:
+        gpu.call("vbm_graph_destroy", g.value)
+        gpu.call("vbm_stream_destroy", s)
+        layer.destroy()
 
 
 def test_prefill_layer_mxfp4_config1_shape(gpu, orc):
