@@ -259,11 +259,13 @@ def test_router_ids_exact(gpu, orc):
     assert di.download(np.int32, 4).tolist() == [1, 2, 4, 7]
 
 
-@pytest.mark.parametrize("n_expert", [300, 1024])
+@pytest.mark.parametrize("n_expert", [100, 128, 200, 256, 257, 300, 1024])
 def test_router_topk_given_logits_canonical_order(gpu, n_expert):
     """Top-k of given logits (the router takes up to 1024 experts and refuses more): ids in the
     canonical order (value descending, lower index first on ties), including rows full of ties and
-    a row whose winners sit in the last lanes; weights are the softmax of the picks within 1e-6."""
+    a row whose winners sit in the last lanes; weights are the softmax of the picks within 1e-6.
+    The expert counts cover each register width of the kernel (2, 4 and 16 logits per lane) at
+    and around its limits."""
     rng = np.random.default_rng(300 + n_expert)
     tokens, top_k = 24, 8
     logits = rng.standard_normal((tokens, n_expert)).astype(np.float32)
