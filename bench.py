@@ -724,6 +724,9 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--experts", type=int, default=128)
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph")
+    ap.add_argument("--decode-schedule", choices=("linked", "two-kernel"), default="linked",
+                    help="linked: one launch per layer boundary (down tiles of layer l-1 + gate_up tiles of "
+                         "layer l, joined by device-side flags); two-kernel: kernels A and B per layer")
     ap.add_argument("--kernel-reps", type=int, default=20, help="launches per layer in the kernel timing pass")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-seconds-1core", type=float, default=8.0)
@@ -772,6 +775,7 @@ def main() -> int:
     log(f"device: {vb.device_name(0)}")
     H, I, E, K, L, T = 2880, 2880, args.experts, 4, args.layers, args.tokens
     stack = Stack(L, E, H, I, K, T)
+    vb.call("vbm_decode_plan_set_linked", stack.plan, 1 if args.decode_schedule == "linked" else 0)
     n_steps = args.warmup + args.steps
     logits_host = vb.synth_normal(SEED, 7, 0, n_steps * L * T * E).reshape(n_steps, L, T, E)
     logits_all = vb.DeviceBuffer.from_array(logits_host)

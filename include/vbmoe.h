@@ -174,8 +174,9 @@ vbm_status vbm_quantize_q8_0(const float * x, int64_t n_rows, int64_t k, int64_t
  * a routed expert whose expert_to_slot entry is -1 (when no host copy was given to check), come
  * out NaN: the reference asserts on both (hybrid-experts.patch:622; quantized_cuda.cu:224-227).
  * Device scratch: the library keeps one per (device, stream), grown stream-ordered only when a
- * call needs more than any earlier call on that stream, so steady-state calls allocate nothing
- * (a call under graph capture must not be the one that grows it); vbm_stream_destroy releases it. */
+ * call needs more than any earlier call on that stream, so steady-state calls allocate nothing;
+ * a call under graph capture that would grow it fails with VBM_ERR_INVALID_ARGUMENT (run it once
+ * on the stream before capturing); vbm_stream_destroy releases it. */
 vbm_status vbm_mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot,
                           const int32_t * expert_to_slot_host, int64_t n_as,
                           int b_type, const void * b, int64_t b_ne1,
@@ -336,6 +337,19 @@ vbm_status vbm_decode_step(vbm_decode_plan * plan, const float * x, const float 
  * launches stream the same bytes. */
 vbm_status vbm_decode_kernel(vbm_decode_plan * plan, int64_t layer, int which, const float * x,
                              const float * logits, void * stream);
+/* Linked step (no reference counterpart: a launch schedule of the same arithmetic), opt-in for
+ * MXFP4 layers with hidden = intermediate = 2880 and at most 128 experts: a step runs
+ * n_layers + 1 launches, launch j holding the down tiles of layer j - 1 and the gate_up tiles of
+ * layer j, which wait on device-side per-tile flags for their input instead of a kernel boundary.
+ * Outputs are bit-identical to the two-kernel step (the default, which is faster on MI355X: the
+ * flag round trips queue behind the weight streams). events then holds [n_layers + 1][2] records
+ * around the launches. set_linked(plan, 1) fails with VBM_ERR_INVALID_ARGUMENT for other shapes. */
+vbm_status vbm_decode_plan_set_linked(vbm_decode_plan * plan, int linked);
+vbm_status vbm_decode_plan_get_linked(const vbm_decode_plan * plan, int * linked);
+/* Synchronizes the device, then reports and clears the device waits of linked steps that timed
+ * out since the last check (*timeouts, optional): VBM_ERR_RUNTIME if any did, since that step's
+ * outputs are unspecified. A wait times out after about 0.17 s. */
+vbm_status vbm_decode_plan_check(vbm_decode_plan * plan, int64_t * timeouts);
 
 /* ----------------------------------------------------------------------------------------------
  * Causal expert admission over one shared pool of n_slots expert slots serving n_layers routed

@@ -124,6 +124,59 @@ def test_expert_branch_nodes_match_oracle_layer(gpu, orc, case):
         layer.up_bank.destroy()
 
 
+def test_expert_branch_nodes_under_graph_capture(gpu, orc):
+    """The expert-branch node list captured as a HIP graph. On a fresh stream the capture is refused
+    (VBM_ERR_INVALID_ARGUMENT: MUL_MAT_ID would have to grow the stream's scratch inside the graph);
+    after one eager run on that stream the capture succeeds, and every replay, with eager work and
+    synchronizations between them, gives the eager bits, which equal the oracle's layer."""
+    from test_gpu_layer import Layer
+    vb = gpu
+    layer = Layer(vb, H.MX, 512, 256, 16, 4, seed=94, router=False, biases=True, activation=vb.ACT_SWIGLU_OAI)
+    T = 6
+    x = vb.synth_normal(94, 6, 0, T * layer.H).reshape(T, layer.H)
+    logits = vb.synth_normal(94, 7, 0, T * layer.E).reshape(T, layer.E)
+    ref = layer.forward_cpu(orc, x, logits)
+    dx, dids = vb.DeviceBuffer.from_array(x), vb.DeviceBuffer.from_array(np.ascontiguousarray(ref["ids"], np.int32))
+    dw = vb.DeviceBuffer.from_array(np.ascontiguousarray(ref["weights"], np.float32))
+    g = Graph(vb)
+    final, bufs = build_expert_branch(vb, g, layer, dx, dids, layer.K, dw, T, True)
+    st = C.c_void_p()
+    vb.call("vbm_stream_create", C.byref(st))
+    s = st.value
+    graph = C.c_void_p()
+    vb.call("vbm_graph_begin_capture", s)
+    with pytest.raises(vb.VbmError) as err:
+        g.compute(order=vb.ORDER_EXACT, stream=s)
+    assert err.value.status == 1, str(err.value)      # VBM_ERR_INVALID_ARGUMENT
+    try:
+        vb.call("vbm_graph_end_capture", s, C.byref(graph))
+    finally:
+        if graph.value:
+            vb.call("vbm_graph_destroy", graph.value)
+    # one eager run grows the stream's scratch; the capture then allocates nothing
+    g.compute(order=vb.ORDER_EXACT, stream=s)
+    vb.call("vbm_stream_synchronize", s)
+    eager = download(vb, final.data, (T, layer.H))
+    assert H.bits_equal(eager, ref["out"]), H.diff_report(eager, ref["out"])
+    graph = C.c_void_p()
+    vb.call("vbm_graph_begin_capture", s)
+    g.compute(order=vb.ORDER_EXACT, stream=s)
+    vb.call("vbm_graph_end_capture", s, C.byref(graph))
+    try:
+        for _ in range(3):
+            vb.call("vbm_memset", final.data, 0, 4 * T * layer.H, s)
+            vb.call("vbm_graph_launch", graph.value, s)
+            vb.call("vbm_stream_synchronize", s)
+            got = download(vb, final.data, (T, layer.H))
+            assert H.bits_equal(got, eager), H.diff_report(got, eager)
+            g.compute(order=vb.ORDER_EXACT)            # eager work on another stream between replays
+            vb.call("vbm_stream_synchronize", None)
+    finally:
+        vb.call("vbm_graph_destroy", graph.value)
+        vb.call("vbm_stream_destroy", s)
+    layer.destroy()
+
+
 def weighted_branch(vb, g, new, x, ids, bias_ids, weights, gu_as, gu_bias, dn_as, dn_bias, dims):
     """MUL_MAT_ID -> ADD_ID -> split views -> GLU (swiglu_oai) -> MUL_MAT_ID -> ADD_ID -> MUL by the
     weights, on a fused gate_up expert tensor (the reference's expert_branch, weights after the FFN)."""

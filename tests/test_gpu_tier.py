@@ -65,13 +65,16 @@ def oracle_chain(orc, host, type_id, act, x, logits_t, H, I, E, K):
 @pytest.mark.parametrize("type_id,policy,margin,mode", [
     (39, 0, 4, "sync"), (39, 1, 1, "sync"), (8, 2, 2, "sync"),
     (39, 0, 4, "deferred"), (39, 1, 1, "deferred"), (8, 2, 2, "graph"), (39, 1, 1, "graph"),
+    (39, 0, 4, "graph_nosync"), (39, 1, 1, "graph_nosync"),
 ])
 def test_tier_matches_resident_plan(gpu, orc, type_id, policy, margin, mode):
     """Synchronous mode (per-layer admission and staging), deferred mode (no host wait inside a
     step: misses read from the pinned host copy, admission at the step boundary) and deferred mode
     with the step's device part captured once as a HIP graph and replayed per token: every token
     bit-identical to the resident plan and to the oracle chain, counters equal to the Python
-    admission fed the same routes."""
+    admission fed the same routes. graph_nosync replays token after token with no host
+    synchronization between them (each begin's own wait on the previous replay's hand-off is
+    what orders the admissions), copying every token's logits in and outputs out on the stream."""
     vb = gpu
     L, E, K, H, I, slots = 3, 16, 4, 256, 256, 4 + 9
     act = vb.ACT_SWIGLU_OAI if type_id == 39 else vb.ACT_SILU
@@ -118,7 +121,7 @@ def test_tier_matches_resident_plan(gpu, orc, type_id, policy, margin, mode):
     stream, graph = None, None
     if mode != "sync":
         vb.call("vbm_tier_set_deferred", tier.value, 1)
-    if mode == "graph":
+    if mode in ("graph", "graph_nosync"):
         st_ = C.c_void_p()
         vb.call("vbm_stream_create", C.byref(st_))
         stream = st_.value
@@ -127,10 +130,27 @@ def test_tier_matches_resident_plan(gpu, orc, type_id, policy, margin, mode):
         vb.call("vbm_tier_step_enqueue", tier.value, x.ptr, dl.ptr, o2.ptr, i2.ptr, stream)
         vb.call("vbm_graph_end_capture", stream, C.byref(g))
         graph = g.value
+    if mode == "graph_nosync":
+        tok_bytes, ids_bytes = logits[0].nbytes, 4 * L * K
+        dl_all = vb.DeviceBuffer.from_array(np.ascontiguousarray(logits))
+        out_all, ids_all = vb.DeviceBuffer(4 * H * tokens), vb.DeviceBuffer(ids_bytes * tokens)
+        for t in range(tokens):
+            vb.call("vbm_tier_step_begin", tier.value)
+            vb.call("vbm_memcpy_d2d", dl.ptr, dl_all.ptr + t * tok_bytes, tok_bytes, stream)
+            vb.call("vbm_graph_launch", graph, stream)
+            vb.call("vbm_memcpy_d2d", out_all.ptr + t * 4 * H, o2.ptr, 4 * H, stream)
+            vb.call("vbm_memcpy_d2d", ids_all.ptr + t * ids_bytes, i2.ptr, ids_bytes, stream)
+        vb.call("vbm_stream_synchronize", stream)
+        tier_out = out_all.download(np.float32, (tokens, H))
+        tier_ids = ids_all.download(np.int32, (tokens, L, K))
     for t in range(tokens):
         dl.upload(logits[t])
         vb.call("vbm_decode_step", plan.value, x.ptr, dl.ptr, o1.ptr, i1.ptr, None, None, None)
-        if mode == "graph":
+        if mode == "graph_nosync":
+            vb.call("vbm_stream_synchronize", None)
+            o2.upload(tier_out[t])
+            i2.upload(tier_ids[t])
+        elif mode == "graph":
             vb.call("vbm_tier_step_begin", tier.value)
             vb.call("vbm_graph_launch", graph, stream)
             vb.call("vbm_stream_synchronize", stream)

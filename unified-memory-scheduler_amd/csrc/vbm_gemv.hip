@@ -1102,6 +1102,363 @@ __global__ __launch_bounds__(kDownThreads) void decode_down_kernel(DecodeDownArg
     }
 }
 
+// ------------------------------------------------------------------------ linked decode layers
+// One launch per layer boundary: launch j runs the down tiles of layer j - 1 (workgroups
+// [0, n_down)) and the gate_up tiles of layer j (the rest), so the two weight streams overlap and
+// a step takes L + 1 launches instead of 2L + 1. Every layer routes on its given logits, so a
+// gate_up tile knows its expert at launch and issues its whole weight tile before its input
+// exists. The input is published tile by tile by the down tiles of the same launch:
+//   - a down tile writes its 32 rows of y[rank] with agent-coherent stores (sc1: written through
+//     past the XCD's L2, read back the same way by any XCD), waits for them, then bumps the
+//     tile's arrival counter (top_k arrivals per launch: no counter is contended);
+//   - the last arriver of a tile combines the top_k ranks of its 32 rows in rank order (ggml MUL
+//     by the routing weight, then ADD), quantizes that 32-element block of the next layer's input
+//     (x86 quantize_row_q8_0) into the shared activation row, waits for those stores and sets the
+//     tile's flag to the step's epoch, in kLinkCopies copies (one per group of pollers);
+//   - in a gate_up workgroup a fifth wave, which issues no weight loads (vector loads retire in
+//     order per wave, so a poll queued behind a weight stream would wait for all of it), polls
+//     the flags with a bounded wait, copies the activation row into LDS and joins the scale-table
+//     build while the four compute waves' weights are landing.
+// No release/acquire fence is used: at agent scope those write back / invalidate a whole L2.
+// Forward progress: down workgroups never wait and precede every gate_up workgroup in dispatch
+// order. A gate_up wait that outlives kLinkPollRounds poll rounds sets the error word and leaves
+// that workgroup's outputs unspecified instead of spinning, so every wave exits.
+// The last launch (no gate_up part) combines into the step output and advances the epoch.
+constexpr int kLinkThreads = 320;                  // 4 compute waves + 1 helper wave
+constexpr int kLinkCopies = 8;
+constexpr int kLinkCopyStride = 1152;              // u32 between flag copies (4.5 KiB)
+// Poll rounds before a wait gives up: each round sleeps 4 x 64 cycles and waits for two loads, so
+// this is more than 0.1 s. (No timer is read: s_memrealtime goes through the memory interface
+// and waits behind the weight streams under full HBM load.)
+constexpr uint32_t kLinkPollRounds = 1u << 20;
+
+struct LinkArgs {
+    int n_down, n_gate_up;      // workgroups of each role in this launch
+    int n_expert, top_k;
+    // down tiles of layer l - 1
+    const uint8_t * dn_bank;
+    Shape dn_shape;
+    XrowLayout dn_lay;          // down activation row (nb = intermediate / 32)
+    const float * dn_act_f;     // [top_k][intermediate] GLU outputs of layer l - 1
+    const int32_t * dn_ids;     // [top_k]
+    const int32_t * dn_slots;   // [top_k]
+    const float * dn_w;         // [top_k]
+    const float * dn_bias;      // [n_expert][hidden] or null
+    float * y;                  // [top_k][hidden], agent-coherent accesses only
+    uint32_t * counters;        // [hidden / 32] arrival counters of layer l - 1
+    float * out;                // step output [hidden] (last launch), else null
+    // the next-layer input row, published by the last arrivers and read by the gate_up tiles
+    uint8_t * xq;               // gate_up activation layout, agent-coherent accesses only
+    uint32_t * flags;           // [kLinkCopies][kLinkCopyStride] flags of layer l
+    // gate_up tiles of layer l
+    const uint8_t * gu_bank;
+    Shape gu_shape;
+    XrowLayout gu_lay;
+    const int32_t * expert_to_slot;
+    const float * logits;       // [n_expert]
+    const float * x_in;         // layer input (first launch), else null
+    const float * gu_bias;      // [n_expert][2 * intermediate] or null
+    float * act_f;              // [top_k][intermediate] GLU outputs of layer l
+    int32_t * route_ids;
+    float * route_w;
+    int32_t * route_slots;
+    int activation;
+    float alpha, limit;
+    uint32_t * epoch;           // step counter: flags of this step hold its value
+    int advance_epoch;          // last launch: workgroup 0 advances it
+    uint32_t * error;           // set to 1 when a wait times out
+};
+
+// Groups of a lane's row slice held in flight from the start: the whole slice.
+constexpr int link_ring_depth(int nb) { return nb / 8; }
+
+template <class T>
+__device__ __forceinline__ T coherent_load(const T * p) {
+    return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ void coherent_store(T * p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Every store this wave issued has been acknowledged (for agent-coherent stores: performed at the
+// point where every XCD reads them); the "memory" clobber keeps the compiler from moving memory
+// operations across it.
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Helper wave: x86 Q8_0 of a row of nb blocks (fp32, global) into the LDS activation row, eight
+// elements per lane and round (thread t = 4b + part of quantize_x8), every load issued first.
+template <int TYPE, int NB>
+__device__ __forceinline__ void helper_quantize_row(const float * src, uint8_t * act, const XrowLayout & L) {
+    constexpr int R = (NB * 4 + 63) / 64;
+    const int lane = threadIdx.x & 63;
+    float xv[R][8];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int t = lane + 64 * i;
+        const int e0 = t < NB * 4 ? t * 8 : 0;
+        const float4 lo = *reinterpret_cast<const float4 *>(src + e0);
+        const float4 hi = *reinterpret_cast<const float4 *>(src + e0 + 4);
+        xv[i][0] = lo.x; xv[i][1] = lo.y; xv[i][2] = lo.z; xv[i][3] = lo.w;
+        xv[i][4] = hi.x; xv[i][5] = hi.y; xv[i][6] = hi.z; xv[i][7] = hi.w;
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int t = lane + 64 * i;
+        if (t < NB * 4) quantize_x8<TYPE>(xv[i], t, act, L, NB);   // quads of lanes stay whole: 4 | NB * 4
+    }
+}
+
+// Helper wave: waits until the n tile flags of this copy hold `epoch` (bounded), then copies the
+// published activation row (codes and block scales) into LDS.
+template <int NB>
+__device__ __forceinline__ void helper_fetch_row(const LinkArgs & A, uint32_t epoch, uint8_t * act) {
+    const int lane = threadIdx.x & 63;
+    const int n = NB;                                 // one flag per 32-element block
+    const uint32_t * f = A.flags + (blockIdx.x % kLinkCopies) * kLinkCopyStride;
+    const int i0 = lane < n ? lane : n - 1, i1 = lane + 64 < n ? lane + 64 : n - 1;
+    for (uint32_t round = 0;; ++round) {
+        const uint32_t v0 = coherent_load(f + i0), v1 = coherent_load(f + i1);
+        if (__ballot(v0 != epoch || v1 != epoch) == 0) break;
+        if (round == kLinkPollRounds) {
+            if (lane == 0) coherent_store(A.error, 1u);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(4);
+    }
+    asm volatile("" ::: "memory");
+    constexpr int kWords = NB * 68 / 8;               // NB x (64 B of f16 codes + 4 B scale)
+    constexpr int W = (kWords + 127) / 128;           // two batches of W words per lane
+    const uint64_t * src = reinterpret_cast<const uint64_t *>(A.xq);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        uint64_t v[W];
+#pragma unroll
+        for (int i = 0; i < W; ++i) {
+            const int w = lane + 64 * (h * W + i);
+            v[i] = coherent_load(src + (w < kWords ? w : 0));
+        }
+#pragma unroll
+        for (int i = 0; i < W; ++i) {
+            const int w = lane + 64 * (h * W + i);
+            if (w < kWords) reinterpret_cast<uint64_t *>(act)[w] = v[i];
+        }
+    }
+}
+
+// Last arriver of down tile `blk`: lanes 0..31 of wave 0 hold the combined next-layer input of
+// the tile's 32 rows, i.e. block blk. x86 Q8_0 of the block (the quantize_x8 arithmetic), the
+// codes and scale stored into the shared row, then the flags.
+__device__ __forceinline__ void publish_block(float x, int blk, const LinkArgs & A, uint32_t epoch) {
+    const int lane = threadIdx.x & 63;
+    const XrowLayout & L = A.gu_lay;
+    const float amax = half_wave_max(lane < 32 ? fmaxf(0.0f, fabsf(x)) : 0.0f);
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    float q = rintf(x * id);
+    q = q > 127.0f ? 127.0f : (q < -128.0f ? -128.0f : q);
+    const unsigned h = __builtin_bit_cast(unsigned short, static_cast<_Float16>(q));
+    const unsigned h1 = __shfl_down(h, 1), h2 = __shfl_down(h, 2), h3 = __shfl_down(h, 3);
+    const uint64_t packed = static_cast<uint64_t>(h | (h1 << 16)) | (static_cast<uint64_t>(h2 | (h3 << 16)) << 32);
+    if (lane < 32 && (lane & 3) == 0)
+        coherent_store(reinterpret_cast<uint64_t *>(A.xq + (static_cast<int64_t>(lane >> 2) * L.nb + blk) * 8), packed);
+    if (lane == 0)
+        coherent_store(reinterpret_cast<float *>(A.xq + L.da_offset()) + blk, static_cast<float>(static_cast<_Float16>(d)));
+    wait_stores();
+    if (lane < kLinkCopies) coherent_store(A.flags + lane * kLinkCopyStride + blk, epoch);
+}
+
+// Down tile (rank, tile) of layer l - 1: as kernel B, with the whole tile preloaded, the GLU row
+// quantized by the helper wave, and the y rows published for the last arriver.
+template <int TYPE, int NB>
+__device__ __forceinline__ void link_down(const LinkArgs & A, int wg, uint8_t * lds_dyn, float (&red)[8][32]) {
+    constexpr int G = link_ring_depth(NB);
+    const Shape S = A.dn_shape;
+    const int tiles = S.rows / 32;
+    const int rank = wg / tiles, tile = wg - rank * tiles;
+    const int mbytes = meta_tile_bytes<TYPE>(NB);
+    uint8_t * lmeta = lds_dyn;
+    uint8_t * act = lmeta + mbytes;
+    float * lscale = reinterpret_cast<float *>(act + ((A.dn_lay.flag_offset() + 15) & ~15ll));
+    const int tid = threadIdx.x, lane = tid & 63, r = lane & 31;
+    const bool compute = tid < kDownThreads;                // waves 0..3; wave 4 is the helper
+    const int k = (tid >> 6) * 2 + (lane >> 5);
+    const int row = tile * 32 + r;
+    const int expert = as_const<int32_t>(A.dn_ids)[rank];
+    const int slot = as_const<int32_t>(A.dn_slots)[rank];
+    const bool slot_ok = slot >= 0 && slot < S.n_slots;
+    const uint8_t * slot_base = A.dn_bank + (slot_ok ? static_cast<size_t>(slot) * S.slot_bytes : 0);
+    const uint8_t * codes_tile = slot_base + static_cast<size_t>(tile) * 32 * NB * 16;
+    Group ring[G];
+    Tail tl;
+    float bias_v = 0.0f;
+    if (compute) {
+        u32x4 mst[2];
+        load_meta<kDownThreads>(mst, slot_base + S.codes_bytes + static_cast<size_t>(tile) * mbytes, mbytes);
+        preload_ring<TYPE, G, true>(ring, codes_tile, nullptr, k, r, NB, true);
+        preload_tail<TYPE, true>(tl, codes_tile, nullptr, k, r, NB, true);
+        if (k == 0 && A.dn_bias) bias_v = A.dn_bias[static_cast<size_t>(expert) * S.rows + row];
+        store_meta<kDownThreads>(mst, lmeta, mbytes);
+    } else {
+        helper_quantize_row<TYPE, NB>(A.dn_act_f + static_cast<size_t>(rank) * NB * 32, act, A.dn_lay);
+    }
+    __syncthreads();
+    build_scales<TYPE, kLinkThreads, 1>(lscale, lmeta, reinterpret_cast<const float *>(act + A.dn_lay.da_offset()), NB, mbytes);
+    __syncthreads();
+    if (compute) {
+        float acc[2] = {0.0f, 0.0f};
+        decode_stream<TYPE, G, NB>(ring, tl, codes_tile, k, r, NB, false,
+                                   act + static_cast<int64_t>(k) * NB * A.dn_lay.code_entry(), lscale + r * 4, acc);
+        red[k][r] = acc[0] + acc[1];
+    }
+    __syncthreads();
+    if (tid >= 64) return;
+    // wave 0: this rank's rows, then the arrival count of the tile
+    if (lane < 32) {
+        const float * l = &red[0][r];
+        const float s0 = l[4 * 32] + l[0], s1 = l[5 * 32] + l[1 * 32];
+        const float s2 = l[6 * 32] + l[2 * 32], s3 = l[7 * 32] + l[3 * 32];
+        float v = (s0 + s2) + (s1 + s3);
+        if (A.dn_bias) v = v + bias_v;
+        if (!slot_ok) v = __builtin_nanf("");      // expert not resident in this bank: loud output
+        coherent_store(A.y + static_cast<size_t>(rank) * S.rows + row, v);
+    }
+    wait_stores();
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(A.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __shfl(old, 0);
+    const uint32_t K = static_cast<uint32_t>(A.top_k);
+    if (old % K != K - 1) return;
+    // last arriver: every rank's rows of this tile are stored; combine in rank order
+    constexpr int kBatch = 8;
+    float x = 0.0f;
+    for (int j0 = 0; j0 < A.top_k; j0 += kBatch) {
+        float yv[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+            yv[j] = lane < 32 && j0 + j < A.top_k ? coherent_load(A.y + static_cast<size_t>(j0 + j) * S.rows + row) : 0.0f;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+            if (j0 + j < A.top_k) {
+                const float term = yv[j] * A.dn_w[j0 + j];
+                x = j0 + j == 0 ? term : x + term;
+            }
+    }
+    if (A.out) {
+        if (lane < 32) A.out[row] = x;
+    } else {
+        publish_block(x, tile, A, coherent_load(A.epoch));
+    }
+}
+
+// Gate_up tile (rank, tile) of layer l: as kernel A, with the whole tile preloaded and the input
+// taken from the published row (or quantized from x_in in the first launch) by the helper wave.
+template <int TYPE, int NPL, int NB, bool FIRST>
+__device__ __forceinline__ void link_gate_up(const LinkArgs & A, int wg, uint8_t * lds_dyn, float (&red)[8][32]) {
+    constexpr int G = link_ring_depth(NB);
+    const Shape S = A.gu_shape;
+    const int tiles = S.rows / 32;
+    const int rank = wg / tiles, tile = wg - rank * tiles;
+    const int mbytes = meta_tile_bytes<TYPE>(NB);
+    uint8_t * lmeta = lds_dyn;
+    uint8_t * act = lmeta + mbytes;
+    float * lscale = reinterpret_cast<float *>(act + ((A.gu_lay.flag_offset() + 15) & ~15ll));
+    const int tid = threadIdx.x, lane = tid & 63, r = lane & 31;
+    const bool compute = tid < kDownThreads;                // waves 0..3; wave 4 is the helper
+    const int k = (tid >> 6) * 2 + (lane >> 5);
+    const int n = A.n_expert;
+    float sel_v = 0.0f;
+    int sel_i = -1;
+    bool slot_ok = false;
+    float bias_v = 0.0f;
+    Group ring[G];
+    Tail tl;
+    const uint8_t * codes_tile = A.gu_bank;
+    if (compute) {
+        // routing keys and slots of experts lane + 64 i (unconditional, clamped loads), this
+        // wave's top-k, then the pick's whole weight tile
+        float lg[NPL];
+        int sl[NPL];
+        const int32_t * map = A.expert_to_slot;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            const int c = lane + 64 * i;
+            lg[i] = A.logits[c < n ? c : 0];
+        }
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            const int c = lane + 64 * i;
+            sl[i] = map ? map[c < n ? c : 0] : c;
+        }
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) lg[i] = route_key(lg[i]);
+        wave_topk_regs<NPL>(lg, n, A.top_k, sel_v, sel_i);
+        const int expert = __builtin_amdgcn_readlane(sel_i, rank);
+        int sv = sl[0];
+#pragma unroll
+        for (int i = 1; i < NPL; ++i)
+            if ((expert >> 6) == i) sv = sl[i];
+        const int slot = __builtin_amdgcn_readlane(sv, expert & 63);
+        slot_ok = slot >= 0 && slot < S.n_slots;
+        const uint8_t * slot_base = A.gu_bank + (slot_ok ? static_cast<size_t>(slot) * S.slot_bytes : 0);
+        codes_tile = slot_base + static_cast<size_t>(tile) * 32 * NB * 16;
+        u32x4 mst[2];
+        load_meta<kDownThreads>(mst, slot_base + S.codes_bytes + static_cast<size_t>(tile) * mbytes, mbytes);
+        preload_ring<TYPE, G, true>(ring, codes_tile, nullptr, k, r, NB, true);
+        preload_tail<TYPE, true>(tl, codes_tile, nullptr, k, r, NB, true);
+        const int grow = static_cast<int>(ggml_row(static_cast<int64_t>(tile) * 32 + r, S.rows, S.interleave));
+        if (k == 0 && A.gu_bias) bias_v = A.gu_bias[static_cast<size_t>(expert) * S.rows + grow];
+        store_meta<kDownThreads>(mst, lmeta, mbytes);
+    } else {
+        if (FIRST) helper_quantize_row<TYPE, NB>(A.x_in, act, A.gu_lay);
+        else helper_fetch_row<NB>(A, coherent_load(A.epoch), act);
+    }
+    __syncthreads();
+    build_scales<TYPE, kLinkThreads, 1>(lscale, lmeta, reinterpret_cast<const float *>(act + A.gu_lay.da_offset()), NB, mbytes);
+    __syncthreads();
+    if (compute) {
+        float acc[2] = {0.0f, 0.0f};
+        decode_stream<TYPE, G, NB>(ring, tl, codes_tile, k, r, NB, false,
+                                   act + static_cast<int64_t>(k) * NB * A.gu_lay.code_entry(), lscale + r * 4, acc);
+        red[k][r] = acc[0] + acc[1];
+    }
+    __syncthreads();
+    if (tid < 32) {
+        const float * l = &red[0][r];
+        const float s0 = l[4 * 32] + l[0], s1 = l[5 * 32] + l[1 * 32];
+        const float s2 = l[6 * 32] + l[2 * 32], s3 = l[7 * 32] + l[3 * 32];
+        float v = (s0 + s2) + (s1 + s3);
+        if (A.gu_bias) v = v + bias_v;
+        red[0][r] = v;                              // rows r: 0..15 gate, 16..31 up
+    }
+    __syncthreads();
+    if (tid < 16) {
+        float g = glu(A.activation, red[0][tid], red[0][tid + 16], A.alpha, A.limit);
+        if (!slot_ok) g = __builtin_nanf("");      // expert not resident in this bank: loud output
+        A.act_f[static_cast<size_t>(rank) * (S.rows / 2) + tile * 16 + tid] = g;
+    }
+    if (tid < 64 && tile == 0 && rank == 0) {
+        const float w = wave_pick_softmax(sel_v, A.top_k);
+        if (lane < A.top_k) {
+            A.route_ids[lane] = sel_i;
+            A.route_w[lane] = w;
+            A.route_slots[lane] = A.expert_to_slot ? A.expert_to_slot[sel_i] : sel_i;
+        }
+    }
+}
+
+template <int TYPE, int NPL, int NB, bool FIRST>
+__global__ __launch_bounds__(kLinkThreads) void decode_link_kernel(LinkArgs A) {
+    __shared__ float red[8][32];
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_dyn[];
+    const int wg = blockIdx.x;
+    if (!FIRST && wg < A.n_down) {
+        link_down<TYPE, NB>(A, wg, lds_dyn, red);
+        if (A.advance_epoch && wg == 0 && threadIdx.x == 0) *A.epoch = *A.epoch + 1u;
+    } else {
+        link_gate_up<TYPE, NPL, NB, FIRST>(A, FIRST ? wg : wg - A.n_down, lds_dyn, red);
+    }
+}
+
 template <int TYPE, int NPL, int NB>
 void launch_gate_up_npl(const DecodeArgs & a, dim3 grid, size_t lds, hipStream_t stream) {
     if (lds > 65536)
@@ -1319,6 +1676,77 @@ void launch_decode_gate_up(const DecodeGateUpArgs & d, hipStream_t stream) {
     a.host_stride = d.host_stride;
     if (bank.type == VBM_TYPE_MXFP4) launch_decode_typed<39>(a, stream);
     else launch_decode_typed<8>(a, stream);
+}
+
+bool decode_link_supported(const vbm_bank & gate_up, const vbm_bank & down, int64_t n_expert, int64_t top_k) {
+    return gate_up.type == VBM_TYPE_MXFP4 && down.type == VBM_TYPE_MXFP4 && gate_up.nb == 90 && down.nb == 90 &&
+           gate_up.interleave && gate_up.rows == 2 * 2880 && down.rows == 2880 && n_expert >= top_k &&
+           n_expert <= 128 && top_k >= 1 && top_k <= 64;
+}
+
+void launch_decode_link(const DecodeLinkParams & d, hipStream_t stream) {
+    static_assert(kLinkFlagWords == int64_t{kLinkCopies} * kLinkCopyStride, "flag region size");
+    require(d.dn_bank != nullptr || d.gu_bank != nullptr, "linked decode launch without work");
+    const vbm_bank * gu = d.gu_bank;
+    const vbm_bank * dn = d.dn_bank;
+    if (gu && dn) require(decode_link_supported(*gu, *dn, d.n_expert, d.top_k), "linked decode shape not supported");
+    if (gu) require(gu->type == VBM_TYPE_MXFP4 && gu->nb == 90 && gu->interleave && gu->rows == 5760 && d.n_expert <= 128,
+                    "linked decode gate_up shape not supported");
+    if (dn) require(dn->type == VBM_TYPE_MXFP4 && dn->nb == 90 && dn->rows == 2880, "linked decode down shape not supported");
+    require(d.top_k >= 1 && d.top_k <= 64 && d.n_expert >= d.top_k, "routing shape out of range");
+    require(dn == nullptr || (d.out != nullptr) != (d.xq != nullptr && d.flags != nullptr),
+            "a down part publishes either the next input row or the output");
+    require(gu == nullptr || d.x_in != nullptr || (d.xq != nullptr && d.flags != nullptr), "gate_up input missing");
+    require(!(gu && dn && d.x_in), "the first launch has no down part");
+    require(d.epoch != nullptr && d.error != nullptr, "linked decode state missing");
+    LinkArgs a{};
+    a.n_expert = static_cast<int>(d.n_expert);
+    a.top_k = static_cast<int>(d.top_k);
+    if (dn) {
+        a.n_down = static_cast<int>(d.top_k * (dn->rows / 32));
+        a.dn_bank = dn->base;
+        a.dn_shape = Shape{static_cast<int>(dn->nb), static_cast<int>(dn->rows), dn->interleave, dn->slot_bytes,
+                           dn->geometry().codes_bytes(), dn->n_slots};
+        a.dn_lay = XrowLayout{dn->nb, dn->type};
+        a.dn_act_f = d.dn_act_f;
+        a.dn_ids = d.dn_ids;
+        a.dn_slots = d.dn_slots;
+        a.dn_w = d.dn_w;
+        a.dn_bias = d.dn_bias;
+        a.y = d.y;
+        a.counters = d.counters;
+        a.out = d.out;
+    }
+    a.xq = d.xq;
+    a.flags = d.flags;
+    if (gu) {
+        a.n_gate_up = static_cast<int>(d.top_k * (gu->rows / 32));
+        a.gu_bank = gu->base;
+        a.gu_shape = Shape{static_cast<int>(gu->nb), static_cast<int>(gu->rows), gu->interleave, gu->slot_bytes,
+                           gu->geometry().codes_bytes(), gu->n_slots};
+        a.gu_lay = XrowLayout{gu->nb, gu->type};
+        a.expert_to_slot = d.expert_to_slot;
+        a.logits = d.logits;
+        a.x_in = d.x_in;
+        a.gu_bias = d.gu_bias;
+        a.act_f = d.act_f;
+        a.route_ids = d.route_ids;
+        a.route_w = d.route_w;
+        a.route_slots = d.route_slots;
+        a.activation = d.activation;
+        a.alpha = d.alpha;
+        a.limit = d.limit;
+    } else {
+        a.gu_lay = XrowLayout{dn->rows / 32, VBM_TYPE_MXFP4};
+    }
+    a.epoch = d.epoch;
+    a.advance_epoch = d.advance_epoch ? 1 : 0;
+    a.error = d.error;
+    const size_t lds = decode_lds_bytes<39>(90);
+    const dim3 grid(static_cast<unsigned>(a.n_down + a.n_gate_up));
+    if (d.x_in) hipLaunchKernelGGL((decode_link_kernel<39, 2, 90, true>), grid, dim3(kLinkThreads), lds, stream, a);
+    else hipLaunchKernelGGL((decode_link_kernel<39, 2, 90, false>), grid, dim3(kLinkThreads), lds, stream, a);
+    check_hip(hipGetLastError(), "linked decode launch");
 }
 
 void launch_decode_down(const DecodeDownParams & d, hipStream_t stream) {

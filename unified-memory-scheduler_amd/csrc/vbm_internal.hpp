@@ -42,6 +42,19 @@ inline void check_hip(hipError_t e, const char * what) {
 }
 inline hipStream_t as_stream(void * s) { return static_cast<hipStream_t>(s); }
 
+inline bool stream_capturing(hipStream_t s) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    check_hip(hipStreamIsCapturing(s, &capture), "hipStreamIsCapturing");
+    return capture == hipStreamCaptureStatusActive;
+}
+// hipEventRecord that, under stream capture, becomes an event-record node of the graph (an
+// external record), so the event is recorded by every replay instead of only ordering the
+// capture.
+inline void record_event(hipEvent_t e, hipStream_t s, const char * what) {
+    if (stream_capturing(s)) check_hip(hipEventRecordWithFlags(e, s, hipEventRecordExternal), what);
+    else check_hip(hipEventRecord(e, s), what);
+}
+
 void set_last_error(const std::string & message);
 void clear_last_error();
 
@@ -267,6 +280,43 @@ struct DecodeDownParams {
     int64_t host_stride = 0;
 };
 void launch_decode_down(const DecodeDownParams & d, hipStream_t stream);
+
+// One launch of the linked single-token decode: the down tiles of layer l - 1 (dn_bank non-null)
+// and the gate_up tiles of layer l (gu_bank non-null) in one grid; the down tiles publish layer
+// l's Q8_0 input row tile by tile (xq, flags) or, in the last launch, combine into `out`.
+struct DecodeLinkParams {
+    const vbm_bank * dn_bank = nullptr;
+    const float * dn_act_f = nullptr;   // [top_k][intermediate] GLU outputs of layer l - 1
+    const int32_t * dn_ids = nullptr;   // routing of layer l - 1 [top_k]
+    const int32_t * dn_slots = nullptr;
+    const float * dn_w = nullptr;
+    const float * dn_bias = nullptr;
+    float * y = nullptr;                // [top_k][hidden]
+    uint32_t * counters = nullptr;      // [hidden / 32] arrival counters of layer l - 1
+    float * out = nullptr;              // last launch: the step output [hidden]
+    uint8_t * xq = nullptr;             // layer l's input row (gate_up activation layout)
+    uint32_t * flags = nullptr;         // layer l's tile flags [kLinkFlagWords]
+    const vbm_bank * gu_bank = nullptr;
+    const int32_t * expert_to_slot = nullptr;
+    const float * logits = nullptr;     // [n_expert] of layer l
+    const float * x_in = nullptr;       // first launch: the layer input
+    const float * gu_bias = nullptr;
+    float * act_f = nullptr;            // [top_k][intermediate] GLU outputs of layer l
+    int32_t * route_ids = nullptr;
+    float * route_w = nullptr;
+    int32_t * route_slots = nullptr;
+    int64_t n_expert = 0, top_k = 0;
+    int activation = 0;
+    float alpha = 1.702f, limit = 7.0f;
+    uint32_t * epoch = nullptr;         // device step counter
+    bool advance_epoch = false;         // last launch
+    uint32_t * error = nullptr;         // device word set to 1 by a timed-out wait
+};
+constexpr int64_t kLinkFlagWords = 8 * 1152;   // flag words per layer (8 copies)
+// Shapes the linked decode is built for: MXFP4, hidden = intermediate = 2880 (90 blocks per row),
+// at most 128 experts.
+bool decode_link_supported(const vbm_bank & gate_up, const vbm_bank & down, int64_t n_expert, int64_t top_k);
+void launch_decode_link(const DecodeLinkParams & d, hipStream_t stream);
 
 // Ops-API device scratch reused per (device, stream); see vbm_ops.cpp.
 void * stream_scratch(hipStream_t s, size_t bytes);

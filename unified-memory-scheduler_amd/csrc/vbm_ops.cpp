@@ -18,9 +18,18 @@ struct vbm_decode_plan {
     int32_t * route_ids = nullptr;   // [L][K]
     float * route_w = nullptr;       // [L][K]
     int32_t * route_slots = nullptr; // [L][K] bank slots of the picks (kernel A -> kernel B)
-    float * act_f = nullptr;         // [K][I] GLU outputs (kernel A -> kernel B)
+    float * act_f = nullptr;         // [2][K][I] GLU outputs (kernel A -> kernel B; the linked step
+                                     // alternates the halves by layer parity)
     XrowLayout act_layout{};
     float * y = nullptr;             // [K][H]
+    // linked step (one launch per layer boundary)
+    bool linked = false;             // the step runs the linked launches
+    bool link_ok = false;            // the plan's shapes allow them
+    uint8_t * xq = nullptr;          // next-layer input row (gate_up activation layout)
+    uint32_t * flags = nullptr;      // [L][kLinkFlagWords]
+    uint32_t * counters = nullptr;   // [L][H / 32]
+    uint32_t * epoch = nullptr;      // step counter (starts at 1; flags start at 0)
+    uint32_t * error = nullptr;      // timed-out waits
 };
 
 namespace {
@@ -179,6 +188,11 @@ void * stream_scratch(hipStream_t s, size_t bytes) {
     std::lock_guard<std::mutex> lock(c.mu);
     auto & e = c.entries[{device, s}];
     if (e.second < bytes) {
+        // Growing is stream-ordered allocation; under capture it would become a graph-owned
+        // allocation that eager calls cannot use and relaunches cannot reuse.
+        require(!stream_capturing(s),
+                "this call needs more ops-API scratch than the capturing stream holds: run it once on the stream "
+                "before capture, or use vbm_mul_mat_id_ws / vbm_mul_mat_id_noalloc");
         if (e.first) check_hip(hipFreeAsync(e.first, s), "scratch release");
         e = {nullptr, 0};
         const size_t cap = std::max<size_t>(bytes + (bytes >> 2), size_t(1) << 20);
@@ -317,8 +331,10 @@ __global__ void copy_kernel(uint4 * __restrict__ dst, const uint4 * __restrict__
         dst[i] = src[i];
 }
 
+// Under stream capture the record becomes an event-record node of the graph, so events bracketing
+// kernels time every replay.
 void record(void * const * events, int i, hipStream_t s) {
-    if (events) check_hip(hipEventRecord(static_cast<hipEvent_t>(events[i]), s), "hipEventRecord");
+    if (events) record_event(static_cast<hipEvent_t>(events[i]), s, "hipEventRecord");
 }
 
 void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits, int64_t n_tokens, float * out,
@@ -596,18 +612,37 @@ vbm_status vbm_decode_plan_create(const vbm_moe_layer_desc * layers, int64_t n_l
         plan->K = layers[0].top_k;
         check_hip(hipGetDevice(&plan->device), "hipGetDevice");
         plan->act_layout = XrowLayout{plan->I / 32, layers[0].down->type};
+        plan->link_ok = true;
+        for (int64_t l = 0; l < n_layers; ++l)
+            plan->link_ok = plan->link_ok && decode_link_supported(*layers[l].gate_up, *layers[l].down, plan->E, plan->K);
+        plan->linked = false;   // opt-in: measured slower than two kernels per layer
+        const XrowLayout xq_layout{plan->H / 32, layers[0].gate_up->type};
         const size_t route = align_up(sizeof(int32_t) * plan->L * plan->K);
         const size_t weights = align_up(sizeof(float) * plan->L * plan->K);
-        const size_t act = align_up(sizeof(float) * plan->K * plan->I);
+        const size_t act = align_up(sizeof(float) * 2 * plan->K * plan->I);
         const size_t y = align_up(sizeof(float) * plan->K * plan->H);
-        check_hip(hipMalloc(reinterpret_cast<void **>(&plan->workspace), 2 * route + weights + act + y),
+        const size_t xq = align_up(static_cast<size_t>(xq_layout.stride()));
+        const size_t flags = align_up(sizeof(uint32_t) * plan->L * kLinkFlagWords);
+        const size_t counters = align_up(sizeof(uint32_t) * plan->L * ((plan->H + 31) / 32));
+        const size_t state = align_up(2 * sizeof(uint32_t));
+        const size_t link = xq + flags + counters + state;
+        check_hip(hipMalloc(reinterpret_cast<void **>(&plan->workspace), 2 * route + weights + act + y + link),
                   "decode plan workspace");
         uint8_t * p = plan->workspace;
         plan->route_ids = reinterpret_cast<int32_t *>(p); p += route;
         plan->route_slots = reinterpret_cast<int32_t *>(p); p += route;
         plan->route_w = reinterpret_cast<float *>(p); p += weights;
         plan->act_f = reinterpret_cast<float *>(p); p += act;
-        plan->y = reinterpret_cast<float *>(p);
+        plan->y = reinterpret_cast<float *>(p); p += y;
+        uint8_t * link_base = p;
+        plan->xq = p; p += xq;
+        plan->flags = reinterpret_cast<uint32_t *>(p); p += flags;
+        plan->counters = reinterpret_cast<uint32_t *>(p); p += counters;
+        plan->epoch = reinterpret_cast<uint32_t *>(p);
+        plan->error = plan->epoch + 1;
+        check_hip(hipMemset(link_base, 0, link), "decode plan state");
+        const uint32_t one = 1;
+        check_hip(hipMemcpy(plan->epoch, &one, sizeof(one), hipMemcpyHostToDevice), "decode plan epoch");
         *out = plan.release();
     });
 }
@@ -664,9 +699,81 @@ void decode_launch_b(const vbm_decode_plan * plan, int64_t l, hipStream_t s) {
     launch_decode_down(b, s);
 }
 
+// Launch j of the linked step: the down tiles of layer j - 1 (j >= 1) and the gate_up tiles of
+// layer j (j < L).
+void decode_launch_link(const vbm_decode_plan * plan, int64_t j, const float * x, const float * logits, float * out,
+                        hipStream_t s) {
+    const int64_t K = plan->K, L = plan->L;
+    DecodeLinkParams p{};
+    p.n_expert = plan->E;
+    p.top_k = K;
+    p.epoch = plan->epoch;
+    p.error = plan->error;
+    if (j >= 1) {
+        const vbm_moe_layer_desc & d = plan->layers[j - 1];
+        p.dn_bank = d.down;
+        p.dn_act_f = plan->act_f + ((j - 1) & 1) * K * plan->I;
+        p.dn_ids = plan->route_ids + (j - 1) * K;
+        p.dn_slots = plan->route_slots + (j - 1) * K;
+        p.dn_w = plan->route_w + (j - 1) * K;
+        p.dn_bias = d.down_bias;
+        p.y = plan->y;
+        p.counters = plan->counters + (j - 1) * ((plan->H + 31) / 32);
+        if (j == L) {
+            p.out = out;
+            p.advance_epoch = true;
+        }
+    }
+    if (j < L) {
+        const vbm_moe_layer_desc & d = plan->layers[j];
+        p.gu_bank = d.gate_up;
+        p.expert_to_slot = d.expert_to_slot;
+        p.logits = logits + j * plan->E;
+        p.x_in = j == 0 ? x : nullptr;
+        p.gu_bias = d.gate_up_bias;
+        p.act_f = plan->act_f + (j & 1) * K * plan->I;
+        p.route_ids = plan->route_ids + j * K;
+        p.route_w = plan->route_w + j * K;
+        p.route_slots = plan->route_slots + j * K;
+        p.activation = d.activation;
+        if (j >= 1) {
+            p.xq = plan->xq;
+            p.flags = plan->flags + j * kLinkFlagWords;
+        }
+    }
+    launch_decode_link(p, s);
+}
+
 }  // namespace
 
 extern "C" {
+
+vbm_status vbm_decode_plan_set_linked(vbm_decode_plan * plan, int linked) {
+    return guarded([&] {
+        require(plan != nullptr, "null plan");
+        require(!linked || plan->link_ok, "the linked decode step does not support this plan's shapes");
+        plan->linked = linked != 0;
+    });
+}
+
+vbm_status vbm_decode_plan_get_linked(const vbm_decode_plan * plan, int * linked) {
+    return guarded([&] {
+        require(plan != nullptr && linked != nullptr, "null argument");
+        *linked = plan->linked ? 1 : 0;
+    });
+}
+
+vbm_status vbm_decode_plan_check(vbm_decode_plan * plan, int64_t * timeouts) {
+    return guarded([&] {
+        require(plan != nullptr, "null plan");
+        check_hip(hipDeviceSynchronize(), "decode plan check");
+        uint32_t e = 0;
+        check_hip(hipMemcpy(&e, plan->error, sizeof(e), hipMemcpyDeviceToHost), "decode plan error word");
+        if (e) check_hip(hipMemset(plan->error, 0, sizeof(e)), "decode plan error reset");
+        if (timeouts) *timeouts = e;
+        if (e) fail(VBM_ERR_RUNTIME, "a linked decode wait timed out: that step's outputs are unspecified");
+    });
+}
 
 vbm_status vbm_decode_step(vbm_decode_plan * plan, const float * x, const float * logits, float * out, int32_t * ids,
                            float * weights, void * const * events, void * stream) {
@@ -675,6 +782,16 @@ vbm_status vbm_decode_step(vbm_decode_plan * plan, const float * x, const float 
         require(reinterpret_cast<uintptr_t>(x) % 16 == 0, "decode input must be 16-byte aligned");
         const hipStream_t s = as_stream(stream);
         const int64_t K = plan->K, H = plan->H;
+        if (plan->linked) {
+            for (int64_t j = 0; j <= plan->L; ++j) {
+                record(events, 2 * j, s);
+                decode_launch_link(plan, j, x, logits, out, s);
+                record(events, 2 * j + 1, s);
+            }
+            if (ids) check_hip(hipMemcpyAsync(ids, plan->route_ids, sizeof(int32_t) * plan->L * K, hipMemcpyDeviceToDevice, s), "ids copy");
+            if (weights) check_hip(hipMemcpyAsync(weights, plan->route_w, sizeof(float) * plan->L * K, hipMemcpyDeviceToDevice, s), "weights copy");
+            return;
+        }
         for (int64_t l = 0; l < plan->L; ++l) {
             void * const * ev = events ? events + 4 * l : nullptr;
             record(ev, 0, s);

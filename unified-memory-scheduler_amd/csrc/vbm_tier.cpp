@@ -77,6 +77,7 @@ struct vbm_tier {
     hipEvent_t step_done = nullptr;   // after that step's id hand-off
     bool step_pending = false;        // its ids still await admission
     bool awaiting = false;            // a step was begun; its device part (eager or a graph replay) follows
+    bool enqueued = false;            // that step's device part was enqueued eagerly
     std::vector<std::pair<int64_t, int64_t>> unpublished;   // (layer, expert) uploads in flight
     bool uploads_timed = false;       // copy_begin / copy_end bracket the uploads in flight
 
@@ -253,8 +254,10 @@ void tier_enqueue_step(vbm_tier & t, const float * x, const float * logits, floa
     if (ids) check_hip(hipMemcpyAsync(ids, t.route_ids, sizeof(int32_t) * L * K, hipMemcpyDeviceToDevice, s), "ids copy");
     check_hip(hipMemcpyAsync(t.step_ids_host, t.route_ids, sizeof(int32_t) * L * K, hipMemcpyDeviceToHost, s),
               "tier id hand-off");
-    check_hip(hipEventRecord(t.step_done, s), "tier step event");
-    check_hip(hipEventRecord(t.last_use, s), "tier last use");
+    // external records under capture: every replay records them, so the host waits on them
+    // (the next flush, seed, reset or mode change) wait for that replay's hand-off and reads
+    record_event(t.step_done, s, "tier step event");
+    record_event(t.last_use, s, "tier last use");
     t.used = true;
 }
 
@@ -264,6 +267,7 @@ void tier_begin_step(vbm_tier & t) {
     if (t.awaiting) t.step_pending = true;
     tier_flush(t);
     t.awaiting = true;
+    t.enqueued = false;
     t.started = true;
 }
 
@@ -433,6 +437,7 @@ vbm_status vbm_tier_step(vbm_tier * t, const float * x, const float * logits, fl
         const hipStream_t s = as_stream(stream);
         if (t->deferred) {
             tier_begin_step(*t);
+            t->enqueued = true;
             tier_enqueue_step(*t, x, logits, out, ids, s);
             return;
         }
@@ -683,7 +688,7 @@ vbm_status vbm_tier_reset(vbm_tier * t, int policy, int64_t recent_window, int64
         t->desc.recent_window = recent_window;
         t->desc.margin = margin;
         t->stats = vbm_tier_stats{};
-        t->step_pending = t->awaiting = false;
+        t->step_pending = t->awaiting = t->enqueued = false;
         t->unpublished.clear();
         t->uploads_timed = false;
         t->started = false;
@@ -707,7 +712,15 @@ vbm_status vbm_tier_step_enqueue(vbm_tier * t, const float * x, const float * lo
         require(t != nullptr && t->deferred, "vbm_tier_step_enqueue needs deferred mode");
         require(x && logits && out, "null buffer");
         require(reinterpret_cast<uintptr_t>(x) % 16 == 0, "decode input must be 16-byte aligned");
-        tier_enqueue_step(*t, x, logits, out, ids, as_stream(stream));
+        const hipStream_t s = as_stream(stream);
+        // An eager enqueue belongs to the step begun last, once: a second one would overwrite that
+        // step's id hand-off and lose its admissions. A captured enqueue is exempt (its replays,
+        // one per begin, cannot be checked from here).
+        if (!stream_capturing(s)) {
+            require(t->awaiting && !t->enqueued, "vbm_tier_step_enqueue needs a vbm_tier_step_begin before it (one enqueue per begin)");
+            t->enqueued = true;
+        }
+        tier_enqueue_step(*t, x, logits, out, ids, s);
     });
 }
 

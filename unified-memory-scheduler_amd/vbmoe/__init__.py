@@ -178,6 +178,9 @@ SIGNATURES = {
     "vbm_decode_plan_destroy": [vp],
     "vbm_decode_step": [vp, vp, vp, vp, vp, vp, vp, vp],
     "vbm_decode_kernel": [vp, i64, C.c_int, vp, vp, vp],
+    "vbm_decode_plan_set_linked": [vp, C.c_int],
+    "vbm_decode_plan_get_linked": [vp, C.POINTER(C.c_int)],
+    "vbm_decode_plan_check": [vp, C.POINTER(i64)],
     "vbm_admission_create": [i64, i64, i64, i64, i64, C.c_int32, C.c_int, C.POINTER(vp)],
     "vbm_admission_destroy": [vp],
     "vbm_admission_seed": [vp, i64, i64, vp],
