@@ -21,8 +21,10 @@
 // exactly lane group q's k range, so a lane's A operand is two dwords of the bank as stored (the
 // staging loads only place them in LDS).
 //
-// A workgroup (4 waves) computes 64 bank rows (a tile pair) x 64 jobs of one expert; wave w owns
-// bank tile 2p + (w & 1) and jobs 32(w >> 1)..+31 as a 2x2 grid of 16x16 fragments.
+// A workgroup (4 waves) computes 64 bank rows (a tile pair) x 128 jobs of one expert; wave w owns
+// bank tile 2p + (w & 1) and jobs 64(w >> 1)..+63 as a 2x4 grid of 16x16 fragments. 128 jobs is
+// the mean group of a 2048-token top-8 prefill over 128 experts, so most experts' weights are
+// read once per row pair, and every weight operand feeds four MFMAs.
 #include <type_traits>
 
 #include "vbm_device.hpp"
@@ -40,7 +42,9 @@ typedef unsigned u32x2g __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_g __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmThreads = 256;
-constexpr int kJobTile = 64;
+constexpr int kJobTile = static_cast<int>(kGemmJobTile);   // jobs per grouped-GEMM workgroup
+constexpr int kJobFrags = kJobTile / 32;                   // 16-job fragment columns per wave
+constexpr int kMxJobTile = 64;                             // the MXFP8 experiment's job tile
 
 template <class T>
 __device__ __forceinline__ const __attribute__((address_space(4))) T * cst(const void * p) {
@@ -67,6 +71,7 @@ struct GemmArgs {
     const int32_t * tile_start;
     const int32_t * n_tiles;
     const float * bias;        // [n_expert][rows] in ggml row order, or null
+    const float * row_scale;   // epilogue 0: per-job factor applied after the bias (routing weights), or null
     float * dst;               // epilogue 0: [job][rows]
     int row_pairs;             // 64-row tile pairs of the bank
     uint8_t * rows_out;        // epilogue 1: GLU output rows for the down projection (out_lay)
@@ -125,14 +130,12 @@ __device__ __forceinline__ half8_t i8_to_f16(long v) {
     return r;
 }
 // Pipeline stages, filled by global-to-LDS DMA: a ring of S chunks of CB blocks, each stage
-// holding everything its chunk reads: the 64 jobs' activation codes and block scales, both tiles'
+// holding everything its chunk reads: the 128 jobs' activation codes and block scales, both tiles'
 // weight dwords of those blocks (Q8_0: the [slice pair][row] interleave of 16-byte units
 // (2q, b), (2q+1, b), (2q, b+1), (2q+1, b+1); MXFP4: [slice][row] dwords, rows of odd slice pairs
 // rotated by 16 against bank conflicts) and their exponent / scale dword per row. Chunk c issues
-// the loads of chunk c + S - 1; one wait and one barrier per chunk. With two stages (17.5 KiB
-// for Q8_0) and no staging registers the VGPRs, not the LDS, bound occupancy (Q8_0 six to seven
-// waves per SIMD), which measured faster than deeper rings at lower occupancy (Q8_0 layer of
-// 2048 tokens: gate_up 343 vs 350 / 364 us with three / four stages).
+// the loads of chunk c + S - 1; one wait and one barrier per chunk. Two stages: a third one, for
+// every operand or for the weights alone, measured no faster (Q8_0 layer of 2048 tokens).
 template <int TYPE>
 struct GemmStage {
     static constexpr int EB = TYPE == 39 ? 2 : 1;                       // bytes per activation code
@@ -192,11 +195,11 @@ __device__ __forceinline__ float mul_half(unsigned h2, float x, float neg_zero) 
 }
 
 template <int TYPE, int EPI, bool FLAGGED>
-__global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) {
+__global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void grouped_gemm_kernel(GemmArgs A) {
     using G = GemmStage<TYPE>;
     constexpr int CB = G::CB;
-    static_assert(G::BYTES >= kJobTile * 68 * 4, "epilogue tile must fit the stage buffers");
-    __shared__ __attribute__((aligned(16))) uint8_t lds[G::BYTES];
+    constexpr int kLdsBytes = G::BYTES > kJobTile * 68 * 4 ? G::BYTES : kJobTile * 68 * 4;   // stages / epilogue tile
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
     float (*tile_vals)[68] = reinterpret_cast<float (*)[68]>(lds);    // epilogue tile [job][pair row], after the K loop
 
     // XCD-aware order: workgroup i runs on XCD i % 8, so hand each XCD a contiguous range of
@@ -253,22 +256,28 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
         return A.rows_in + row_index * A.lay.stride();
     };
 
-    // This lane's fragment columns (jobs 32(w>>1) + 16jh + lr) and the -128 flags of the wave.
+    // This lane's fragment columns (jobs 64(w>>1) + 16jh + lr) and the -128 flags of the wave.
     // Rows converted from caller-quantized Q8_0 data (FLAGGED) may hold -128 codes.
-    bool jlive[2];
-    int job[2];
+    constexpr int JF = kJobFrags;
+    const int wj = 64 * (wave >> 1);                   // the wave's first job in the tile
+    bool jlive[JF];
+    int job[JF];
     int flagged = 0;
 #pragma unroll
-    for (int jh = 0; jh < 2; ++jh) {
-        const int jl = 32 * (wave >> 1) + 16 * jh + lr;
+    for (int jh = 0; jh < JF; ++jh) {
+        const int jl = wj + 16 * jh + lr;
         jlive[jh] = j0 + jl < count;
         job[jh] = jlive[jh] ? A.jobs[joff + j0 + jl] : 0;
         if (FLAGGED && jlive[jh]) flagged |= *reinterpret_cast<const int *>(row_of(jl) + A.lay.flag_offset());
     }
-    // A fragment column of 16 jobs none of which is live (the tile's live jobs are a prefix) costs
-    // the wave no matrix or scale work: the last tile of an expert is often nearly empty.
+    // Fragment columns of 16 jobs none of which is live (the tile's live jobs are a prefix) cost the
+    // wave no matrix or scale work: the last tile of an expert is often nearly empty. The K loop
+    // is instantiated per count of live columns (nf, wave-uniform), so its body carries no
+    // per-column branch and the compiler can interleave the columns' MFMAs and VALU work.
+    static_assert(JF == 4, "the K loop is instantiated for 0..4 live fragment columns");
     const int wq = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 7));
-    const bool frag_live[2] = {j0 + 32 * wq < count, j0 + 32 * wq + 16 < count};
+    const int live_in_half = count - j0 - 64 * wq;
+    const int nf = live_in_half <= 0 ? 0 : (live_in_half >= 64 ? JF : (live_in_half + 15) / 16);
     // Workgroup-uniform: every wave then runs the same K-loop instantiation, so each of its
     // barriers is reached from one control path (every thread gets here: the exits above are
     // uniform per workgroup).
@@ -282,7 +291,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
     //     the 16-byte parts of row r sit at part p ^ s(r) (s(r) = (r >> 1) & 3, resp. r & 7) so
     //     the fragment reads of 16 consecutive rows spread over the banks; a row past the tile's
     //     jobs reads the first job's row (its columns are never stored);
-    //   - block scales: lanes 0..31 of wave w load jobs 16w..16w+15 x 2 blocks;
+    //   - block scales: lane l of wave w loads job 32w + l / 2, block l % 2;
     //   - weights: dword loads; Q8_0 load I = 4w + i covers tile I >> 3, slice pair (I >> 1) & 3,
     //     rows 16 (I & 1) .. +15 (lane: row l >> 2, unit dword l & 3); MXFP4 load I = 2w + i covers
     //     tile I >> 2, slices 2 (I & 3) and 2 (I & 3) + 1 (lane: slice l >> 5, position l & 31);
@@ -299,7 +308,8 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
         const int part = TYPE == 39 ? (lane & 7) ^ (jr & 7) : (lane & 3) ^ ((jr >> 1) & 3);
         act_src[j] = row_of(j0 + jr < count ? jr : 0) + 16 * part;
     }
-    const int jd = 16 * wave + ((lane & 31) >> 1);
+    static_assert(G::DA == kGemmThreads * 4, "one block-scale dword per thread and chunk");
+    const int jd = 32 * wave + (lane >> 1);
     const uint8_t * da_src = row_of(j0 + jd < count ? jd : 0) + A.lay.da_offset() + 4 * (lane & 1);
     // weight dword of this lane within its load's group-relative source
     uint32_t woff;
@@ -318,7 +328,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
 #pragma unroll
         for (int j = 0; j < G::ACT_DMA; ++j)
             lds_dma_x4(act_src[j] + static_cast<int64_t>(c) * G::ROW, sb + (wu * G::ACT_DMA + j) * 1024);
-        if (lane < 32) lds_dma_x1(da_src + static_cast<int64_t>(c) * CB * 4, sb + G::OFF_DA + wu * 128);
+        lds_dma_x1(da_src + static_cast<int64_t>(c) * CB * 4, sb + G::OFF_DA + wu * 256);
 #pragma unroll
         for (int i = 0; i < G::W_DMA; ++i) {
             const int I = wu * G::W_DMA + i;
@@ -339,11 +349,11 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
         if (lane < 16) lds_dma_x1_s(mbase, moff, sb + G::OFF_M + wu * 64);
     };
 
-    f32x4 acc[2][2];
+    f32x4 acc[2][JF];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int jh = 0; jh < 2; ++jh) acc[i][jh] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int jh = 0; jh < JF; ++jh) acc[i][jh] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     // One block: weight operands a_op[i] (row halves i), activation operand and scale of job half
     // jh from bsrc(jh) / dsrc(jh); factor(i, j, da) is the block's fp32 scale for output row
@@ -351,11 +361,11 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
     // exact -128 correction, accumulated into the same MFMA result (its operands scaled by 256
     // are exact in fp16).
     const float neg_zero = -0.0f;
-    auto block_step = [&](auto slow_c, const auto & a_op, auto && factor, auto && bsrc, auto && dsrc) {
+    auto block_step = [&](auto slow_c, auto nf_c, const auto & a_op, auto && factor, auto && bsrc, auto && dsrc) {
         constexpr bool SLOW = decltype(slow_c)::value;
+        constexpr int NF = decltype(nf_c)::value;
 #pragma unroll
-        for (int jh = 0; jh < 2; ++jh) {
-            if (!frag_live[jh]) continue;
+        for (int jh = 0; jh < NF; ++jh) {
             const float da = dsrc(jh);
             const auto bv = bsrc(jh);
 #pragma unroll
@@ -379,9 +389,11 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
         }
     };
 
-    // The K loop, instantiated with and without the -128 correction (wave-uniform choice).
+    // The K loop, instantiated with and without the -128 correction (workgroup-uniform choice) and
+    // per count of live fragment columns.
     const int n_chunks = groups * G::CPG;
-    auto k_loop = [&](auto slow_c) {
+    auto k_loop = [&](auto slow_c, auto nf_c) {
+        constexpr int NF = decltype(nf_c)::value;
         // weight dwords of A rows lr + 16i, slices 2q / 2q + 1 (MXFP4: row r of an odd slice pair
         // at position r ^ 16), or their 16-byte unit (Q8_0)
         const uint8_t * w_lds[2];
@@ -391,14 +403,14 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                                                      : (wave & 1) * 2048 + (q * 32 + 16 * i + lr) * 16);
         const uint8_t * m_lds = lds + G::OFF_M + ((wave & 1) * 32 + 4 * q) * 4;   // output rows 4q + j (+16i)
         const uint8_t * ma_lds = lds + G::OFF_M + ((wave & 1) * 32 + lr) * 4;     // A rows lr (+16i)
-        const float * d_lds = reinterpret_cast<const float *>(lds + G::OFF_DA) + (32 * (wave >> 1) + lr) * CB;
-        // fragment columns' activation codes: row rr = 32(w >> 1) + 16jh + lr, block bb, codes 8q..8q+7
-        uint32_t aoff[2][2];
+        const float * d_lds = reinterpret_cast<const float *>(lds + G::OFF_DA) + (wj + lr) * CB;
+        // fragment columns' activation codes: row rr = 64(w >> 1) + 16jh + lr, block bb, codes 8q..8q+7
+        uint32_t aoff[JF][2];
 #pragma unroll
-        for (int jh = 0; jh < 2; ++jh)
+        for (int jh = 0; jh < JF; ++jh)
 #pragma unroll
             for (int bb = 0; bb < 2; ++bb) {
-                const int rr = 32 * (wave >> 1) + 16 * jh + lr;
+                const int rr = wj + 16 * jh + lr;
                 aoff[jh][bb] = TYPE == 39 ? rr * 128 + (((4 * bb + q) ^ (rr & 7)) << 4)
                                           : rr * 64 + (((2 * bb + (q >> 1)) ^ ((rr >> 1) & 3)) << 4) + 8 * (q & 1);
             }
@@ -407,8 +419,10 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
             const int sub = c % G::CPG;
             // this chunk's loads: the stage of chunk c + S - 1, clamped to the last chunk
             // (the stage it fills is free either way)
+            // this chunk's loads: the stage of chunk c + S - 1, clamped to the last chunk
+            // (the stage it fills is free either way)
             dma_stage(c + G::S - 1 < n_chunks ? c + G::S - 1 : n_chunks - 1, (c + G::S - 1) % G::S);
-            const int ab = c % G::S;
+            const int ab = c % G::S, wb = ab;
             const uint8_t * st = lds + ab * G::STAGE;     // this chunk's stage
             // This chunk's blocks 2sub, 2sub+1 in the group: weight dwords of slices 2q, 2q+1
             // (MXFP4: one dword holds both blocks; Q8_0: one dword each).
@@ -416,11 +430,11 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 if constexpr (TYPE == 39) {
-                    const uint8_t * w = w_lds[i] + ab * G::STAGE;
+                    const uint8_t * w = w_lds[i] + wb * G::STAGE;
                     w0[i][0] = w0[i][1] = *reinterpret_cast<const unsigned *>(w);
                     w1[i][0] = w1[i][1] = *reinterpret_cast<const unsigned *>(w + 32 * 4);
                 } else {
-                    const u32x4g v = *reinterpret_cast<const u32x4g *>(w_lds[i] + ab * G::STAGE);
+                    const u32x4g v = *reinterpret_cast<const u32x4g *>(w_lds[i] + wb * G::STAGE);
                     w0[i][0] = v[0], w1[i][0] = v[1], w0[i][1] = v[2], w1[i][1] = v[3];
                 }
             }
@@ -434,7 +448,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                 bool ok = true;
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
-                    const unsigned ea = *reinterpret_cast<const uint16_t *>(ma_lds + ab * G::STAGE + i * 16 * 4 + (sub & 1) * 2);
+                    const unsigned ea = *reinterpret_cast<const uint16_t *>(ma_lds + wb * G::STAGE + i * 16 * 4 + (sub & 1) * 2);
 #pragma unroll
                     for (int bb = 0; bb < 2; ++bb) {
                         const int e = static_cast<signed char>(ea >> (8 * bb));
@@ -451,8 +465,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
 #pragma unroll
                     for (int i = 0; i < 2; ++i) a_op[i] = mx_a_operand(w0[i][bb], w1[i][bb], bb, fsc[i][bb]);
 #pragma unroll
-                    for (int jh = 0; jh < 2; ++jh) {
-                        if (!frag_live[jh]) continue;
+                    for (int jh = 0; jh < NF; ++jh) {
                         const float da = d_lds[ab * (G::STAGE / 4) + 16 * jh * CB + bb];
                         const half8_t bv = *reinterpret_cast<const half8_t *>(st + aoff[jh][bb]);
 #pragma unroll
@@ -470,11 +483,11 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                 // the exact fp32 product of two fp16 values (11-bit significands) plus zeros:
                 // the value the per-output VALU product gives, off the vector ALU.
                 const unsigned sel[2] = {lane < 16 ? 0x0000FFFFu : 0u, lane < 16 ? 0xFFFF0000u : 0u};
-                unsigned dw_row[2], da_pk[2];
+                unsigned dw_row[2], da_pk[JF];
 #pragma unroll
-                for (int i = 0; i < 2; ++i) dw_row[i] = *reinterpret_cast<const unsigned *>(ma_lds + ab * G::STAGE + i * 16 * 4);
+                for (int i = 0; i < 2; ++i) dw_row[i] = *reinterpret_cast<const unsigned *>(ma_lds + wb * G::STAGE + i * 16 * 4);
 #pragma unroll
-                for (int jh = 0; jh < 2; ++jh) {
+                for (int jh = 0; jh < NF; ++jh) {
                     // d_act holds fp16 values, so the packing conversion is exact
                     const float * dp = d_lds + ab * (G::STAGE / 4) + 16 * jh * CB;
                     da_pk[jh] = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(dp[0], dp[1]));
@@ -489,8 +502,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                         as[i] = __builtin_bit_cast(half4_g, u32x2g{dw_row[i] & sel[bb], 0u});
                     }
 #pragma unroll
-                    for (int jh = 0; jh < 2; ++jh) {
-                        if (!frag_live[jh]) continue;
+                    for (int jh = 0; jh < NF; ++jh) {
                         const long bv = *reinterpret_cast<const long *>(st + aoff[jh][bb]);
                         const half4_g bs = __builtin_bit_cast(half4_g, u32x2g{da_pk[jh] & sel[bb], 0u});
 #pragma unroll
@@ -512,9 +524,9 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         if constexpr (TYPE == 39)
-                            mw[i][j] = *reinterpret_cast<const uint16_t *>(m_lds + ab * G::STAGE + (16 * i + j) * 4 + (sub & 1) * 2);
+                            mw[i][j] = *reinterpret_cast<const uint16_t *>(m_lds + wb * G::STAGE + (16 * i + j) * 4 + (sub & 1) * 2);
                         else
-                            mw[i][j] = *reinterpret_cast<const unsigned *>(m_lds + ab * G::STAGE + (16 * i + j) * 4);
+                            mw[i][j] = *reinterpret_cast<const unsigned *>(m_lds + wb * G::STAGE + (16 * i + j) * 4);
                     }
                 auto do_block = [&](int bb) {
                     auto bsrc = [&](int jh) {
@@ -530,7 +542,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                         half8_t a_op[2];
 #pragma unroll
                         for (int i = 0; i < 2; ++i) a_op[i] = mx_a_operand(w0[i][bb], w1[i][bb], bb);
-                        block_step(slow_c, a_op, factor, bsrc, dsrc);
+                        block_step(slow_c, nf_c, a_op, factor, bsrc, dsrc);
                     } else {
                         auto factor = [&](int i, int j, float da) {
                             return bb ? mul_half<1>(mw[i][j], da, neg_zero) : mul_half<0>(mw[i][j], da, neg_zero);
@@ -539,7 +551,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
 #pragma unroll
                         for (int i = 0; i < 2; ++i)
                             a_op[i] = static_cast<long>(static_cast<uint64_t>(w0[i][bb]) | (static_cast<uint64_t>(w1[i][bb]) << 32));
-                        block_step(slow_c, a_op, factor, bsrc, dsrc);
+                        block_step(slow_c, nf_c, a_op, factor, bsrc, dsrc);
                     }
                 };
                 if constexpr (decltype(slow_c)::value) {
@@ -576,9 +588,9 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                 if constexpr (TYPE == 39) return __builtin_amdgcn_ldexpf(da, static_cast<signed char>(m[i][j]));
                 else return half_bits_to_float(static_cast<uint16_t>(m[i][j])) * da;
             };
-            const uint8_t * brow[2];
+            const uint8_t * brow[JF];
 #pragma unroll
-            for (int jh = 0; jh < 2; ++jh) brow[jh] = jlive[jh] ? row_of(32 * (wave >> 1) + 16 * jh + lr) : nullptr;
+            for (int jh = 0; jh < JF; ++jh) brow[jh] = jlive[jh] ? row_of(wj + 16 * jh + lr) : nullptr;
             auto bsrc = [&](int jh) {
                 if constexpr (TYPE == 39) {
                     half8_t v = half8_t{};
@@ -604,7 +616,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                     const half2_g p0 = fp4x2(w0, 0), p1 = fp4x2(w0, 1), p2 = fp4x2(w1, 0), p3 = fp4x2(w1, 1);
                     a[i] = half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
                 }
-                block_step(slow_c, a, factor, bsrc, dsrc);
+                block_step(slow_c, nf_c, a, factor, bsrc, dsrc);
             } else {
                 long a[2];
 #pragma unroll
@@ -617,7 +629,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
                     }
                     a[i] = static_cast<long>(w0 | (w1 << 32));
                 }
-                block_step(slow_c, a, factor, bsrc, dsrc);
+                block_step(slow_c, nf_c, a, factor, bsrc, dsrc);
             }
         }
     };
@@ -627,20 +639,37 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
         lds_dma_wait<0>();
     }
     __syncthreads();
+    // Waves of one workgroup may take different instantiations (their job halves hold different
+    // numbers of live columns); every instantiation issues the same stage loads and reaches one
+    // barrier per chunk.
+    auto k_loop_nf = [&](auto slow_c) {
+        switch (nf) {
+            case 4: k_loop(slow_c, std::integral_constant<int, 4>{}); break;
+            case 3: k_loop(slow_c, std::integral_constant<int, 3>{}); break;
+            case 2: k_loop(slow_c, std::integral_constant<int, 2>{}); break;
+            case 1: k_loop(slow_c, std::integral_constant<int, 1>{}); break;
+            default: k_loop(slow_c, std::integral_constant<int, 0>{}); break;
+        }
+    };
     if constexpr (FLAGGED) {
-        if (slow) k_loop(std::true_type{});
-        else k_loop(std::false_type{});
+        if (slow) k_loop_nf(std::true_type{});
+        else k_loop_nf(std::false_type{});
     } else {
-        k_loop(std::false_type{});
+        k_loop_nf(std::false_type{});
     }
     // The clamped loads of the last chunks may still be landing in the stages the epilogue reuses.
     lds_dma_wait<0>();
     __syncthreads();
 
-    // Epilogue: biases (ggml row order), then either fp32 rows or GLU + Q8_0 requantization. The
-    // fp32 rows go through the LDS tile too when the output allows 16-byte stores, so that each
-    // job's 64 rows leave as four full 64-byte segments instead of 4-byte scatter.
+    // Epilogue: biases (ggml row order), then either fp32 rows (times the job's routing weight when
+    // row_scale is given: ggml's ADD_ID, then MUL, hybrid-experts.patch:1636-1646) or GLU + Q8_0
+    // requantization. The fp32 rows go through the LDS tile too when the output allows 16-byte
+    // stores, so that each job's 64 rows leave as four full 64-byte segments instead of 4-byte
+    // scatter.
     const bool via_lds = EPI == 1 || A.dst_vec4;
+    float rscale[JF];
+#pragma unroll
+    for (int jh = 0; jh < JF; ++jh) rscale[jh] = EPI == 0 && A.row_scale && jlive[jh] ? A.row_scale[job[jh]] : 1.0f;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -649,90 +678,93 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_kernel(GemmArgs A) 
             const int grow = static_cast<int>(ggml_row(static_cast<int64_t>(tile) * 32 + orow, S.rows, S.interleave));
             const float bv = (A.bias && tile_live) ? A.bias[static_cast<size_t>(expert) * S.rows + grow] : 0.0f;
 #pragma unroll
-            for (int jh = 0; jh < 2; ++jh) {
+            for (int jh = 0; jh < JF; ++jh) {
                 float v = acc[i][jh][j];
                 if (A.bias) v = v + bv;
+                if (EPI == 0 && A.row_scale) v = v * rscale[jh];
                 if (!via_lds) {
                     if (jlive[jh] && tile_live) A.dst[static_cast<size_t>(job[jh]) * S.rows + grow] = v;
                 } else {
-                    tile_vals[32 * (wave >> 1) + 16 * jh + lr][32 * (wave & 1) + orow] = v;
+                    tile_vals[wj + 16 * jh + lr][32 * (wave & 1) + orow] = v;
                 }
             }
         }
     }
-    if (EPI == 0 && via_lds) {
-        __syncthreads();
-        // four threads per job, 16 pair rows each; aligned runs of 4 device rows are 4
-        // consecutive ggml rows (also in interleaved gate|up banks)
-        const int jl = threadIdx.x >> 2, seg = threadIdx.x & 3;
-        if (j0 + jl < count) {
-            float * out = A.dst + static_cast<size_t>(A.jobs[joff + j0 + jl]) * S.rows;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int col = seg * 16 + 4 * k;
-                const int64_t brow = static_cast<int64_t>(pair) * 64 + col;
-                if (brow < S.rows)
-                    *reinterpret_cast<float4 *>(out + ggml_row(brow, S.rows, S.interleave)) =
-                        *reinterpret_cast<const float4 *>(&tile_vals[jl][col]);
-            }
-        }
-    }
-    if (EPI == 1) {
-        __syncthreads();
-        // one 32-element GLU block per job: four threads per job, eight elements each
-        const int jl = threadIdx.x >> 2, part = threadIdx.x & 3;
+    if (!via_lds) return;
+    __syncthreads();
+    for (int jl = threadIdx.x >> 2; jl < kJobTile; jl += kGemmThreads / 4) {   // four threads per job
         const int jj = j0 + jl;
-        const bool live = jj < count;
-        float x[8];
+        if (EPI == 0) {
+            // 16 pair rows per thread; aligned runs of 4 device rows are 4 consecutive ggml rows
+            // (also in interleaved gate|up banks)
+            const int seg = threadIdx.x & 3;
+            if (jj < count) {
+                float * out = A.dst + static_cast<size_t>(A.jobs[joff + jj]) * S.rows;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const int e = part * 8 + t;                 // element of the block
-            const int tl = e >> 4;                      // bank tile of the pair
-            const float g = tile_vals[jl][32 * tl + (e & 15)];
-            const float u = tile_vals[jl][32 * tl + 16 + (e & 15)];
-            x[t] = glu(A.activation, g, u, A.alpha, A.limit);
-        }
-        float amax = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) amax = fmaxf(amax, fabsf(x[t]));
-        amax = quad_max(amax);
-        if (live) {
-            const float d = amax / 127.0f;
-            const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-            const int jb = A.jobs[joff + jj];
-            uint8_t * out = A.rows_out + static_cast<int64_t>(jb) * A.out_lay.stride();
-            const int64_t e0 = static_cast<int64_t>(pair) * 32 + part * 8;
-            if (A.out_lay.weight_type == 39) {
-                half8_t c;
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    float v = rintf(x[t] * id);
-                    v = v > 127.0f ? 127.0f : (v < -128.0f ? -128.0f : v);
-                    c[t] = static_cast<_Float16>(v);
+                for (int k = 0; k < 4; ++k) {
+                    const int col = seg * 16 + 4 * k;
+                    const int64_t brow = static_cast<int64_t>(pair) * 64 + col;
+                    if (brow < S.rows)
+                        *reinterpret_cast<float4 *>(out + ggml_row(brow, S.rows, S.interleave)) =
+                            *reinterpret_cast<const float4 *>(&tile_vals[jl][col]);
                 }
-                *reinterpret_cast<half8_t *>(out + e0 * 2) = c;
-            } else {
-                uint64_t c = 0;
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    float v = rintf(x[t] * id);
-                    v = v > 127.0f ? 127.0f : (v < -128.0f ? -128.0f : v);
-                    c |= static_cast<uint64_t>(static_cast<uint8_t>(static_cast<signed char>(v))) << (8 * t);
-                }
-                *reinterpret_cast<uint64_t *>(out + e0) = c;
             }
-            if (part == 0) {
-                reinterpret_cast<float *>(out + A.out_lay.da_offset())[pair] = static_cast<float>(static_cast<_Float16>(d));
-                if (pair == 0) *reinterpret_cast<int *>(out + A.out_lay.flag_offset()) = 0;   // never -128
+        } else {
+            // one 32-element GLU block per job, eight elements per thread
+            const int part = threadIdx.x & 3;
+            const bool live = jj < count;
+            float x[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int e = part * 8 + t;                 // element of the block
+                const int tl = e >> 4;                      // bank tile of the pair
+                const float g = tile_vals[jl][32 * tl + (e & 15)];
+                const float u = tile_vals[jl][32 * tl + 16 + (e & 15)];
+                x[t] = glu(A.activation, g, u, A.alpha, A.limit);
+            }
+            float amax = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) amax = fmaxf(amax, fabsf(x[t]));
+            amax = quad_max(amax);
+            if (live) {
+                const float d = amax / 127.0f;
+                const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+                const int jb = A.jobs[joff + jj];
+                uint8_t * out = A.rows_out + static_cast<int64_t>(jb) * A.out_lay.stride();
+                const int64_t e0 = static_cast<int64_t>(pair) * 32 + part * 8;
+                if (A.out_lay.weight_type == 39) {
+                    half8_t c;
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        float v = rintf(x[t] * id);
+                        v = v > 127.0f ? 127.0f : (v < -128.0f ? -128.0f : v);
+                        c[t] = static_cast<_Float16>(v);
+                    }
+                    *reinterpret_cast<half8_t *>(out + e0 * 2) = c;
+                } else {
+                    uint64_t c = 0;
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        float v = rintf(x[t] * id);
+                        v = v > 127.0f ? 127.0f : (v < -128.0f ? -128.0f : v);
+                        c |= static_cast<uint64_t>(static_cast<uint8_t>(static_cast<signed char>(v))) << (8 * t);
+                    }
+                    *reinterpret_cast<uint64_t *>(out + e0) = c;
+                }
+                if (part == 0) {
+                    reinterpret_cast<float *>(out + A.out_lay.da_offset())[pair] = static_cast<float>(static_cast<_Float16>(d));
+                    if (pair == 0) *reinterpret_cast<int *>(out + A.out_lay.flag_offset()) = 0;   // never -128
+                }
             }
         }
     }
 }
 
-// Tiles of kJobTile jobs per active expert, in active order: one workgroup, wave scans plus a
+// Tiles of job_tile jobs per active expert, in active order: one workgroup, wave scans plus a
 // scan of the 16 wave totals.
 __global__ __launch_bounds__(1024) void gemm_tiles_kernel(const int32_t * counts, const int32_t * active,
-                                                          const int32_t * n_active, const int32_t * filter, int max_tiles,
+                                                          const int32_t * n_active, const int32_t * filter, int job_tile,
+                                                          int max_tiles,
                                                           int32_t * tile_expert, int32_t * tile_start, int32_t * n_tiles,
                                                           int32_t * error) {
     __shared__ int s_wave[16];
@@ -740,7 +772,7 @@ __global__ __launch_bounds__(1024) void gemm_tiles_kernel(const int32_t * counts
     const int a = threadIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int e = a < na ? active[a] : 0;
     const bool kept = a < na && (filter == nullptr || filter[e] >= 0);   // filtered experts get no tiles
-    const int nt = kept ? (counts[e] + kJobTile - 1) / kJobTile : 0;
+    const int nt = kept ? (counts[e] + job_tile - 1) / job_tile : 0;
     int incl = nt;
     for (int off = 1; off < 64; off <<= 1) {
         const int v = __shfl_up(incl, off);
@@ -754,7 +786,7 @@ __global__ __launch_bounds__(1024) void gemm_tiles_kernel(const int32_t * counts
     for (int t = 0; t < nt; ++t) {
         if (base + t < max_tiles) {
             tile_expert[base + t] = e;
-            tile_start[base + t] = t * kJobTile;
+            tile_start[base + t] = t * job_tile;
         } else {
             *error = 1;
         }
@@ -1111,12 +1143,13 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(MxArgs A) {
 
 }  // namespace
 
-int64_t gemm_max_tiles(int64_t n_as, int64_t n_entries) {
-    return (n_entries + kJobTile - 1) / kJobTile + (n_as < n_entries ? n_as : n_entries);
+int64_t gemm_max_tiles(int64_t n_as, int64_t n_entries, int job_tile) {
+    return (n_entries + job_tile - 1) / job_tile + (n_as < n_entries ? n_as : n_entries);
 }
 
+// sized for the smaller job tile of the two kernels that share it
 size_t gemm_tiles_bytes(int64_t n_as, int64_t n_entries) {
-    return static_cast<size_t>((2 * gemm_max_tiles(n_as, n_entries) + 8) * sizeof(int32_t));
+    return static_cast<size_t>((2 * gemm_max_tiles(n_as, n_entries, kMxJobTile) + 8) * sizeof(int32_t));
 }
 
 void launch_gemm_rows_from_f32(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, const GemmRowLayout & lay,
@@ -1146,15 +1179,15 @@ void launch_grouped_gemm(const GemmParams & p, hipStream_t stream) {
             "GLU epilogue needs an interleaved gate|up bank with rows % 64 == 0 and a matching output layout");
     require(p.epilogue == 1 || p.dst != nullptr, "missing GEMM output");
     require(p.n_as >= 1 && p.n_as <= 1024 && p.n_entries >= 1, "GEMM group shape out of range");
-    const int64_t max_tiles = gemm_max_tiles(p.n_as, p.n_entries);
+    const int64_t max_tiles = gemm_max_tiles(p.n_as, p.n_entries, kJobTile);
     require(max_tiles <= 65535, "too many GEMM tiles for one launch");
     int32_t * tile_expert = static_cast<int32_t *>(p.tiles);
     int32_t * tile_start = tile_expert + max_tiles;
     int32_t * n_tiles = tile_start + max_tiles;
     if (!p.tiles_ready) {
         hipLaunchKernelGGL(gemm_tiles_kernel, dim3(1), dim3(1024), 0, stream, p.group.counts, p.group.active,
-                           p.group.n_active, p.tile_filter, static_cast<int>(max_tiles), tile_expert, tile_start, n_tiles,
-                           p.group.error);
+                           p.group.n_active, p.tile_filter, kJobTile, static_cast<int>(max_tiles), tile_expert, tile_start,
+                           n_tiles, p.group.error);
         check_hip(hipGetLastError(), "GEMM tile list launch");
     }
     GemmArgs a{};
@@ -1173,6 +1206,7 @@ void launch_grouped_gemm(const GemmParams & p, hipStream_t stream) {
     a.tile_start = tile_start;
     a.n_tiles = n_tiles;
     a.bias = p.bias;
+    a.row_scale = p.row_scale;
     a.dst = p.dst;
     a.dst_vec4 = p.dst != nullptr && reinterpret_cast<uintptr_t>(p.dst) % 16 == 0 && bank.rows % 4 == 0;
     a.rows_out = p.rows_out;
@@ -1211,13 +1245,13 @@ void launch_mx_gemm(const vbm_bank & bank, const int32_t * expert_to_slot, const
                     float * dst, hipStream_t stream) {
     require(bank.type == VBM_TYPE_MXFP4, "the MXFP8 experiment runs on MXFP4 banks");
     require(n_as >= 1 && n_as <= 1024 && n_entries >= 1, "GEMM group shape out of range");
-    const int64_t max_tiles = gemm_max_tiles(n_as, n_entries);
+    const int64_t max_tiles = gemm_max_tiles(n_as, n_entries, kMxJobTile);
     require(max_tiles <= 65535, "too many GEMM tiles for one launch");
     int32_t * tile_expert = static_cast<int32_t *>(tiles);
     int32_t * tile_start = tile_expert + max_tiles;
     int32_t * n_tiles = tile_start + max_tiles;
     hipLaunchKernelGGL(gemm_tiles_kernel, dim3(1), dim3(1024), 0, stream, group.counts, group.active, group.n_active,
-                       nullptr, static_cast<int>(max_tiles), tile_expert, tile_start, n_tiles, group.error);
+                       nullptr, kMxJobTile, static_cast<int>(max_tiles), tile_expert, tile_start, n_tiles, group.error);
     check_hip(hipGetLastError(), "GEMM tile list launch");
     MxArgs a{};
     a.bank = bank.base;

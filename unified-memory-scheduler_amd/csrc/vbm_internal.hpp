@@ -106,6 +106,8 @@ void launch_quantize_q8_0(const float * x, int64_t n_rows, int64_t k, int64_t x_
 void launch_router(const float * router_w, const float * router_b, const float * x, int64_t hidden,
                    float * logits, int64_t n_expert, int64_t n_tokens, int64_t top_k, int32_t * ids,
                    float * weights, hipStream_t stream);
+// out[t] = sum over ranks r in order of y[t][r] * weights[t][r] (ggml MUL then ADDs); weights
+// NULL: the rows are already weighted, out[t] = sum of y[t][r] in rank order.
 void launch_combine(const float * y, const float * weights, int64_t rows, int64_t n_ids, int64_t n_tokens,
                     float * out, hipStream_t stream);
 void launch_glu(int activation, const float * gate, const float * up, float * out, int64_t n_rows,
@@ -185,6 +187,7 @@ struct GemmParams {
     GroupBuffers group;
     void * tiles;                     // gemm_tiles_bytes(n_as, n_entries) of scratch
     const float * bias;
+    const float * row_scale;          // epilogue 0: per-job factor after the bias (routing weights), or null
     float * dst;                      // epilogue 0: [job][rows]
     uint8_t * rows_out;               // epilogue 1: GLU + Q8_0 rows per job (out_layout)
     GemmRowLayout out_layout;
@@ -195,7 +198,8 @@ struct GemmParams {
     int64_t grid_tiles;               // > 0: bound on the tiles left by tile_filter (launch size), else 0
     bool tiles_ready;                 // `tiles` already holds this group's list (same group and filter)
 };
-int64_t gemm_max_tiles(int64_t n_as, int64_t n_entries);
+constexpr int64_t kGemmJobTile = 128;   // jobs per grouped-GEMM workgroup (one expert's job tile)
+int64_t gemm_max_tiles(int64_t n_as, int64_t n_entries, int job_tile);
 size_t gemm_tiles_bytes(int64_t n_as, int64_t n_entries);
 void launch_grouped_gemm(const GemmParams & p, hipStream_t stream);
 // MXFP4 x MXFP8 experiment on the block-scaled matrix cores: OCP MX quantization of fp32 rows
@@ -231,14 +235,17 @@ LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint
 // Prefill through the grouped GEMM in steps: the input rows and the token->expert grouping once,
 // then one or more passes over disjoint expert subsets (experts whose expert_to_slot entry is
 // -1 are skipped: their workgroups exit without writing), each writing the down outputs y of its
-// entries; the combine of y runs once all entries are written. events (optional) [4]: around the
+// entries (times the entries' routing weights route_w when given: ggml's ADD_ID then MUL, so the
+// combine is then the rank-ordered ADDs alone); the combine of y runs once all entries are
+// written. events (optional) [4]: around the
 // pass's gate_up and down GEMMs. grid_tiles > 0: the pass's expert->slot map also filters the tile
-// list, and grid_tiles bounds its tiles (sum over its experts of ceil(count / 64)), so a pass over a
+// list, and grid_tiles bounds its tiles (sum over its experts of ceil(count / kGemmJobTile)), so a pass over a
 // few experts launches only their workgroups.
 void prefill_prepare(const vbm_moe_layer_desc & d, const float * x, const int32_t * ids, int64_t n_tokens,
                      const LayerWorkspace & w, hipStream_t s);
 void prefill_pass(const vbm_moe_layer_desc & d, const int32_t * expert_to_slot, int64_t n_tokens,
-                  const LayerWorkspace & w, void * const * events, hipStream_t s, int64_t grid_tiles = 0);
+                  const LayerWorkspace & w, const float * route_w, void * const * events, hipStream_t s,
+                  int64_t grid_tiles = 0);
 
 // Kernel A of the fused single-token decode: routing, input combine + Q8_0, gate_up GEMV, GLU,
 // requantization into the down activation rows.

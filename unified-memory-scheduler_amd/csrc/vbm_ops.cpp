@@ -124,7 +124,8 @@ void prefill_prepare(const vbm_moe_layer_desc & d, const float * x, const int32_
 }
 
 void prefill_pass(const vbm_moe_layer_desc & d, const int32_t * expert_to_slot, int64_t n_tokens,
-                  const LayerWorkspace & w, void * const * events, hipStream_t s, int64_t grid_tiles) {
+                  const LayerWorkspace & w, const float * route_w, void * const * events, hipStream_t s,
+                  int64_t grid_tiles) {
     const int64_t K = d.top_k;
     const GemmRowLayout gx{d.hidden / 32, d.gate_up->type}, ga{d.intermediate / 32, d.down->type};
     GemmParams p{};
@@ -158,6 +159,7 @@ void prefill_pass(const vbm_moe_layer_desc & d, const int32_t * expert_to_slot, 
     p.lay = ga;
     p.b_ne1 = K;
     p.bias = d.down_bias;
+    p.row_scale = route_w;
     p.dst = w.y;
     p.rows_out = nullptr;
     p.epilogue = 0;
@@ -354,8 +356,8 @@ void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits
     if (use_gemm(*d, n_tokens) && gemm_pays(n_tokens, K, d->n_expert)) {
         // Prefill-sized groups: MFMA grouped GEMM (exact block dots, fp32 accumulation order).
         prefill_prepare(*d, x, ids_d, n_tokens, w, s);
-        prefill_pass(*d, d->expert_to_slot, n_tokens, w, events, s);
-        launch_combine(w.y, w_d, H, K, n_tokens, out, s);
+        prefill_pass(*d, d->expert_to_slot, n_tokens, w, w_d, events, s);
+        launch_combine(w.y, nullptr, H, K, n_tokens, out, s);   // rows weighted in the down epilogue
         return;
     }
     const XrowLayout lx{H / 32, d->gate_up->type}, la{I / 32, d->down->type};

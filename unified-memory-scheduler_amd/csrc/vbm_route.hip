@@ -201,6 +201,12 @@ __global__ void combine_kernel(const float * __restrict__ y, const float * __res
     if (i >= rows) return;
     const int64_t idx = t * rows + i;
     const float * yt = y + t * n_ids * rows + i;
+    if (w == nullptr) {   // rows already weighted (the grouped GEMM's epilogue): the rank-ordered ADDs
+        float acc = yt[0];
+        for (int r = 1; r < n_ids; ++r) acc = acc + yt[r * rows];
+        out[idx] = acc;
+        return;
+    }
     const float * wt = w + t * n_ids;
     float acc = yt[0] * wt[0];
     for (int r = 1; r < n_ids; ++r) {

@@ -587,7 +587,7 @@ vbm_status vbm_tier_prefill(vbm_tier * t, int64_t layer, const float * x, const 
         check_status(vbm_admission_slot_map(t->admission, layer, maps), "prefill slot map");
         std::vector<int64_t> count(static_cast<size_t>(E), 0);
         for (int64_t i = 0; i < T * K; ++i) ++count[static_cast<size_t>(t->pf_ids_host[i])];
-        auto tiles_of = [&](int64_t e) { return (count[static_cast<size_t>(e)] + 63) / 64; };   // GEMM job tiles
+        auto tiles_of = [&](int64_t e) { return (count[static_cast<size_t>(e)] + kGemmJobTile - 1) / kGemmJobTile; };   // GEMM job tiles
         std::vector<char> routed(static_cast<size_t>(E), 0);
         for (int64_t e = 0; e < E; ++e) routed[static_cast<size_t>(e)] = count[static_cast<size_t>(e)] > 0;
         std::vector<int32_t> cold;
@@ -613,7 +613,7 @@ vbm_status vbm_tier_prefill(vbm_tier * t, int64_t layer, const float * x, const 
         }
         check_hip(hipMemcpyAsync(t->pf_maps, maps, sizeof(int32_t) * E * (n_chunks + 1), hipMemcpyHostToDevice, s),
                   "prefill maps");
-        if (resident_hits) prefill_pass(desc, t->pf_maps, T, w, nullptr, s, resident_tiles);
+        if (resident_hits) prefill_pass(desc, t->pf_maps, T, w, w.weights, nullptr, s, resident_tiles);
         for (int64_t j = 0; j < n_chunks; ++j) {
             const int b = K >= 2 ? static_cast<int>(j % 2) : 0;
             if (j >= (K >= 2 ? 2 : 1))    // the half's previous chunk must be consumed first
@@ -626,11 +626,11 @@ vbm_status vbm_tier_prefill(vbm_tier * t, int64_t layer, const float * x, const 
             }
             check_hip(hipEventRecord(t->pf_ready[b], t->copy_stream), "prefill ready");
             check_hip(hipStreamWaitEvent(s, t->pf_ready[b], 0), "prefill publish");
-            prefill_pass(desc, t->pf_maps + (j + 1) * E, T, w, nullptr, s, chunk_tiles);
+            prefill_pass(desc, t->pf_maps + (j + 1) * E, T, w, w.weights, nullptr, s, chunk_tiles);
             check_hip(hipEventRecord(t->pf_done[b], s), "prefill done");
         }
         // 3. rank-ordered weighted combine of every (token, rank) down output
-        launch_combine(w.y, w.weights, H, K, T, out, s);
+        launch_combine(w.y, nullptr, H, K, T, out, s);   // rows weighted in the down epilogues
         if (ids) check_hip(hipMemcpyAsync(ids, w.ids, sizeof(int32_t) * T * K, hipMemcpyDeviceToDevice, s), "ids copy");
         if (weights) check_hip(hipMemcpyAsync(weights, w.weights, sizeof(float) * T * K, hipMemcpyDeviceToDevice, s),
                                "weights copy");
