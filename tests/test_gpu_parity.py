@@ -348,6 +348,39 @@ def test_mul_mat_id_every_chunk_width_bitwise(gpu, orc, type_id):
     bank.destroy()
 
 
+def test_mul_mat_id_mxfp4_matrix_path_exponent_ranges_bitwise(gpu, orc):
+    """The MXFP4 batched GEMV runs chunks of 3..8 tokens on the matrix cores and folds the block
+    exponents into the weight conversion only when every exponent of a tile pair's rows lies in
+    [-14, 12] (ggml e8m0 bytes 114..140); other tile pairs take ldexp per output. Per expert:
+    all in range (the generator's), both boundaries (114 and 140) in range, one byte just outside
+    (113 or 141) in one tile pair only, a tail block outside (K = 576: two groups of eight blocks
+    and a two-block tail), and every byte far outside (90..180, finite results); top-1 ids with
+    counts 3, 4, 5, 8 and 12 reach widths 4 and 8 (12 = 8 + 4), rows 96 (a half-live pair)."""
+    k, rows = 576, 96
+    nb = k // 32
+    counts = [4, 8, 3, 5, 12, 8]
+    experts = len(counts)
+    w = H.synth_weights(H.MX, 77, 1, experts, rows, k).reshape(experts, rows, nb, 17)
+    w[1, 0, 0, 0], w[1, 95, nb - 1, 0] = 114, 140              # boundaries: still folded
+    w[2, 5, 3, 0] = 113                                        # pair 0 unfolded, pair 1 folded
+    w[3, 70, 9, 0] = 141                                       # pair 1 unfolded, pair 0 folded
+    w[4, 33, nb - 1, 0] = 100                                  # a tail block of pair 0
+    rng = np.random.default_rng(77)
+    w[5, :, :, 0] = rng.integers(90, 181, size=(rows, nb)).astype(np.uint8)
+    w = w.reshape(-1)
+    bank = H.make_bank(H.MX, w, experts, rows, k)
+    ids = rng.permutation(np.repeat(np.arange(experts), counts)).astype(np.int32).reshape(-1, 1)
+    tokens = ids.shape[0]
+    bias = gpu.synth_normal(77, 2, 0, experts * rows, 0.0, 0.02)
+    x = gpu.synth_normal(77, 3, 0, tokens * k).reshape(tokens, 1, k)
+    print(f"[matrix path exponents] tokens={tokens} counts={counts}", flush=True)
+    got = H.mul_mat_id(bank, experts, x, gpu.TYPE_F32, 1, ids, 1, bias=bias)
+    ref = orc.mul_mat_id(39, w, k, rows, experts, 0, x, 1, ids, 1, tokens, 1, bias=bias)
+    assert np.all(np.isfinite(ref))
+    assert H.bits_equal(got, ref), H.diff_report(got, ref)
+    bank.destroy()
+
+
 def test_mul_mat_id_randomized_shapes_bitwise(gpu, orc):
     """24 seeded random MUL_MAT_ID cases in the exact order against the oracle, bit for bit:
     MXFP4 or Q8_0 weights, 1..40 experts, top-k 1..8 (distinct per token, some -1 masks), 1..48

@@ -151,11 +151,15 @@ struct GemmStage {
     static constexpr int OFF_DA = ACT, OFF_W = OFF_DA + DA, OFF_M = OFF_W + W;
     static constexpr int STAGE = OFF_M + M;
     static constexpr int BYTES = S * STAGE;
-    // DMA instructions per wave and chunk: activation rows (1 KiB each), block scales, weights, meta
+    // DMA instructions per wave and chunk: activation rows (1 KiB each, ACT_JOBS job rows), block
+    // scales, weights, meta. A wave skips the activation loads whose job rows are all past the
+    // tile's live jobs, so its count per chunk varies; the wait before each chunk's barrier drains
+    // every load of the wave, which the two-stage ring allows (the next chunk's loads are issued
+    // after it).
+    static constexpr int ACT_JOBS = 1024 / ROW;
     static constexpr int ACT_DMA = ACT / 1024 / 4;
     static constexpr int W_DMA = W / 256 / 4;
-    static constexpr int PER_CHUNK = ACT_DMA + 1 + W_DMA + 1;
-    static_assert((S - 2) * PER_CHUNK < 64, "vmcnt range");
+    static_assert(S == 2, "the per-chunk wait is vmcnt(0)");
 };
 
 // Global-to-LDS DMA (global_load_lds_*): lane l's bytes land at LDS address m0 + l * size. The
@@ -284,13 +288,14 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
     bool slow = false;
     if constexpr (FLAGGED) slow = __syncthreads_or(flagged != 0) != 0;
 
-    // Stage loaders (global-to-LDS DMA). Every wave issues the same G::PER_CHUNK loads per chunk
-    // (lanes that have nothing to load are masked, clamped sources keep every address inside the
-    // operands), so the wait before each barrier is a constant count.
+    // Stage loaders (global-to-LDS DMA). Lanes that have nothing to load are masked, and clamped
+    // sources keep every address inside the operands.
     //   - activations: wave w's x4 loads j cover 16 (Q8_0) or 8 (MXFP4) job rows of the chunk;
     //     the 16-byte parts of row r sit at part p ^ s(r) (s(r) = (r >> 1) & 3, resp. r & 7) so
-    //     the fragment reads of 16 consecutive rows spread over the banks; a row past the tile's
-    //     jobs reads the first job's row (its columns are never stored);
+    //     the fragment reads of 16 consecutive rows spread over the banks; within a load that
+    //     holds a live job, a row past the tile's jobs reads the first job's row, and a load
+    //     whose rows are all past them is skipped (wave-uniform): those LDS rows keep stale
+    //     bytes, which reach only the matrix columns of jobs that are never stored;
     //   - block scales: lane l of wave w loads job 32w + l / 2, block l % 2;
     //   - weights: dword loads; Q8_0 load I = 4w + i covers tile I >> 3, slice pair (I >> 1) & 3,
     //     rows 16 (I & 1) .. +15 (lane: row l >> 2, unit dword l & 3); MXFP4 load I = 2w + i covers
@@ -298,6 +303,7 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
     //     a tile past the bank's rows reads the pair's first tile (its rows are never stored);
     //   - meta: lanes 0..15 of wave w load the dword of rows 16 (w & 1) .. +15 of tile w >> 1.
     const int wu = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int live_rows = __builtin_amdgcn_readfirstlane(count - j0);   // the tile's live jobs
     // LDS address of the stage buffers: a generic pointer to LDS is the aperture base plus the
     // LDS address in its low 32 bits.
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
@@ -327,7 +333,8 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
         const uint32_t sb = lds0 + st * G::STAGE;
 #pragma unroll
         for (int j = 0; j < G::ACT_DMA; ++j)
-            lds_dma_x4(act_src[j] + static_cast<int64_t>(c) * G::ROW, sb + (wu * G::ACT_DMA + j) * 1024);
+            if (G::ACT_JOBS * (wu * G::ACT_DMA + j) < live_rows)
+                lds_dma_x4(act_src[j] + static_cast<int64_t>(c) * G::ROW, sb + (wu * G::ACT_DMA + j) * 1024);
         lds_dma_x1(da_src + static_cast<int64_t>(c) * CB * 4, sb + G::OFF_DA + wu * 256);
 #pragma unroll
         for (int i = 0; i < G::W_DMA; ++i) {
@@ -562,9 +569,8 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
                     for (int bb = 0; bb < CB; ++bb) do_block(bb);
                 }
             }
-            // the stage of chunk c + 1, issued S - 1 chunks before it is read: only the loads of
-            // the last S - 2 chunks may remain in flight
-            lds_dma_wait<(G::S - 2) * G::PER_CHUNK>();
+            // the stage of chunk c + 1, issued at the top of this chunk
+            lds_dma_wait<0>();
             __syncthreads();
         }
 

@@ -30,6 +30,8 @@ namespace vbm {
 namespace {
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef const __attribute__((address_space(4))) uint8_t * cptr;   // constant: uniform loads -> s_load
@@ -354,6 +356,157 @@ __device__ __forceinline__ void stream_groups_buf(Group (&ring)[D], const BufLan
     }
 }
 
+// ------------------------------------------------------ batched MXFP4 GEMV on the matrix cores
+// Chunks of four or more tokens without the -128 correction take the lane slices' integer dots
+// from v_mfma_f32_4x4x4_16b_f16, whose output register r of lane l is the dot over k of
+// A(lane 4(l/4) + r, k) and B(lane l, k). A is the lane's own row slice (lane = row, as in the
+// scalar path) and B the activation slice of token 4g + l % 4, so register r of lane l holds the
+// slice dot of row 4(l/4) + r and token 4g + l % 4: one instruction gives the wave's 64 rows x 4
+// tokens, each the value the two v_dot2 of the scalar path give (integers below 2^24 are exact
+// in any order). Every (row, token, slice) keeps the CPU's chains: one FMA per block into the even
+// or odd chain of the block.
+//
+// FOLD: when every exponent e of the tile pair's rows lies in [-14, 12], the conversion
+// scales the e2m1 values by 2^(e+1) (exact normal f16), the dot comes out as 2^e * dot, and the
+// chain's FMA takes d_act alone: d_act * (2^e * dot) is exactly the product ldexp(d_act, e) * dot
+// (no overflow or underflow in that range), rounded once inside the same FMA. Otherwise each
+// output takes ldexp(d_act, e) with e broadcast from its row's lane within the quad.
+template <int MT>
+using MmAcc = float[MT / 4][4][2];
+
+// One block for the MT / 4 token groups: `a[g]` is token group g's activation slice (4 f16 codes)
+// and `d[g]` its block scale, both for the lane's token 4g + l % 4.
+template <int MT, int SEL, int PAR, bool FOLD>
+__device__ __forceinline__ void mx_block_mm(unsigned dw, int e, const u32x2 (&a)[MT / 4], const float (&d)[MT / 4],
+                                            MmAcc<MT> & acc) {
+    constexpr int G = MT / 4;
+    const float sc = FOLD ? __builtin_bit_cast(float, (e + 128) << 23) : 2.0f;
+    const half2_t w01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, sc, SEL);
+    const half2_t w23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, sc, SEL + 1);
+    const half4_t wv = half4_t{w01.x, w01.y, w23.x, w23.y};
+    f32x4_t v[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        v[g] = __builtin_amdgcn_mfma_f32_4x4x4f16(wv, __builtin_bit_cast(half4_t, a[g]), f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    if constexpr (FOLD) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[g][r][PAR] = __builtin_fmaf(d[g], v[g][r], acc[g][r][PAR]);
+    } else {
+        int eq[4];
+        eq[0] = __builtin_amdgcn_mov_dpp(e, 0x00, 0xf, 0xf, false);   // quad_perm [r, r, r, r]
+        eq[1] = __builtin_amdgcn_mov_dpp(e, 0x55, 0xf, 0xf, false);
+        eq[2] = __builtin_amdgcn_mov_dpp(e, 0xAA, 0xf, 0xf, false);
+        eq[3] = __builtin_amdgcn_mov_dpp(e, 0xFF, 0xf, 0xf, false);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[g][r][PAR] = __builtin_fmaf(__builtin_amdgcn_ldexpf(d[g], eq[r]), v[g][r], acc[g][r][PAR]);
+    }
+}
+
+// Two consecutive blocks b, b + 1 of one code dword (e0, e1 their exponents); `a2[g]` holds both
+// blocks' activation slices of token group g, `d0[g]` / `d1[g]` their scales.
+template <int MT, bool FOLD>
+__device__ __forceinline__ void mx_pair_mm(unsigned dw, int e0, int e1, const u32x4 (&a2)[MT / 4], const float (&d0)[MT / 4],
+                                           const float (&d1)[MT / 4], MmAcc<MT> & acc) {
+    constexpr int G = MT / 4;
+    u32x2 a0[G], a1[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        a0[g] = u32x2{a2[g].x, a2[g].y};
+        a1[g] = u32x2{a2[g].z, a2[g].w};
+    }
+    mx_block_mm<MT, 0, 0, FOLD>(dw, e0, a0, d0, acc);
+    mx_block_mm<MT, 2, 1, FOLD>(dw, e1, a1, d1, acc);
+}
+
+// One group of eight blocks starting at block b; each block reads its activation slices and
+// scales itself, and the fence after it keeps the scheduler from hoisting every read of the group
+// (register spills otherwise).
+template <int MT, bool FOLD>
+__device__ __forceinline__ void mx_group_mm(const u32x4 & c, const u32x2 & m, int b, const uint8_t * la_lane,
+                                            const uint8_t * lda_lane, int tok_bytes, MmAcc<MT> & acc) {
+    constexpr int G = MT / 4;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const unsigned dw = c[j >> 1];
+        const int e = static_cast<signed char>((j < 4 ? m.x : m.y) >> (8 * (j & 3)));
+        u32x2 a[G];
+        float d[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            a[g] = *reinterpret_cast<const u32x2 *>(la_lane + 4 * g * tok_bytes + (b + j) * 8);
+            d[g] = *reinterpret_cast<const float *>(lda_lane + 4 * g * tok_bytes + (b + j) * 4);
+        }
+        if (j & 1) mx_block_mm<MT, 2, 1, FOLD>(dw, e, a, d, acc);
+        else mx_block_mm<MT, 0, 0, FOLD>(dw, e, a, d, acc);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Sixteen exponent bytes, each (signed) in [-14, 12].
+__device__ __forceinline__ bool exps_foldable(const u32x4 & w) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int e = static_cast<signed char>(w[i >> 2] >> (8 * (i & 3)));
+        ok = ok && e >= -14 && e <= 12;
+    }
+    return ok;
+}
+
+template <int MT, int D, bool FOLD>
+__device__ __forceinline__ void stream_groups_mm(Group (&ring)[D], const BufLane & B, int nb, const uint8_t * la_lane,
+                                                 const uint8_t * lda_lane, int tok_bytes, MmAcc<MT> & acc) {
+    const int groups = nb / 8;
+    for (int g0 = 0; g0 < groups; g0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const int g = g0 + i;
+            if (g < groups) {
+                const Group cur = ring[i];
+                if (g + D < groups) ring[i] = load_group_buf(B, g + D);
+                mx_group_mm<MT, FOLD>(cur.c, cur.m, g * 8, la_lane, lda_lane, tok_bytes, acc);
+            }
+        }
+    }
+}
+
+// The tail blocks (after the full groups, in chain order) with the unfolded scales.
+template <int MT>
+__device__ __forceinline__ void apply_tail_mm(const Tail & tl, int nb, const uint8_t * la_lane, const uint8_t * lda_lane,
+                                              int tok_bytes, MmAcc<MT> & acc) {
+    constexpr int G = MT / 4;
+    const int groups = nb / 8, n = (nb % 8) / 2;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        if (i < n) {
+            const int b = groups * 8 + 2 * i;
+            u32x4 a2[G];
+            float d0[G], d1[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                a2[g] = *reinterpret_cast<const u32x4 *>(la_lane + 4 * g * tok_bytes + b * 8);
+                const float * dp = reinterpret_cast<const float *>(lda_lane + 4 * g * tok_bytes + b * 4);
+                d0[g] = dp[0];
+                d1[g] = dp[1];
+            }
+            mx_pair_mm<MT, false>(tl.c[i], static_cast<signed char>(tl.m[i] & 0xFFu), static_cast<signed char>(tl.m[i] >> 8),
+                                  a2, d0, d1, acc);
+        }
+    }
+}
+
+// The matrix-core path serves MXFP4 chunks of four or more tokens in the kernels for rows this
+// library quantized (never -128); the kernels for caller-quantized rows keep the scalar path.
+template <int TYPE, int M, bool NEG>
+constexpr bool use_mfma() {
+    return TYPE == 39 && M >= 4 && !NEG;
+}
+
 // Stages the exponents / scales of a workgroup's (up to) two consecutive tiles: loads are issued
 // into registers first (ahead of the code stream, so waiting for them never waits for codes),
 // then written to LDS by store_meta.
@@ -592,6 +745,16 @@ __device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane &
     constexpr int D = 2;
     Group ring[D];
     preload_ring_buf<TYPE, D>(ring, B, nb);
+    // The matrix path folds the block exponents into the weight conversion when every exponent of
+    // the tile pair's live rows lies in [-14, 12]: one 16-byte load per thread (K <= 4096: at most
+    // 8 KiB of exponents), issued with the ring and checked at the staging barrier.
+    u32x4 ex = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (use_mfma<TYPE, M, NEG>()) {
+        const int pair_tiles = (2 * static_cast<int>(blockIdx.x) + 1) * 32 < S.rows ? 2 : 1;
+        const int meta0 = static_cast<int>(S.codes_bytes) + 2 * static_cast<int>(blockIdx.x) * 32 * nb;
+        if (static_cast<int>(threadIdx.x) * 16 < pair_tiles * 32 * nb)
+            ex = __builtin_amdgcn_raw_buffer_load_b128(B.rsrc, meta0 + static_cast<int>(threadIdx.x) * 16, 0, 0);
+    }
     // Stage the chunk's activation rows (and their -128 flags) in LDS.
     if (threadIdx.x == 0) *s_flag = 0;
     __syncthreads();
@@ -608,24 +771,46 @@ __device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane &
         if (threadIdx.x == 0) flag |= *reinterpret_cast<const int *>(xr + A.lay.flag_offset());
     }
     if (threadIdx.x == 0 && flag) *s_flag = 1;
-    __syncthreads();
-    float acc[M][2];
-#pragma unroll
-    for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.0f;
-    // widths 1 and 2 only ever carry full chunks: a constant count drops the per-token checks
-    const int mc = M <= 2 ? M : mcount;
+    bool fold = false;
+    if constexpr (use_mfma<TYPE, M, NEG>()) fold = __syncthreads_and(exps_foldable(ex) ? 1 : 0) != 0;
+    else __syncthreads();
     Tail tl;
-    if (NEG && *s_flag) {
-        stream_groups_buf<TYPE, M, true, D>(ring, B, nb, la, lda, tok_bytes, mc, acc);
-        preload_tail_buf<TYPE>(tl, B, nb);
-        apply_tail<TYPE, M, true, false>(tl, nullptr, r, nb, la, lda, tok_bytes, mc, acc);
-    } else {
-        stream_groups_buf<TYPE, M, false, D>(ring, B, nb, la, lda, tok_bytes, mc, acc);
-        preload_tail_buf<TYPE>(tl, B, nb);
-        apply_tail<TYPE, M, false, false>(tl, nullptr, r, nb, la, lda, tok_bytes, mc, acc);
-    }
+    if constexpr (use_mfma<TYPE, M, NEG>()) {
+        MmAcc<M> acc;
 #pragma unroll
-    for (int m = 0; m < M; ++m) red[(m * 8 + k) * 64 + lane] = acc[m][0] + acc[m][1];
+        for (int g = 0; g < M / 4; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[g][i][0] = acc[g][i][1] = 0.0f;
+        const uint8_t * la_lane = la + (lane & 3) * tok_bytes;   // token 4g + lane % 4
+        const uint8_t * lda_lane = reinterpret_cast<const uint8_t *>(lda) + (lane & 3) * tok_bytes;
+        if (fold) stream_groups_mm<M, D, true>(ring, B, nb, la_lane, lda_lane, tok_bytes, acc);
+        else stream_groups_mm<M, D, false>(ring, B, nb, la_lane, lda_lane, tok_bytes, acc);
+        preload_tail_buf<TYPE>(tl, B, nb);
+        apply_tail_mm<M>(tl, nb, la_lane, lda_lane, tok_bytes, acc);
+        // register i of lane l: row 4(l / 4) + i (the red layout's lane index) of token 4g + l % 4
+#pragma unroll
+        for (int g = 0; g < M / 4; ++g)
+            *reinterpret_cast<float4 *>(&red[((4 * g + (lane & 3)) * 8 + k) * 64 + 4 * (lane >> 2)]) =
+                float4{acc[g][0][0] + acc[g][0][1], acc[g][1][0] + acc[g][1][1], acc[g][2][0] + acc[g][2][1],
+                       acc[g][3][0] + acc[g][3][1]};
+    } else {
+        float acc[M][2];
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.0f;
+        // widths 1 and 2 only ever carry full chunks: a constant count drops the per-token checks
+        const int mc = M <= 2 ? M : mcount;
+        if (NEG && *s_flag) {
+            stream_groups_buf<TYPE, M, true, D>(ring, B, nb, la, lda, tok_bytes, mc, acc);
+            preload_tail_buf<TYPE>(tl, B, nb);
+            apply_tail<TYPE, M, true, false>(tl, nullptr, r, nb, la, lda, tok_bytes, mc, acc);
+        } else {
+            stream_groups_buf<TYPE, M, false, D>(ring, B, nb, la, lda, tok_bytes, mc, acc);
+            preload_tail_buf<TYPE>(tl, B, nb);
+            apply_tail<TYPE, M, false, false>(tl, nullptr, r, nb, la, lda, tok_bytes, mc, acc);
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) red[(m * 8 + k) * 64 + lane] = acc[m][0] + acc[m][1];
+    }
     __syncthreads();
     for (int mi = k; mi < mcount; mi += 8) {                           // wave k reduces tokens k, k+8, ...
         if (live) {
@@ -652,7 +837,7 @@ __device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane &
 // narrow width keeps the per-block token loop short).
 template <int TYPE, int MT, bool NEG>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void expert_gemv_kernel(KernelArgs A) {
-    __shared__ float red[MT * 8 * 64];
+    __shared__ __attribute__((aligned(16))) float red[MT * 8 * 64];
     __shared__ float vals[MT * 64];
     __shared__ int s_flag;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_tok[];   // MT activation rows
