@@ -3,22 +3,22 @@
 //
 // The CPU dot (tools/trace/cpu_mxfp4_vnni.cpp:49-68) splits every 32-element block into eight
 // 4-element lanes and keeps per-lane FMA chains (even/odd blocks for MXFP4; one chain for Q8_0),
-// then reduces the eight lanes with a fixed tree. Here one wavefront owns one lane slice k for 64
-// rows: lane = row, wave = slice, so
+// then reduces the eight lanes with a fixed tree. Here one wavefront owns one lane slice k of a
+// tile pair's rows: lane = row, wave = slice, so
 //   - every lane keeps exactly the CPU's chains for its (row, slice) and the final tree over the
-//     eight waves reproduces the CPU bits;
-//   - the activation slice a wave needs is the same for all its lanes, so it comes through scalar
-//     loads (SGPR operands of v_dot2 / v_dot4), costing no VGPRs and no LDS;
-//   - each lane loads its whole row slice of weights (K=2880 MXFP4: 180 B codes + 90 B exponents)
-//     into VGPRs up front: ~270 B in flight per lane saturates HBM even at batch 1, and the
-//     weights are then reused from registers for every token routed to the expert.
-// A 512-thread workgroup covers 64 rows (two 32-row bank tiles) of one active expert.
+//     eight slices (through LDS) reproduces the CPU bits;
+//   - each lane streams its row slice of weights (16 B of codes per group of blocks) through a
+//     register ring of coalesced 128-bit loads, and the weights are reused from registers for
+//     every token routed to the expert;
+//   - the activation rows are staged in LDS; a wave reads only its slice of them.
 //
-// Integer part (MXFP4): v_cvt_scalef32_pk_f16_fp4 with scale 2 turns two e2m1 nibbles into the
-// doubled-e2m1 integers {0,1,2,3,4,6,8,12,...} as f16; v_dot2 against f16 activation codes gives
-// the lane's 4-product integer exactly (all partial sums are integers below 2^24). The VPSIGNB
-// corner case (activation code -128 against a negative weight, cpu_mxfp4_vnni.cpp:43-44) runs on
-// a uniform slow path selected per activation row.
+// Integer part (MXFP4): v_cvt_scalef32_pk_f16_fp4 with scale 2 turns the slice's four e2m1
+// nibbles into the doubled-e2m1 integers {0,1,2,3,4,6,8,12,...} as f16, and the slice dot against
+// the f16 activation codes is exact (integers below 2^24). The decode kernels and the batched
+// chunks of three or more tokens take it from v_mfma_f32_4x4x4_16b_f16 (16 blocks of 4 rows x 4
+// tokens with K = 4: exactly one slice); chunks of one or two tokens take two v_dot2. Q8_0 uses
+// v_dot4. The VPSIGNB corner case (activation code -128 against a negative weight,
+// cpu_mxfp4_vnni.cpp:43-44) runs on a uniform slow path selected per activation row.
 //
 // Epilogue 1 (fused gate|up bank): the workgroup's 64 rows are gate rows 32p..32p+31 and up rows
 // 32p..32p+31, i.e. exactly one 32-element Q8_0 block p of the GLU output; it applies the biases
@@ -539,21 +539,18 @@ __device__ __forceinline__ void store_meta(const u32x4 (&st)[2], uint8_t * lds, 
 // the batched path does per lane), laid out [tile][block / 4][row][block % 4] so one 16-byte read
 // per lane brings four consecutive blocks without bank conflicts.
 
-// v_dot2_f32_f16 with an inline zero accumulator (one VOP3P instruction instead of a register
-// clear plus v_dot2c).
-__device__ __forceinline__ float dot2_zero(half2_t a, half2_t b) {
-    float r;
-    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-}
-
+// One MXFP4 block of the lane's row slice against the wave's (uniform) activation slice `a`: the
+// slice dot comes from v_mfma_f32_4x4x4_16b_f16 with the row slice as B (lane = row) and `a` as A
+// in every lane, so register 0 of lane l is the dot of row l (exact: integers below 2^24), taken
+// off the vector ALU where two v_dot2 did it (120B-shape decode step: 1627-1643 -> 1660-1678
+// tok/s, kernel A 10.1 -> 9.6-9.9 us isolated).
 template <int SEL, int PAR>
 __device__ __forceinline__ void mx_block_s(unsigned dw, float s, u32x2 a, float (&acc)[2]) {
     const half2_t w01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, SEL);
     const half2_t w23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, SEL + 1);
-    float v = dot2_zero(w23, as_half2(a.y));
-    v = __builtin_amdgcn_fdot2(w01, as_half2(a.x), v, false);
-    acc[PAR] = __builtin_fmaf(s, v, acc[PAR]);
+    const f32x4_t v = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, a), half4_t{w01.x, w01.y, w23.x, w23.y},
+                                                         f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    acc[PAR] = __builtin_fmaf(s, v[0], acc[PAR]);
 }
 
 __device__ __forceinline__ void q8_block_s(unsigned w, float s, unsigned a, float (&acc)[2]) {
