@@ -1149,6 +1149,14 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(MxArgs A) {
 
 }  // namespace
 
+void launch_job_tiles(const GroupBuffers & g, const int32_t * filter, int job_tile, int64_t max_tiles,
+                      int32_t * tile_expert, int32_t * tile_start, int32_t * n_tiles, hipStream_t stream) {
+    require(job_tile >= 1 && max_tiles >= 1 && max_tiles < (1ll << 31), "job tile list shape out of range");
+    hipLaunchKernelGGL(gemm_tiles_kernel, dim3(1), dim3(1024), 0, stream, g.counts, g.active, g.n_active, filter, job_tile,
+                       static_cast<int>(max_tiles), tile_expert, tile_start, n_tiles, g.error);
+    check_hip(hipGetLastError(), "job tile list launch");
+}
+
 int64_t gemm_max_tiles(int64_t n_as, int64_t n_entries, int job_tile) {
     return (n_entries + job_tile - 1) / job_tile + (n_as < n_entries ? n_as : n_entries);
 }

@@ -99,6 +99,10 @@ struct KernelArgs {
     const int32_t * rows_list;
     const int32_t * active;
     const int32_t * n_active;
+    const int32_t * chunk_expert;   // [n_chunks] expert of each chunk of up to MT jobs
+    const int32_t * chunk_start;    // [n_chunks] its first job within the expert's jobs
+    const int32_t * n_chunks;       // [1]
+    int pairs;                      // 64-row tile pairs of the bank
     const float * bias;
     float * dst;
     uint8_t * dst_xrows;
@@ -727,8 +731,8 @@ __device__ __forceinline__ void glu_requant_block(const float * vals, int lane, 
 // write the outputs (or the GLU block). M is the narrowest token width holding the chunk.
 template <int TYPE, int M, bool NEG>
 __device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane & B, const __attribute__((address_space(4))) int32_t * jobs,
-                                           int expert, int c0, int mcount, int k, int lane, int r, int tile, bool live,
-                                           uint8_t * lds_tok, float * red, float * vals, int * s_flag) {
+                                           int expert, int c0, int mcount, int pair, int k, int lane, int r, int tile,
+                                           bool live, uint8_t * lds_tok, float * red, float * vals, int * s_flag) {
     const Shape S = A.shape;
     const int nb = S.nb;
     const int copy_bytes = static_cast<int>(A.lay.flag_offset());        // codes + scales of a row
@@ -747,8 +751,8 @@ __device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane &
     // 8 KiB of exponents), issued with the ring and checked at the staging barrier.
     u32x4 ex = u32x4{0u, 0u, 0u, 0u};
     if constexpr (use_mfma<TYPE, M, NEG>()) {
-        const int pair_tiles = (2 * static_cast<int>(blockIdx.x) + 1) * 32 < S.rows ? 2 : 1;
-        const int meta0 = static_cast<int>(S.codes_bytes) + 2 * static_cast<int>(blockIdx.x) * 32 * nb;
+        const int pair_tiles = (2 * pair + 1) * 32 < S.rows ? 2 : 1;
+        const int meta0 = static_cast<int>(S.codes_bytes) + 2 * pair * 32 * nb;
         if (static_cast<int>(threadIdx.x) * 16 < pair_tiles * 32 * nb)
             ex = __builtin_amdgcn_raw_buffer_load_b128(B.rsrc, meta0 + static_cast<int>(threadIdx.x) * 16, 0, 0);
     }
@@ -784,6 +788,7 @@ __device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane &
         else stream_groups_mm<M, D, false>(ring, B, nb, la_lane, lda_lane, tok_bytes, acc);
         preload_tail_buf<TYPE>(tl, B, nb);
         apply_tail_mm<M>(tl, nb, la_lane, lda_lane, tok_bytes, acc);
+        __syncthreads();   // `red` reuses the staged activation rows the other waves may still read
         // register i of lane l: row 4(l / 4) + i (the red layout's lane index) of token 4g + l % 4
 #pragma unroll
         for (int g = 0; g < M / 4; ++g)
@@ -805,6 +810,7 @@ __device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane &
             preload_tail_buf<TYPE>(tl, B, nb);
             apply_tail<TYPE, M, false, false>(tl, nullptr, r, nb, la, lda, tok_bytes, mc, acc);
         }
+        __syncthreads();   // `red` reuses the staged activation rows the other waves may still read
 #pragma unroll
         for (int m = 0; m < M; ++m) red[(m * 8 + k) * 64 + lane] = acc[m][0] + acc[m][1];
     }
@@ -822,45 +828,61 @@ __device__ __forceinline__ void gemv_chunk(const KernelArgs & A, const BufLane &
         __syncthreads();
         for (int mi = k; mi < mcount; mi += 8)
             if (lane < 32)
-                glu_requant_block(vals + mi * 64, lane, blockIdx.x, A.dst_xrows + static_cast<size_t>(jobs[c0 + mi]) * A.dst_lay.stride(),
+                glu_requant_block(vals + mi * 64, lane, pair, A.dst_xrows + static_cast<size_t>(jobs[c0 + mi]) * A.dst_lay.stride(),
                                   A.dst_lay, A.activation, A.alpha, A.limit);
     }
     __syncthreads();
 }
 
-// Batched GEMV: one workgroup per (tile pair, active expert); the expert's jobs go through in
-// chunks of up to MT tokens, each chunk with the narrowest token width in {1, 2, 4, 8} that
-// holds it (a uniform branch: most experts of a small decode batch see one or two tokens, and a
-// narrow width keeps the per-block token loop short).
+// Batched GEMV: one workgroup per (tile pair, chunk), a chunk being up to MT consecutive jobs of
+// one active expert (the chunk list holds each chunk's expert and first job, built on the device
+// from the grouping). Each XCD takes a contiguous range of (pair, chunk) items with the chunk
+// fastest, so the chunks of one expert run side by side on one XCD and share the tile pair's
+// weight stream through its L2, where a workgroup walking an expert's chunks in turn streamed the
+// weights once per chunk (config 1 shape at 64 tokens: 40 % of the experts hold more than eight
+// jobs). A chunk runs at the narrowest token width in {1, 2, 4, 8} that holds it (a uniform
+// branch: most experts of a small decode batch see one or two tokens, and a narrow width keeps
+// the per-block token loop short).
 template <int TYPE, int MT, bool NEG>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void expert_gemv_kernel(KernelArgs A) {
-    __shared__ __attribute__((aligned(16))) float red[MT * 8 * 64];
     __shared__ float vals[MT * 64];
     __shared__ int s_flag;
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds_tok[];   // MT activation rows
+    // MT activation rows; after the weight stream, the [MT][8 slices][64 rows] partial sums
+    // (8 KiB less LDS per token of width than separate buffers: three workgroups per CU at MT = 8
+    // with K = 2880)
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_tok[];
+    float * red = reinterpret_cast<float *>(lds_tok);
     // Per-expert metadata is read through the constant address space so it stays scalar.
-    const int a_index = blockIdx.y;
-    if (a_index >= *as_const<int32_t>(A.n_active)) return;
-    const int expert = as_const<int32_t>(A.active)[a_index];
+    const int n_items = *as_const<int32_t>(A.n_chunks);
+    const int total = n_items * A.pairs;
+    const int per_xcd = (total + 7) >> 3;
+    const int slot8 = static_cast<int>(blockIdx.x >> 3);
+    const int item_pair = static_cast<int>(blockIdx.x & 7) * per_xcd + slot8;
+    if (slot8 >= per_xcd || item_pair >= total) return;
+    const int pair = item_pair / n_items;
+    const int item = item_pair - pair * n_items;
+    const int expert = as_const<int32_t>(A.chunk_expert)[item];
+    const int c0 = as_const<int32_t>(A.chunk_start)[item];
     const int count = as_const<int32_t>(A.counts)[expert];
     const __attribute__((address_space(4))) int32_t * jobs = as_const<int32_t>(A.rows_list) + as_const<int32_t>(A.offsets)[expert];
     const int slot = A.expert_to_slot ? as_const<int32_t>(A.expert_to_slot)[expert] : expert;
-    if (count <= 0) return;
+    const int mcount = count - c0 < MT ? count - c0 : MT;
+    if (mcount <= 0) return;
     if (slot < 0 || slot >= A.shape.n_slots) {
-        // Expert not resident in this bank: its jobs' outputs of this tile pair become NaN, as in
-        // the decode kernels, so a bad expert->slot map can never leave stale workspace data in a
-        // result. Epilogue 1 poisons the block scale of the GLU block this workgroup owns.
+        // Expert not resident in this bank: the chunk's outputs of this tile pair become NaN, as
+        // in the decode kernels, so a bad expert->slot map can never leave stale workspace data in
+        // a result. Epilogue 1 poisons the block scale of the GLU block this workgroup owns.
         const float nan = __builtin_nanf("");
         if (A.epilogue == 0) {
-            for (int i = threadIdx.x; i < count * 64; i += kThreads) {
-                const int64_t brow = static_cast<int64_t>(blockIdx.x) * 64 + (i & 63);
+            for (int i = threadIdx.x; i < mcount * 64; i += kThreads) {
+                const int64_t brow = static_cast<int64_t>(pair) * 64 + (i & 63);
                 if (brow < A.shape.rows)
-                    A.dst[static_cast<size_t>(jobs[i >> 6]) * A.shape.rows + ggml_row(brow, A.shape.rows, A.shape.interleave)] = nan;
+                    A.dst[static_cast<size_t>(jobs[c0 + (i >> 6)]) * A.shape.rows + ggml_row(brow, A.shape.rows, A.shape.interleave)] = nan;
             }
         } else {
-            for (int j = threadIdx.x; j < count; j += kThreads)
-                reinterpret_cast<float *>(A.dst_xrows + static_cast<size_t>(jobs[j]) * A.dst_lay.stride() +
-                                          A.dst_lay.da_offset())[blockIdx.x] = nan;
+            for (int j = threadIdx.x; j < mcount; j += kThreads)
+                reinterpret_cast<float *>(A.dst_xrows + static_cast<size_t>(jobs[c0 + j]) * A.dst_lay.stride() +
+                                          A.dst_lay.da_offset())[pair] = nan;
         }
         return;
     }
@@ -869,21 +891,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const int k = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // lane slice, wave-uniform
     const int lane = threadIdx.x & 63;
     const int r = lane & 31;
-    const int tile = blockIdx.x * 2 + (lane >> 5);
+    const int tile = pair * 2 + (lane >> 5);
     const bool live = tile * 32 < S.rows;                              // the last tile pair may be half
     const uint8_t * slot_base = A.bank + static_cast<size_t>(slot) * S.slot_bytes;
     const BufLane B = buf_lane<TYPE>(slot_base, S.slot_bytes, S.codes_bytes, live ? tile : 0, k, r, S.nb);
-    for (int c0 = 0; c0 < count; c0 += MT) {
-        const int mcount = count - c0 < MT ? count - c0 : MT;
-        if (MT >= 8 && mcount > 4)
-            gemv_chunk<TYPE, (MT >= 8 ? 8 : 1), NEG>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
-        else if (MT >= 4 && mcount > 2)
-            gemv_chunk<TYPE, (MT >= 4 ? 4 : 1), NEG>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
-        else if (MT >= 2 && mcount > 1)
-            gemv_chunk<TYPE, (MT >= 2 ? 2 : 1), NEG>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
-        else
-            gemv_chunk<TYPE, 1, NEG>(A, B, jobs, expert, c0, mcount, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
-    }
+    if (MT >= 8 && mcount > 4)
+        gemv_chunk<TYPE, (MT >= 8 ? 8 : 1), NEG>(A, B, jobs, expert, c0, mcount, pair, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
+    else if (MT >= 4 && mcount > 2)
+        gemv_chunk<TYPE, (MT >= 4 ? 4 : 1), NEG>(A, B, jobs, expert, c0, mcount, pair, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
+    else if (MT >= 2 && mcount > 1)
+        gemv_chunk<TYPE, (MT >= 2 ? 2 : 1), NEG>(A, B, jobs, expert, c0, mcount, pair, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
+    else
+        gemv_chunk<TYPE, 1, NEG>(A, B, jobs, expert, c0, mcount, pair, k, lane, r, tile, live, lds_tok, red, vals, &s_flag);
 }
 
 // ------------------------------------------------------------------------------ fused decode
@@ -1753,10 +1772,22 @@ __global__ __launch_bounds__(256) void expand_q8_kernel(const uint8_t * __restri
 }
 
 template <int TYPE, int MT, bool NEG>
-void launch_typed(const GemvArgs & g, const KernelArgs & ka, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>((ka.shape.rows + 63) / 64), static_cast<unsigned>(g.max_active));
+void launch_typed(const GemvArgs & g, KernelArgs ka, hipStream_t stream) {
+    // chunks: at most one partial chunk per active expert plus entries / MT full ones
+    const int64_t max_items = g.max_active + g.n_entries / MT;
+    require(max_items <= g.group.chunk_list_items, "chunk list exceeds its workspace");
+    // the kernel hands each XCD ceil(items / 8) consecutive items: the grid is a multiple of 8
+    const int64_t blocks = (static_cast<int64_t>(ka.pairs) * max_items + 7) / 8 * 8;
+    require(blocks > 0 && blocks < (1ll << 31), "expert GEMV grid out of range");
+    ka.chunk_expert = g.group.chunk_list;
+    ka.chunk_start = g.group.chunk_list + max_items;
+    ka.n_chunks = g.group.chunk_list + 2 * max_items;
+    launch_job_tiles(g.group, nullptr, MT, max_items, g.group.chunk_list, g.group.chunk_list + max_items,
+                     g.group.chunk_list + 2 * max_items, stream);
     const size_t tok_bytes = (static_cast<size_t>(ka.lay.flag_offset()) + 15) & ~static_cast<size_t>(15);
-    hipLaunchKernelGGL((expert_gemv_kernel<TYPE, MT, NEG>), grid, dim3(kThreads), MT * tok_bytes, stream, ka);
+    const size_t lds = std::max<size_t>(MT * tok_bytes, static_cast<size_t>(MT) * 8 * 64 * sizeof(float));
+    hipLaunchKernelGGL((expert_gemv_kernel<TYPE, MT, NEG>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream,
+                       ka);
     check_hip(hipGetLastError(), "expert GEMV launch");
 }
 
@@ -1809,6 +1840,7 @@ void launch_gemv(const GemvArgs & g, hipStream_t stream) {
     ka.rows_list = g.group.rows;
     ka.active = g.group.active;
     ka.n_active = g.group.n_active;
+    ka.pairs = static_cast<int>((bank.rows + 63) / 64);
     ka.bias = g.bias;
     ka.dst = g.dst;
     ka.dst_xrows = g.dst_xrows;

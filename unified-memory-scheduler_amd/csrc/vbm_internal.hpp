@@ -94,6 +94,8 @@ struct GroupBuffers {
     int32_t * n_active;  // [1]
     int32_t * error;     // [1]
     int32_t * chunk_counts;  // [group_chunk_ints]: per-chunk histograms, then chunk bases
+    int32_t * chunk_list;    // [2 * chunk_list_items + 1]: the batched GEMV's job chunks
+    int64_t chunk_list_items;
 };
 int64_t group_chunk_ints(int64_t n_as, int64_t n_entries);
 size_t group_workspace_bytes(int64_t n_as, int64_t n_entries);
@@ -148,6 +150,7 @@ struct GemvArgs {
     GroupBuffers group;
     int64_t max_active;               // host bound on the number of active experts
     int64_t max_per_expert;           // host bound on jobs per expert (selects the token chunk)
+    int64_t n_entries;                // routed (token, rank) entries of the grouping
     const float * bias;               // [n_as][rows] ggml row order, or null
     float * dst;                      // epilogue 0
     uint8_t * dst_xrows;              // epilogue 1
@@ -161,6 +164,11 @@ struct GemvArgs {
     bool may_have_neg128 = true;
 };
 void launch_gemv(const GemvArgs & a, hipStream_t stream);
+
+// Chunks of `job_tile` consecutive jobs per active expert (experts with filter[e] < 0 skipped),
+// in active order: tile_expert / tile_start per chunk and their count, at most max_tiles.
+void launch_job_tiles(const GroupBuffers & g, const int32_t * filter, int job_tile, int64_t max_tiles,
+                      int32_t * tile_expert, int32_t * tile_start, int32_t * n_tiles, hipStream_t stream);
 
 // Activation row of the MFMA grouped GEMM: row-major codes (f16 for MXFP4 weights, int8 for
 // Q8_0), fp16-rounded fp32 block scales, and the row's -128 flag; 256-byte aligned stride.

@@ -300,6 +300,7 @@ void mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot, const int
     a.group = g;
     a.max_active = std::min<int64_t>(n_as, entries);
     a.max_per_expert = entries;
+    a.n_entries = entries;
     a.bias = bias;
     a.dst = dst;
     a.epilogue = 0;
@@ -370,6 +371,7 @@ void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits
     a.group = g;
     a.max_active = std::min<int64_t>(d->n_expert, entries);
     a.max_per_expert = n_tokens;                 // top-k experts are distinct within a token
+    a.n_entries = entries;
     a.activation = d->activation;
     a.alpha = 1.702f;
     a.limit = 7.0f;

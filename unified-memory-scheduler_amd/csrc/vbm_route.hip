@@ -243,7 +243,8 @@ int64_t group_chunk_ints(int64_t n_as, int64_t n_entries) {
 }
 
 size_t group_workspace_bytes(int64_t n_as, int64_t n_entries) {
-    return static_cast<size_t>(n_as + (n_as + 1) + n_entries + n_as + 1 + 1 + group_chunk_ints(n_as, n_entries) + 8) *
+    return static_cast<size_t>(n_as + (n_as + 1) + n_entries + n_as + 1 + 1 + group_chunk_ints(n_as, n_entries) +
+                               2 * (n_as + n_entries) + 1 + 8) *
            sizeof(int32_t);
 }
 
@@ -256,7 +257,9 @@ GroupBuffers carve_group(void * base, int64_t n_as, int64_t n_entries) {
     g.active = p; p += n_as;
     g.n_active = p; p += 1;
     g.error = p; p += 1;
-    g.chunk_counts = p;
+    g.chunk_counts = p; p += group_chunk_ints(n_as, n_entries);
+    g.chunk_list = p;
+    g.chunk_list_items = n_as + n_entries;
     return g;
 }
 
