@@ -428,7 +428,7 @@ def batch_line(descs, T: int, order: int, reps: int, seed_stream: int, slot_byte
     distinct = distinct_experts(ids_host)
     step_bytes = distinct * slot_bytes
     return {"tokens": T, "order": "exact" if order == vb.ORDER_EXACT else "fast",
-            "path": "MFMA grouped GEMM" if (order == vb.ORDER_FAST and T >= 16 and T * K >= 5 * E) else "batched GEMV",
+            "path": "MFMA grouped GEMM" if (order == vb.ORDER_FAST and T >= 16 and T * K >= 12 * E) else "batched GEMV",
             "tok_s": round(T / (ms / 1e3), 1), "ms_per_step": round(ms, 4),
             "distinct_experts_per_layer": round(distinct / L, 2),
             "expert_bytes_per_step": int(step_bytes), "expert_gbs": round(step_bytes / (ms / 1e3) / 1e9, 1)}

@@ -189,10 +189,10 @@ def test_gemm_mxfp4_exponent_ranges_exact(gpu, orc):
 
 
 def test_gemm_mul_mat_id_fast_within_tolerance_and_broadcast(gpu, orc):
-    """Config 0/1 gate_up shape (5760 x 2880, interleaved) with biases, T = 64, broadcast and
-    per-rank activations."""
+    """Config 0/1 gate_up shape (5760 x 2880, interleaved) with biases, T = 96 (12 routed rows per
+    expert: the grouped GEMM), broadcast and per-rank activations."""
     rng = np.random.default_rng(72)
-    experts, k, rows, n_ids, tokens = 32, 2880, 5760, 4, 64
+    experts, k, rows, n_ids, tokens = 32, 2880, 5760, 4, 96
     w = H.synth_weights(H.MX, 72, 1, experts, rows, k)
     bank = H.make_bank(H.MX, w, experts, rows, k, True)
     bias = gpu.synth_normal(72, 3, 0, experts * rows, 0.0, 0.02)
@@ -290,9 +290,10 @@ def test_prefill_layer_graph_replays_match_eager(gpu):
 
 
 def test_prefill_layer_mxfp4_config1_shape(gpu, orc):
-    """Config 1 layer (MXFP4, 32 experts, top-4, 2880, SwiGLU-OAI, biases) at T = 64, fast order."""
+    """Config 1 layer (MXFP4, 32 experts, top-4, 2880, SwiGLU-OAI, biases) at T = 96 (12 routed rows
+    per expert, the grouped GEMM's threshold), fast order."""
     layer = Layer(gpu, H.MX, 2880, 2880, 32, 4, seed=78, order=gpu.ORDER_FAST)
-    T = 64
+    T = 96
     x = gpu.synth_normal(78, 6, 0, T * 2880).reshape(T, 2880)
     out, ids, w = layer.forward_gpu(x)
     ref = layer.forward_cpu(orc, x)
@@ -303,12 +304,12 @@ def test_prefill_layer_mxfp4_config1_shape(gpu, orc):
     layer.destroy()
 
 
-@pytest.mark.parametrize("experts,tokens", [(128, 32), (32, 24)])
+@pytest.mark.parametrize("experts,tokens", [(128, 32), (32, 24), (32, 64)])
 def test_fast_order_small_groups_take_the_exact_gemv(gpu, orc, experts, tokens):
-    """Below 5 routed rows per expert on average a fast-order call runs the exact-order GEMV (the
-    GEMM would pad most of its tiles): the layer output is bit-identical to the exact order's and
-    to the oracle's."""
-    assert tokens * 4 < 5 * experts and tokens >= 16
+    """Below 12 routed rows per expert on average a fast-order call runs the exact-order GEMV
+    (faster there than the grouped GEMM): the layer output is bit-identical to the exact order's
+    and to the oracle's."""
+    assert tokens * 4 < 12 * experts and tokens >= 16
     fast = Layer(gpu, H.MX, 2880, 2880, experts, 4, seed=91, router=False, order=gpu.ORDER_FAST)
     x = gpu.synth_normal(91, 6, 0, tokens * 2880).reshape(tokens, 2880)
     logits = gpu.synth_normal(91, 7, 0, tokens * experts).reshape(tokens, experts)
@@ -324,7 +325,7 @@ def test_fast_order_small_groups_take_the_exact_gemv(gpu, orc, experts, tokens):
 
 def test_gemm_randomized_shapes_within_tolerance(gpu, orc):
     """8 seeded random fast-order MUL_MAT_ID calls large enough for the MFMA grouped GEMM
-    (>= 16 tokens, 5..200 routed rows per expert on average): both weight types, 2..16 experts, top-1..4,
+    (>= 16 tokens, 12..200 routed rows per expert on average): both weight types, 2..16 experts, top-1..4,
     rows 64..320, k 64..1024, fp32 or ggml Q8_0 (with -128 codes) inputs, with or without biases,
     against the oracle within the fast order's tolerance (max error / max |ref| <= 1e-3, cosine >=
     0.99999)."""
@@ -333,8 +334,8 @@ def test_gemm_randomized_shapes_within_tolerance(gpu, orc):
         type_id = H.MX if case % 2 == 0 else H.Q8
         experts = int(rng.integers(2, 17))
         active = int(rng.integers(1, min(4, experts) + 1))
-        # 5..200 routed jobs per expert on average: one to four 64-job tiles per expert
-        tokens = max(16, -(-int(rng.integers(5, 201)) * experts // active))
+        # 12..200 routed jobs per expert on average: one or two 128-job tiles per expert
+        tokens = max(16, -(-int(rng.integers(12, 201)) * experts // active))
         rows, k = 64 * int(rng.integers(1, 6)), 64 * int(rng.integers(1, 17))
         q8_input = rng.random() < 0.4
         ids = np.stack([rng.choice(experts, active, replace=False) for _ in range(tokens)]).astype(np.int32)

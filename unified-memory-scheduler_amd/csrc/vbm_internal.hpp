@@ -232,9 +232,11 @@ struct LayerWorkspace {
     size_t total;
 };
 constexpr int64_t kGemmMinTokens = 16;
-// Below 5 routed rows per expert on average the exact-order batched GEMV outruns the MFMA
-// grouped GEMM (measured crossover between 4 and 6 rows at 32 and 128 experts, top-4).
-constexpr int64_t kGemmMinRowsPerExpert = 5;
+// Below 12 routed rows per expert on average the exact-order batched GEMV (matrix-core slice
+// dots, one workgroup per job chunk) outruns the MFMA grouped GEMM: 6-layer stacks of the
+// 2880 x 2880 MXFP4 shape, top-4, 32 / 128 experts, GEMV vs GEMM tok/s at 8 rows 47.6k vs 38.6k /
+// 56.8k vs 44.6k, at 12 rows 54.8k vs 56.4k / 62.0k vs 64.7k, at 16 rows 60.4k vs 72.4k.
+constexpr int64_t kGemmMinRowsPerExpert = 12;
 bool use_gemm(const vbm_moe_layer_desc & d, int64_t n_tokens);
 inline bool gemm_pays(int64_t n_tokens, int64_t top_k, int64_t n_expert) {
     return n_tokens >= kGemmMinTokens && n_tokens * top_k >= kGemmMinRowsPerExpert * n_expert;
