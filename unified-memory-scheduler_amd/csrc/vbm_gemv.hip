@@ -1775,8 +1775,7 @@ __global__ __launch_bounds__(256) void expand_q8_kernel(const uint8_t * __restri
 
 template <int TYPE, int MT, bool NEG>
 void launch_typed(const GemvArgs & g, KernelArgs ka, hipStream_t stream) {
-    // chunks: at most one partial chunk per active expert plus entries / MT full ones
-    const int64_t max_items = g.max_active + g.n_entries / MT;
+    const int64_t max_items = gemv_max_chunks(g.max_active, g.n_entries, MT);
     require(max_items <= g.group.chunk_list_items, "chunk list exceeds its workspace");
     // the kernel hands each XCD ceil(items / 8) consecutive items: the grid is a multiple of 8
     const int64_t blocks = (static_cast<int64_t>(ka.pairs) * max_items + 7) / 8 * 8;
@@ -1784,8 +1783,9 @@ void launch_typed(const GemvArgs & g, KernelArgs ka, hipStream_t stream) {
     ka.chunk_expert = g.group.chunk_list;
     ka.chunk_start = g.group.chunk_list + max_items;
     ka.n_chunks = g.group.chunk_list + 2 * max_items;
-    launch_job_tiles(g.group, nullptr, MT, max_items, g.group.chunk_list, g.group.chunk_list + max_items,
-                     g.group.chunk_list + 2 * max_items, stream);
+    if (!g.chunks_built)
+        launch_job_tiles(g.group, nullptr, MT, max_items, g.group.chunk_list, g.group.chunk_list + max_items,
+                         g.group.chunk_list + 2 * max_items, stream);
     const size_t tok_bytes = (static_cast<size_t>(ka.lay.flag_offset()) + 15) & ~static_cast<size_t>(15);
     const size_t lds = std::max<size_t>(MT * tok_bytes, static_cast<size_t>(MT) * 8 * 64 * sizeof(float));
     hipLaunchKernelGGL((expert_gemv_kernel<TYPE, MT, NEG>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream,
@@ -1795,10 +1795,12 @@ void launch_typed(const GemvArgs & g, KernelArgs ka, hipStream_t stream) {
 
 template <int TYPE, bool NEG>
 void launch_mt(const GemvArgs & g, const KernelArgs & ka, hipStream_t stream) {
-    if (g.max_per_expert <= 1) launch_typed<TYPE, 1, NEG>(g, ka, stream);
-    else if (g.max_per_expert <= 2) launch_typed<TYPE, 2, NEG>(g, ka, stream);
-    else if (g.max_per_expert <= 4) launch_typed<TYPE, 4, NEG>(g, ka, stream);
-    else launch_typed<TYPE, 8, NEG>(g, ka, stream);
+    switch (gemv_chunk_tokens(g.max_per_expert)) {
+        case 1: launch_typed<TYPE, 1, NEG>(g, ka, stream); break;
+        case 2: launch_typed<TYPE, 2, NEG>(g, ka, stream); break;
+        case 4: launch_typed<TYPE, 4, NEG>(g, ka, stream); break;
+        default: launch_typed<TYPE, 8, NEG>(g, ka, stream); break;
+    }
 }
 
 }  // namespace

@@ -100,8 +100,18 @@ struct GroupBuffers {
 int64_t group_chunk_ints(int64_t n_as, int64_t n_entries);
 size_t group_workspace_bytes(int64_t n_as, int64_t n_entries);
 GroupBuffers carve_group(void * base, int64_t n_as, int64_t n_entries);
+// job_tile > 0: also the batched GEMV's job chunks of that many tokens (gemv_chunk_tokens) into
+// g.chunk_list, laid out for gemv_max_chunks entries.
 void launch_group(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride, int64_t n_as,
-                  const GroupBuffers & g, hipStream_t stream);
+                  const GroupBuffers & g, hipStream_t stream, int job_tile = 0);
+// Token width of the batched GEMV's job chunks for a bound on jobs per expert, and the bound on
+// the number of chunks: at most one partial chunk per active expert plus entries / width full ones.
+inline int gemv_chunk_tokens(int64_t max_per_expert) {
+    return max_per_expert <= 1 ? 1 : (max_per_expert <= 2 ? 2 : (max_per_expert <= 4 ? 4 : 8));
+}
+inline int64_t gemv_max_chunks(int64_t max_active, int64_t n_entries, int width) {
+    return max_active + n_entries / width;
+}
 
 void launch_quantize_q8_0(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, uint8_t * dst,
                           hipStream_t stream);
@@ -151,6 +161,8 @@ struct GemvArgs {
     int64_t max_active;               // host bound on the number of active experts
     int64_t max_per_expert;           // host bound on jobs per expert (selects the token chunk)
     int64_t n_entries;                // routed (token, rank) entries of the grouping
+    bool chunks_built = false;        // launch_group already wrote the job chunk list (job_tile =
+                                      // gemv_chunk_tokens(max_per_expert))
     const float * bias;               // [n_as][rows] ggml row order, or null
     float * dst;                      // epilogue 0
     uint8_t * dst_xrows;              // epilogue 1

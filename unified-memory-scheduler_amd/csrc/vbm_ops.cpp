@@ -289,7 +289,7 @@ void mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot, const int
         launch_quantize_expand(static_cast<const float *>(b), n_b, bank->k, b_row_stride, lay, q, nullptr, s);
     else
         launch_expand_q8(static_cast<const uint8_t *>(b), n_b, bank->nb * 34, lay, q, s);
-    launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s);
+    launch_group(ids, n_ids, n_tokens, ids_stride, n_as, g, s, gemv_chunk_tokens(entries));
     init_dst(dst, ids, n_ids, n_tokens, ids_stride, n_as, bank->rows, s);
     GemvArgs a{};
     a.bank = bank;
@@ -301,6 +301,7 @@ void mul_mat_id(const vbm_bank * bank, const int32_t * expert_to_slot, const int
     a.max_active = std::min<int64_t>(n_as, entries);
     a.max_per_expert = entries;
     a.n_entries = entries;
+    a.chunks_built = true;
     a.bias = bias;
     a.dst = dst;
     a.epilogue = 0;
@@ -363,7 +364,7 @@ void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits
     }
     const XrowLayout lx{H / 32, d->gate_up->type}, la{I / 32, d->down->type};
     launch_quantize_expand(x, n_tokens, H, H, lx, w.xrows_x, nullptr, s);
-    launch_group(ids_d, K, n_tokens, K, d->n_expert, g, s);
+    launch_group(ids_d, K, n_tokens, K, d->n_expert, g, s, gemv_chunk_tokens(n_tokens));
 
     GemvArgs a{};
     a.expert_to_slot = d->expert_to_slot;
@@ -372,6 +373,7 @@ void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits
     a.max_active = std::min<int64_t>(d->n_expert, entries);
     a.max_per_expert = n_tokens;                 // top-k experts are distinct within a token
     a.n_entries = entries;
+    a.chunks_built = true;                       // by launch_group, for both projections
     a.activation = d->activation;
     a.alpha = 1.702f;
     a.limit = 7.0f;

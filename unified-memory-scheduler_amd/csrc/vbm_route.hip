@@ -50,11 +50,16 @@ __global__ __launch_bounds__(kGroupThreads) void group_count_kernel(const int32_
     if (t == 0) row[n_as] = s_bad;
 }
 
+// One workgroup, thread t = expert t: per-expert totals and chunk bases, offsets, the active
+// list and, when job_tile > 0, the batched GEMV's job chunks (up to job_tile consecutive jobs of an
+// active expert each, in active order: expert at [0, max_tiles), first job at [max_tiles,
+// 2 max_tiles), their count at [2 max_tiles]).
 __global__ __launch_bounds__(kGroupThreads) void group_scan_kernel(int n_chunks, int n_as, int32_t * chunk_counts,
                                                                     int32_t * counts, int32_t * offsets,
                                                                     int32_t * active, int32_t * n_active,
-                                                                    int32_t * error) {
-    __shared__ int s_wave_sum[2][kGroupThreads / 64];
+                                                                    int32_t * error, int job_tile, int max_tiles,
+                                                                    int32_t * tiles) {
+    __shared__ int s_wave_sum[3][kGroupThreads / 64];
     __shared__ int s_bad;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     if (t == 0) s_bad = 0;
@@ -71,27 +76,40 @@ __global__ __launch_bounds__(kGroupThreads) void group_scan_kernel(int n_chunks,
     }
     for (int k = t; k < n_chunks; k += kGroupThreads)
         if (chunk_counts[static_cast<int64_t>(k) * (n_as + 1) + n_as]) s_bad = 1;
-    // two-level exclusive scans of the totals and of (total > 0)
+    // two-level exclusive scans of the totals, of (total > 0) and of the job chunks
     const int live = c > 0 ? 1 : 0;
-    int inc_c = c, inc_l = live;
+    const int nk = job_tile > 0 ? (c + job_tile - 1) / job_tile : 0;
+    int inc_c = c, inc_l = live, inc_k = nk;
     for (int off = 1; off < 64; off <<= 1) {
-        const int oc = __shfl_up(inc_c, off), ol = __shfl_up(inc_l, off);
-        if (lane >= off) { inc_c += oc; inc_l += ol; }
+        const int oc = __shfl_up(inc_c, off), ol = __shfl_up(inc_l, off), ok = __shfl_up(inc_k, off);
+        if (lane >= off) { inc_c += oc; inc_l += ol; inc_k += ok; }
     }
-    if (lane == 63) { s_wave_sum[0][wave] = inc_c; s_wave_sum[1][wave] = inc_l; }
+    if (lane == 63) { s_wave_sum[0][wave] = inc_c; s_wave_sum[1][wave] = inc_l; s_wave_sum[2][wave] = inc_k; }
     __syncthreads();
-    int base_c = 0, base_l = 0;
-    for (int w = 0; w < wave; ++w) { base_c += s_wave_sum[0][w]; base_l += s_wave_sum[1][w]; }
-    const int ex_c = base_c + inc_c - c, ex_l = base_l + inc_l - live;
+    int base_c = 0, base_l = 0, base_k = 0;
+    for (int w = 0; w < wave; ++w) { base_c += s_wave_sum[0][w]; base_l += s_wave_sum[1][w]; base_k += s_wave_sum[2][w]; }
+    const int ex_c = base_c + inc_c - c, ex_l = base_l + inc_l - live, ex_k = base_k + inc_k - nk;
+    bool over = false;
     if (t < n_as) {
         counts[t] = c;
         offsets[t] = ex_c;
         if (live) active[ex_l] = t;
+        for (int j = 0; j < nk; ++j) {
+            if (ex_k + j < max_tiles) {
+                tiles[ex_k + j] = t;
+                tiles[max_tiles + ex_k + j] = j * job_tile;
+            } else {
+                over = true;
+            }
+        }
         if (t == n_as - 1) {
             offsets[n_as] = ex_c + c;
             *n_active = ex_l + live;
+            if (job_tile > 0) tiles[2 * max_tiles] = ex_k + nk < max_tiles ? ex_k + nk : max_tiles;
         }
     }
+    if (over) s_bad = 1;   // (cannot happen with the launch bound: flagged as a grouping error)
+    __syncthreads();
     if (t == 0) *error = s_bad;
 }
 
@@ -264,7 +282,7 @@ GroupBuffers carve_group(void * base, int64_t n_as, int64_t n_entries) {
 }
 
 void launch_group(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride, int64_t n_as,
-                  const GroupBuffers & g, hipStream_t stream) {
+                  const GroupBuffers & g, hipStream_t stream, int job_tile) {
     require(n_as > 0 && n_as <= kMaxExperts, "grouping supports 1..1024 experts");
     require(n_ids > 0 && n_tokens > 0 && n_ids * n_tokens <= (1ll << 24), "grouping entry count out of range");
     require(ids_stride >= n_ids, "ids token stride must be >= n_ids");
@@ -276,8 +294,14 @@ void launch_group(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t 
     hipLaunchKernelGGL(group_count_kernel, dim3(n_chunks), dim3(kGroupThreads), 0, stream, ids, static_cast<int>(n_ids), n,
                        ids_stride, static_cast<int>(n_as), g.chunk_counts);
     check_hip(hipGetLastError(), "grouping count launch");
+    int64_t max_tiles = 0;
+    if (job_tile > 0) {
+        max_tiles = gemv_max_chunks(std::min(n_as, n), n, job_tile);
+        require(g.chunk_list != nullptr && max_tiles <= g.chunk_list_items, "job chunk list exceeds its workspace");
+    }
     hipLaunchKernelGGL(group_scan_kernel, dim3(1), dim3(kGroupThreads), 0, stream, n_chunks, static_cast<int>(n_as),
-                       g.chunk_counts, g.counts, g.offsets, g.active, g.n_active, g.error);
+                       g.chunk_counts, g.counts, g.offsets, g.active, g.n_active, g.error, job_tile,
+                       static_cast<int>(max_tiles), g.chunk_list);
     check_hip(hipGetLastError(), "grouping scan launch");
     hipLaunchKernelGGL(group_place_kernel, dim3(n_chunks), dim3(kGroupThreads), 0, stream, ids, static_cast<int>(n_ids), n,
                        ids_stride, static_cast<int>(n_as), id_bits, g.chunk_counts, g.offsets, g.rows);
