@@ -130,12 +130,19 @@ __device__ __forceinline__ half8_t i8_to_f16(long v) {
     return r;
 }
 // Pipeline stages, filled by global-to-LDS DMA: a ring of S chunks of CB blocks, each stage
-// holding everything its chunk reads: the 128 jobs' activation codes and block scales, both tiles'
-// weight dwords of those blocks (Q8_0: the [slice pair][row] interleave of 16-byte units
-// (2q, b), (2q+1, b), (2q, b+1), (2q+1, b+1); MXFP4: [slice][row] dwords, rows of odd slice pairs
-// rotated by 16 against bank conflicts) and their exponent / scale dword per row. Chunk c issues
-// the loads of chunk c + S - 1; one wait and one barrier per chunk. Two stages: a third one, for
-// every operand or for the weights alone, measured no faster (Q8_0 layer of 2048 tokens).
+// holding the 128 jobs' activation codes and block scales of its chunk and, for MXFP4, both tiles'
+// weight dwords of those blocks ([slice][row] dwords, rows of odd slice pairs rotated by 16
+// against bank conflicts) and their exponent dword per row. Q8_0 (GROUPED): a tile's weights of
+// one 4-block bank group are 4 KB contiguous in the bank, so both tiles' group weights are staged
+// once per group by 16-byte DMAs into a two-slot group ring beside the chunk ring ([tile][slice]
+// [row] 16-byte units, the bank's own order), with the group's fp16 scales ([tile][row] 8 bytes)
+// and the 128 jobs' activation block scales of the group ([job][4 blocks], 16 bytes each):
+// a third of the chunk's DMA instructions, whose issue (not their bytes) bounded the kernel
+// (doubling the weight DMAs of the former per-chunk dword staging added 55 us to a 345 us
+// gate_up launch, doubling the activation DMAs 30 us). Chunk c issues the loads of chunk c + 1
+// (and of the next group at its last chunk); one wait and one barrier per chunk. Two stages: a
+// third one, for every operand or for the weights alone, measured no faster (Q8_0 layer of 2048
+// tokens).
 template <int TYPE>
 struct GemmStage {
     static constexpr int EB = TYPE == 39 ? 2 : 1;                       // bytes per activation code
@@ -145,12 +152,17 @@ struct GemmStage {
     static constexpr int S = 2;                                         // ring depth
     static constexpr int ROW = CB * 32 * EB;                            // bytes per job row and chunk
     static constexpr int ACT = kJobTile * ROW;
-    static constexpr int DA = kJobTile * CB * 4;
-    static constexpr int W = TYPE == 39 ? 2 * 8 * 32 * 4 : 2 * 4 * 32 * 16;
-    static constexpr int M = 2 * 32 * 4;
+    static constexpr bool GROUPED = TYPE == 8;
+    static constexpr int DA = GROUPED ? 0 : kJobTile * CB * 4;
+    static constexpr int W = GROUPED ? 0 : 2 * 8 * 32 * 4;
+    static constexpr int M = GROUPED ? 0 : 2 * 32 * 4;
     static constexpr int OFF_DA = ACT, OFF_W = OFF_DA + DA, OFF_M = OFF_W + W;
     static constexpr int STAGE = OFF_M + M;
-    static constexpr int BYTES = S * STAGE;
+    static constexpr int WG = GROUPED ? 2 * 8 * 32 * 16 : 0;   // group weight slot: [tile][slice][row] x 16 B
+    static constexpr int MG = GROUPED ? 2 * 32 * 8 : 0;        // group scale slot: [tile][row] x 4 fp16
+    static constexpr int DG = GROUPED ? kJobTile * GB * 4 : 0;   // group block-scale slot: [job][4 blocks] fp32
+    static constexpr int OFF_WG = S * STAGE, OFF_MG = OFF_WG + 2 * WG, OFF_DG = OFF_MG + 2 * MG;
+    static constexpr int BYTES = OFF_DG + 2 * DG;
     // DMA instructions per wave and chunk: activation rows (1 KiB each, ACT_JOBS job rows), block
     // scales, weights, meta. A wave skips the activation loads whose job rows are all past the
     // tile's live jobs, so its count per chunk varies; the wait before each chunk's barrier drains
@@ -159,7 +171,9 @@ struct GemmStage {
     static constexpr int ACT_JOBS = 1024 / ROW;
     static constexpr int ACT_DMA = ACT / 1024 / 4;
     static constexpr int W_DMA = W / 256 / 4;
+    static constexpr int WG_DMA = WG / 1024 / 4;   // 16-byte group weight loads per wave
     static_assert(S == 2, "the per-chunk wait is vmcnt(0)");
+    static_assert(!GROUPED || (CPG == 2 && WG_DMA == 2), "Q8_0 group staging: two chunks per group, two loads per wave");
 };
 
 // Global-to-LDS DMA (global_load_lds_*): lane l's bytes land at LDS address m0 + l * size. The
@@ -181,6 +195,9 @@ __device__ __forceinline__ void lds_dma_x1(const void * src, uint32_t m0) {
 }
 __device__ __forceinline__ void lds_dma_x1_s(const void * base, uint32_t off, uint32_t m0) {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m0) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma_x4_s(const void * base, uint32_t off, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0) : "memory", "m0");
 }
 #pragma clang diagnostic pop
 template <int N>
@@ -314,9 +331,11 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
         const int part = TYPE == 39 ? (lane & 7) ^ (jr & 7) : (lane & 3) ^ ((jr >> 1) & 3);
         act_src[j] = row_of(j0 + jr < count ? jr : 0) + 16 * part;
     }
-    static_assert(G::DA == kGemmThreads * 4, "one block-scale dword per thread and chunk");
-    const int jd = 32 * wave + (lane >> 1);
-    const uint8_t * da_src = row_of(j0 + jd < count ? jd : 0) + A.lay.da_offset() + 4 * (lane & 1);
+    // block scales: per chunk, lane l of wave w loads job 32w + l / 2, block l % 2; grouped (Q8_0),
+    // per group, lane l of waves 0 and 1 loads the 16 bytes of job 64w + l
+    static_assert(G::GROUPED || G::DA == kGemmThreads * 4, "one block-scale dword per thread and chunk");
+    const int jd = G::GROUPED ? 64 * (wave & 1) + lane : 32 * wave + (lane >> 1);
+    const uint8_t * da_src = row_of(j0 + jd < count ? jd : 0) + A.lay.da_offset() + (G::GROUPED ? 0 : 4 * (lane & 1));
     // weight dword of this lane within its load's group-relative source
     uint32_t woff;
     if constexpr (TYPE == 39) {
@@ -328,14 +347,39 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
     const uint32_t moff = static_cast<uint32_t>(lane) * 8;
     const size_t tile_bytes = static_cast<size_t>(32) * nb * kCodeRow, meta_tile_bytes = static_cast<size_t>(32) * nb * kMetaRow;
     auto tsel = [&](int t) -> size_t { return (pair * 2 + t) * 32 < S.rows ? pair * 2 + t : pair * 2; };
-    auto dma_stage = [&](int c, int st) {
+    // new_group: also stage chunk c's bank group (Q8_0), into group slot grp & 1; the slot of the
+    // group before it is still being read, the one before that is free since the barrier that
+    // ended its last chunk.
+    auto dma_stage = [&](int c, int st, bool new_group) {
         const int grp = c / G::CPG, sub = c % G::CPG;
         const uint32_t sb = lds0 + st * G::STAGE;
 #pragma unroll
         for (int j = 0; j < G::ACT_DMA; ++j)
             if (G::ACT_JOBS * (wu * G::ACT_DMA + j) < live_rows)
                 lds_dma_x4(act_src[j] + static_cast<int64_t>(c) * G::ROW, sb + (wu * G::ACT_DMA + j) * 1024);
-        lds_dma_x1(da_src + static_cast<int64_t>(c) * CB * 4, sb + G::OFF_DA + wu * 256);
+        if constexpr (!G::GROUPED) lds_dma_x1(da_src + static_cast<int64_t>(c) * CB * 4, sb + G::OFF_DA + wu * 256);
+        if constexpr (G::GROUPED) {
+            if (new_group) {
+                // load I = 2w + i: tile I >> 2, the 1 KiB quarter I & 3 of its group (lane l: the
+                // 16-byte unit 64 (I & 3) + l, i.e. slice 2 (I & 3) + l / 32, row l % 32)
+                const uint32_t wslot = lds0 + G::OFF_WG + (grp & 1) * G::WG;
+#pragma unroll
+                for (int i = 0; i < G::WG_DMA; ++i) {
+                    const int I = wu * G::WG_DMA + i, t = I >> 2, part = I & 3;
+                    const uint8_t * base = slot_base + tsel(t) * tile_bytes + static_cast<size_t>(grp) * 4096 + part * 1024;
+                    lds_dma_x4_s(base, static_cast<uint32_t>(lane) * 16, wslot + t * 4096 + part * 1024);
+                }
+                // the group's scales: lanes 0..31 of wave 0, 16 bytes (two rows) each, tile l / 16
+                if (wu == 0 && lane < 32)
+                    lds_dma_x4(slot_base + S.codes_bytes + tsel(lane >> 4) * meta_tile_bytes + static_cast<size_t>(grp) * 256 +
+                                   (lane & 15) * 16,
+                               lds0 + G::OFF_MG + (grp & 1) * G::MG);
+                if (wu < 2)
+                    lds_dma_x4(da_src + 16 * grp,
+                               __builtin_amdgcn_readfirstlane(lds0 + G::OFF_DG + (grp & 1) * G::DG + wu * 1024));
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < G::W_DMA; ++i) {
             const int I = wu * G::W_DMA + i;
@@ -403,14 +447,20 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
         constexpr int NF = decltype(nf_c)::value;
         // weight dwords of A rows lr + 16i, slices 2q / 2q + 1 (MXFP4: row r of an odd slice pair
         // at position r ^ 16), or their 16-byte unit (Q8_0)
+        // (Q8_0: unit (2q, row) of the group slot; slice 2q + 1's unit is 512 bytes on)
         const uint8_t * w_lds[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            w_lds[i] = lds + G::OFF_W + (TYPE == 39 ? ((wave & 1) * 256 + 2 * q * 32 + 16 * (i ^ (q & 1)) + lr) * 4
-                                                     : (wave & 1) * 2048 + (q * 32 + 16 * i + lr) * 16);
-        const uint8_t * m_lds = lds + G::OFF_M + ((wave & 1) * 32 + 4 * q) * 4;   // output rows 4q + j (+16i)
-        const uint8_t * ma_lds = lds + G::OFF_M + ((wave & 1) * 32 + lr) * 4;     // A rows lr (+16i)
-        const float * d_lds = reinterpret_cast<const float *>(lds + G::OFF_DA) + (wj + lr) * CB;
+            w_lds[i] = TYPE == 39 ? lds + G::OFF_W + ((wave & 1) * 256 + 2 * q * 32 + 16 * (i ^ (q & 1)) + lr) * 4
+                                  : lds + G::OFF_WG + (wave & 1) * 4096 + (2 * q * 32 + 16 * i + lr) * 16;
+        // exponent dword (MXFP4, per chunk stage) or the group's 8 scale bytes (Q8_0, group slot)
+        // of output rows 4q + j (+16i) and of A rows lr (+16i)
+        const uint8_t * m_lds = TYPE == 39 ? lds + G::OFF_M + ((wave & 1) * 32 + 4 * q) * 4
+                                           : lds + G::OFF_MG + ((wave & 1) * 32 + 4 * q) * 8;
+        const uint8_t * ma_lds = TYPE == 39 ? lds + G::OFF_M + ((wave & 1) * 32 + lr) * 4
+                                            : lds + G::OFF_MG + ((wave & 1) * 32 + lr) * 8;
+        const float * d_lds = G::GROUPED ? reinterpret_cast<const float *>(lds + G::OFF_DG) + (wj + lr) * G::GB
+                                         : reinterpret_cast<const float *>(lds + G::OFF_DA) + (wj + lr) * CB;
         // fragment columns' activation codes: row rr = 64(w >> 1) + 16jh + lr, block bb, codes 8q..8q+7
         uint32_t aoff[JF][2];
 #pragma unroll
@@ -423,12 +473,10 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
             }
 #pragma clang loop unroll(disable)
         for (int c = 0; c < n_chunks; ++c) {
-            const int sub = c % G::CPG;
-            // this chunk's loads: the stage of chunk c + S - 1, clamped to the last chunk
-            // (the stage it fills is free either way)
-            // this chunk's loads: the stage of chunk c + S - 1, clamped to the last chunk
-            // (the stage it fills is free either way)
-            dma_stage(c + G::S - 1 < n_chunks ? c + G::S - 1 : n_chunks - 1, (c + G::S - 1) % G::S);
+            const int sub = c % G::CPG, gs = (c / G::CPG) & 1;   // gs: this chunk's group slot
+            // this chunk's loads: the stage of chunk c + 1, clamped to the last chunk (the stage
+            // it fills is free either way), and chunk c + 1's bank group when it starts one
+            dma_stage(c + 1 < n_chunks ? c + 1 : n_chunks - 1, (c + 1) % G::S, c + 1 < n_chunks && (c + 1) % G::CPG == 0);
             const int ab = c % G::S, wb = ab;
             const uint8_t * st = lds + ab * G::STAGE;     // this chunk's stage
             // This chunk's blocks 2sub, 2sub+1 in the group: weight dwords of slices 2q, 2q+1
@@ -441,8 +489,9 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
                     w0[i][0] = w0[i][1] = *reinterpret_cast<const unsigned *>(w);
                     w1[i][0] = w1[i][1] = *reinterpret_cast<const unsigned *>(w + 32 * 4);
                 } else {
-                    const u32x4g v = *reinterpret_cast<const u32x4g *>(w_lds[i] + wb * G::STAGE);
-                    w0[i][0] = v[0], w1[i][0] = v[1], w0[i][1] = v[2], w1[i][1] = v[3];
+                    const uint8_t * w = w_lds[i] + gs * G::WG + 8 * sub;
+                    const u32x2g a = *reinterpret_cast<const u32x2g *>(w), b = *reinterpret_cast<const u32x2g *>(w + 512);
+                    w0[i][0] = a[0], w0[i][1] = a[1], w1[i][0] = b[0], w1[i][1] = b[1];
                 }
             }
             // MXFP4 fast path: when every exponent e of the wave's A rows (16i + lr) lies in
@@ -492,11 +541,11 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
                 const unsigned sel[2] = {lane < 16 ? 0x0000FFFFu : 0u, lane < 16 ? 0xFFFF0000u : 0u};
                 unsigned dw_row[2], da_pk[JF];
 #pragma unroll
-                for (int i = 0; i < 2; ++i) dw_row[i] = *reinterpret_cast<const unsigned *>(ma_lds + wb * G::STAGE + i * 16 * 4);
+                for (int i = 0; i < 2; ++i) dw_row[i] = *reinterpret_cast<const unsigned *>(ma_lds + gs * G::MG + i * 16 * 8 + 4 * sub);
 #pragma unroll
                 for (int jh = 0; jh < NF; ++jh) {
                     // d_act holds fp16 values, so the packing conversion is exact
-                    const float * dp = d_lds + ab * (G::STAGE / 4) + 16 * jh * CB;
+                    const float * dp = d_lds + gs * (G::DG / 4) + 16 * jh * G::GB + CB * sub;
                     da_pk[jh] = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(dp[0], dp[1]));
                 }
 #pragma unroll
@@ -533,7 +582,7 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
                         if constexpr (TYPE == 39)
                             mw[i][j] = *reinterpret_cast<const uint16_t *>(m_lds + wb * G::STAGE + (16 * i + j) * 4 + (sub & 1) * 2);
                         else
-                            mw[i][j] = *reinterpret_cast<const unsigned *>(m_lds + wb * G::STAGE + (16 * i + j) * 4);
+                            mw[i][j] = *reinterpret_cast<const unsigned *>(m_lds + gs * G::MG + (16 * i + j) * 8 + 4 * sub);
                     }
                 auto do_block = [&](int bb) {
                     auto bsrc = [&](int jh) {
@@ -541,7 +590,10 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
                         if constexpr (TYPE == 39) return *reinterpret_cast<const half8_t *>(p);
                         else return *reinterpret_cast<const long *>(p);
                     };
-                    auto dsrc = [&](int jh) { return d_lds[ab * (G::STAGE / 4) + 16 * jh * CB + bb]; };
+                    auto dsrc = [&](int jh) {
+                        if constexpr (G::GROUPED) return d_lds[gs * (G::DG / 4) + 16 * jh * G::GB + CB * sub + bb];
+                        else return d_lds[ab * (G::STAGE / 4) + 16 * jh * CB + bb];
+                    };
                     if constexpr (TYPE == 39) {
                         auto factor = [&](int i, int j, float da) {
                             return __builtin_amdgcn_ldexpf(da, static_cast<signed char>(mw[i][j] >> (8 * bb)));
@@ -641,7 +693,7 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
     };
     // Prologue: stages 0 .. S - 2 (clamped).
     if (groups > 0) {
-        for (int c = 0; c < G::S - 1; ++c) dma_stage(c < n_chunks ? c : n_chunks - 1, c);
+        dma_stage(0, 0, true);
         lds_dma_wait<0>();
     }
     __syncthreads();
