@@ -139,7 +139,9 @@ __device__ __forceinline__ half8_t i8_to_f16(long v) {
 // and the 128 jobs' activation block scales of the group ([job][4 blocks], 16 bytes each):
 // a third of the chunk's DMA instructions, whose issue (not their bytes) bounded the kernel
 // (doubling the weight DMAs of the former per-chunk dword staging added 55 us to a 345 us
-// gate_up launch, doubling the activation DMAs 30 us). Chunk c issues the loads of chunk c + 1
+// gate_up launch, doubling the activation DMAs 30 us). The same group staging for MXFP4 (8-block
+// groups over four chunks, 2 waves per SIMD) measured slower, 1215-1280 against 1110-1136 us for
+// the MXFP4 gate_up of 2048 tokens top-4, so MXFP4 keeps per-chunk staging. Chunk c issues the loads of chunk c + 1
 // (and of the next group at its last chunk); one wait and one barrier per chunk. Two stages: a
 // third one, for every operand or for the weights alone, measured no faster (Q8_0 layer of 2048
 // tokens).
