@@ -612,8 +612,9 @@ def tier_measure(args, stack) -> dict:
             f"{live_policy['hit_rate']}, {live_policy['uploaded_gb']} GB uploaded")
     deferred = None
     if args.tier_deferred:
-        # deferred mode: no host wait inside a step (misses streamed from the pinned host copy by the
-        # decode kernels, admission at the step boundary); the same trace under classic and LRU
+        # deferred mode: no host wait inside a step (misses read once from the pinned host copy by
+        # the decode kernels, which keep a device copy; admission at the step boundary copies the
+        # admitted experts from there); the same trace under classic and LRU
         deferred = {}
         sync_counters = {"classic": (int(st.hits), int(st.admissions), int(st.evictions))}
         if live_policy is not None and args.tier_live_policy == "lru":
@@ -641,14 +642,16 @@ def tier_measure(args, stack) -> dict:
                      "unit": "tok/s", "host_wall_s": round(wall3, 2), "hit_rate": round(st3.hits / (tokens * L * K), 4),
                      "admissions": int(st3.admissions), "experts_read_from_host": int(st3.host_reads),
                      "uploaded_gb": round(st3.uploaded_bytes / 1e9, 2),
-                     "host_read_gb": round(st3.host_reads * group_bytes / 1e9, 2)}
+                     "host_read_gb": round(st3.host_reads * group_bytes / 1e9, 2),
+                     "admission_copy_gb": round(st3.device_copy_bytes / 1e9, 2)}
             ref_counters = sync_counters.get(name)
             if ref_counters is not None:
                 mine = (int(st3.hits), int(st3.admissions), int(st3.evictions))
                 entry["counters_match_sync"] = ref_counters == mine
             deferred[name] = entry
             log(f"tier deferred ({name}): {entry['value']} tok/s, hit rate {entry['hit_rate']}, "
-                f"{entry['host_read_gb']} GB read from host by the kernels, {entry['uploaded_gb']} GB uploaded")
+                f"{entry['host_read_gb']} GB read from host by the kernels, {entry['uploaded_gb']} GB uploaded, "
+                f"{entry['admission_copy_gb']} GB of admissions copied on the device")
     vb.call("vbm_tier_destroy", tier.value)
     lookups = tokens * L * K
     h2d = st.uploaded_bytes / (st.copy_ms * 1e-3) / 1e9 if st.copy_ms > 0 else None
@@ -850,11 +853,46 @@ def main() -> int:
         vb.call("vbm_event_elapsed_ms", ev0.value, ev1.value, C.byref(t))
         return t.value / args.kernel_reps
 
+    # Sweep timing: a HIP graph of two passes over all layers launching only kernel A (then only
+    # kernel B), so every launch streams weights that no recent launch has read (36 layers of
+    # either kernel exceed the 256 MB memory-side cache), as in the step; per-launch time.
+    def time_sweep(which: int, passes: int = 2) -> float:
+        g = C.c_void_p()
+        vb.call("vbm_graph_begin_capture", stream)
+        for _ in range(passes):
+            for layer in range(L):
+                vb.call("vbm_decode_kernel", stack.plan, layer, which, stack.x0.ptr, stack.logits_cur.ptr, stream)
+        vb.call("vbm_graph_end_capture", stream, C.byref(g))
+        vb.call("vbm_graph_launch", g.value, stream)            # warm
+        vb.call("vbm_event_record", ev0.value, stream)
+        vb.call("vbm_graph_launch", g.value, stream)
+        vb.call("vbm_event_record", ev1.value, stream)
+        vb.call("vbm_stream_synchronize", stream)
+        vb.call("vbm_graph_destroy", g.value)
+        t = C.c_float()
+        vb.call("vbm_event_elapsed_ms", ev0.value, ev1.value, C.byref(t))
+        return t.value / (passes * L)
+
+    # The per-step logits copy that precedes every timed graph launch, timed alone (20 copies of the
+    # last step's logits, which the buffer already holds).
+    def time_step_copy(n: int = 20) -> float:
+        vb.call("vbm_event_record", ev0.value, stream)
+        for _ in range(n):
+            vb.call("vbm_memcpy_d2d", stack.logits_cur.ptr, logits_all.ptr + (n_steps - 1) * step_bytes, step_bytes, stream)
+        vb.call("vbm_event_record", ev1.value, stream)
+        vb.call("vbm_stream_synchronize", stream)
+        t = C.c_float()
+        vb.call("vbm_event_elapsed_ms", ev0.value, ev1.value, C.byref(t))
+        return t.value / n
+
     if args.kernel_reps > 0 and args.decode_schedule == "two-kernel":
         gu_avg_us = sum(time_kernel(l, 0) for l in range(L)) / L * 1e3
         dn_avg_us = sum(time_kernel(l, 1) for l in range(L)) / L * 1e3
+        gu_sw_us, dn_sw_us = time_sweep(0) * 1e3, time_sweep(1) * 1e3
+        copy_us = time_step_copy() * 1e3
     else:   # counter-collection runs (and the linked schedule, whose launches hold both kernels' work)
-        gu_avg_us = dn_avg_us = float("nan")
+        gu_avg_us = dn_avg_us = gu_sw_us = dn_sw_us = float("nan")
+        copy_us = 0.0
     last_ids = np.stack([np.lexsort((np.arange(E), -logits_host[n_steps - 1, l, 0]))[:K] for l in range(L)])
     # Algorithmic bytes per launch of kernel A: K experts x (5760 rows x 1530 B + 5760 fp32 biases)
     # + logits (E x 4 B) + previous layer outputs (K x 2880 x 4 B) + fp32 GLU outputs (K x 2880 x
@@ -867,12 +905,13 @@ def main() -> int:
     dn_gbs = dn_bytes / (dn_avg_us * 1e-6) / 1e9
     # Kernel times inside the timed step. An event record between two kernels of a graph costs
     # about 4 us on this GPU (a step with one around every kernel took 1.25 instead of 0.62 ms),
-    # so the step is timed whole and each layer's share (ms_per_step / L) is split between kernels
-    # A and B in the ratio of their isolated launch times. The committed rocprofv3 kernel trace of
+    # so the step is timed whole: its time less the logits copy before each graph launch, per
+    # layer, is split between kernels A and B in the ratio of their sweep launch times (cold
+    # weights and back-to-back launches, as in the step). The committed rocprofv3 kernel trace of
     # this command measures the in-step kernel durations directly.
-    layer_us = ms_per_step * 1e3 / L
-    gu_in_us = gu_avg_us * layer_us / (gu_avg_us + dn_avg_us)
-    dn_in_us = dn_avg_us * layer_us / (gu_avg_us + dn_avg_us)
+    layer_us = (ms_per_step * 1e3 - copy_us) / L
+    gu_in_us = gu_sw_us * layer_us / (gu_sw_us + dn_sw_us)
+    dn_in_us = dn_sw_us * layer_us / (gu_sw_us + dn_sw_us)
     gu_in_gbs = gu_bytes / (gu_in_us * 1e-6) / 1e9
     dn_in_gbs = dn_bytes / (dn_in_us * 1e-6) / 1e9
     step_gbs = step_weight_bytes / (ms_per_step / 1e3) / 1e9
@@ -883,6 +922,8 @@ def main() -> int:
         f"{dn_in_gbs:.0f} GB/s; step {step_gbs:.0f} GB/s = {step_gbs / HBM_PEAK_GBS:.3f} of peak")
     log(f"isolated repeats: kernel A (route + combine + quantize + gate_up GEMV): {gu_avg_us:.2f} us avg over {L} x "
         f"{args.kernel_reps} launches -> {gu_gbs:.0f} GB/s; kernel B (down GEMV): {dn_avg_us:.2f} us -> {dn_gbs:.0f} GB/s")
+    log(f"sweeps over all layers: kernel A {gu_sw_us:.2f} us, kernel B {dn_sw_us:.2f} us per launch; "
+        f"logits copy {copy_us:.2f} us per step")
     traffic = read_traffic(REPO / "profiles" / "decode_gate_up_120b_bs1_pmc.md")
 
     batched = None if args.no_batched else batched_measure(args, stack)
@@ -936,8 +977,10 @@ def main() -> int:
             "traffic_source": "profiles/decode_gate_up_120b_bs1_pmc.md (rocprofv3 FETCH_SIZE + WRITE_SIZE)",
             "bytes_per_launch": round(gu_bytes),
             "avg_launch_us": num(gu_in_us, 3),
-            "timing": "kernel A's share of the timed step: ms_per_step / layers split between kernels A and B in "
-                      "the ratio of their isolated launch times (events around graphs of back-to-back launches)",
+            "timing": "kernel A's share of the timed step: (ms_per_step - the per-step logits copy) / layers split "
+                      "between kernels A and B in the ratio of their launch times in sweeps over all layers (events "
+                      "around graphs of back-to-back launches of one kernel, cold weights)",
+            "sweep": {"gate_up_us": num(gu_sw_us, 3), "down_us": num(dn_sw_us, 3), "step_copy_us": num(copy_us, 3)},
             "step_frac": num(step_gbs / HBM_PEAK_GBS, 4),
             "step_achieved": num(step_gbs, 1),
             "down_kernel": {"achieved": num(dn_in_gbs, 1), "avg_launch_us": num(dn_in_us, 3),

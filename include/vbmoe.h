@@ -582,6 +582,8 @@ typedef struct {
     uint64_t prefill_streamed;           /* routed experts streamed through the reserved slots    */
     uint64_t host_reads;                 /* deferred mode: routed experts the decode kernels read  */
                                          /* from the pinned host copy (not visible in the map)    */
+    uint64_t device_copy_bytes;          /* deferred mode: bytes copied on the device to admit    */
+                                         /* experts (staging area -> slot; no host upload)         */
 } vbm_tier_stats;
 
 typedef struct vbm_tier vbm_tier;
@@ -627,14 +629,16 @@ vbm_status vbm_tier_reset(vbm_tier * tier, int policy, int64_t recent_window, in
 /* Deferred mode (enable = 1; 0 returns to the synchronous per-layer mode), the device-side
  * counterpart of the reference's hosted flush (llama-b11669-hybrid-experts.patch:2953-3005) and
  * event-protected ID hand-off (:3421-3453): a step's layers run back to back with no host wait,
- * reading each layer's expert->slot map from the device and streaming the weights of routed
- * experts that are not visible there straight from the pinned host copy; the step's routed ids
- * come back behind an event, and the next step (or vbm_tier_flush) runs admission on them, uploads
- * the admitted experts on the copy stream and publishes them one flush later. Admission sees the
- * same routes in the same order as the synchronous mode, so the counters (staged included: the
- * misses that mode would stage) and outputs are the same; `host_reads` counts the routed experts
- * the kernels actually read from host memory. Stats lag one step until vbm_tier_flush. No
- * routing trace is recorded in this mode. */
+ * reading each layer's expert->slot map from the device; a routed expert that is not visible
+ * there is read once from the pinned host copy by the decode kernels, which keep a copy of it in
+ * a device staging area ([n_layers][top_k] expert copies, allocated when the mode is enabled);
+ * the step's routed ids come back behind an event, and the next step (or vbm_tier_flush) runs
+ * admission on them, copies each admitted expert from the staging area into its slot (device to
+ * device: an admitted expert crosses PCIe once) and publishes it in the same flush. Admission
+ * sees the same routes in the same order as the synchronous mode, so the counters (staged
+ * included: the misses that mode would stage) and outputs are the same; `host_reads` counts the
+ * routed experts the kernels read from host memory (exactly the misses). Stats lag one step until
+ * vbm_tier_flush. No routing trace is recorded in this mode. */
 vbm_status vbm_tier_set_deferred(vbm_tier * tier, int enable);
 /* Deferred mode: waits for the step in flight, runs its admission and publishes every upload. */
 vbm_status vbm_tier_flush(vbm_tier * tier);

@@ -69,7 +69,8 @@ def oracle_chain(orc, host, type_id, act, x, logits_t, H, I, E, K):
 ])
 def test_tier_matches_resident_plan(gpu, orc, type_id, policy, margin, mode):
     """Synchronous mode (per-layer admission and staging), deferred mode (no host wait inside a
-    step: misses read from the pinned host copy, admission at the step boundary) and deferred mode
+    step: misses read from the pinned host copy into the device staging area, admission at the step
+    boundary, admitted experts copied into their slots from their staged copies) and deferred mode
     with the step's device part captured once as a HIP graph and replayed per token: every token
     bit-identical to the resident plan and to the oracle chain, counters equal to the Python
     admission fed the same routes. graph_nosync replays token after token with no host
@@ -176,10 +177,17 @@ def test_tier_matches_resident_plan(gpu, orc, type_id, policy, margin, mode):
     assert (st.dispatches, st.hits, st.admissions, st.evictions) == (tokens * L, py.hits, py.admissions, py.evictions)
     assert st.staged == staged and st.admissions > 0
     assert st.staged > 0 or policy == ref.LRU          # lru with margin 1 admits every miss
+    group_bytes = (2 * I * (H // 32) + H * (I // 32)) * (17 if type_id == 39 else 34)
     if mode == "sync":
-        assert st.host_reads == 0
-    else:   # every miss, and every admission not yet published, streamed from the host copy
-        assert st.host_reads >= tokens * L * K - st.hits > 0
+        assert st.host_reads == 0 and st.device_copy_bytes == 0
+    else:
+        # every pick read from the host copy was a miss (admissions are visible from the next step
+        # on; a miss can also be a pick that sat in a slot during the step and was evicted by an
+        # earlier rank's admission of its layer); every admission copied into its slot on the
+        # device; the only host uploads are the two seeds
+        assert 0 < st.host_reads <= tokens * L * K - st.hits
+        assert st.admissions * group_bytes <= st.device_copy_bytes <= 2 * st.admissions * group_bytes
+        assert st.uploaded_bytes == 2 * group_bytes
     if graph is not None:
         vb.call("vbm_graph_destroy", graph)
         vb.call("vbm_stream_destroy", stream)

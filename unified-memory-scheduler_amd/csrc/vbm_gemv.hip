@@ -528,6 +528,32 @@ __device__ __forceinline__ void load_meta(u32x4 (&st)[2], const uint8_t * meta, 
         if (off < bytes) st[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(meta + off));
     }
 }
+// Copies one 32-row tile of a slot (its codes tile and its meta tile, the bytes the decode
+// kernels read for it) from `src` to `dst`, both in the bank's slot layout, with NT threads:
+// 16-byte units, four loads in flight per thread before their stores. The deferred host tier
+// uses it to keep, in device memory, the copy of an expert that a kernel streams from pinned
+// host memory. The caller's barrier (a workgroup-scope release: every store has reached L2)
+// makes the copy readable by the workgroup's loads that follow; no other workgroup reads it.
+template <int TYPE, int NT>
+__device__ __forceinline__ void copy_slot_tile(const uint8_t * src, uint8_t * dst, int tile, int nb, int64_t codes_bytes) {
+    const int64_t tile_codes = 32ll * nb * (TYPE == 39 ? 16 : 32);
+    const int n_codes = static_cast<int>(tile_codes / 16), n = n_codes + meta_tile_bytes<TYPE>(nb) / 16;
+    const int64_t codes0 = tile * tile_codes, meta0 = codes_bytes + static_cast<int64_t>(tile) * meta_tile_bytes<TYPE>(nb);
+    for (int base = 0; base < n; base += 4 * NT) {
+        u32x4 v[4];
+        int64_t off[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = base + j * NT + static_cast<int>(threadIdx.x);
+            off[j] = i < n_codes ? codes0 + static_cast<int64_t>(i) * 16 : meta0 + static_cast<int64_t>(i - n_codes) * 16;
+            if (i < n) v[j] = *reinterpret_cast<const u32x4 *>(src + off[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (base + j * NT + static_cast<int>(threadIdx.x) < n) *reinterpret_cast<u32x4 *>(dst + off[j]) = v[j];
+    }
+}
+
 template <int NT>
 __device__ __forceinline__ void store_meta(const u32x4 (&st)[2], uint8_t * lds, int bytes) {
 #pragma unroll
@@ -940,6 +966,8 @@ struct DecodeArgs {
     float alpha, limit;
     const uint8_t * host_base; // pinned host copy of the layer's experts (slot layout), or null
     int64_t host_stride;
+    uint8_t * stage;           // device copies of host-read picks: rank r at stage + r * stage_stride, or null
+    int64_t stage_stride;
 };
 
 constexpr int kDownThreads = 256;
@@ -1056,7 +1084,10 @@ size_t decode_lds_bytes(int nb) {
 // the routing weight, then ADD in rank order) and quantized, thread t owning elements 8t..8t+7
 // and 8(t + 256).., straight from registers into the activation row. The tile's 16 GLU outputs
 // go out as fp32; kernel B quantizes each 32-element block of them (the pair of tiles).
-template <int TYPE, int NPL, int NB>
+// STAGE (launches with a staging area, the deferred host tier): a workgroup whose pick is read
+// from the pinned host copy copies its tile into the staging area first and streams that copy.
+// A separate instantiation, so the resident-only kernels carry none of that code.
+template <int TYPE, int NPL, int NB, bool STAGE>
 __global__ __launch_bounds__(kDownThreads) __attribute__((amdgpu_waves_per_eu(3))) void decode_gate_up_kernel(DecodeArgs A) {
     constexpr int D = gate_up_depth<TYPE>();
     constexpr int kChunks = 2;                     // 8-element input chunks per thread (hidden <= 4096)
@@ -1125,6 +1156,15 @@ __global__ __launch_bounds__(kDownThreads) __attribute__((amdgpu_waves_per_eu(3)
     const bool slot_ok = in_bank || A.host_base != nullptr;
     const uint8_t * slot_base = in_bank ? A.bank + static_cast<size_t>(slot) * S.slot_bytes
                                         : (slot_ok ? A.host_base + static_cast<size_t>(expert) * A.host_stride : A.bank);
+    if constexpr (STAGE) {
+        if (!in_bank && slot_ok) {
+            // a host-read pick: copy the tile into the staging area once, then stream the copy
+            uint8_t * staged = A.stage + static_cast<size_t>(rank) * A.stage_stride;
+            copy_slot_tile<TYPE, kDownThreads>(slot_base, staged, tile, nb, S.codes_bytes);
+            __syncthreads();
+            slot_base = staged;
+        }
+    }
     const uint8_t * codes_tile = slot_base + static_cast<size_t>(tile) * 32 * nb * (TYPE == 39 ? 16 : 32);
     const int mbytes = meta_tile_bytes<TYPE>(nb);
     u32x4 mst[2];
@@ -1229,13 +1269,15 @@ struct DecodeDownArgs {
     float * y;                 // [top_k][rows]
     const uint8_t * host_base; // pinned host copy of the layer's experts (slot layout), or null
     int64_t host_stride;
+    uint8_t * stage;           // as in DecodeArgs (the down part of each rank's copy)
+    int64_t stage_stride;
 };
 
 // Kernel B: one 32-row tile of one rank; wave w holds lane slices 2w (lanes 0..31) and 2w + 1
 // (lanes 32..63) of the tile's rows. Its prologue requantizes the rank's GLU outputs (x86
 // quantize_row_q8_0 per 32-element block, the arithmetic of the reference's activation
 // quantization) into the LDS activation row while its weight stream is in flight.
-template <int TYPE, int NB>
+template <int TYPE, int NB, bool STAGE>
 __global__ __launch_bounds__(kDownThreads) void decode_down_kernel(DecodeDownArgs A) {
     constexpr int D = down_depth<TYPE>();
     __shared__ float red[8][32];
@@ -1268,6 +1310,14 @@ __global__ __launch_bounds__(kDownThreads) void decode_down_kernel(DecodeDownArg
     const bool slot_ok = in_bank || A.host_base != nullptr;
     const uint8_t * slot_base = in_bank ? A.bank + static_cast<size_t>(slot) * S.slot_bytes
                                         : (slot_ok ? A.host_base + static_cast<size_t>(expert) * A.host_stride : A.bank);
+    if constexpr (STAGE) {                        // as in kernel A
+        if (!in_bank && slot_ok) {
+            uint8_t * staged = A.stage + static_cast<size_t>(rank) * A.stage_stride;
+            copy_slot_tile<TYPE, kDownThreads>(slot_base, staged, tile, nb, S.codes_bytes);
+            __syncthreads();
+            slot_base = staged;
+        }
+    }
     const uint8_t * codes_tile = slot_base + static_cast<size_t>(tile) * 32 * nb * (TYPE == 39 ? 16 : 32);
     const int mbytes = meta_tile_bytes<TYPE>(nb);
     u32x4 mst[2];
@@ -1664,11 +1714,14 @@ __global__ __launch_bounds__(kLinkThreads) void decode_link_kernel(LinkArgs A) {
 
 template <int TYPE, int NPL, int NB>
 void launch_gate_up_npl(const DecodeArgs & a, dim3 grid, size_t lds, hipStream_t stream) {
-    if (lds > 65536)
-        check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_gate_up_kernel<TYPE, NPL, NB>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)),
-                  "decode gate_up LDS attribute");
-    hipLaunchKernelGGL((decode_gate_up_kernel<TYPE, NPL, NB>), grid, dim3(kDownThreads), lds, stream, a);
+    auto launch = [&](auto kernel) {
+        if (lds > 65536)
+            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          static_cast<int>(lds)), "decode gate_up LDS attribute");
+        hipLaunchKernelGGL(kernel, grid, dim3(kDownThreads), lds, stream, a);
+    };
+    if (a.stage) launch(&decode_gate_up_kernel<TYPE, NPL, NB, true>);
+    else launch(&decode_gate_up_kernel<TYPE, NPL, NB, false>);
 }
 
 // Row lengths (blocks) with a fully unrolled weight stream: hidden = intermediate = 2880 (MXFP4,
@@ -1699,8 +1752,14 @@ void launch_decode_down_typed(const DecodeDownArgs & a, int top_k, hipStream_t s
     const size_t lds = decode_lds_bytes<TYPE>(a.shape.nb);
     const dim3 grid(static_cast<unsigned>(a.shape.rows / 32), static_cast<unsigned>(top_k));
     constexpr int kFixed = fixed_down_nb<TYPE>();
-    if (a.shape.nb == kFixed) hipLaunchKernelGGL((decode_down_kernel<TYPE, kFixed>), grid, dim3(kDownThreads), lds, stream, a);
-    else hipLaunchKernelGGL((decode_down_kernel<TYPE, 0>), grid, dim3(kDownThreads), lds, stream, a);
+    const bool fixed = a.shape.nb == kFixed;
+    if (a.stage) {
+        if (fixed) hipLaunchKernelGGL((decode_down_kernel<TYPE, kFixed, true>), grid, dim3(kDownThreads), lds, stream, a);
+        else hipLaunchKernelGGL((decode_down_kernel<TYPE, 0, true>), grid, dim3(kDownThreads), lds, stream, a);
+    } else {
+        if (fixed) hipLaunchKernelGGL((decode_down_kernel<TYPE, kFixed, false>), grid, dim3(kDownThreads), lds, stream, a);
+        else hipLaunchKernelGGL((decode_down_kernel<TYPE, 0, false>), grid, dim3(kDownThreads), lds, stream, a);
+    }
     check_hip(hipGetLastError(), "decode down launch");
 }
 
@@ -1892,6 +1951,11 @@ void launch_decode_gate_up(const DecodeGateUpArgs & d, hipStream_t stream) {
     require(d.host_base == nullptr || d.host_stride >= static_cast<int64_t>(bank.slot_bytes), "host copy stride too small");
     a.host_base = d.host_base;
     a.host_stride = d.host_stride;
+    require(d.stage == nullptr || (d.host_base != nullptr && d.stage_stride >= static_cast<int64_t>(bank.slot_bytes) &&
+                                   reinterpret_cast<uintptr_t>(d.stage) % 16 == 0 && d.stage_stride % 16 == 0),
+            "staging area needs a host copy, 16-byte alignment and a stride of at least a slot");
+    a.stage = d.stage;
+    a.stage_stride = d.stage_stride;
     if (bank.type == VBM_TYPE_MXFP4) launch_decode_typed<39>(a, stream);
     else launch_decode_typed<8>(a, stream);
 }
@@ -1986,6 +2050,11 @@ void launch_decode_down(const DecodeDownParams & d, hipStream_t stream) {
     require(d.host_base == nullptr || d.host_stride >= static_cast<int64_t>(bank.slot_bytes), "host copy stride too small");
     a.host_base = d.host_base;
     a.host_stride = d.host_stride;
+    require(d.stage == nullptr || (d.host_base != nullptr && d.stage_stride >= static_cast<int64_t>(bank.slot_bytes) &&
+                                   reinterpret_cast<uintptr_t>(d.stage) % 16 == 0 && d.stage_stride % 16 == 0),
+            "staging area needs a host copy, 16-byte alignment and a stride of at least a slot");
+    a.stage = d.stage;
+    a.stage_stride = d.stage_stride;
     if (bank.type == VBM_TYPE_MXFP4) launch_decode_down_typed<39>(a, static_cast<int>(d.top_k), stream);
     else launch_decode_down_typed<8>(a, static_cast<int>(d.top_k), stream);
 }

@@ -291,6 +291,12 @@ struct DecodeGateUpArgs {
     // its weights from there instead of being poisoned.
     const uint8_t * host_base = nullptr;
     int64_t host_stride = 0;
+    // Optional with host_base: device staging area of the layer's picks (rank r's slot copy at
+    // stage + r * stage_stride). A workgroup whose pick streams from the host copy first copies
+    // its tile there and then reads that copy, so the whole expert is in device memory after the
+    // launch.
+    uint8_t * stage = nullptr;
+    int64_t stage_stride = 0;
 };
 void launch_decode_gate_up(const DecodeGateUpArgs & d, hipStream_t stream);
 
@@ -307,6 +313,8 @@ struct DecodeDownParams {
     float * y;                        // [top_k][hidden]
     const uint8_t * host_base = nullptr;   // as in DecodeGateUpArgs (the down bank's slot layout)
     int64_t host_stride = 0;
+    uint8_t * stage = nullptr;             // as in DecodeGateUpArgs
+    int64_t stage_stride = 0;
 };
 void launch_decode_down(const DecodeDownParams & d, hipStream_t stream);
 

@@ -20,12 +20,13 @@
 // reference's hosted flush (llama-b11669-hybrid-experts.patch:2953-3005) and its event-protected ID
 // hand-off (:3421-3453): the layers of a step run back to back on the device against per-layer
 // expert->slot maps published at the step boundary; a routed expert that is not visible in the map
-// streams its weights from the pinned host copy inside the decode kernels (the device-side
-// counterpart of the reference's CPU miss path, :1728-1847). The step's routed ids come back
-// asynchronously behind an event; the next step's flush runs admission on them, issues the
-// admitted experts' uploads into their victim slots on the copy stream, and publishes those
-// experts one flush later, after the copy event. Victims leave the map in the same flush that
-// starts overwriting them, and the previous step has finished by then, so no reader races a copy.
+// is read from the pinned host copy inside the decode kernels (the device-side counterpart of the
+// reference's CPU miss path, :1728-1847), each workgroup copying its tile into a device staging
+// area ([layer][rank] expert copies) and computing from that copy. The step's routed ids come back
+// asynchronously behind an event; the next step's flush runs admission on them and copies each
+// admitted expert from the staging area into its victim slot (device to device, so an admitted
+// expert crosses PCIe once), waits for those copies and publishes the admitted experts at once.
+// The previous step has finished before the flush overwrites a victim or a staging copy.
 #include "vbm_internal.hpp"
 
 #include <algorithm>
@@ -78,8 +79,7 @@ struct vbm_tier {
     bool step_pending = false;        // its ids still await admission
     bool awaiting = false;            // a step was begun; its device part (eager or a graph replay) follows
     bool enqueued = false;            // that step's device part was enqueued eagerly
-    std::vector<std::pair<int64_t, int64_t>> unpublished;   // (layer, expert) uploads in flight
-    bool uploads_timed = false;       // copy_begin / copy_end bracket the uploads in flight
+    uint8_t * staged = nullptr;       // device [L][K] expert copies (gate_up | down) of host-read picks
 
     ~vbm_tier() {
         (void)hipSetDevice(device);
@@ -108,6 +108,7 @@ struct vbm_tier {
         if (host_maps) (void)hipHostFree(host_maps);
         if (step_ids_host) (void)hipHostFree(step_ids_host);
         if (step_done) (void)hipEventDestroy(step_done);
+        if (staged) (void)hipFree(staged);
     }
 
     uint8_t * host_expert(int64_t layer, int64_t expert) const {
@@ -134,33 +135,37 @@ void stage(vbm_tier & t, int64_t layer, int64_t expert, int64_t slot) {
     t.stats.uploaded_bytes += t.gu_bytes + t.dn_bytes;
 }
 
-// Deferred mode, at a step boundary: (1) wait for the last step and publish the uploads of the
-// previous flush (their copies were issued a step ago); (2) run admission on the last step's
-// routed ids, layer by layer, as the synchronous mode does per layer; (3) issue the admitted
-// experts' uploads on the copy stream; (4) rebuild the per-layer maps: the admission's slot map
-// minus the uploads still in flight. The maps reach the device at the start of the next step.
+// Copies `bytes` from one device range to another on the copy stream (device_copy_bytes).
+void copy_device(vbm_tier & t, uint8_t * dst, const uint8_t * src, size_t bytes, const char * what) {
+    check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, t.copy_stream), what);
+    t.stats.device_copy_bytes += bytes;
+}
+
+// Deferred mode, at a step boundary: (1) wait for the last step; (2) run admission on its routed
+// ids, layer by layer, as the synchronous mode does per layer; (3) copy each admitted expert into
+// its slot from the device copy the step left: a pick that was not in the step's map was read from
+// the host copy by the step's decode kernels, which left its copy in the staging area (rank r of
+// layer l); a pick that was in a slot during the step but is admitted again (an earlier rank's
+// admission of the same layer evicted it) is first saved from that slot into its own, unused,
+// staging entry, before any slot is overwritten; then every admitted expert is copied from the
+// staging area into its slot, all on the copy stream in that order (an upload from the host copy
+// only for a pick outside the step's ids, which admission does not produce); (4) wait for the
+// copies and rebuild the per-layer maps from the admission's slot maps, admitted experts
+// included. The maps reach the device at the start of the next step.
 void tier_flush(vbm_tier & t) {
     const vbm_tier_desc & d = t.desc;
     const int64_t L = d.n_layers, E = d.n_expert, K = d.top_k;
-    if (t.step_pending) check_hip(hipEventSynchronize(t.step_done), "tier step hand-off");
-    if (!t.unpublished.empty()) {
-        check_hip(hipEventSynchronize(t.copy_end), "tier upload");
-        if (t.uploads_timed) {
-            float ms = 0.0f;
-            check_hip(hipEventElapsedTime(&ms, t.copy_begin, t.copy_end), "tier copy timing");
-            t.stats.copy_ms += ms;
-        }
-        t.unpublished.clear();
-        t.uploads_timed = false;
-    }
-    std::vector<std::pair<int64_t, int64_t>> uploads;
     if (t.step_pending) {
+        check_hip(hipEventSynchronize(t.step_done), "tier step hand-off");
         std::vector<int32_t> hits(static_cast<size_t>(K)), slots(static_cast<size_t>(K)),
             experts(static_cast<size_t>(K)), evicted(static_cast<size_t>(K));
         std::vector<int32_t> map(static_cast<size_t>(E));
+        struct Admitted { int64_t layer, rank, expert, slot, old_slot; };
+        std::vector<Admitted> admitted;
         for (int64_t l = 0; l < L; ++l) {
             const int32_t * ids = t.step_ids_host + l * K;
-            for (int64_t r = 0; r < K; ++r) t.stats.host_reads += t.host_maps[l * E + ids[r]] < 0;   // the step's map
+            const int32_t * step_map = t.host_maps + l * E;     // the map the step ran with
+            for (int64_t r = 0; r < K; ++r) t.stats.host_reads += step_map[ids[r]] < 0;
             int64_t n_admitted = 0;
             check_status(vbm_admission_admit(t.admission, l, ids, hits.data(), slots.data(), experts.data(),
                                              evicted.data(), &n_admitted), "tier admission");
@@ -173,39 +178,50 @@ void tier_flush(vbm_tier & t) {
             t.stats.admissions += static_cast<uint64_t>(n_admitted);
             for (int64_t i = 0; i < n_admitted; ++i) {
                 t.stats.evictions += evicted[i] >= 0;
-                uploads.emplace_back(l, experts[i]);
-            }
-            if (n_admitted > 0) {
-                if (!t.uploads_timed) {
-                    check_hip(hipEventRecord(t.copy_begin, t.copy_stream), "tier copy event");
-                    t.uploads_timed = true;
-                }
-                for (int64_t i = 0; i < n_admitted; ++i) stage(t, l, experts[i], slots[i]);
+                const int64_t rank = std::find(ids, ids + K, experts[i]) - ids;
+                admitted.push_back({l, rank, experts[i], slots[i], rank < K ? step_map[experts[i]] : -1});
             }
         }
         t.step_pending = false;
+        if (!admitted.empty()) {
+            const size_t stride = t.gu_bytes + t.dn_bytes;
+            auto staged_of = [&](const Admitted & a) { return t.staged + static_cast<size_t>(a.layer * K + a.rank) * stride; };
+            check_hip(hipEventRecord(t.copy_begin, t.copy_stream), "tier copy event");
+            for (const Admitted & a : admitted)
+                if (a.rank < K && a.old_slot >= 0) {
+                    copy_device(t, staged_of(a), t.gate_up->base + static_cast<size_t>(a.old_slot) * t.gu_bytes, t.gu_bytes,
+                                "tier gate_up save");
+                    copy_device(t, staged_of(a) + t.gu_bytes, t.down->base + static_cast<size_t>(a.old_slot) * t.dn_bytes,
+                                t.dn_bytes, "tier down save");
+                }
+            for (const Admitted & a : admitted) {
+                if (a.rank < K) {
+                    copy_device(t, t.gate_up->base + static_cast<size_t>(a.slot) * t.gu_bytes, staged_of(a), t.gu_bytes,
+                                "tier gate_up admission copy");
+                    copy_device(t, t.down->base + static_cast<size_t>(a.slot) * t.dn_bytes, staged_of(a) + t.gu_bytes,
+                                t.dn_bytes, "tier down admission copy");
+                } else {
+                    stage(t, a.layer, a.expert, a.slot);
+                }
+            }
+            check_hip(hipEventRecord(t.copy_end, t.copy_stream), "tier copy event");
+            check_hip(hipEventSynchronize(t.copy_end), "tier admission copies");
+            float ms = 0.0f;
+            check_hip(hipEventElapsedTime(&ms, t.copy_begin, t.copy_end), "tier copy timing");
+            t.stats.copy_ms += ms;
+        }
     }
-    if (!uploads.empty()) check_hip(hipEventRecord(t.copy_end, t.copy_stream), "tier copy event");
-    t.unpublished = std::move(uploads);
     for (int64_t l = 0; l < L; ++l)
         check_status(vbm_admission_slot_map(t.admission, l, t.host_maps + l * E), "tier slot map");
-    for (const auto & u : t.unpublished) t.host_maps[u.first * E + u.second] = -1;
 }
 
-// Completes everything in flight and publishes it (before a prefill, a mode change or teardown).
+// Completes the step in flight, its admissions and their copies (before a prefill, a seed, a
+// mode change or teardown).
 void tier_quiesce(vbm_tier & t) {
     if (!t.deferred) return;
     if (t.awaiting) t.step_pending = true;
     t.awaiting = false;
     tier_flush(t);
-    if (!t.unpublished.empty()) {
-        check_hip(hipEventSynchronize(t.copy_end), "tier upload");
-        t.unpublished.clear();
-        t.uploads_timed = false;
-        const int64_t L = t.desc.n_layers, E = t.desc.n_expert;
-        for (int64_t l = 0; l < L; ++l)
-            check_status(vbm_admission_slot_map(t.admission, l, t.host_maps + l * E), "tier slot map");
-    }
 }
 
 // The device part of a deferred step (no host waits): publish the maps, the layers back to back
@@ -236,6 +252,8 @@ void tier_enqueue_step(vbm_tier & t, const float * x, const float * logits, floa
         a.limit = 7.0f;
         a.host_base = layer_host;
         a.host_stride = stride;
+        a.stage = t.staged + static_cast<size_t>(l * K) * static_cast<size_t>(stride);
+        a.stage_stride = stride;
         launch_decode_gate_up(a, s);
         DecodeDownParams b{};
         b.bank = t.down;
@@ -248,6 +266,8 @@ void tier_enqueue_step(vbm_tier & t, const float * x, const float * logits, floa
         b.y = t.y;
         b.host_base = layer_host + t.gu_bytes;
         b.host_stride = stride;
+        b.stage = a.stage + t.gu_bytes;
+        b.stage_stride = stride;
         launch_decode_down(b, s);
     }
     launch_combine(t.y, t.route_w + (L - 1) * K, H, K, 1, out, s);
@@ -659,6 +679,8 @@ vbm_status vbm_tier_set_deferred(vbm_tier * t, int enable) {
                 check_hip(hipHostMalloc(reinterpret_cast<void **>(&t->step_ids_host), sizeof(int32_t) * L * K,
                                         hipHostMallocDefault), "tier ids");
                 check_hip(hipEventCreateWithFlags(&t->step_done, hipEventDisableTiming), "tier event");
+                check_hip(hipMalloc(reinterpret_cast<void **>(&t->staged),
+                                    static_cast<size_t>(L * K) * (t->gu_bytes + t->dn_bytes)), "tier staging area");
             }
             if (t->used) check_hip(hipEventSynchronize(t->last_use), "tier mode change");
             check_hip(hipStreamSynchronize(t->copy_stream), "tier mode change");
@@ -689,8 +711,6 @@ vbm_status vbm_tier_reset(vbm_tier * t, int policy, int64_t recent_window, int64
         t->desc.margin = margin;
         t->stats = vbm_tier_stats{};
         t->step_pending = t->awaiting = t->enqueued = false;
-        t->unpublished.clear();
-        t->uploads_timed = false;
         t->started = false;
         t->used = false;
         if (t->deferred)

@@ -35,7 +35,7 @@ class TierStats(C.Structure):
     _fields_ = [
         ("dispatches", u64), ("hits", u64), ("admissions", u64), ("evictions", u64), ("staged", u64),
         ("uploaded_bytes", u64), ("copy_ms", C.c_double), ("prefill_tokens", u64), ("prefill_resident", u64),
-        ("prefill_streamed", u64), ("host_reads", u64),
+        ("prefill_streamed", u64), ("host_reads", u64), ("device_copy_bytes", u64),
     ]
 
 
