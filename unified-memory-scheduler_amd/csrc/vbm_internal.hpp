@@ -100,10 +100,14 @@ struct GroupBuffers {
 int64_t group_chunk_ints(int64_t n_as, int64_t n_entries);
 size_t group_workspace_bytes(int64_t n_as, int64_t n_entries);
 GroupBuffers carve_group(void * base, int64_t n_as, int64_t n_entries);
-// job_tile > 0: also the batched GEMV's job chunks of that many tokens (gemv_chunk_tokens) into
-// g.chunk_list, laid out for gemv_max_chunks entries.
+// job_tile > 0: also the job tiles of that many jobs per active expert, in active order: by
+// default the batched GEMV's job chunks (gemv_chunk_tokens) into g.chunk_list, laid out for
+// gemv_max_chunks entries; with tiles_out, the grouped GEMM's tile list (expert at [0, tiles_max),
+// first job at [tiles_max, 2 tiles_max), count at [2 tiles_max]), as gemm_tiles_kernel writes it
+// without a tile filter.
 void launch_group(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride, int64_t n_as,
-                  const GroupBuffers & g, hipStream_t stream, int job_tile = 0);
+                  const GroupBuffers & g, hipStream_t stream, int job_tile = 0, int32_t * tiles_out = nullptr,
+                  int64_t tiles_max = 0);
 // Token width of the batched GEMV's job chunks for a bound on jobs per expert, and the bound on
 // the number of chunks: at most one partial chunk per active expert plus entries / width full ones.
 inline int gemv_chunk_tokens(int64_t max_per_expert) {
@@ -263,11 +267,13 @@ LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint
 // pass's gate_up and down GEMMs. grid_tiles > 0: the pass's expert->slot map also filters the tile
 // list, and grid_tiles bounds its tiles (sum over its experts of ceil(count / kGemmJobTile)), so a pass over a
 // few experts launches only their workgroups.
+// gemm_tiles: prepare also writes the grouped GEMM's unfiltered tile list (then a pass with no
+// grid_tiles may take tiles_ready = true and skip gemm_tiles_kernel).
 void prefill_prepare(const vbm_moe_layer_desc & d, const float * x, const int32_t * ids, int64_t n_tokens,
-                     const LayerWorkspace & w, hipStream_t s);
+                     const LayerWorkspace & w, hipStream_t s, bool gemm_tiles = false);
 void prefill_pass(const vbm_moe_layer_desc & d, const int32_t * expert_to_slot, int64_t n_tokens,
                   const LayerWorkspace & w, const float * route_w, void * const * events, hipStream_t s,
-                  int64_t grid_tiles = 0);
+                  int64_t grid_tiles = 0, bool tiles_ready = false);
 
 // Kernel A of the fused single-token decode: routing, input combine + Q8_0, gate_up GEMV, GLU,
 // requantization into the down activation rows.

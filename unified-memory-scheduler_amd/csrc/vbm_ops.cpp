@@ -116,16 +116,21 @@ LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint
 }
 
 void prefill_prepare(const vbm_moe_layer_desc & d, const float * x, const int32_t * ids, int64_t n_tokens,
-                     const LayerWorkspace & w, hipStream_t s) {
+                     const LayerWorkspace & w, hipStream_t s, bool gemm_tiles) {
     const GemmRowLayout gx{d.hidden / 32, d.gate_up->type};
     launch_gemm_rows_from_f32(x, n_tokens, d.hidden, d.hidden, gx, w.xrows_x, s);
-    const GroupBuffers g = carve_group(w.group, d.n_expert, n_tokens * d.top_k);
-    launch_group(ids, d.top_k, n_tokens, d.top_k, d.n_expert, g, s);
+    const int64_t entries = n_tokens * d.top_k;
+    const GroupBuffers g = carve_group(w.group, d.n_expert, entries);
+    if (gemm_tiles)   // the grouping scan also writes the GEMM's (unfiltered) job tile list
+        launch_group(ids, d.top_k, n_tokens, d.top_k, d.n_expert, g, s, static_cast<int>(kGemmJobTile),
+                     static_cast<int32_t *>(w.tiles), gemm_max_tiles(d.n_expert, entries, static_cast<int>(kGemmJobTile)));
+    else
+        launch_group(ids, d.top_k, n_tokens, d.top_k, d.n_expert, g, s);
 }
 
 void prefill_pass(const vbm_moe_layer_desc & d, const int32_t * expert_to_slot, int64_t n_tokens,
                   const LayerWorkspace & w, const float * route_w, void * const * events, hipStream_t s,
-                  int64_t grid_tiles) {
+                  int64_t grid_tiles, bool tiles_ready) {
     const int64_t K = d.top_k;
     const GemmRowLayout gx{d.hidden / 32, d.gate_up->type}, ga{d.intermediate / 32, d.down->type};
     GemmParams p{};
@@ -142,6 +147,7 @@ void prefill_pass(const vbm_moe_layer_desc & d, const int32_t * expert_to_slot, 
         p.tile_filter = expert_to_slot;
         p.grid_tiles = grid_tiles;
     }
+    p.tiles_ready = tiles_ready;
     p.bank = d.gate_up;
     p.rows_in = w.xrows_x;
     p.lay = gx;
@@ -357,8 +363,8 @@ void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits
     const GroupBuffers g = carve_group(w.group, d->n_expert, entries);
     if (use_gemm(*d, n_tokens) && gemm_pays(n_tokens, K, d->n_expert)) {
         // Prefill-sized groups: MFMA grouped GEMM (exact block dots, fp32 accumulation order).
-        prefill_prepare(*d, x, ids_d, n_tokens, w, s);
-        prefill_pass(*d, d->expert_to_slot, n_tokens, w, w_d, events, s);
+        prefill_prepare(*d, x, ids_d, n_tokens, w, s, true);
+        prefill_pass(*d, d->expert_to_slot, n_tokens, w, w_d, events, s, 0, true);
         launch_combine(w.y, nullptr, H, K, n_tokens, out, s);   // rows weighted in the down epilogue
         return;
     }

@@ -210,7 +210,41 @@ __global__ __launch_bounds__(64) void topk_softmax_kernel(const float * __restri
     wave_topk_softmax<NPL>(logits + t * n_expert, n_expert, top_k, ids + t * top_k, weights + t * top_k);
 }
 
-// out[t][i] = ((w0*y0 + w1*y1) + w2*y2) + ... : ggml MUL by the weight then sequential ADD.
+// out[t][i] = ((w0*y0 + w1*y1) + w2*y2) + ... : ggml MUL by the weight then sequential ADD, or the
+// ADDs alone when the rows are already weighted (w null: the grouped GEMM's epilogue weighted them).
+// Workgroup (token, 1024-row segment); each thread owns 4 consecutive rows and issues the 16-byte
+// loads of up to 8 ranks before adding them in rank order (rows % 4 == 0, 16-byte aligned).
+template <bool WEIGHTED>
+__global__ __launch_bounds__(256) void combine4_kernel(const float * __restrict__ y, const float * __restrict__ w,
+                                                       int64_t rows, int n_ids, float * __restrict__ out) {
+    const int64_t t = blockIdx.x;
+    const int64_t i = (blockIdx.y * 256ll + threadIdx.x) * 4;
+    if (i >= rows) return;
+    const float * yt = y + t * n_ids * rows + i;
+    const float * wt = WEIGHTED ? w + t * n_ids : nullptr;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int r0 = 0; r0 < n_ids; r0 += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (r0 + j < n_ids) v[j] = *reinterpret_cast<const float4 *>(yt + static_cast<int64_t>(r0 + j) * rows);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int r = r0 + j;
+            if (r < n_ids) {
+                float4 term = v[j];
+                if constexpr (WEIGHTED) {
+                    const float wr = wt[r];
+                    term = make_float4(term.x * wr, term.y * wr, term.z * wr, term.w * wr);
+                }
+                acc = r == 0 ? term : make_float4(acc.x + term.x, acc.y + term.y, acc.z + term.z, acc.w + term.w);
+            }
+        }
+    }
+    *reinterpret_cast<float4 *>(out + t * rows + i) = acc;
+}
+
+// The same sum one row per thread, for rows not a multiple of 4 or unaligned buffers.
 // Workgroup (token, 256-row segment).
 __global__ void combine_kernel(const float * __restrict__ y, const float * __restrict__ w, int64_t rows,
                                int n_ids, int64_t n_tokens, float * __restrict__ out) {
@@ -282,7 +316,7 @@ GroupBuffers carve_group(void * base, int64_t n_as, int64_t n_entries) {
 }
 
 void launch_group(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t ids_stride, int64_t n_as,
-                  const GroupBuffers & g, hipStream_t stream, int job_tile) {
+                  const GroupBuffers & g, hipStream_t stream, int job_tile, int32_t * tiles_out, int64_t tiles_max) {
     require(n_as > 0 && n_as <= kMaxExperts, "grouping supports 1..1024 experts");
     require(n_ids > 0 && n_tokens > 0 && n_ids * n_tokens <= (1ll << 24), "grouping entry count out of range");
     require(ids_stride >= n_ids, "ids token stride must be >= n_ids");
@@ -295,13 +329,20 @@ void launch_group(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t 
                        ids_stride, static_cast<int>(n_as), g.chunk_counts);
     check_hip(hipGetLastError(), "grouping count launch");
     int64_t max_tiles = 0;
-    if (job_tile > 0) {
+    int32_t * tiles = g.chunk_list;
+    if (job_tile > 0 && tiles_out) {
+        // every active expert's tiles fit: at most entries / job_tile full ones plus one partial each
+        require(tiles_max >= (n + job_tile - 1) / job_tile + std::min(n_as, n) && tiles_max < (1ll << 31),
+                "job tile list bound too small");
+        max_tiles = tiles_max;
+        tiles = tiles_out;
+    } else if (job_tile > 0) {
         max_tiles = gemv_max_chunks(std::min(n_as, n), n, job_tile);
         require(g.chunk_list != nullptr && max_tiles <= g.chunk_list_items, "job chunk list exceeds its workspace");
     }
     hipLaunchKernelGGL(group_scan_kernel, dim3(1), dim3(kGroupThreads), 0, stream, n_chunks, static_cast<int>(n_as),
                        g.chunk_counts, g.counts, g.offsets, g.active, g.n_active, g.error, job_tile,
-                       static_cast<int>(max_tiles), g.chunk_list);
+                       static_cast<int>(max_tiles), tiles);
     check_hip(hipGetLastError(), "grouping scan launch");
     hipLaunchKernelGGL(group_place_kernel, dim3(n_chunks), dim3(kGroupThreads), 0, stream, ids, static_cast<int>(n_ids), n,
                        ids_stride, static_cast<int>(n_as), id_bits, g.chunk_counts, g.offsets, g.rows);
@@ -340,8 +381,15 @@ void launch_router(const float * router_w, const float * router_b, const float *
 void launch_combine(const float * y, const float * weights, int64_t rows, int64_t n_ids, int64_t n_tokens, float * out,
                     hipStream_t stream) {
     require(n_tokens > 0 && n_tokens < (1ll << 31) && rows > 0 && (rows + 255) / 256 <= 65535, "combine shape out of range");
-    hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(n_tokens), static_cast<unsigned>((rows + 255) / 256)), dim3(256),
-                       0, stream, y, weights, rows, static_cast<int>(n_ids), n_tokens, out);
+    const bool vec = rows % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    if (vec) {
+        const dim3 grid(static_cast<unsigned>(n_tokens), static_cast<unsigned>((rows + 1023) / 1024));
+        if (weights) hipLaunchKernelGGL(combine4_kernel<true>, grid, dim3(256), 0, stream, y, weights, rows, static_cast<int>(n_ids), out);
+        else hipLaunchKernelGGL(combine4_kernel<false>, grid, dim3(256), 0, stream, y, weights, rows, static_cast<int>(n_ids), out);
+    } else {
+        hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(n_tokens), static_cast<unsigned>((rows + 255) / 256)),
+                           dim3(256), 0, stream, y, weights, rows, static_cast<int>(n_ids), n_tokens, out);
+    }
     check_hip(hipGetLastError(), "combine launch");
 }
 
