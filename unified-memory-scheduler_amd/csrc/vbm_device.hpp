@@ -26,10 +26,11 @@ __device__ __forceinline__ float glu(int activation, float g0, float u0, float a
 // One wavefront: top-k of `logits[0..n)` in the total order (value desc, then lower index;
 // tools/trace/topk-tie-probe.cpp:111-113), pick j being the best element strictly after pick j-1,
 // then ggml soft_max over the k selected values (expf(v - max), sum in double, scale by
-// (float)(1/sum)). Lane 0 writes ids[0..k) and weights[0..k). k <= 64.
-// NPL: logits per lane (n <= 64 * NPL, chosen by the launcher).
+// (float)(1/sum)). Lanes 0..k-1 write ids[0..k) and weights[0..k), and the ids to `ids_lds` too
+// when it is given. k <= 64. NPL: logits per lane (n <= 64 * NPL, chosen by the launcher).
 template <int NPL>
-__device__ __forceinline__ void wave_topk_softmax(const float * logits, int n, int k, int32_t * ids, float * weights) {
+__device__ __forceinline__ void wave_topk_softmax(const float * logits, int n, int k, int32_t * ids, float * weights,
+                                                  int32_t * ids_lds = nullptr) {
     const int lane = threadIdx.x & 63;
     float prev_v = INFINITY;
     int prev_i = -1;
@@ -73,6 +74,7 @@ __device__ __forceinline__ void wave_topk_softmax(const float * logits, int n, i
     if (lane < k) {
         ids[lane] = sel_i;
         weights[lane] = e * scale;
+        if (ids_lds) ids_lds[lane] = sel_i;
     }
 }
 
@@ -161,5 +163,47 @@ __device__ __forceinline__ float route_softmax(const float * s_val, const int32_
     for (int j = 0; j < k; ++j) sum += static_cast<double>(__shfl(e, j));
     return e * static_cast<float>(1.0 / sum);
 }
+
+// x86 quantize_row_q8_0 of one block by one 32-lane group: block bg (row bg / nb, block bg % nb)
+// of the fp32 rows x, written into activation rows of the GEMV layout `Layout` (and optionally as
+// a ggml Q8_0 block). Lane 0 of block 0 clears the row's -128 flag (this quantizer never produces
+// -128). Every lane of the group must call it.
+template <class Layout>
+__device__ __forceinline__ void quantize_expand_block(const float * __restrict__ x, int64_t n_rows, int nb, int64_t x_stride,
+                                                      const Layout & L, uint8_t * __restrict__ xrows,
+                                                      uint8_t * __restrict__ q8, int64_t bg, int e) {
+    const int64_t total = n_rows * nb;
+    const bool live = bg < total;
+    const int64_t row = live ? bg / nb : 0, b = live ? bg % nb : 0;
+    const float v = live ? x[row * x_stride + b * 32 + e] : 0.0f;
+    float amax = fabsf(v);
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    if (!live) return;
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    float q = rintf(v * id);
+    q = q > 127.0f ? 127.0f : (q < -128.0f ? -128.0f : q);
+    const _Float16 dh = static_cast<_Float16>(d);
+    uint8_t * out = xrows + row * L.stride();
+    const int sk = e >> 2, pos = e & 3;
+    if (L.weight_type == 39)
+        reinterpret_cast<_Float16 *>(out + (static_cast<int64_t>(sk) * nb + b) * 8)[pos] = static_cast<_Float16>(q);
+    else
+        reinterpret_cast<signed char *>(out + (static_cast<int64_t>(sk) * nb + b) * 4)[pos] = static_cast<signed char>(q);
+    if (e == 0) {
+        reinterpret_cast<float *>(out + L.da_offset())[b] = static_cast<float>(dh);
+        if (b == 0) *reinterpret_cast<int *>(out + L.flag_offset()) = 0;
+    }
+    if (q8) {
+        uint8_t * blk = q8 + bg * 34;
+        blk[2 + e] = static_cast<uint8_t>(static_cast<signed char>(q));
+        if (e == 0) {
+            const uint16_t h = __builtin_bit_cast(uint16_t, dh);
+            blk[0] = static_cast<uint8_t>(h & 0xFF);
+            blk[1] = static_cast<uint8_t>(h >> 8);
+        }
+    }
+}
+
 
 }  // namespace vbm

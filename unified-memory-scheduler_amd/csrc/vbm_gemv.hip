@@ -1764,45 +1764,12 @@ void launch_decode_down_typed(const DecodeDownArgs & a, int top_k, hipStream_t s
 }
 
 // ------------------------------------------------------------------------------ activation rows
-// One 32-lane group per (row, block): x86 quantize_row_q8_0, written as an xrow (and optionally
-// as ggml Q8_0 blocks). Lane 0 of block 0 clears the row's -128 flag (this quantizer never
-// produces -128).
+// One 32-lane group per (row, block): x86 quantize_row_q8_0 into xrows (quantize_expand_block).
 __global__ __launch_bounds__(256) void quantize_expand_kernel(const float * __restrict__ x, int64_t n_rows, int nb,
                                                               int64_t x_stride, XrowLayout L, uint8_t * __restrict__ xrows,
                                                               uint8_t * __restrict__ q8) {
-    const int64_t total = n_rows * nb;
-    const int64_t bg = blockIdx.x * 8ll + (threadIdx.x >> 5);
-    const int e = threadIdx.x & 31;
-    const bool live = bg < total;
-    const int64_t row = live ? bg / nb : 0, b = live ? bg % nb : 0;
-    const float v = live ? x[row * x_stride + b * 32 + e] : 0.0f;
-    float amax = fabsf(v);
-    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-    if (!live) return;
-    const float d = amax / 127.0f;
-    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    float q = rintf(v * id);
-    q = q > 127.0f ? 127.0f : (q < -128.0f ? -128.0f : q);
-    const _Float16 dh = static_cast<_Float16>(d);
-    uint8_t * out = xrows + row * L.stride();
-    const int sk = e >> 2, pos = e & 3;
-    if (L.weight_type == 39)
-        reinterpret_cast<_Float16 *>(out + (static_cast<int64_t>(sk) * nb + b) * 8)[pos] = static_cast<_Float16>(q);
-    else
-        reinterpret_cast<signed char *>(out + (static_cast<int64_t>(sk) * nb + b) * 4)[pos] = static_cast<signed char>(q);
-    if (e == 0) {
-        reinterpret_cast<float *>(out + L.da_offset())[b] = static_cast<float>(dh);
-        if (b == 0) *reinterpret_cast<int *>(out + L.flag_offset()) = 0;
-    }
-    if (q8) {
-        uint8_t * blk = q8 + bg * 34;
-        blk[2 + e] = static_cast<uint8_t>(static_cast<signed char>(q));
-        if (e == 0) {
-            const uint16_t h = __builtin_bit_cast(uint16_t, dh);
-            blk[0] = static_cast<uint8_t>(h & 0xFF);
-            blk[1] = static_cast<uint8_t>(h >> 8);
-        }
-    }
+    quantize_expand_block(x, n_rows, nb, x_stride, L, xrows, q8, blockIdx.x * 8ll + (threadIdx.x >> 5),
+                          static_cast<int>(threadIdx.x & 31));
 }
 
 // One workgroup per row: ggml Q8_0 blocks -> xrow, with the row's -128 flag.

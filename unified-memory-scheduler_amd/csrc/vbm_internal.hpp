@@ -119,9 +119,10 @@ inline int64_t gemv_max_chunks(int64_t max_active, int64_t n_entries, int width)
 
 void launch_quantize_q8_0(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, uint8_t * dst,
                           hipStream_t stream);
+// Router logits (when router_w is given) and, unless topk is false, top-k + softmax per token.
 void launch_router(const float * router_w, const float * router_b, const float * x, int64_t hidden,
                    float * logits, int64_t n_expert, int64_t n_tokens, int64_t top_k, int32_t * ids,
-                   float * weights, hipStream_t stream);
+                   float * weights, hipStream_t stream, bool topk = true);
 // out[t] = sum over ranks r in order of y[t][r] * weights[t][r] (ggml MUL then ADDs); weights
 // NULL: the rows are already weighted, out[t] = sum of y[t][r] in rank order.
 void launch_combine(const float * y, const float * weights, int64_t rows, int64_t n_ids, int64_t n_tokens,
@@ -145,6 +146,16 @@ struct XrowLayout {
     VBM_HD int64_t stride() const { return (flag_offset() + 4 + 63) / 64 * 64; }
 };
 
+// A batched decode layer's top-k + softmax (given logits), grouping (with the batched GEMV's job
+// chunks) and input quantization into xrows, in one launch; for route_group_fits shapes.
+bool route_group_fits(int64_t n_expert, int64_t n_tokens, int64_t top_k);
+// Top-k + softmax (given logits) and the input quantization into xrows in one launch.
+void launch_topk_quantize(const float * logits, int64_t n_expert, int64_t n_tokens, int64_t top_k, int32_t * ids,
+                          float * weights, const float * x, int64_t hidden, const XrowLayout & lay, uint8_t * xrows,
+                          hipStream_t stream);
+void launch_route_group_quantize(const float * logits, int64_t n_expert, int64_t n_tokens, int64_t top_k, int32_t * ids,
+                                 float * weights, const GroupBuffers & g, const float * x, int64_t hidden,
+                                 const XrowLayout & lay, uint8_t * xrows, hipStream_t stream);
 // fp32 rows -> Q8_0 (x86 contract) -> xrows (and optionally ggml Q8_0 blocks).
 void launch_quantize_expand(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, const XrowLayout & lay,
                             uint8_t * xrows, uint8_t * q8_blocks, hipStream_t stream);

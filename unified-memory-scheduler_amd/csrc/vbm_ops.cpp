@@ -359,9 +359,11 @@ void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits
     int32_t * ids_d = ids ? ids : w.ids;
     float * w_d = weights ? weights : w.weights;
     float * logits_d = logits ? logits : w.logits;
-    launch_router(d->router_w, d->router_b, x, H, logits_d, d->n_expert, n_tokens, K, ids_d, w_d, s);
     const GroupBuffers g = carve_group(w.group, d->n_expert, entries);
-    if (use_gemm(*d, n_tokens) && gemm_pays(n_tokens, K, d->n_expert)) {
+    const bool gemm = use_gemm(*d, n_tokens) && gemm_pays(n_tokens, K, d->n_expert);
+    const bool one_launch = !gemm && route_group_fits(d->n_expert, n_tokens, K);
+    launch_router(d->router_w, d->router_b, x, H, logits_d, d->n_expert, n_tokens, K, ids_d, w_d, s, gemm);
+    if (gemm) {
         // Prefill-sized groups: MFMA grouped GEMM (exact block dots, fp32 accumulation order).
         prefill_prepare(*d, x, ids_d, n_tokens, w, s, true);
         prefill_pass(*d, d->expert_to_slot, n_tokens, w, w_d, events, s, 0, true);
@@ -369,8 +371,13 @@ void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits
         return;
     }
     const XrowLayout lx{H / 32, d->gate_up->type}, la{I / 32, d->down->type};
-    launch_quantize_expand(x, n_tokens, H, H, lx, w.xrows_x, nullptr, s);
-    launch_group(ids_d, K, n_tokens, K, d->n_expert, g, s, gemv_chunk_tokens(n_tokens));
+    if (one_launch) {
+        // top-k + softmax, grouping with the job chunks, and the input's activation rows
+        launch_route_group_quantize(logits_d, d->n_expert, n_tokens, K, ids_d, w_d, g, x, H, lx, w.xrows_x, s);
+    } else {
+        launch_topk_quantize(logits_d, d->n_expert, n_tokens, K, ids_d, w_d, x, H, lx, w.xrows_x, s);
+        launch_group(ids_d, K, n_tokens, K, d->n_expert, g, s, gemv_chunk_tokens(n_tokens));
+    }
 
     GemvArgs a{};
     a.expert_to_slot = d->expert_to_slot;

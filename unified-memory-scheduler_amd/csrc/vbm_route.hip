@@ -146,6 +146,127 @@ __global__ __launch_bounds__(kGroupThreads) void group_place_kernel(const int32_
     rows[pos] = static_cast<int32_t>(i);
 }
 
+// Small groupings (n <= 1024 entries, every decode batch here) in one launch instead of three:
+// workgroup 0 counts in LDS, scans (thread t = expert t) and places, with the same arithmetic as
+// group_count / group_scan / group_place over a single chunk, so the outputs are the same. With
+// ROUTE it first routes every token itself (one wave per token, wave_topk_softmax, the ids kept in
+// LDS for the grouping); the other workgroups, when there are any, quantize the layer input into
+// its activation rows (one 32-lane group per block), so a batched decode layer's routing, grouping
+// and input quantization take one launch.
+struct SmallGroupArgs {
+    const float * logits;     // ROUTE: [n / n_ids][n_expert]
+    int n_expert;
+    int32_t * ids_out;        // ROUTE: [n / n_ids][n_ids]
+    float * weights;          // ROUTE: [n / n_ids][n_ids]
+    const int32_t * ids;      // without ROUTE: ids[token * ids_stride + rank]
+    int64_t ids_stride;
+    int n_ids, n, n_as, id_bits;
+    GroupBuffers g;
+    int job_tile, max_tiles;
+    int32_t * tiles;
+    const float * x;          // workgroups 1..: fp32 rows -> activation rows
+    int64_t q_rows, x_stride;
+    int q_nb;
+    XrowLayout lay;
+    uint8_t * xrows;
+};
+
+template <int NPL, bool ROUTE>
+__global__ __launch_bounds__(kGroupThreads) void group_small_kernel(SmallGroupArgs a) {
+    if (blockIdx.x > 0) {
+        quantize_expand_block(a.x, a.q_rows, a.q_nb, a.x_stride, a.lay, a.xrows, static_cast<uint8_t *>(nullptr),
+                              (blockIdx.x - 1) * static_cast<int64_t>(kGroupThreads / 32) + (threadIdx.x >> 5),
+                              static_cast<int>(threadIdx.x & 31));
+        return;
+    }
+    constexpr int kWaves = kGroupThreads / 64;
+    __shared__ int s_hist[kMaxExperts];
+    __shared__ int s_off[kMaxExperts];
+    __shared__ int16_t s_wave_count[kWaves][kMaxExperts];   // counts <= 64
+    __shared__ int32_t s_ids[kGroupChunk];
+    __shared__ int s_wave_sum[3][kWaves];
+    __shared__ int s_bad;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int n_as = a.n_as, n = a.n;
+    for (int e = t; e < n_as; e += kGroupThreads) s_hist[e] = 0;
+    for (int k = t; k < kWaves * n_as; k += kGroupThreads) s_wave_count[k / n_as][k % n_as] = 0;
+    if (t == 0) s_bad = 0;
+    if constexpr (ROUTE) {
+        const int n_tok = n / a.n_ids;
+        for (int tok = wave; tok < n_tok; tok += kWaves)
+            wave_topk_softmax<NPL>(a.logits + static_cast<int64_t>(tok) * a.n_expert, a.n_expert, a.n_ids,
+                                   a.ids_out + static_cast<int64_t>(tok) * a.n_ids,
+                                   a.weights + static_cast<int64_t>(tok) * a.n_ids, s_ids + tok * a.n_ids);
+    }
+    __syncthreads();
+    // count
+    int id = -2;
+    if (t < n) {
+        if constexpr (ROUTE) {
+            id = s_ids[t];
+        } else {
+            bool bad;
+            id = group_id(a.ids, t, a.n_ids, a.ids_stride, n_as, bad);
+            if (bad) s_bad = 1;
+        }
+    }
+    if (id >= 0) atomicAdd(&s_hist[id], 1);
+    __syncthreads();
+    // scan: totals, offsets, the active list and the job chunks, two-level exclusive scans
+    const int c = t < n_as ? s_hist[t] : 0;
+    const int live = c > 0 ? 1 : 0;
+    const int nk = a.job_tile > 0 ? (c + a.job_tile - 1) / a.job_tile : 0;
+    int inc_c = c, inc_l = live, inc_k = nk;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int oc = __shfl_up(inc_c, off), ol = __shfl_up(inc_l, off), ok = __shfl_up(inc_k, off);
+        if (lane >= off) { inc_c += oc; inc_l += ol; inc_k += ok; }
+    }
+    if (lane == 63) { s_wave_sum[0][wave] = inc_c; s_wave_sum[1][wave] = inc_l; s_wave_sum[2][wave] = inc_k; }
+    __syncthreads();
+    int base_c = 0, base_l = 0, base_k = 0;
+    for (int w = 0; w < wave; ++w) { base_c += s_wave_sum[0][w]; base_l += s_wave_sum[1][w]; base_k += s_wave_sum[2][w]; }
+    const int ex_c = base_c + inc_c - c, ex_l = base_l + inc_l - live, ex_k = base_k + inc_k - nk;
+    if (t < n_as) {
+        a.g.counts[t] = c;
+        a.g.offsets[t] = ex_c;
+        s_off[t] = ex_c;
+        if (live) a.g.active[ex_l] = t;
+        bool over = false;
+        for (int j = 0; j < nk; ++j) {
+            if (ex_k + j < a.max_tiles) {
+                a.tiles[ex_k + j] = t;
+                a.tiles[a.max_tiles + ex_k + j] = j * a.job_tile;
+            } else {
+                over = true;
+            }
+        }
+        if (over) s_bad = 1;   // (cannot happen with the launch bound: flagged as a grouping error)
+        if (t == n_as - 1) {
+            a.g.offsets[n_as] = ex_c + c;
+            *a.g.n_active = ex_l + live;
+            if (a.job_tile > 0) a.tiles[2 * a.max_tiles] = ex_k + nk < a.max_tiles ? ex_k + nk : a.max_tiles;
+        }
+    }
+    // place: the entry's rank among the wave's lanes holding its expert (one ballot per id bit),
+    // plus the counts of that expert in the earlier waves and the expert's offset
+    const bool valid = id >= 0;
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < a.id_bits; ++b) {
+        const bool bit = valid && ((id >> b) & 1);
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+    }
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    const int rank = __popcll(peers & below);
+    if (valid && rank == 0) s_wave_count[wave][id] = static_cast<int16_t>(__popcll(peers));
+    __syncthreads();
+    if (t == 0) *a.g.error = s_bad;
+    if (!valid) return;
+    int pos = s_off[id] + rank;
+    for (int w = 0; w < wave; ++w) pos += s_wave_count[w][id];
+    a.g.rows[pos] = t;
+}
+
 // x86 quantize_row_q8_0: one 32-lane group per block.
 __global__ __launch_bounds__(256) void quantize_kernel(const float * __restrict__ x, int64_t n_rows, int nb,
                                                        int64_t x_stride, uint8_t * __restrict__ dst) {
@@ -325,8 +446,9 @@ void launch_group(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t 
     const int n_chunks = static_cast<int>((n + kGroupChunk - 1) / kGroupChunk);
     int id_bits = 0;
     while ((1ll << id_bits) < n_as) ++id_bits;
-    hipLaunchKernelGGL(group_count_kernel, dim3(n_chunks), dim3(kGroupThreads), 0, stream, ids, static_cast<int>(n_ids), n,
-                       ids_stride, static_cast<int>(n_as), g.chunk_counts);
+    if (n > kGroupChunk)
+        hipLaunchKernelGGL(group_count_kernel, dim3(n_chunks), dim3(kGroupThreads), 0, stream, ids, static_cast<int>(n_ids), n,
+                           ids_stride, static_cast<int>(n_as), g.chunk_counts);
     check_hip(hipGetLastError(), "grouping count launch");
     int64_t max_tiles = 0;
     int32_t * tiles = g.chunk_list;
@@ -340,6 +462,22 @@ void launch_group(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t 
         max_tiles = gemv_max_chunks(std::min(n_as, n), n, job_tile);
         require(g.chunk_list != nullptr && max_tiles <= g.chunk_list_items, "job chunk list exceeds its workspace");
     }
+    if (n <= kGroupChunk) {   // one workgroup, one launch
+        SmallGroupArgs a{};
+        a.ids = ids;
+        a.ids_stride = ids_stride;
+        a.n_ids = static_cast<int>(n_ids);
+        a.n = static_cast<int>(n);
+        a.n_as = static_cast<int>(n_as);
+        a.id_bits = id_bits;
+        a.g = g;
+        a.job_tile = job_tile;
+        a.max_tiles = static_cast<int>(max_tiles);
+        a.tiles = tiles;
+        hipLaunchKernelGGL((group_small_kernel<2, false>), dim3(1), dim3(kGroupThreads), 0, stream, a);
+        check_hip(hipGetLastError(), "grouping launch");
+        return;
+    }
     hipLaunchKernelGGL(group_scan_kernel, dim3(1), dim3(kGroupThreads), 0, stream, n_chunks, static_cast<int>(n_as),
                        g.chunk_counts, g.counts, g.offsets, g.active, g.n_active, g.error, job_tile,
                        static_cast<int>(max_tiles), tiles);
@@ -347,6 +485,92 @@ void launch_group(const int32_t * ids, int64_t n_ids, int64_t n_tokens, int64_t 
     hipLaunchKernelGGL(group_place_kernel, dim3(n_chunks), dim3(kGroupThreads), 0, stream, ids, static_cast<int>(n_ids), n,
                        ids_stride, static_cast<int>(n_as), id_bits, g.chunk_counts, g.offsets, g.rows);
     check_hip(hipGetLastError(), "grouping place launch");
+}
+
+void launch_route_group_quantize(const float * logits, int64_t n_expert, int64_t n_tokens, int64_t top_k, int32_t * ids,
+                                 float * weights, const GroupBuffers & g, const float * x, int64_t hidden,
+                                 const XrowLayout & lay, uint8_t * xrows, hipStream_t stream) {
+    const int64_t n = n_tokens * top_k;
+    require(route_group_fits(n_expert, n_tokens, top_k), "one-launch routing needs n_tokens * top_k <= 1024");
+    require(top_k > 0 && top_k <= n_expert && top_k <= 64 && n_expert > 0 && n_expert <= kMaxExperts,
+            "router supports 1..1024 experts and top_k <= 64");
+    require(x != nullptr && hidden > 0 && hidden % 32 == 0 && lay.nb == hidden / 32, "quantize shape mismatch");
+    int id_bits = 0;
+    while ((1ll << id_bits) < n_expert) ++id_bits;
+    const int job_tile = gemv_chunk_tokens(n_tokens);
+    const int64_t max_tiles = gemv_max_chunks(std::min(n_expert, n), n, job_tile);
+    require(g.chunk_list != nullptr && max_tiles <= g.chunk_list_items, "job chunk list exceeds its workspace");
+    SmallGroupArgs a{};
+    a.logits = logits;
+    a.n_expert = static_cast<int>(n_expert);
+    a.ids_out = ids;
+    a.weights = weights;
+    a.n_ids = static_cast<int>(top_k);
+    a.n = static_cast<int>(n);
+    a.n_as = static_cast<int>(n_expert);
+    a.id_bits = id_bits;
+    a.g = g;
+    a.job_tile = job_tile;
+    a.max_tiles = static_cast<int>(max_tiles);
+    a.tiles = g.chunk_list;
+    a.x = x;
+    a.q_rows = n_tokens;
+    a.x_stride = hidden;
+    a.q_nb = static_cast<int>(hidden / 32);
+    a.lay = lay;
+    a.xrows = xrows;
+    const int64_t q_groups = (n_tokens * (hidden / 32) + kGroupThreads / 32 - 1) / (kGroupThreads / 32);
+    const dim3 grid(static_cast<unsigned>(1 + q_groups));
+    if (n_expert <= 128) hipLaunchKernelGGL((group_small_kernel<2, true>), grid, dim3(kGroupThreads), 0, stream, a);
+    else if (n_expert <= 256) hipLaunchKernelGGL((group_small_kernel<4, true>), grid, dim3(kGroupThreads), 0, stream, a);
+    else hipLaunchKernelGGL((group_small_kernel<16, true>), grid, dim3(kGroupThreads), 0, stream, a);
+    check_hip(hipGetLastError(), "routing + grouping + quantize launch");
+}
+
+// One token per wave of the routing workgroup: beyond 16 tokens its waves route several tokens in
+// turn and the one-launch form measured slower (64 tokens top-4, 32 experts) than the parallel
+// top-k launch.
+bool route_group_fits(int64_t n_expert, int64_t n_tokens, int64_t top_k) {
+    return n_expert <= kMaxExperts && n_tokens * top_k <= kGroupChunk && n_tokens <= kGroupThreads / 64;
+}
+
+// Top-k + softmax of n_tokens tokens (workgroups 0..n_tokens-1, wave 0 of each) and the input's
+// activation rows (the other workgroups, one 32-lane group per block) in one launch.
+template <int NPL>
+__global__ __launch_bounds__(256) void topk_quantize_kernel(const float * __restrict__ logits, int n_expert, int top_k,
+                                                            int32_t * __restrict__ ids, float * __restrict__ weights,
+                                                            int64_t n_tokens, const float * __restrict__ x, int nb,
+                                                            int64_t x_stride, XrowLayout lay, uint8_t * __restrict__ xrows) {
+    const int64_t b = blockIdx.x;
+    if (b < n_tokens) {
+        if (threadIdx.x < 64)
+            wave_topk_softmax<NPL>(logits + b * n_expert, n_expert, top_k, ids + b * top_k, weights + b * top_k);
+        return;
+    }
+    quantize_expand_block(x, n_tokens, nb, x_stride, lay, xrows, static_cast<uint8_t *>(nullptr),
+                          (b - n_tokens) * 8 + (threadIdx.x >> 5), static_cast<int>(threadIdx.x & 31));
+}
+
+void launch_topk_quantize(const float * logits, int64_t n_expert, int64_t n_tokens, int64_t top_k, int32_t * ids,
+                          float * weights, const float * x, int64_t hidden, const XrowLayout & lay, uint8_t * xrows,
+                          hipStream_t stream) {
+    require(n_expert > 0 && n_expert <= 1024 && top_k > 0 && top_k <= n_expert && top_k <= 64 && n_tokens > 0,
+            "router supports 1..1024 experts and top_k <= 64");
+    require(x != nullptr && hidden > 0 && hidden % 32 == 0 && lay.nb == hidden / 32, "quantize shape mismatch");
+    const int64_t q_wgs = (n_tokens * (hidden / 32) + 7) / 8;
+    require(n_tokens + q_wgs < (1ll << 31), "too many rows for one launch");
+    const dim3 grid(static_cast<unsigned>(n_tokens + q_wgs));
+    const int ne = static_cast<int>(n_expert), tk = static_cast<int>(top_k), nb = static_cast<int>(hidden / 32);
+    if (n_expert <= 128)
+        hipLaunchKernelGGL(topk_quantize_kernel<2>, grid, dim3(256), 0, stream, logits, ne, tk, ids, weights, n_tokens, x, nb,
+                           hidden, lay, xrows);
+    else if (n_expert <= 256)
+        hipLaunchKernelGGL(topk_quantize_kernel<4>, grid, dim3(256), 0, stream, logits, ne, tk, ids, weights, n_tokens, x, nb,
+                           hidden, lay, xrows);
+    else
+        hipLaunchKernelGGL(topk_quantize_kernel<16>, grid, dim3(256), 0, stream, logits, ne, tk, ids, weights, n_tokens, x,
+                           nb, hidden, lay, xrows);
+    check_hip(hipGetLastError(), "top-k + quantize launch");
 }
 
 void launch_quantize_q8_0(const float * x, int64_t n_rows, int64_t k, int64_t x_stride, uint8_t * dst,
@@ -360,7 +584,7 @@ void launch_quantize_q8_0(const float * x, int64_t n_rows, int64_t k, int64_t x_
 
 void launch_router(const float * router_w, const float * router_b, const float * x, int64_t hidden, float * logits,
                    int64_t n_expert, int64_t n_tokens, int64_t top_k, int32_t * ids, float * weights,
-                   hipStream_t stream) {
+                   hipStream_t stream, bool topk) {
     require(n_expert > 0 && n_expert <= 1024 && top_k > 0 && top_k <= n_expert && top_k <= 64 && n_tokens > 0,
             "router supports 1..1024 experts and top_k <= 64");
     if (router_w) {
@@ -370,6 +594,7 @@ void launch_router(const float * router_w, const float * router_b, const float *
                            static_cast<int>(n_tokens), logits);
         check_hip(hipGetLastError(), "router logits launch");
     }
+    if (!topk) return;
     const dim3 grid(static_cast<unsigned>(n_tokens));
     const int ne = static_cast<int>(n_expert), tk = static_cast<int>(top_k);
     if (n_expert <= 128) hipLaunchKernelGGL(topk_softmax_kernel<2>, grid, dim3(64), 0, stream, logits, ne, tk, ids, weights);
