@@ -117,6 +117,24 @@ def test_layer_glu_epilogue_many_tokens_per_expert(gpu, orc):
     layer.destroy()
 
 
+@pytest.mark.parametrize("tokens,experts,hidden,inter", [(16, 64, 1024, 512), (17, 64, 1024, 512), (1, 1024, 256, 128),
+                                                         (3, 1024, 256, 128)])
+def test_layer_one_launch_routing_boundary(gpu, orc, tokens, experts, hidden, inter):
+    """Up to 16 tokens the batched layer routes, groups and quantizes its input in one launch;
+    from 17 tokens the top-k runs beside the quantization and the grouping follows. Both sides of
+    the boundary, and 1024 experts (16 logits per lane), bitwise against the oracle in the exact
+    order."""
+    layer = Layer(gpu, H.MX, hidden, inter, experts, 4, seed=505 + tokens, router=False)
+    x = gpu.synth_normal(505, 6, tokens, tokens * hidden).reshape(tokens, hidden)
+    logits = gpu.synth_normal(505, 7, tokens, tokens * experts).reshape(tokens, experts)
+    out, ids, w = layer.forward_gpu(x, logits)
+    ref = layer.forward_cpu(orc, x, logits)
+    assert np.array_equal(ids, ref["ids"])
+    assert np.allclose(w, ref["weights"], rtol=1e-6, atol=0)
+    assert np.array_equal(out.view(np.uint32), ref["out"].view(np.uint32)), H.diff_report(out, ref["out"])
+    layer.destroy()
+
+
 def test_layer_randomized_shapes_bitwise(gpu, orc):
     """10 seeded random fused layers in the exact order against the oracle's layer: both weight
     types and activations, hidden 64..1024, intermediate 64..768, 2..48 experts, top-1..6, 1..24

@@ -238,6 +238,27 @@ def test_grouping_duplicates_strides_single_expert_and_bad_ids(gpu, orc):
     assert err == 1 and np.array_equal(c, rc) and np.array_equal(o, ro) and np.array_equal(r, rr)
 
 
+def test_grouping_single_workgroup_edges(gpu, orc):
+    """Groupings of at most 1024 entries take the one-workgroup kernel (count, scan and place in
+    LDS): exactly 1024 entries over 1024 experts, a token stride wider than n_ids with -1 ids, one
+    expert, 1023 entries, and ids outside [-1, n_as) (error flag set, entries skipped)."""
+    rng = np.random.default_rng(14)
+    for n_as, n_ids, tokens, stride in [(1024, 4, 256, 4), (16, 5, 204, 7), (1, 3, 341, 3), (300, 8, 128, 8),
+                                        (1024, 1, 1, 1)]:
+        full = rng.integers(-1, n_as, size=(tokens, stride)).astype(np.int32)
+        full[:, n_ids:] = 10**6                   # columns beyond n_ids are never read
+        c, o, r, err = _group_on_gpu(gpu, full, n_ids, tokens, stride, n_as)
+        rc, ro, rr = orc.group_by_expert(full, n_ids, tokens, stride, n_as)
+        assert np.array_equal(c, rc) and np.array_equal(o, ro) and np.array_equal(r, rr) and err == 0, (n_as, tokens)
+    ids = rng.integers(0, 64, size=(200, 4)).astype(np.int32)
+    bad = rng.random(ids.shape) < 0.03
+    ids[bad] = np.where(rng.random(bad.sum()) < 0.5, 64, -5)
+    c, o, r, err = _group_on_gpu(gpu, ids, 4, 200, 4, 64)
+    clean = np.where(bad, -1, ids).astype(np.int32)
+    rc, ro, rr = orc.group_by_expert(clean, 4, 200, 4, 64)
+    assert err == 1 and np.array_equal(c, rc) and np.array_equal(o, ro) and np.array_equal(r, rr)
+
+
 def test_router_ids_exact(gpu, orc):
     for n_expert, hidden, tokens, top_k in [(32, 2880, 8, 4), (128, 2880, 32, 4), (128, 2048, 16, 8)]:
         w = gpu.synth_normal(5, 1, 0, n_expert * hidden, 0.0, 0.02).reshape(n_expert, hidden)
