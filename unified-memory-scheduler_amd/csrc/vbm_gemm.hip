@@ -42,8 +42,12 @@ typedef unsigned u32x2g __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_g __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmThreads = 256;
-constexpr int kJobTile = static_cast<int>(kGemmJobTile);   // jobs per grouped-GEMM workgroup
-constexpr int kJobFrags = kJobTile / 32;                   // 16-job fragment columns per wave
+// Jobs per grouped-GEMM workgroup (gemm_job_tile) and 16-job fragment columns per wave: the two
+// wave halves of a workgroup split its live jobs evenly.
+template <int TYPE>
+constexpr int job_tile() {
+    return TYPE == 39 ? 128 : 192;
+}
 constexpr int kMxJobTile = 64;                             // the MXFP8 experiment's job tile
 
 template <class T>
@@ -148,6 +152,7 @@ __device__ __forceinline__ half8_t i8_to_f16(long v) {
 // instead of 4 workgroups per CU, and measured slower: 0.625 against 0.555 ms per layer.
 template <int TYPE>
 struct GemmStage {
+    static constexpr int kJobTile = job_tile<TYPE>();
     static constexpr int EB = TYPE == 39 ? 2 : 1;                       // bytes per activation code
     static constexpr int GB = TYPE == 39 ? 8 : 4;                       // blocks per bank group
     static constexpr int CB = 2;                                        // blocks per chunk
@@ -177,6 +182,7 @@ struct GemmStage {
     static constexpr int WG_DMA = WG / 1024 / 4;   // 16-byte group weight loads per wave
     static_assert(S == 2, "the per-chunk wait is vmcnt(0)");
     static_assert(!GROUPED || (CPG == 2 && WG_DMA == 2), "Q8_0 group staging: two chunks per group, two loads per wave");
+    static_assert(ACT % 4096 == 0 && (!GROUPED || kJobTile % 64 == 0), "whole activation and block-scale DMAs per wave");
 };
 
 // Global-to-LDS DMA (global_load_lds_*): lane l's bytes land at LDS address m0 + l * size. The
@@ -219,9 +225,10 @@ __device__ __forceinline__ float mul_half(unsigned h2, float x, float neg_zero) 
 }
 
 template <int TYPE, int EPI, bool FLAGGED>
-__global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void grouped_gemm_kernel(GemmArgs A) {
+__global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 3 : 1) void grouped_gemm_kernel(GemmArgs A) {
     using G = GemmStage<TYPE>;
     constexpr int CB = G::CB;
+    constexpr int kJobTile = G::kJobTile;
     constexpr int kLdsBytes = G::BYTES > kJobTile * 68 * 4 ? G::BYTES : kJobTile * 68 * 4;   // stages / epilogue tile
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
     float (*tile_vals)[68] = reinterpret_cast<float (*)[68]>(lds);    // epilogue tile [job][pair row], after the K loop
@@ -280,28 +287,34 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
         return A.rows_in + row_index * A.lay.stride();
     };
 
-    // This lane's fragment columns (jobs 64(w>>1) + 16jh + lr) and the -128 flags of the wave.
+    // The two wave halves (waves 0-1, 2-3) split the tile's live jobs at a multiple of 16: jobs
+    // [0, split) and [split, live), so a tile of n jobs costs each half about n / 2 of them (a
+    // 64-job tile gives each half 32 instead of all 64 to the first). This lane's fragment columns
+    // are jobs wj + 16jh + lr of its half; the -128 flags of the wave.
     // Rows converted from caller-quantized Q8_0 data (FLAGGED) may hold -128 codes.
-    constexpr int JF = kJobFrags;
-    const int wj = 64 * (wave >> 1);                   // the wave's first job in the tile
+    constexpr int JF = kJobTile / 32;
+    const int wq = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 7));   // the wave's half
+    const int live_jobs = count - j0 < kJobTile ? count - j0 : kJobTile;
+    const int split = 16 * ((live_jobs + 31) / 32);
+    const int wj = wq * split;                         // the wave's first job in the tile
+    const int half_end = wq ? live_jobs : (split < live_jobs ? split : live_jobs);
     bool jlive[JF];
     int job[JF];
     int flagged = 0;
 #pragma unroll
     for (int jh = 0; jh < JF; ++jh) {
         const int jl = wj + 16 * jh + lr;
-        jlive[jh] = j0 + jl < count;
+        jlive[jh] = jl < half_end;
         job[jh] = jlive[jh] ? A.jobs[joff + j0 + jl] : 0;
         if (FLAGGED && jlive[jh]) flagged |= *reinterpret_cast<const int *>(row_of(jl) + A.lay.flag_offset());
     }
-    // Fragment columns of 16 jobs none of which is live (the tile's live jobs are a prefix) cost the
-    // wave no matrix or scale work: the last tile of an expert is often nearly empty. The K loop
-    // is instantiated per count of live columns (nf, wave-uniform), so its body carries no
-    // per-column branch and the compiler can interleave the columns' MFMAs and VALU work.
-    static_assert(JF == 4, "the K loop is instantiated for 0..4 live fragment columns");
-    const int wq = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 7));
-    const int live_in_half = count - j0 - 64 * wq;
-    const int nf = live_in_half <= 0 ? 0 : (live_in_half >= 64 ? JF : (live_in_half + 15) / 16);
+    // Fragment columns of 16 jobs none of which is live (a half's live jobs are a prefix of it) cost
+    // the wave no matrix or scale work. The K loop is instantiated per count of live columns (nf,
+    // wave-uniform), so its body carries no per-column branch and the compiler can interleave the
+    // columns' MFMAs and VALU work.
+    static_assert(JF == 4 || JF == 6, "the K loop is instantiated for 0..6 live fragment columns");
+    const int live_in_half = half_end - wj;
+    const int nf = live_in_half <= 0 ? 0 : (live_in_half + 15) / 16;
     // Workgroup-uniform: every wave then runs the same K-loop instantiation, so each of its
     // barriers is reached from one control path (every thread gets here: the exits above are
     // uniform per workgroup).
@@ -335,9 +348,9 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
         act_src[j] = row_of(j0 + jr < count ? jr : 0) + 16 * part;
     }
     // block scales: per chunk, lane l of wave w loads job 32w + l / 2, block l % 2; grouped (Q8_0),
-    // per group, lane l of waves 0 and 1 loads the 16 bytes of job 64w + l
+    // per group, lane l of waves w < kJobTile / 64 loads the 16 bytes of job 64w + l
     static_assert(G::GROUPED || G::DA == kGemmThreads * 4, "one block-scale dword per thread and chunk");
-    const int jd = G::GROUPED ? 64 * (wave & 1) + lane : 32 * wave + (lane >> 1);
+    const int jd = G::GROUPED ? 64 * (wave < kJobTile / 64 ? wave : 0) + lane : 32 * wave + (lane >> 1);
     const uint8_t * da_src = row_of(j0 + jd < count ? jd : 0) + A.lay.da_offset() + (G::GROUPED ? 0 : 4 * (lane & 1));
     // weight dword of this lane within its load's group-relative source
     uint32_t woff;
@@ -377,7 +390,7 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
                     lds_dma_x4(slot_base + S.codes_bytes + tsel(lane >> 4) * meta_tile_bytes + static_cast<size_t>(grp) * 256 +
                                    (lane & 15) * 16,
                                lds0 + G::OFF_MG + (grp & 1) * G::MG);
-                if (wu < 2)
+                if (wu < kJobTile / 64)
                     lds_dma_x4(da_src + 16 * grp,
                                __builtin_amdgcn_readfirstlane(lds0 + G::OFF_DG + (grp & 1) * G::DG + wu * 1024));
             }
@@ -705,6 +718,8 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
     // barrier per chunk.
     auto k_loop_nf = [&](auto slow_c) {
         switch (nf) {
+            case 6: if constexpr (JF >= 6) k_loop(slow_c, std::integral_constant<int, 6>{}); break;
+            case 5: if constexpr (JF >= 5) k_loop(slow_c, std::integral_constant<int, 5>{}); break;
             case 4: k_loop(slow_c, std::integral_constant<int, 4>{}); break;
             case 3: k_loop(slow_c, std::integral_constant<int, 3>{}); break;
             case 2: k_loop(slow_c, std::integral_constant<int, 2>{}); break;
@@ -745,7 +760,7 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 4 : 1) void
                 if (EPI == 0 && A.row_scale) v = v * rscale[jh];
                 if (!via_lds) {
                     if (jlive[jh] && tile_live) A.dst[static_cast<size_t>(job[jh]) * S.rows + grow] = v;
-                } else {
+                } else if (jlive[jh]) {   // columns past the half's jobs belong to the other half
                     tile_vals[wj + 16 * jh + lr][32 * (wave & 1) + orow] = v;
                 }
             }
@@ -1248,14 +1263,15 @@ void launch_grouped_gemm(const GemmParams & p, hipStream_t stream) {
             "GLU epilogue needs an interleaved gate|up bank with rows % 64 == 0 and a matching output layout");
     require(p.epilogue == 1 || p.dst != nullptr, "missing GEMM output");
     require(p.n_as >= 1 && p.n_as <= 1024 && p.n_entries >= 1, "GEMM group shape out of range");
-    const int64_t max_tiles = gemm_max_tiles(p.n_as, p.n_entries, kJobTile);
+    const int job_tile_n = gemm_job_tile(bank.type);
+    const int64_t max_tiles = gemm_max_tiles(p.n_as, p.n_entries, job_tile_n);
     require(max_tiles <= 65535, "too many GEMM tiles for one launch");
     int32_t * tile_expert = static_cast<int32_t *>(p.tiles);
     int32_t * tile_start = tile_expert + max_tiles;
     int32_t * n_tiles = tile_start + max_tiles;
     if (!p.tiles_ready) {
         hipLaunchKernelGGL(gemm_tiles_kernel, dim3(1), dim3(1024), 0, stream, p.group.counts, p.group.active,
-                           p.group.n_active, p.tile_filter, kJobTile, static_cast<int>(max_tiles), tile_expert, tile_start,
+                           p.group.n_active, p.tile_filter, job_tile_n, static_cast<int>(max_tiles), tile_expert, tile_start,
                            n_tiles, p.group.error);
         check_hip(hipGetLastError(), "GEMM tile list launch");
     }

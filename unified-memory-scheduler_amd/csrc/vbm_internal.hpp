@@ -233,7 +233,10 @@ struct GemmParams {
     int64_t grid_tiles;               // > 0: bound on the tiles left by tile_filter (launch size), else 0
     bool tiles_ready;                 // `tiles` already holds this group's list (same group and filter)
 };
-constexpr int64_t kGemmJobTile = 128;   // jobs per grouped-GEMM workgroup (one expert's job tile)
+// Jobs per grouped-GEMM workgroup (one expert's job tile): 192 for Q8_0 banks, whose expert groups
+// at 2048 tokens top-8 over 128 experts hold 96-158 jobs (one tile each instead of a nearly empty
+// second tile for half of them), 128 for MXFP4.
+inline int gemm_job_tile(int bank_type) { return bank_type == VBM_TYPE_MXFP4 ? 128 : 192; }
 int64_t gemm_max_tiles(int64_t n_as, int64_t n_entries, int job_tile);
 size_t gemm_tiles_bytes(int64_t n_as, int64_t n_entries);
 void launch_grouped_gemm(const GemmParams & p, hipStream_t stream);
@@ -276,7 +279,7 @@ LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint
 // combine is then the rank-ordered ADDs alone); the combine of y runs once all entries are
 // written. events (optional) [4]: around the
 // pass's gate_up and down GEMMs. grid_tiles > 0: the pass's expert->slot map also filters the tile
-// list, and grid_tiles bounds its tiles (sum over its experts of ceil(count / kGemmJobTile)), so a pass over a
+// list, and grid_tiles bounds its tiles (sum over its experts of ceil(count / gemm_job_tile)), so a pass over a
 // few experts launches only their workgroups.
 // gemm_tiles: prepare also writes the grouped GEMM's unfiltered tile list (then a pass with no
 // grid_tiles may take tiles_ready = true and skip gemm_tiles_kernel).

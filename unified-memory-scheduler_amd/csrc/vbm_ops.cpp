@@ -122,8 +122,8 @@ void prefill_prepare(const vbm_moe_layer_desc & d, const float * x, const int32_
     const int64_t entries = n_tokens * d.top_k;
     const GroupBuffers g = carve_group(w.group, d.n_expert, entries);
     if (gemm_tiles)   // the grouping scan also writes the GEMM's (unfiltered) job tile list
-        launch_group(ids, d.top_k, n_tokens, d.top_k, d.n_expert, g, s, static_cast<int>(kGemmJobTile),
-                     static_cast<int32_t *>(w.tiles), gemm_max_tiles(d.n_expert, entries, static_cast<int>(kGemmJobTile)));
+        launch_group(ids, d.top_k, n_tokens, d.top_k, d.n_expert, g, s, gemm_job_tile(d.gate_up->type),
+                     static_cast<int32_t *>(w.tiles), gemm_max_tiles(d.n_expert, entries, gemm_job_tile(d.gate_up->type)));
     else
         launch_group(ids, d.top_k, n_tokens, d.top_k, d.n_expert, g, s);
 }

@@ -607,7 +607,8 @@ vbm_status vbm_tier_prefill(vbm_tier * t, int64_t layer, const float * x, const 
         check_status(vbm_admission_slot_map(t->admission, layer, maps), "prefill slot map");
         std::vector<int64_t> count(static_cast<size_t>(E), 0);
         for (int64_t i = 0; i < T * K; ++i) ++count[static_cast<size_t>(t->pf_ids_host[i])];
-        auto tiles_of = [&](int64_t e) { return (count[static_cast<size_t>(e)] + kGemmJobTile - 1) / kGemmJobTile; };   // GEMM job tiles
+        const int64_t job_tile = gemm_job_tile(desc.gate_up->type);
+        auto tiles_of = [&](int64_t e) { return (count[static_cast<size_t>(e)] + job_tile - 1) / job_tile; };   // GEMM job tiles
         std::vector<char> routed(static_cast<size_t>(E), 0);
         for (int64_t e = 0; e < E; ++e) routed[static_cast<size_t>(e)] = count[static_cast<size_t>(e)] > 0;
         std::vector<int32_t> cold;
