@@ -875,11 +875,11 @@ __global__ __launch_bounds__(1024) void gemm_tiles_kernel(const int32_t * counts
 
 // x86 quantize_row_q8_0 of fp32 rows into GEMM activation rows (row-major codes as f16 or int8,
 // fp16-rounded fp32 block scales, and a 0 flag: this quantizer never produces -128).
-__global__ __launch_bounds__(256) void gemm_rows_from_f32_kernel(const float * __restrict__ x, int vec4, int nb,
-                                                                 int64_t x_stride, GemmRowLayout L, uint8_t * __restrict__ out) {
-    // workgroup (row, 64-block segment); four threads per block, eight elements each
-    const int64_t row = blockIdx.x;
-    const int bq = static_cast<int>(blockIdx.y) * 64 + static_cast<int>(threadIdx.x >> 2);
+// Workgroup (row, 64-block segment seg) of it; four threads per block, eight elements each.
+__device__ __forceinline__ void gemm_rows_segment(const float * __restrict__ x, int vec4, int nb, int64_t x_stride,
+                                                  const GemmRowLayout & L, uint8_t * __restrict__ out, int64_t row,
+                                                  int seg) {
+    const int bq = seg * 64 + static_cast<int>(threadIdx.x >> 2);
     const bool live = bq < nb;
     const int b = live ? bq : 0;
     const int part = static_cast<int>(threadIdx.x & 3);
@@ -925,6 +925,30 @@ __global__ __launch_bounds__(256) void gemm_rows_from_f32_kernel(const float * _
         reinterpret_cast<float *>(o + L.da_offset())[b] = static_cast<float>(static_cast<_Float16>(d));
         if (b == 0) *reinterpret_cast<int *>(o + L.flag_offset()) = 0;
     }
+}
+
+__global__ __launch_bounds__(256) void gemm_rows_from_f32_kernel(const float * __restrict__ x, int vec4, int nb,
+                                                                 int64_t x_stride, GemmRowLayout L, uint8_t * __restrict__ out) {
+    gemm_rows_segment(x, vec4, nb, x_stride, L, out, blockIdx.x, static_cast<int>(blockIdx.y));
+}
+
+// The prefill's top-k + softmax (given logits; workgroups 0 .. ceil(T / 4) - 1, one wave per
+// token) and its GEMM activation rows (the other workgroups, one per (row, 64-block segment)) in
+// one launch: the two only share the launch.
+template <int NPL>
+__global__ __launch_bounds__(256) void topk_gemm_rows_kernel(const float * __restrict__ logits, int n_expert, int top_k,
+                                                             int32_t * __restrict__ ids, float * __restrict__ weights,
+                                                             int64_t n_tokens, int64_t topk_wgs, const float * __restrict__ x,
+                                                             int vec4, int nb, int64_t x_stride, GemmRowLayout L,
+                                                             int segments, uint8_t * __restrict__ out) {
+    const int64_t b = blockIdx.x;
+    if (b < topk_wgs) {
+        const int64_t t = b * 4 + (threadIdx.x >> 6);
+        if (t < n_tokens) wave_topk_softmax<NPL>(logits + t * n_expert, n_expert, top_k, ids + t * top_k, weights + t * top_k);
+        return;
+    }
+    const int64_t r = b - topk_wgs;
+    gemm_rows_segment(x, vec4, nb, x_stride, L, out, r / segments, static_cast<int>(r % segments));
 }
 
 // ggml Q8_0 block rows -> GEMM activation rows, with each row's -128 flag.
@@ -1245,6 +1269,30 @@ void launch_gemm_rows_from_f32(const float * x, int64_t n_rows, int64_t k, int64
     hipLaunchKernelGGL(gemm_rows_from_f32_kernel, dim3(static_cast<unsigned>(n_rows), segments), dim3(256), 0, stream,
                        x, vec4, static_cast<int>(k / 32), x_stride, lay, rows);
     check_hip(hipGetLastError(), "GEMM quantize launch");
+}
+
+void launch_topk_gemm_rows(const float * logits, int64_t n_expert, int64_t top_k, int32_t * ids, float * weights,
+                           const float * x, int64_t n_rows, int64_t k, const GemmRowLayout & lay, uint8_t * rows,
+                           hipStream_t stream) {
+    require(k > 0 && k % 32 == 0 && n_rows > 0 && lay.nb == k / 32, "GEMM quantize shape mismatch");
+    require(n_expert > 0 && n_expert <= 1024 && top_k > 0 && top_k <= n_expert && top_k <= 64,
+            "router supports 1..1024 experts and top_k <= 64");
+    const int segments = static_cast<int>((k / 32 + 63) / 64);
+    const int64_t topk_wgs = (n_rows + 3) / 4, total = topk_wgs + n_rows * segments;
+    require(total < (1ll << 31), "too many GEMM activation rows for one launch");
+    const int vec4 = reinterpret_cast<uintptr_t>(x) % 16 == 0 && k % 4 == 0;
+    const int ne = static_cast<int>(n_expert), tk = static_cast<int>(top_k), nb = static_cast<int>(k / 32);
+    const dim3 grid(static_cast<unsigned>(total));
+    if (n_expert <= 128)
+        hipLaunchKernelGGL(topk_gemm_rows_kernel<2>, grid, dim3(256), 0, stream, logits, ne, tk, ids, weights, n_rows, topk_wgs,
+                           x, vec4, nb, k, lay, segments, rows);
+    else if (n_expert <= 256)
+        hipLaunchKernelGGL(topk_gemm_rows_kernel<4>, grid, dim3(256), 0, stream, logits, ne, tk, ids, weights, n_rows, topk_wgs,
+                           x, vec4, nb, k, lay, segments, rows);
+    else
+        hipLaunchKernelGGL(topk_gemm_rows_kernel<16>, grid, dim3(256), 0, stream, logits, ne, tk, ids, weights, n_rows,
+                           topk_wgs, x, vec4, nb, k, lay, segments, rows);
+    check_hip(hipGetLastError(), "top-k + GEMM rows launch");
 }
 
 void launch_gemm_rows_from_q8(const uint8_t * q8, int64_t n_rows, int64_t row_bytes, const GemmRowLayout & lay,

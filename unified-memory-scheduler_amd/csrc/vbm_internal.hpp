@@ -211,6 +211,10 @@ void launch_gemm_rows_from_f32(const float * x, int64_t n_rows, int64_t k, int64
                                uint8_t * rows, hipStream_t stream);
 void launch_gemm_rows_from_q8(const uint8_t * q8, int64_t n_rows, int64_t row_bytes, const GemmRowLayout & lay,
                               uint8_t * rows, hipStream_t stream);
+// Top-k + softmax of given logits and the GEMM activation rows of x (row stride k) in one launch.
+void launch_topk_gemm_rows(const float * logits, int64_t n_expert, int64_t top_k, int32_t * ids, float * weights,
+                           const float * x, int64_t n_rows, int64_t k, const GemmRowLayout & lay, uint8_t * rows,
+                           hipStream_t stream);
 
 // Grouped expert GEMM on MFMA (exact block dots, fp32 accumulation across blocks).
 struct GemmParams {
@@ -283,8 +287,11 @@ LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint
 // few experts launches only their workgroups.
 // gemm_tiles: prepare also writes the grouped GEMM's unfiltered tile list (then a pass with no
 // grid_tiles may take tiles_ready = true and skip gemm_tiles_kernel).
+// With logits (and weights), prepare also runs the top-k + softmax into ids / weights, in the
+// launch that writes the activation rows.
 void prefill_prepare(const vbm_moe_layer_desc & d, const float * x, const int32_t * ids, int64_t n_tokens,
-                     const LayerWorkspace & w, hipStream_t s, bool gemm_tiles = false);
+                     const LayerWorkspace & w, hipStream_t s, bool gemm_tiles = false, const float * logits = nullptr,
+                     float * weights = nullptr);
 void prefill_pass(const vbm_moe_layer_desc & d, const int32_t * expert_to_slot, int64_t n_tokens,
                   const LayerWorkspace & w, const float * route_w, void * const * events, hipStream_t s,
                   int64_t grid_tiles = 0, bool tiles_ready = false);

@@ -116,9 +116,13 @@ LayerWorkspace plan_layer(const vbm_moe_layer_desc & d, int64_t max_tokens, uint
 }
 
 void prefill_prepare(const vbm_moe_layer_desc & d, const float * x, const int32_t * ids, int64_t n_tokens,
-                     const LayerWorkspace & w, hipStream_t s, bool gemm_tiles) {
+                     const LayerWorkspace & w, hipStream_t s, bool gemm_tiles, const float * logits, float * weights) {
     const GemmRowLayout gx{d.hidden / 32, d.gate_up->type};
-    launch_gemm_rows_from_f32(x, n_tokens, d.hidden, d.hidden, gx, w.xrows_x, s);
+    if (logits)
+        launch_topk_gemm_rows(logits, d.n_expert, d.top_k, const_cast<int32_t *>(ids), weights, x, n_tokens, d.hidden, gx,
+                              w.xrows_x, s);
+    else
+        launch_gemm_rows_from_f32(x, n_tokens, d.hidden, d.hidden, gx, w.xrows_x, s);
     const int64_t entries = n_tokens * d.top_k;
     const GroupBuffers g = carve_group(w.group, d.n_expert, entries);
     if (gemm_tiles)   // the grouping scan also writes the GEMM's (unfiltered) job tile list
@@ -362,10 +366,11 @@ void layer_forward(const vbm_moe_layer_desc * d, const float * x, float * logits
     const GroupBuffers g = carve_group(w.group, d->n_expert, entries);
     const bool gemm = use_gemm(*d, n_tokens) && gemm_pays(n_tokens, K, d->n_expert);
     const bool one_launch = !gemm && route_group_fits(d->n_expert, n_tokens, K);
-    launch_router(d->router_w, d->router_b, x, H, logits_d, d->n_expert, n_tokens, K, ids_d, w_d, s, gemm);
+    launch_router(d->router_w, d->router_b, x, H, logits_d, d->n_expert, n_tokens, K, ids_d, w_d, s, false);
     if (gemm) {
-        // Prefill-sized groups: MFMA grouped GEMM (exact block dots, fp32 accumulation order).
-        prefill_prepare(*d, x, ids_d, n_tokens, w, s, true);
+        // Prefill-sized groups: MFMA grouped GEMM (exact block dots, fp32 accumulation order); the
+        // top-k runs in the launch that writes the activation rows.
+        prefill_prepare(*d, x, ids_d, n_tokens, w, s, true, logits_d, w_d);
         prefill_pass(*d, d->expert_to_slot, n_tokens, w, w_d, events, s, 0, true);
         launch_combine(w.y, nullptr, H, K, n_tokens, out, s);   // rows weighted in the down epilogue
         return;

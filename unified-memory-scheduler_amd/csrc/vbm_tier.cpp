@@ -589,8 +589,7 @@ vbm_status vbm_tier_prefill(vbm_tier * t, int64_t layer, const float * x, const 
         }
         const LayerWorkspace w = plan_layer(desc, T, t->pf_work);
         // 1. routing, input rows and grouping; the routed ids come to the host
-        launch_router(nullptr, nullptr, nullptr, H, const_cast<float *>(logits), E, T, K, w.ids, w.weights, s);
-        prefill_prepare(desc, x, w.ids, T, w, s);
+        prefill_prepare(desc, x, w.ids, T, w, s, false, logits, w.weights);   // top-k in the rows launch
         check_hip(hipMemcpyAsync(t->pf_ids_host, w.ids, sizeof(int32_t) * T * K, hipMemcpyDeviceToHost, s), "prefill ids");
         check_hip(hipStreamSynchronize(s), "prefill ids synchronize");
         int prefill_summary = 0;
