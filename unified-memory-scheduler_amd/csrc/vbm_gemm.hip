@@ -299,13 +299,11 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 3 : 1) void
     const int wj = wq * split;                         // the wave's first job in the tile
     const int half_end = wq ? live_jobs : (split < live_jobs ? split : live_jobs);
     bool jlive[JF];
-    int job[JF];
     int flagged = 0;
 #pragma unroll
     for (int jh = 0; jh < JF; ++jh) {
         const int jl = wj + 16 * jh + lr;
         jlive[jh] = jl < half_end;
-        job[jh] = jlive[jh] ? A.jobs[joff + j0 + jl] : 0;
         if (FLAGGED && jlive[jh]) flagged |= *reinterpret_cast<const int *>(row_of(jl) + A.lay.flag_offset());
     }
     // Fragment columns of 16 jobs none of which is live (a half's live jobs are a prefix of it) cost
@@ -743,9 +741,15 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 3 : 1) void
     // stores, so that each job's 64 rows leave as four full 64-byte segments instead of 4-byte
     // scatter.
     const bool via_lds = EPI == 1 || A.dst_vec4;
+    // the fragment columns' jobs and routing weights, loaded only now (held through the K loop they
+    // cost registers it needs)
+    int job[JF];
     float rscale[JF];
 #pragma unroll
-    for (int jh = 0; jh < JF; ++jh) rscale[jh] = EPI == 0 && A.row_scale && jlive[jh] ? A.row_scale[job[jh]] : 1.0f;
+    for (int jh = 0; jh < JF; ++jh) {
+        job[jh] = jlive[jh] ? A.jobs[joff + j0 + wj + 16 * jh + lr] : 0;
+        rscale[jh] = EPI == 0 && A.row_scale && jlive[jh] ? A.row_scale[job[jh]] : 1.0f;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
