@@ -64,14 +64,20 @@ __global__ __launch_bounds__(kGroupThreads) void group_scan_kernel(int n_chunks,
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     if (t == 0) s_bad = 0;
     __syncthreads();
-    // expert e = t: chunk bases (exclusive prefix over chunks) and the total
+    // expert e = t: chunk bases (exclusive prefix over chunks) and the total; eight chunks' counts
+    // are loaded before their bases are stored, so their loads are in flight together
     int c = 0;
     if (t < n_as) {
-        for (int k = 0; k < n_chunks; ++k) {
-            int32_t * cell = chunk_counts + static_cast<int64_t>(k) * (n_as + 1) + t;
-            const int v = *cell;
-            *cell = c;
-            c += v;
+        for (int k0 = 0; k0 < n_chunks; k0 += 8) {
+            int v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                v[j] = k0 + j < n_chunks ? chunk_counts[static_cast<int64_t>(k0 + j) * (n_as + 1) + t] : 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (k0 + j < n_chunks) chunk_counts[static_cast<int64_t>(k0 + j) * (n_as + 1) + t] = c;
+                c += v[j];
+            }
         }
     }
     for (int k = t; k < n_chunks; k += kGroupThreads)
