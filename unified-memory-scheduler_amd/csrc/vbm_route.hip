@@ -415,6 +415,23 @@ __global__ void glu_kernel(int activation, const float * __restrict__ gate, cons
 
 unsigned blocks_for(int64_t n, int threads) { return static_cast<unsigned>((n + threads - 1) / threads); }
 
+// Top-k + softmax of n_tokens tokens (workgroups 0..n_tokens-1, wave 0 of each) and the input's
+// activation rows (the other workgroups, one 32-lane group per block) in one launch.
+template <int NPL>
+__global__ __launch_bounds__(256) void topk_quantize_kernel(const float * __restrict__ logits, int n_expert, int top_k,
+                                                            int32_t * __restrict__ ids, float * __restrict__ weights,
+                                                            int64_t n_tokens, const float * __restrict__ x, int nb,
+                                                            int64_t x_stride, XrowLayout lay, uint8_t * __restrict__ xrows) {
+    const int64_t b = blockIdx.x;
+    if (b < n_tokens) {
+        if (threadIdx.x < 64)
+            wave_topk_softmax<NPL>(logits + b * n_expert, n_expert, top_k, ids + b * top_k, weights + b * top_k);
+        return;
+    }
+    quantize_expand_block(x, n_tokens, nb, x_stride, lay, xrows, static_cast<uint8_t *>(nullptr),
+                          (b - n_tokens) * 8 + (threadIdx.x >> 5), static_cast<int>(threadIdx.x & 31));
+}
+
 }  // namespace
 
 int64_t group_chunk_ints(int64_t n_as, int64_t n_entries) {
@@ -538,23 +555,6 @@ void launch_route_group_quantize(const float * logits, int64_t n_expert, int64_t
 // top-k launch.
 bool route_group_fits(int64_t n_expert, int64_t n_tokens, int64_t top_k) {
     return n_expert <= kMaxExperts && n_tokens * top_k <= kGroupChunk && n_tokens <= kGroupThreads / 64;
-}
-
-// Top-k + softmax of n_tokens tokens (workgroups 0..n_tokens-1, wave 0 of each) and the input's
-// activation rows (the other workgroups, one 32-lane group per block) in one launch.
-template <int NPL>
-__global__ __launch_bounds__(256) void topk_quantize_kernel(const float * __restrict__ logits, int n_expert, int top_k,
-                                                            int32_t * __restrict__ ids, float * __restrict__ weights,
-                                                            int64_t n_tokens, const float * __restrict__ x, int nb,
-                                                            int64_t x_stride, XrowLayout lay, uint8_t * __restrict__ xrows) {
-    const int64_t b = blockIdx.x;
-    if (b < n_tokens) {
-        if (threadIdx.x < 64)
-            wave_topk_softmax<NPL>(logits + b * n_expert, n_expert, top_k, ids + b * top_k, weights + b * top_k);
-        return;
-    }
-    quantize_expand_block(x, n_tokens, nb, x_stride, lay, xrows, static_cast<uint8_t *>(nullptr),
-                          (b - n_tokens) * 8 + (threadIdx.x >> 5), static_cast<int>(threadIdx.x & 31));
 }
 
 void launch_topk_quantize(const float * logits, int64_t n_expert, int64_t n_tokens, int64_t top_k, int32_t * ids,
