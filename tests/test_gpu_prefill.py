@@ -95,12 +95,14 @@ def test_gemm_power_of_two_scales_exact(gpu, orc, type_id):
 
 
 @pytest.mark.parametrize("type_id", [H.MX, H.Q8])
-@pytest.mark.parametrize("experts,n_ids,tokens", [(2, 2, 190), (3, 2, 257), (4, 2, 300), (2, 2, 300)])
+@pytest.mark.parametrize("experts,n_ids,tokens", [(2, 2, 190), (3, 2, 257), (4, 2, 300), (2, 2, 300), (2, 2, 192),
+                                                   (2, 2, 193), (2, 2, 385)])
 def test_gemm_multi_tile_experts_exact(gpu, orc, type_id, experts, n_ids, tokens):
-    """Experts with 130..300 routed jobs run the grouped GEMM over two or three 128-job tiles (full
-    ones and a partial last one). With unit scales every fp32 sum is an exact integer, so the GEMM must
-    match the oracle bit for bit, for fp32 inputs and for ggml Q8_0 inputs carrying -128 codes
-    (the flagged kernel)."""
+    """Experts with 150..385 routed jobs run the grouped GEMM over one to three job tiles (128 jobs
+    for MXFP4, 192 for Q8_0: full ones and a partial last one, down to a single job), each tile's
+    live jobs split between its two wave halves. With unit scales every fp32 sum is an exact
+    integer, so the GEMM must match the oracle bit for bit, for fp32 inputs and for ggml Q8_0
+    inputs carrying -128 codes (the flagged kernel)."""
     rng = np.random.default_rng(7000 + experts)
     rows, k = 128, 256
     w = (unit_scale_mxfp4 if type_id == H.MX else unit_scale_q8)(experts, rows, k, rng)
