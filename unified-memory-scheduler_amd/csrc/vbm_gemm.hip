@@ -21,10 +21,12 @@
 // exactly lane group q's k range, so a lane's A operand is two dwords of the bank as stored (the
 // staging loads only place them in LDS).
 //
-// A workgroup (4 waves) computes 64 bank rows (a tile pair) x 128 jobs of one expert; wave w owns
-// bank tile 2p + (w & 1) and jobs 64(w >> 1)..+63 as a 2x4 grid of 16x16 fragments. 128 jobs is
-// the mean group of a 2048-token top-8 prefill over 128 experts, so most experts' weights are
-// read once per row pair, and every weight operand feeds four MFMAs.
+// A workgroup (4 waves) computes 64 bank rows (a tile pair) x one job tile of one expert (192 jobs
+// for Q8_0, 128 for MXFP4); wave w owns bank tile 2p + (w & 1) and half w >> 1 of the tile's live
+// jobs (the halves split at a multiple of 16) as a 2 x (up to 6, resp. 4) grid of 16x16
+// fragments. A 2048-token top-8 prefill over 128 experts gives every expert 96-158 jobs, one Q8_0
+// tile, so each expert's weights are read once per row pair and every weight operand feeds up to
+// five MFMAs per wave.
 #include <type_traits>
 
 #include "vbm_device.hpp"
@@ -134,13 +136,13 @@ __device__ __forceinline__ half8_t i8_to_f16(long v) {
     return r;
 }
 // Pipeline stages, filled by global-to-LDS DMA: a ring of S chunks of CB blocks, each stage
-// holding the 128 jobs' activation codes and block scales of its chunk and, for MXFP4, both tiles'
+// holding the job tile's activation codes and block scales of its chunk and, for MXFP4, both tiles'
 // weight dwords of those blocks ([slice][row] dwords, rows of odd slice pairs rotated by 16
 // against bank conflicts) and their exponent dword per row. Q8_0 (GROUPED): a tile's weights of
 // one 4-block bank group are 4 KB contiguous in the bank, so both tiles' group weights are staged
 // once per group by 16-byte DMAs into a two-slot group ring beside the chunk ring ([tile][slice]
 // [row] 16-byte units, the bank's own order), with the group's fp16 scales ([tile][row] 8 bytes)
-// and the 128 jobs' activation block scales of the group ([job][4 blocks], 16 bytes each):
+// and the job tile's activation block scales of the group ([job][4 blocks], 16 bytes each):
 // a third of the chunk's DMA instructions, whose issue (not their bytes) bounded the kernel
 // (doubling the weight DMAs of the former per-chunk dword staging added 55 us to a 345 us
 // gate_up launch, doubling the activation DMAs 30 us). The same group staging for MXFP4 (8-block
@@ -475,7 +477,7 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 3 : 1) void
                                             : lds + G::OFF_MG + ((wave & 1) * 32 + lr) * 8;
         const float * d_lds = G::GROUPED ? reinterpret_cast<const float *>(lds + G::OFF_DG) + (wj + lr) * G::GB
                                          : reinterpret_cast<const float *>(lds + G::OFF_DA) + (wj + lr) * CB;
-        // fragment columns' activation codes: row rr = 64(w >> 1) + 16jh + lr, block bb, codes 8q..8q+7
+        // fragment columns' activation codes: row rr = wj + 16jh + lr, block bb, codes 8q..8q+7
         uint32_t aoff[JF][2];
 #pragma unroll
         for (int jh = 0; jh < JF; ++jh)
