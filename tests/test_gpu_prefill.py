@@ -359,3 +359,42 @@ def test_gemm_randomized_shapes_within_tolerance(gpu, orc):
         max_rel, cos = H.rel_err_and_cos(got, ref)
         assert max_rel <= 1e-3 and cos >= 0.99999, f"{label}: max_rel={max_rel:.3e} cos={cos:.9f}"
         bank.destroy()
+
+
+@pytest.mark.parametrize("type_id", [H.MX, H.Q8])
+def test_prefill_layer_unmapped_expert_poisons_its_tokens(gpu, type_id):
+    """Fast-order layer on the grouped GEMMs with one expert mapped to no slot: its workgroups
+    poison their GLU blocks and down rows, so exactly the tokens routed to it come out NaN after
+    the rank-ordered combine, every other token is bit-identical to the run with every expert
+    mapped, and repeated calls through the same workspace give the same bits."""
+    E, K, Hd, I, T = 8, 2, 256, 256, 256
+    layer = Layer(gpu, type_id, Hd, I, E, K, seed=5150 + type_id, router=False,
+                  activation=1 if type_id == H.MX else 0, order=gpu.ORDER_FAST)
+    x = gpu.synth_normal(5150 + type_id, 6, 0, T * Hd).reshape(T, Hd)
+    logits = gpu.synth_normal(5150 + type_id, 7, 0, T * E).reshape(T, E)
+    full, ids, _ = layer.forward_gpu(x, logits)
+    assert np.all(np.isfinite(full))
+    again, _, _ = layer.forward_gpu(x, logits)
+    assert H.bits_equal(again, full)
+    dead = 3
+    slot_map = np.arange(E, dtype=np.int32)
+    slot_map[dead] = -1
+    dmap = gpu.DeviceBuffer.from_array(slot_map)
+    d = layer.desc()
+    d.expert_to_slot = dmap.ptr
+    ws = C.c_size_t()
+    gpu.call("vbm_moe_layer_workspace", C.byref(d), T, C.byref(ws))
+    work = gpu.DeviceBuffer(ws.value)
+    dx, dl = gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer.from_array(logits)
+    out = gpu.DeviceBuffer(4 * T * Hd)
+    for rep in range(2):
+        gpu.call("vbm_memset", out.ptr, 0, 4 * T * Hd, None)
+        gpu.call("vbm_moe_layer_forward", C.byref(d), dx.ptr, dl.ptr, T, out.ptr, None, None, work.ptr, ws.value, None)
+        gpu.call("vbm_stream_synchronize", None)
+        got = out.download(np.float32, (T, Hd))
+        hit = np.any(ids == dead, axis=1)
+        print(f"[prefill unmapped expert type={type_id} rep={rep}] tokens on expert {dead}: {int(hit.sum())}", flush=True)
+        assert 0 < hit.sum() < T
+        assert np.all(np.isnan(got[hit]))
+        assert H.bits_equal(got[~hit], full[~hit]), H.diff_report(got[~hit], full[~hit])
+    layer.destroy()
