@@ -14,9 +14,9 @@
 //
 // Integer part (MXFP4): v_cvt_scalef32_pk_f16_fp4 with scale 2 turns the slice's four e2m1
 // nibbles into the doubled-e2m1 integers {0,1,2,3,4,6,8,12,...} as f16, and the slice dot against
-// the f16 activation codes is exact (integers below 2^24). The decode kernels and the batched
-// chunks of three or more tokens take it from v_mfma_f32_4x4x4_16b_f16 (16 blocks of 4 rows x 4
-// tokens with K = 4: exactly one slice); chunks of one or two tokens take two v_dot2. Q8_0 uses
+// the f16 activation codes is exact (integers below 2^24). The decode kernels and every batched
+// chunk without the -128 correction take it from v_mfma_f32_4x4x4_16b_f16 (16 blocks of 4 x 4
+// outputs with K = 4: exactly one slice); the correction path takes two v_dot2. Q8_0 uses
 // v_dot4. The VPSIGNB corner case (activation code -128 against a negative weight,
 // cpu_mxfp4_vnni.cpp:43-44) runs on a uniform slow path selected per activation row.
 //
@@ -130,12 +130,30 @@ __device__ __forceinline__ Group load_group(const uint8_t * cp, const uint8_t * 
 
 // One MXFP4 block of one lane for MT tokens: bytes SEL, SEL+1 of `dw` are the slice's 4 nibbles;
 // the activation slice (4 f16 codes, 8 B per block) and the block scale of each token are read
-// from LDS with wave-uniform addresses (broadcast).
+// from LDS (broadcast). Called by every lane of the wave (uniform control flow): the one- and
+// two-token form is a matrix-core instruction over the whole wave.
 template <int MT, bool SLOW, int SEL, int PAR>
 __device__ __forceinline__ void mx_block(unsigned dw, int e, int b, const uint8_t * la, const float * lda,
                                          int tok_bytes, int mcount, float (&acc)[MT][2]) {
     const half2_t w01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, SEL);
     const half2_t w23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(dw, 2.0f, SEL + 1);
+    if constexpr (MT <= 2 && !SLOW) {
+        // One v_mfma_f32_4x4x4_16b_f16 gives every token's slice dot: the row slice is B (lane =
+        // row) and lane 4q + r holds token r's activation slice as A, so register m of lane l is
+        // token m's dot with row l (exact: integers below 2^24), as in the single-token decode.
+        const int am = (threadIdx.x & 3) < mcount ? (threadIdx.x & 3) : 0;
+        const u32x2 a = *reinterpret_cast<const u32x2 *>(la + am * tok_bytes + b * 8);
+        const f32x4_t v = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, a), half4_t{w01.x, w01.y, w23.x, w23.y},
+                                                             f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m < mcount) {
+                const float d = *reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(lda) + m * tok_bytes + b * 4);
+                acc[m][PAR] = __builtin_fmaf(__builtin_amdgcn_ldexpf(d, e), v[m], acc[m][PAR]);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         if (m < mcount) {
