@@ -216,6 +216,19 @@ __device__ __forceinline__ void lds_dma_wait() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// The GLU of the fast accumulation order's epilogue: the formulas of glu() (SwiGLU-OAI with its
+// clamps, or SiLU), with the device library's fast exp (__expf) and a fast divide (__fdividef)
+// instead of the correctly rounded exp and the IEEE division the exact order needs. The fast
+// order is held to the tolerance of the fp32 layer outputs, not to bits.
+__device__ __forceinline__ float glu_fast(int activation, float g0, float u0, float alpha, float limit) {
+    if (activation == VBM_ACT_SWIGLU_OAI) {
+        const float g = limit < g0 ? limit : g0;
+        const float u = u0 < -limit ? -limit : (limit < u0 ? limit : u0);
+        return __fdividef(g, 1.0f + __expf(alpha * (-g))) * (u + 1.0f);
+    }
+    return __fdividef(g0, 1.0f + __expf(-g0)) * u0;
+}
+
 // fp16 x fp32 product on one instruction: v_fma_mix_f32 with the half in the low (HI = 0) or high
 // half of `h2` and -0 as the addend, i.e. exactly float(h) * x rounded once, signed zeros included.
 template <int HI>
@@ -802,7 +815,7 @@ __global__ __launch_bounds__(kGemmThreads, (TYPE == 8 && !FLAGGED) ? 3 : 1) void
                 const int tl = e >> 4;                      // bank tile of the pair
                 const float g = tile_vals[jl][32 * tl + (e & 15)];
                 const float u = tile_vals[jl][32 * tl + 16 + (e & 15)];
-                x[t] = glu(A.activation, g, u, A.alpha, A.limit);
+                x[t] = glu_fast(A.activation, g, u, A.alpha, A.limit);
             }
             float amax = 0.0f;
 #pragma unroll
