@@ -56,7 +56,8 @@ enum {
  *   VBM_ORDER_EXACT: the ggml x86 CPU contract — per 32-block integer dots split in eight
  *     4-element lanes, per-lane fp32 FMA chains (even/odd blocks for MXFP4), fixed final tree.
  *     Bit-identical to the CPU vec_dot.
- *   VBM_ORDER_FAST: per-block integer dots are still exact; the fp32 accumulation order is free.
+ *   VBM_ORDER_FAST: per-block integer dots are still exact; the fp32 accumulation order is free,
+ *     and a fused layer's GLU (gate_up GEMM epilogue) uses a fast exp and divide.
  *     Calls of >= 16 tokens with >= 12 routed rows per expert on average run the MFMA grouped GEMM;
  *     the others run the exact-order GEMV (faster there, and its results satisfy either order). */
 enum { VBM_ORDER_EXACT = 0, VBM_ORDER_FAST = 1 };
